@@ -1,0 +1,300 @@
+// INT8 block quantisation, router tile pooling and block top-k for gfx950.
+//
+// This translation unit is compiled with -ffp-contract=off: every fp32
+// product and sum below rounds separately, in the order written, so the
+// results are bit-identical to the CPU restatement in oracle/.
+//
+// Reference semantics:
+//   quantisation  models/sla2_vendor/kernel_sparse_qat.py:120-151
+//   tile pooling  models/mla_video_sparse_jvp.py:506-529, 545-562
+//   scores+top-k  models/mla_video_sparse_jvp.py:563-565, 292-294
+#include "common.h"
+
+namespace sla2h {
+
+constexpr int kTile = 64;  // E = D = 64
+
+struct QuantPoolArgs {
+  const uint16_t* x[2];   // (BH, L, 64) 16-bit
+  int8_t* xq[2];          // (BH, L, 64)
+  float* xs[2];           // (BH, Nb)
+  float* pool[2];         // q: (BH, Nb, 64); k: (BH, 64, npool) transposed; may be null
+  const float* proj[2];   // (64, 64) or null
+  int npool[2];           // number of leading blocks to pool
+  int64_t pool_len[2];    // rows that count for pooling (L for q, Np*E for k)
+  int transposed[2];
+  int BH;
+  int64_t L;
+  int Nb;
+};
+
+// One 64x64 tile per workgroup of 256 threads; blockIdx.y = tensor * BH + bh.
+template <typename T16>
+__global__ __launch_bounds__(256) void quant_pool_kernel(QuantPoolArgs a) {
+  __shared__ float tile[kTile][kTile + 1];
+  __shared__ float red[4];
+  __shared__ float vec[kTile];
+
+  const int tid = threadIdx.x;
+  const int blk = blockIdx.x;
+  const int t = blockIdx.y / a.BH;
+  const int bh = blockIdx.y % a.BH;
+  const int r = tid >> 2;
+  const int c0 = (tid & 3) * 16;
+  const int64_t row = (int64_t)blk * kTile + r;
+  const bool valid = row < a.L;
+  const int64_t off = ((int64_t)bh * a.L + row) * kTile + c0;
+
+  float xv[16];
+  if (valid) {
+    const uint4* src = reinterpret_cast<const uint4*>(a.x[t] + off);
+    uint4 u0 = src[0], u1 = src[1];
+    uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      xv[2 * i] = T16::to_f32((uint16_t)(w[i] & 0xffff));
+      xv[2 * i + 1] = T16::to_f32((uint16_t)(w[i] >> 16));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xv[i] = 0.f;
+  }
+
+  // block absmax (max is order-independent, so any reduction tree is exact)
+  float am = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) am = fmaxf(am, fabsf(xv[i]));
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) am = fmaxf(am, __shfl_xor(am, m, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = am;
+  __syncthreads();
+  am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = am / 127.0f + 1e-12f;  // IEEE division, then add
+
+  if (valid) {
+    uint32_t w[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      uint32_t acc = 0;
+#pragma unroll
+      for (int b = 0; b < 4; ++b) {
+        const float y = xv[4 * i + b] / s;
+        const int qv = (int)roundf(y);  // round half away from zero
+        acc |= ((uint32_t)(qv & 0xff)) << (8 * b);
+      }
+      w[i] = acc;
+    }
+    *reinterpret_cast<uint4*>(a.xq[t] + off) = make_uint4(w[0], w[1], w[2], w[3]);
+  }
+  if (tid == 0) a.xs[t][(int64_t)bh * a.Nb + blk] = s;
+
+  if (a.pool[t] == nullptr || blk >= a.npool[t]) return;
+
+  // ---- pooling: sequential per-channel fp32 sum over the real rows ----
+#pragma unroll
+  for (int i = 0; i < 16; ++i) tile[r][c0 + i] = xv[i];
+  __syncthreads();
+  const int64_t rem = a.pool_len[t] - (int64_t)blk * kTile;
+  const int cnt = rem < kTile ? (int)rem : kTile;
+  if (tid < kTile) {
+    float acc = 0.f;
+    for (int rr = 0; rr < cnt; ++rr) acc = acc + tile[rr][tid];
+    vec[tid] = acc / (float)cnt;
+  }
+  __syncthreads();
+  if (tid < kTile) {
+    float outv = vec[tid];
+    if (a.proj[t] != nullptr) {
+      const float* pr = a.proj[t] + tid * kTile;  // row e of proj: out[e] = sum_d x[d] P[e,d]
+      float acc = 0.f;
+      for (int d = 0; d < kTile; ++d) acc = acc + vec[d] * pr[d];
+      outv = acc;
+    }
+    if (a.transposed[t])
+      a.pool[t][((int64_t)bh * kTile + tid) * a.npool[t] + blk] = outv;
+    else
+      a.pool[t][((int64_t)bh * a.Nb + blk) * kTile + tid] = outv;
+  }
+}
+
+// Orderable 64-bit key: high word = monotone map of the fp32 score
+// (NaN -> +NaN, the largest, as torch.topk orders; -0 -> +0), low word =
+// ~index so that equal scores rank the lower index first.
+__device__ inline uint64_t score_key(float sc, int n) {
+  uint32_t u = __builtin_bit_cast(uint32_t, sc);
+  if (sc != sc) u = 0x7fc00000u;
+  if (u == 0x80000000u) u = 0u;
+  const uint32_t ord = (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+  return ((uint64_t)ord << 32) | (uint64_t)(0xffffffffu - (uint32_t)n);
+}
+
+// ROWS query blocks of one (b,h) per workgroup: scores into LDS, one
+// bitonic sort (descending) per row over P2 = next_pow2(Np) keys, emit top T.
+template <int ROWS>
+__global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict__ qpool,
+                                                         const float* __restrict__ kpool_t,
+                                                         int Mb, int Np, int T, float scale,
+                                                         int P2, int32_t* __restrict__ lut,
+                                                         uint8_t* __restrict__ mask) {
+  extern __shared__ __align__(16) unsigned char smem[];
+  uint64_t* keys = reinterpret_cast<uint64_t*>(smem);                 // ROWS * P2
+  float* qsh = reinterpret_cast<float*>(smem + (size_t)ROWS * P2 * 8);  // ROWS * 64
+  uint8_t* sel = smem + (size_t)ROWS * P2 * 8 + ROWS * kTile * 4;      // ROWS * P2
+
+  const int tid = threadIdx.x;
+  const int bh = blockIdx.y;
+  const int m0 = blockIdx.x * ROWS;
+
+  for (int idx = tid; idx < ROWS * kTile; idx += 256) {
+    const int rr = idx / kTile, d = idx % kTile;
+    const int m = m0 + rr;
+    qsh[idx] = (m < Mb) ? qpool[((int64_t)bh * Mb + m) * kTile + d] : 0.f;
+  }
+  for (int idx = tid; idx < ROWS * P2; idx += 256) sel[idx] = 0;
+  __syncthreads();
+
+  const float* kt = kpool_t + (int64_t)bh * kTile * Np;
+  for (int n = tid; n < P2; n += 256) {
+    if (n < Np) {
+      float acc[ROWS];
+#pragma unroll
+      for (int rr = 0; rr < ROWS; ++rr) acc[rr] = 0.f;
+      for (int d = 0; d < kTile; ++d) {
+        const float kv = kt[(int64_t)d * Np + n];
+#pragma unroll
+        for (int rr = 0; rr < ROWS; ++rr) acc[rr] = acc[rr] + qsh[rr * kTile + d] * kv;
+      }
+#pragma unroll
+      for (int rr = 0; rr < ROWS; ++rr) keys[rr * P2 + n] = score_key(acc[rr] * scale, n);
+    } else {
+#pragma unroll
+      for (int rr = 0; rr < ROWS; ++rr) keys[rr * P2 + n] = 0ull;  // below every real key
+    }
+  }
+  __syncthreads();
+
+  const int half = P2 >> 1;
+  for (int k = 2; k <= P2; k <<= 1) {
+    for (int j = k >> 1; j > 0; j >>= 1) {
+      for (int idx = tid; idx < ROWS * half; idx += 256) {
+        const int rr = idx / half, h = idx % half;
+        const int i = (h / j) * 2 * j + (h % j);
+        const int l = i + j;
+        uint64_t* row = keys + rr * P2;
+        const uint64_t ki = row[i], kl = row[l];
+        const bool desc = (i & k) == 0;  // overall order: descending
+        if (desc ? (ki < kl) : (ki > kl)) {
+          row[i] = kl;
+          row[l] = ki;
+        }
+      }
+      __syncthreads();
+    }
+  }
+
+  for (int idx = tid; idx < ROWS * T; idx += 256) {
+    const int rr = idx / T, jj = idx % T;
+    const int m = m0 + rr;
+    const uint32_t n = 0xffffffffu - (uint32_t)(keys[rr * P2 + jj] & 0xffffffffull);
+    if (m < Mb) lut[((int64_t)bh * Mb + m) * T + jj] = (int32_t)n;
+    sel[rr * P2 + n] = 1;
+  }
+  if (mask == nullptr) return;
+  __syncthreads();
+  for (int idx = tid; idx < ROWS * Np; idx += 256) {
+    const int rr = idx / Np, n = idx % Np;
+    const int m = m0 + rr;
+    if (m < Mb) mask[((int64_t)bh * Mb + m) * Np + n] = sel[rr * P2 + n];
+  }
+}
+
+}  // namespace sla2h
+
+using namespace sla2h;
+
+static int launch_quant_pool(const QuantPoolArgs& a, int ntens, int dtype, hipStream_t st) {
+  dim3 grid(a.Nb, ntens * a.BH);
+  if (dtype == SLA2H_DTYPE_BF16)
+    quant_pool_kernel<BF16><<<grid, 256, 0, st>>>(a);
+  else
+    quant_pool_kernel<F16><<<grid, 256, 0, st>>>(a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_version(void) { return 1; }
+
+extern "C" const char* sla2h_error_string(int code) {
+  return hipGetErrorString((hipError_t)code);
+}
+
+extern "C" int sla2h_quantize(const void* x, int dtype, int64_t BH, int64_t L, int D, int E,
+                              int8_t* xq, float* xs, void* stream) {
+  SLA2H_CHECK_ARG(x && xq && xs);
+  SLA2H_CHECK_ARG(D == kTile && E == kTile);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(BH > 0 && BH <= 65535 && L > 0);
+  if (BH * L * D == 0) return 0;
+  QuantPoolArgs a = {};
+  a.x[0] = static_cast<const uint16_t*>(x);
+  a.xq[0] = xq;
+  a.xs[0] = xs;
+  a.BH = (int)BH;
+  a.L = L;
+  a.Nb = (int)((L + E - 1) / E);
+  return launch_quant_pool(a, 1, dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sla2h_quant_pool_qk(const void* q, const void* k, int dtype, int B, int H,
+                                   int64_t L, int D, int E, int Np, const float* proj_q,
+                                   const float* proj_k, int8_t* q8, float* qs, int8_t* k8,
+                                   float* ks, float* qpool, float* kpool_t, void* stream) {
+  SLA2H_CHECK_ARG(q && k && q8 && qs && k8 && ks && qpool && kpool_t);
+  SLA2H_CHECK_ARG(D == kTile && E == kTile);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && (int64_t)B * H * 2 <= 65535);
+  SLA2H_CHECK_ARG(Np > 0 && (int64_t)Np * E <= L);
+  QuantPoolArgs a = {};
+  a.BH = B * H;
+  a.L = L;
+  a.Nb = (int)((L + E - 1) / E);
+  a.x[0] = static_cast<const uint16_t*>(q);
+  a.x[1] = static_cast<const uint16_t*>(k);
+  a.xq[0] = q8;
+  a.xq[1] = k8;
+  a.xs[0] = qs;
+  a.xs[1] = ks;
+  a.pool[0] = qpool;
+  a.pool[1] = kpool_t;
+  a.proj[0] = proj_q;
+  a.proj[1] = proj_k;
+  a.npool[0] = a.Nb;
+  a.npool[1] = Np;
+  a.pool_len[0] = L;
+  a.pool_len[1] = (int64_t)Np * E;
+  a.transposed[0] = 0;
+  a.transposed[1] = 1;
+  return launch_quant_pool(a, 2, dtype, static_cast<hipStream_t>(stream));
+}
+
+extern "C" int sla2h_route_topk(const float* qpool, const float* kpool_t, int B, int H, int Mb,
+                                int Np, int D, int T, float scale, int32_t* lut, uint8_t* mask,
+                                void* stream) {
+  SLA2H_CHECK_ARG(qpool && kpool_t && lut);
+  SLA2H_CHECK_ARG(D == kTile);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && Mb > 0);
+  SLA2H_CHECK_ARG(Np > 0 && Np <= 4096 && T >= 1 && T <= Np);
+  int P2 = 1;
+  while (P2 < Np) P2 <<= 1;
+  if (P2 < 2) P2 = 2;
+  const int rows = P2 <= 512 ? 8 : (P2 <= 1024 ? 4 : (P2 <= 2048 ? 2 : 1));
+  const size_t shmem = (size_t)rows * P2 * 8 + (size_t)rows * kTile * 4 + (size_t)rows * P2;
+  dim3 grid((Mb + rows - 1) / rows, B * H);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  switch (rows) {
+    case 8: route_topk_kernel<8><<<grid, 256, shmem, st>>>(qpool, kpool_t, Mb, Np, T, scale, P2, lut, mask); break;
+    case 4: route_topk_kernel<4><<<grid, 256, shmem, st>>>(qpool, kpool_t, Mb, Np, T, scale, P2, lut, mask); break;
+    case 2: route_topk_kernel<2><<<grid, 256, shmem, st>>>(qpool, kpool_t, Mb, Np, T, scale, P2, lut, mask); break;
+    default: route_topk_kernel<1><<<grid, 256, shmem, st>>>(qpool, kpool_t, Mb, Np, T, scale, P2, lut, mask); break;
+  }
+  return (int)hipGetLastError();
+}

@@ -1,0 +1,348 @@
+// Linear-branch states (phi(K)^T V per video tile, their tangents and global
+// sums), the transposed value tiles used by the attention kernel, and the
+// per-query-block complement records.
+//
+// Reference semantics:
+//   phi / states   models/sla2_cube_qat.py:911-958 (_phi_states_kernel)
+//   global sums    models/sla2_cube_qat.py:645-648
+//   complement     models/sla2_cube_qat.py:510-523, 570-578
+#include "common.h"
+
+namespace sla2h {
+
+constexpr int kT = 64;          // E = D = 64
+constexpr int kLds = kT + 8;    // padded LDS row (16-bit elements)
+constexpr size_t kRecBytes = 2 * 16384 + 2 * 256;
+
+// One tile (b,h,n) per workgroup.  n < Np: phi, states; every n < Nb:
+// transposed value tiles vt/dvt (rows past L are zero).
+//
+// Products phi^T V run on 16-bit MFMA with phi split into hi + lo halves of
+// the input's 16-bit type (about 16 significant bits), fp32 accumulate.
+template <typename T16, bool TAN>
+__global__ __launch_bounds__(256) void linear_states_kernel(
+    const uint16_t* __restrict__ K, const uint16_t* __restrict__ dK,
+    const uint16_t* __restrict__ V, const uint16_t* __restrict__ dV, int64_t L, int Np, int Nb,
+    float* __restrict__ Hb, float* __restrict__ dHb, float* __restrict__ zb,
+    float* __restrict__ dzb, uint16_t* __restrict__ vt, uint16_t* __restrict__ dvt) {
+  __shared__ __align__(16) uint16_t phiT[2][kT][kLds];   // [hi/lo][d][r]
+  __shared__ __align__(16) uint16_t dphiT[2][kT][kLds];
+  __shared__ __align__(16) uint16_t vT[kT][kLds];        // [c][r]
+  __shared__ __align__(16) uint16_t dvT[kT][kLds];
+  __shared__ float zred[2][4][kT];
+
+  const int tid = threadIdx.x;
+  const int n = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int r = tid >> 2;
+  const int c0 = (tid & 3) * 16;
+  const int64_t row = (int64_t)n * kT + r;
+  const bool valid = row < L;
+  const int64_t off = ((int64_t)bh * L + row) * kT + c0;
+
+  auto load16 = [&](const uint16_t* src, uint16_t* dst) {
+    if (valid) {
+      const uint4* s = reinterpret_cast<const uint4*>(src + off);
+      uint4 u0 = s[0], u1 = s[1];
+      uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        dst[2 * i] = (uint16_t)(w[i] & 0xffff);
+        dst[2 * i + 1] = (uint16_t)(w[i] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dst[i] = 0;
+    }
+  };
+
+  uint16_t vb[16], dvb[16];
+  load16(V, vb);
+  if (TAN) load16(dV, dvb);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    vT[c0 + i][r] = vb[i];
+    if (TAN) dvT[c0 + i][r] = dvb[i];
+  }
+
+  const bool states = n < Np;  // uniform over the workgroup
+  if (states) {
+    uint16_t kb[16], dkb[16];
+    load16(K, kb);
+    if (TAN) load16(dK, dkb);
+    float x[16], phi[16], dphi[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x[i] = T16::to_f32(kb[i]);
+      mx = fmaxf(mx, x[i]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    float den = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      phi[i] = __expf(x[i] - mx);
+      den += phi[i];
+    }
+    den += __shfl_xor(den, 1, 64);
+    den += __shfl_xor(den, 2, 64);
+#pragma unroll
+    for (int i = 0; i < 16; ++i) phi[i] = phi[i] / den;
+    if (TAN) {
+      float dot = 0.f;
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dot += phi[i] * T16::to_f32(dkb[i]);
+      dot += __shfl_xor(dot, 1, 64);
+      dot += __shfl_xor(dot, 2, 64);
+#pragma unroll
+      for (int i = 0; i < 16; ++i) dphi[i] = phi[i] * (T16::to_f32(dkb[i]) - dot);
+    }
+    if (!valid) {  // cannot happen for video tiles; keeps padding rows inert
+#pragma unroll
+      for (int i = 0; i < 16; ++i) phi[i] = dphi[i] = 0.f;
+    }
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint16_t hi = T16::from_f32(phi[i]);
+      phiT[0][c0 + i][r] = hi;
+      phiT[1][c0 + i][r] = T16::from_f32(phi[i] - T16::to_f32(hi));
+      if (TAN) {
+        const uint16_t dhi = T16::from_f32(dphi[i]);
+        dphiT[0][c0 + i][r] = dhi;
+        dphiT[1][c0 + i][r] = T16::from_f32(dphi[i] - T16::to_f32(dhi));
+      }
+    }
+    // column sums over the 64 rows: 16 rows per wave by shuffles, then LDS
+    const int w = tid >> 6;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      float s = phi[i];
+      float ds = TAN ? dphi[i] : 0.f;
+#pragma unroll
+      for (int m = 4; m <= 32; m <<= 1) {
+        s += __shfl_xor(s, m, 64);
+        if (TAN) ds += __shfl_xor(ds, m, 64);
+      }
+      if ((tid & 63) < 4) {
+        zred[0][w][c0 + i] = s;
+        if (TAN) zred[1][w][c0 + i] = ds;
+      }
+    }
+  }
+  __syncthreads();
+
+  // transposed value tiles: vt[bh, n, c, r]
+  {
+    const int c = tid >> 2;
+    const int r0 = (tid & 3) * 16;
+    const int64_t vo = (((int64_t)bh * Nb + n) * kT + c) * kT + r0;
+    const uint4* s = reinterpret_cast<const uint4*>(&vT[c][r0]);
+    uint4* d = reinterpret_cast<uint4*>(vt + vo);
+    d[0] = s[0];
+    d[1] = s[1];
+    if (TAN) {
+      const uint4* s2 = reinterpret_cast<const uint4*>(&dvT[c][r0]);
+      uint4* d2 = reinterpret_cast<uint4*>(dvt + vo);
+      d2[0] = s2[0];
+      d2[1] = s2[1];
+    }
+  }
+  if (!states) return;
+
+  if (tid < kT) {
+    const int64_t zo = ((int64_t)bh * Np + n) * kT + tid;
+    zb[zo] = (zred[0][0][tid] + zred[0][1][tid]) + (zred[0][2][tid] + zred[0][3][tid]);
+    if (TAN) dzb[zo] = (zred[1][0][tid] + zred[1][1][tid]) + (zred[1][2][tid] + zred[1][3][tid]);
+  }
+
+  // Hb[d][v] = sum_r phi[r][d] V[r][v]: wave w owns d rows 16w..16w+15.
+  const int w = tid >> 6, l = tid & 63, lr = l & 15, g = l >> 4;
+  const int drow = 16 * w + lr;
+  f32x4 acc[4], dacc[4];
+#pragma unroll
+  for (int vt_ = 0; vt_ < 4; ++vt_) {
+    acc[vt_] = f32x4{0.f, 0.f, 0.f, 0.f};
+    dacc[vt_] = acc[vt_];
+  }
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const int k0 = 32 * ks + 8 * g;
+    const u32x4 ah = *reinterpret_cast<const u32x4*>(&phiT[0][drow][k0]);
+    const u32x4 al = *reinterpret_cast<const u32x4*>(&phiT[1][drow][k0]);
+    u32x4 dah, dal;
+    if (TAN) {
+      dah = *reinterpret_cast<const u32x4*>(&dphiT[0][drow][k0]);
+      dal = *reinterpret_cast<const u32x4*>(&dphiT[1][drow][k0]);
+    }
+#pragma unroll
+    for (int vt_ = 0; vt_ < 4; ++vt_) {
+      const u32x4 bv = *reinterpret_cast<const u32x4*>(&vT[16 * vt_ + lr][k0]);
+      acc[vt_] = mfma_16x16x32<T16>(ah, bv, acc[vt_]);
+      acc[vt_] = mfma_16x16x32<T16>(al, bv, acc[vt_]);
+      if (TAN) {
+        const u32x4 bdv = *reinterpret_cast<const u32x4*>(&dvT[16 * vt_ + lr][k0]);
+        dacc[vt_] = mfma_16x16x32<T16>(dah, bv, dacc[vt_]);
+        dacc[vt_] = mfma_16x16x32<T16>(dal, bv, dacc[vt_]);
+        dacc[vt_] = mfma_16x16x32<T16>(ah, bdv, dacc[vt_]);
+        dacc[vt_] = mfma_16x16x32<T16>(al, bdv, dacc[vt_]);
+      }
+    }
+  }
+  const int64_t hbase = ((int64_t)bh * Np + n) * kT * kT;
+#pragma unroll
+  for (int vt_ = 0; vt_ < 4; ++vt_) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int64_t o = hbase + (int64_t)(16 * w + 4 * g + i) * kT + 16 * vt_ + lr;
+      Hb[o] = acc[vt_][i];
+      if (TAN) dHb[o] = dacc[vt_][i];
+    }
+  }
+}
+
+// Global sums over the Np tiles, sequential in n (deterministic).
+// Column index e spans [Hb 4096 | dHb 4096 | zb 64 | dzb 64].
+__global__ __launch_bounds__(256) void states_sum_kernel(const float* __restrict__ Hb,
+                                                        const float* __restrict__ dHb,
+                                                        const float* __restrict__ zb,
+                                                        const float* __restrict__ dzb, int Np,
+                                                        float* __restrict__ Hall,
+                                                        float* __restrict__ dHall,
+                                                        float* __restrict__ zall,
+                                                        float* __restrict__ dzall) {
+  const int e = blockIdx.x * 256 + threadIdx.x;
+  const int bh = blockIdx.y;
+  const float* src;
+  float* dst;
+  int stride, col;
+  if (e < 4096) {
+    src = Hb; dst = Hall; stride = 4096; col = e;
+  } else if (e < 8192) {
+    src = dHb; dst = dHall; stride = 4096; col = e - 4096;
+  } else if (e < 8256) {
+    src = zb; dst = zall; stride = 64; col = e - 8192;
+  } else if (e < 8320) {
+    src = dzb; dst = dzall; stride = 64; col = e - 8256;
+  } else {
+    return;
+  }
+  if (src == nullptr) return;
+  const float* p = src + (int64_t)bh * Np * stride + col;
+  float acc = 0.f;
+  for (int nn = 0; nn < Np; ++nn) acc += p[(int64_t)nn * stride];
+  dst[(int64_t)bh * stride + col] = acc;
+}
+
+// Complement record of query block m: Hc = Hall - sum_j Hb[lut[m,j]] in LUT
+// order (fp32), stored as bf16 hi/lo MFMA A-operand fragments:
+//   u16 index (((vt*2 + ks)*64 + lane)*16 + j [+8 for lo]),
+//   v = 16 vt + lane%16, d = 32 ks + 8 (lane/16) + j, value Hc[d][v];
+// then dHc at byte 16384, zc at 32768, dzc at 33024 (fp32).
+__global__ __launch_bounds__(256) void complement_kernel(
+    const float* __restrict__ Hb, const float* __restrict__ dHb, const float* __restrict__ zb,
+    const float* __restrict__ dzb, const float* __restrict__ Hall,
+    const float* __restrict__ dHall, const float* __restrict__ zall,
+    const float* __restrict__ dzall, const int32_t* __restrict__ lut, int Mb, int Np, int T,
+    unsigned char* __restrict__ comp) {
+  const int m = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int32_t* lrow = lut + ((int64_t)bh * Mb + m) * T;
+  unsigned char* rec = comp + ((int64_t)bh * Mb + m) * kRecBytes;
+  const bool tan = dHb != nullptr;
+  for (int e = threadIdx.x; e < 8320; e += 256) {
+    const float* src;
+    const float* all;
+    int stride, col, part;
+    if (e < 4096) {
+      src = Hb; all = Hall; stride = 4096; col = e; part = 0;
+    } else if (e < 8192) {
+      src = dHb; all = dHall; stride = 4096; col = e - 4096; part = 1;
+    } else if (e < 8256) {
+      src = zb; all = zall; stride = 64; col = e - 8192; part = 2;
+    } else {
+      src = dzb; all = dzall; stride = 64; col = e - 8256; part = 3;
+    }
+    if (!tan && (part & 1)) continue;
+    float acc = all[(int64_t)bh * stride + col];
+    const float* sb = src + (int64_t)bh * Np * stride + col;
+    for (int j = 0; j < T; ++j) {
+      const int nn = lrow[j];
+      if ((unsigned)nn < (unsigned)Np) acc -= sb[(int64_t)nn * stride];  // ignore corrupt ids
+    }
+    if (part >= 2) {
+      reinterpret_cast<float*>(rec + 32768 + (part - 2) * 256)[col] = acc;
+    } else {
+      const int d = col >> 6, v = col & 63;
+      const int vt_ = v >> 4, lr = v & 15, ks = d >> 5, g = (d & 31) >> 3, j = d & 7;
+      const int lane = g * 16 + lr;
+      uint16_t* base = reinterpret_cast<uint16_t*>(rec + part * 16384);
+      const uint16_t hi = bf16_bits(acc);
+      const uint16_t lo = bf16_bits(acc - bf16_val(hi));
+      const int idx = ((vt_ * 2 + ks) * 64 + lane) * 16 + j;
+      base[idx] = hi;
+      base[idx + 8] = lo;
+    }
+  }
+}
+
+}  // namespace sla2h
+
+using namespace sla2h;
+
+extern "C" size_t sla2h_complement_record_bytes(int D) { return D == kT ? kRecBytes : 0; }
+
+extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v, const void* dv,
+                                   int dtype, int B, int H, int64_t L, int D, int E, int Np,
+                                   float* Hb, float* dHb, float* zb, float* dzb, float* Hall,
+                                   float* dHall, float* zall, float* dzall, void* vt, void* dvt,
+                                   void* stream) {
+  SLA2H_CHECK_ARG(k && v && Hb && zb && Hall && zall && vt);
+  SLA2H_CHECK_ARG(D == kT && E == kT);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535);
+  SLA2H_CHECK_ARG(Np > 0 && (int64_t)Np * E <= L);
+  const bool tan = dk != nullptr;
+  if (tan) SLA2H_CHECK_ARG(dv && dHb && dzb && dHall && dzall && dvt);
+  const int Nb = (int)((L + E - 1) / E);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(Nb, B * H);
+  auto K = static_cast<const uint16_t*>(k);
+  auto dK = static_cast<const uint16_t*>(dk);
+  auto V = static_cast<const uint16_t*>(v);
+  auto dV = static_cast<const uint16_t*>(dv);
+  auto VT = static_cast<uint16_t*>(vt);
+  auto dVT = static_cast<uint16_t*>(dvt);
+  if (dtype == SLA2H_DTYPE_BF16) {
+    if (tan)
+      linear_states_kernel<BF16, true><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT, dVT);
+    else
+      linear_states_kernel<BF16, false><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT, dVT);
+  } else {
+    if (tan)
+      linear_states_kernel<F16, true><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT, dVT);
+    else
+      linear_states_kernel<F16, false><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT, dVT);
+  }
+  int err = (int)hipGetLastError();
+  if (err) return err;
+  dim3 g2((8320 + 255) / 256, B * H);
+  states_sum_kernel<<<g2, 256, 0, st>>>(Hb, tan ? dHb : nullptr, zb, tan ? dzb : nullptr, Np, Hall,
+                                        dHall, zall, dzall);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_complement(const float* Hb, const float* dHb, const float* zb,
+                                const float* dzb, const float* Hall, const float* dHall,
+                                const float* zall, const float* dzall, const int32_t* lut, int B,
+                                int H, int Mb, int Np, int D, int T, void* comp, void* stream) {
+  SLA2H_CHECK_ARG(Hb && zb && Hall && zall && lut && comp);
+  SLA2H_CHECK_ARG(D == kT);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && Mb > 0 && Np > 0 && T >= 1 && T <= Np);
+  if (dHb) SLA2H_CHECK_ARG(dzb && dHall && dzall);
+  dim3 grid(Mb, B * H);
+  complement_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
+      Hb, dHb, zb, dzb, Hall, dHall, zall, dzall, lut, Mb, Np, T,
+      static_cast<unsigned char*>(comp));
+  return (int)hipGetLastError();
+}

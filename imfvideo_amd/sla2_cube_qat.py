@@ -1,0 +1,173 @@
+"""SLA2 cube-tile sparse-linear attention with INT8 QAT: forward and forward-mode JVP.
+
+Same module and function names, signatures and return conventions as the
+reference's models/sla2_cube_qat.py, computed by gfx950 HIP kernels through
+the C ABI of include/sla2h.h:
+
+  sla2_cube_qat_jvp_fused  (reference :605-672)  quant+pool -> route -> states
+                           -> complement -> fused attention kernel
+  sla2_cube_qat_jvp        (reference :210-289)  same kernels
+  _sparse_primal_only      (reference :172-207)  sparse branch only
+  SLA2CubeQATAttentionImpl (reference :295-439)  the attn_impl module
+
+Inputs are (B, H, L, D) tile-major tensors (L = Np*E + P, the P prefix
+tokens last).  16-bit inputs keep their type (bf16 or fp16); fp32 inputs are
+rounded to ``COMPUTE_DTYPE`` (bfloat16) -- the reference rounds to fp16.
+"""
+
+import math
+
+import torch
+import torch.nn as nn
+
+from . import ops
+from .mla_video_sparse_jvp import _plenty_of_vram, route_tiles, route_tiles_fast, tile_permutation
+
+__all__ = ["SLA2CubeQATAttentionImpl", "sla2_cube_qat_jvp", "sla2_cube_qat_jvp_fused"]
+
+_EPS_L = 1e-5
+COMPUTE_DTYPE = torch.bfloat16
+
+
+def _c16(x, dtype=None):
+    if dtype is None:
+        dtype = x.dtype if x.dtype in (torch.float16, torch.bfloat16) else COMPUTE_DTYPE
+    return x.to(dtype).contiguous()
+
+
+def _alpha_tensor(alpha, H, Mb, device):
+    """(H, Mb) fp32 mix ratio from a tensor or a scalar."""
+    if torch.is_tensor(alpha) and alpha.dim() == 2:
+        return alpha.detach().to(device, torch.float32)
+    a = float(alpha.item() if torch.is_tensor(alpha) else alpha)
+    return torch.full((H, Mb), a, device=device, dtype=torch.float32)
+
+
+def _check_geometry(L, Np, E, prefix_len):
+    assert E == ops.E_TILE, f"E must be {ops.E_TILE} (quantisation block = tile), got {E}"
+    assert L == Np * E + prefix_len, (L, Np, E, prefix_len)
+
+
+@torch.no_grad()
+def sla2_cube_qat_jvp_fused(q, k, v, dq, dk, dv, alpha, topk_frac, Np, E, prefix_len,
+                            proj_q=None, proj_k=None, lut=None, T=None):
+    """Fused cube-QAT JVP: both branches and the mix in one attention kernel.
+
+    Args:
+        q..dv: (B, H, L, D) primal / tangent, tile-major order.
+        alpha: (H, Mb) mixing ratio in (0, 1) (after the sigmoid), or scalar.
+        topk_frac: routed fraction of the Np video tiles (ignored when lut given).
+        Np, E, prefix_len: tiling geometry; E = 64.
+        proj_q, proj_k: optional (D, D) router projections.
+        lut, T: optional precomputed routing (B, H, Mb, T).
+
+    Returns:
+        (o, do): (B, H, L, D) fp32.
+    """
+    B, H, L, D = q.shape
+    _check_geometry(L, Np, E, prefix_len)
+    dt = _c16(q).dtype
+    qc, kc, vc, dqc, dkc, dvc = (_c16(t, dt) for t in (q, k, v, dq, dk, dv))
+    Mb = -(-L // E)
+    a = _alpha_tensor(alpha, H, Mb, q.device)
+    return ops.cube_jvp(qc, kc, vc, dqc, dkc, dvc, a, topk_frac, Np, prefix_len,
+                        proj_q, proj_k, lut=lut, T=T)
+
+
+def sla2_cube_qat_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, Np, E, prefix_len,
+                      proj_q=None, proj_k=None, lut=None, T=None):
+    """Cube-block QAT attention (primal, tangent) -- reference :210-289.
+
+    Same kernels as ``sla2_cube_qat_jvp_fused``.  The reference's unfused
+    variant differs from the fused one only at rounding level (fp16-accumulated
+    tangent dots, unsigned linear-branch epsilon); this build serves both
+    names with the fused kernel.
+    """
+    return sla2_cube_qat_jvp_fused(q, k, v, dq, dk, dv, alpha, topk_frac, Np, E, prefix_len,
+                                   proj_q, proj_k, lut, T)
+
+
+@torch.no_grad()
+def _sparse_primal_only(q, k, v, lut, T, Np, E, prefix_len):
+    """Primal sparse branch only (INT8 scores, 16-bit P.V) -> o_s (B,H,L,D) fp32."""
+    B, H, L, D = q.shape
+    _check_geometry(L, Np, E, prefix_len)
+    dt = _c16(q).dtype
+    qc, kc, vc = (_c16(t, dt) for t in (q, k, v))
+    lut = lut.to(torch.int32).contiguous()
+    q8, qs, k8, ks, _, _ = ops.quant_pool_qk(qc, kc, Np, E)
+    st = ops.linear_states(kc, vc, Np)
+    o, _ = ops.fwd_jvp(qc, kc, q8, k8, qs, ks, st, None, None, lut, Np, sparse_only=True)
+    return o
+
+
+class SLA2CubeQATAttentionImpl(nn.Module):
+    """attn_impl: cube-block sparse-linear attention with INT8 QAT (reference :295-439).
+
+    Args:
+        head_dim: qk head dim D (= v head dim, 64).
+        seq_len: L = prefix + patches.
+        num_heads: H.
+        grid: (T, Hh, Ww) patch grid.
+        tile: (tt, th, tw) 3D tile, prod = E = 64.
+        topk: routed fraction of video tiles.
+        alpha_init: initial sparse/linear mixing ratio in (0, 1).
+        use_int8: INT8 primal scores (the only mode of this build).
+        pre_permuted: tokens are already tile-major.
+
+    The forward runs the fused INT8 primal kernel (the JVP kernel's INT8
+    semantics).  The autograd backward of the training path is not part of
+    this build yet: calling the module with gradients required raises.
+    """
+
+    TILE_MAJOR = True
+
+    def __init__(self, head_dim, seq_len, num_heads, grid, tile=(4, 4, 4), topk=0.03,
+                 alpha_init=0.9, use_int8=True, pre_permuted=False):
+        super().__init__()
+        self.pre_permuted = pre_permuted
+        self.E = tile[0] * tile[1] * tile[2]
+        self.topk_frac = topk
+        self.use_int8 = use_int8
+        n_patch = grid[0] * grid[1] * grid[2]
+        self.prefix_len = seq_len - n_patch
+        perm, inv, self.Np = tile_permutation(grid, tile, self.prefix_len, torch.device("cpu"))
+        self.register_buffer("perm", perm, persistent=False)
+        self.register_buffer("inv", inv, persistent=False)
+        self.n_tail = -(-self.prefix_len // self.E)
+        self.Mb = self.Np + self.n_tail
+        rows = torch.arange(seq_len)
+        self.register_buffer("a_index", torch.clamp(rows // self.E, max=self.Mb - 1),
+                             persistent=False)
+        self.Nb = math.ceil(seq_len / self.E)
+        self.proj_q = nn.Parameter(torch.eye(head_dim))
+        self.proj_k = nn.Parameter(torch.eye(head_dim))
+        init = torch.logit(torch.tensor(float(alpha_init)))
+        self.alpha_logit = nn.Parameter(torch.full((num_heads, self.Mb), init.item()))
+
+    def forward(self, q, k, v):
+        """q, k, v: (b, l, H, hd) -> (b, l, H, hd) attention output in q.dtype."""
+        needs_grad = torch.is_grad_enabled() and (
+            q.requires_grad or k.requires_grad or v.requires_grad
+            or self.alpha_logit.requires_grad)
+        if needs_grad:
+            raise NotImplementedError(
+                "SLA2CubeQATAttentionImpl: the INT8 training backward is not implemented in "
+                "this build; call under torch.no_grad() or use sla2_cube_qat_jvp_fused")
+        B, L, H, D = q.shape
+
+        def tm(x):
+            x = x.permute(0, 2, 1, 3)
+            if not self.pre_permuted:
+                x = x[:, :, self.perm]
+            return _c16(x)
+
+        qh, kh, vh = tm(q), tm(k), tm(v.to(q.dtype))
+        lut, T = route_tiles_fast(qh, kh, self.topk_frac, self.Np, self.E, self.prefix_len,
+                                  proj_q=self.proj_q, proj_k=self.proj_k)
+        a = torch.sigmoid(self.alpha_logit.detach().float())
+        o, _ = ops.cube_jvp(qh, kh, vh, None, None, None, a, self.topk_frac, self.Np,
+                            self.prefix_len, lut=lut, T=T)
+        if self.pre_permuted:
+            return o.permute(0, 2, 1, 3).to(q.dtype)
+        return o[:, :, self.inv].permute(0, 2, 1, 3).to(q.dtype)

@@ -1,0 +1,143 @@
+/*
+ * sla2h.h -- C ABI of the MI355X (gfx950) SLA2 INT8 cube-attention hot path.
+ *
+ * Every entry point:
+ *   - takes raw device pointers, sizes and a hipStream_t (passed as void*),
+ *   - never allocates device memory (the caller owns inputs, outputs and the
+ *     workspaces whose sizes the *_bytes() queries report),
+ *   - is asynchronous on `stream` and re-entrant across streams,
+ *   - returns 0 (hipSuccess) or a hipError_t code; 1 (hipErrorInvalidValue)
+ *     for bad arguments.  sla2h_error_string() names a code.
+ *
+ * Tensor conventions (all contiguous, row-major):
+ *   B batch, H heads, L tokens (tile-major order: Np video tiles of E tokens,
+ *   then the P-token prefix as ceil(P/E) tail blocks), D head dim.
+ *   E = D = 64 (one quantisation block = one attention tile = one MFMA tile).
+ *   Nb = ceil(L/E) key/query blocks; Mb = Nb query blocks (LUT rows);
+ *   n_tail = Nb - Np prefix tail blocks, always attended by the sparse branch.
+ *   dtype: 0 = float16, 1 = bfloat16 (the 16-bit storage of q,k,v,dq,dk,dv).
+ */
+#ifndef SLA2H_H
+#define SLA2H_H
+
+#include <stdint.h>
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define SLA2H_DTYPE_F16 0
+#define SLA2H_DTYPE_BF16 1
+
+/* sla2h_fwd_jvp flags */
+#define SLA2H_FLAG_SPARSE_ONLY 1  /* write the sparse branch o_s only (no linear branch, no alpha mix) */
+
+/* Library version and error names. */
+int sla2h_version(void);
+const char* sla2h_error_string(int code);
+
+/*
+ * Per-(b,h,64-token block) symmetric INT8 quantisation of one tensor.
+ *   x  : (BH, L, D) 16-bit       -> xq (BH, L, D) int8,  xs (BH, ceil(L/E)) fp32
+ *   s  = fl32(fl32(max|x|) / 127) + fl32(1e-12);  xq = round_half_away(x / s).
+ * Replaces quantize_qkv / _quant_blocks
+ * (models/sla2_vendor/kernel_sparse_qat.py:120-151).
+ */
+int sla2h_quantize(const void* x, int dtype, int64_t BH, int64_t L, int D, int E,
+                   int8_t* xq, float* xs, void* stream);
+
+/*
+ * Fused INT8 quantisation of Q and K plus router tile pooling, one launch.
+ *   q8,k8 (B,H,L,D) int8; qs,ks (B,H,Nb) fp32 (as sla2h_quantize);
+ *   qpool (B,H,Nb,D) fp32: per-block mean of q over its real rows (sequential
+ *     fp32 sum over rows, then / count), then optional projection
+ *     qpool <- qpool @ proj_q^T (sequential fp32 dot, no FMA contraction);
+ *   kpool_t (B,H,D,Np) fp32: the same for the Np video tiles of k, stored
+ *     transposed (channel-major) for the router's coalesced score loop.
+ *   proj_q / proj_k: (D,D) fp32 or NULL (identity).
+ * Replaces the quantize_qkv(Q), quantize_qkv(K) calls of
+ * sla2_cube_qat_jvp_fused (models/sla2_cube_qat.py:629-631) and the
+ * _route_pool_kernel launches + projections of route_tiles_fast
+ * (models/mla_video_sparse_jvp.py:506-562).
+ */
+int sla2h_quant_pool_qk(const void* q, const void* k, int dtype, int B, int H,
+                        int64_t L, int D, int E, int Np,
+                        const float* proj_q, const float* proj_k,
+                        int8_t* q8, float* qs, int8_t* k8, float* ks,
+                        float* qpool, float* kpool_t, void* stream);
+
+/*
+ * Block router: scores pc[m,n] = (sum_d qpool[m,d]*kpool[n,d]) * scale
+ * (sequential fp32, no FMA), per row the T largest, ties to the lower index.
+ *   lut (B,H,Mb,T) int32, each row ordered by descending score.
+ *   mask (B,H,Mb,Np) uint8 or NULL: 1 where selected.
+ * Np <= 8192.  Replaces the score GEMM + torch.topk of route_tiles_fast
+ * (models/mla_video_sparse_jvp.py:563-565) and route_tiles (:292-294).
+ */
+int sla2h_route_topk(const float* qpool, const float* kpool_t, int B, int H,
+                     int Mb, int Np, int D, int T, float scale,
+                     int32_t* lut, uint8_t* mask, void* stream);
+
+/*
+ * Linear-branch states of the Np video tiles, phi = softmax over D:
+ *   Hb  (B,H,Np,D,D) fp32 = phi(K_n)^T V_n
+ *   dHb (B,H,Np,D,D) fp32 = dphi(K_n)^T V_n + phi(K_n)^T dV_n
+ *   zb, dzb (B,H,Np,D) fp32 = column sums of phi(K_n), dphi(K_n)
+ *   Hall,dHall (B,H,D,D), zall,dzall (B,H,D): sums over n (in n order).
+ * Also writes the transposed value tiles used by sla2h_fwd_jvp:
+ *   vt, dvt (B,H,Nb,D,E) 16-bit: vt[b,h,n,c,r] = v[b,h,n*E+r,c], zero past L.
+ * dk, dv, dHb, dzb, dHall, dzall, dvt may all be NULL (primal only).
+ * Replaces _phi_states_kernel + the torch sums of sla2_cube_qat_jvp_fused
+ * (models/sla2_cube_qat.py:634-648, 911-958).
+ */
+int sla2h_linear_states(const void* k, const void* dk, const void* v, const void* dv,
+                        int dtype, int B, int H, int64_t L, int D, int E, int Np,
+                        float* Hb, float* dHb, float* zb, float* dzb,
+                        float* Hall, float* dHall, float* zall, float* dzall,
+                        void* vt, void* dvt, void* stream);
+
+/* Bytes of one per-query-block complement record (see sla2h_complement). */
+size_t sla2h_complement_record_bytes(int D);
+
+/*
+ * Complement (non-selected video tiles) linear-branch states per query block:
+ *   Hc[m] = Hall - sum_{j<T} Hb[lut[m,j]]   (fp32, subtracted in LUT order)
+ *   and dHc, zc, dzc likewise, written as one record of
+ *   sla2h_complement_record_bytes(D) bytes per (b,h,m) in the operand layout
+ *   that sla2h_fwd_jvp consumes.  Tangent parts skipped when dHb == NULL.
+ * Replaces the in-loop state subtraction of _cube_fused_jvp_kernel
+ * (models/sla2_cube_qat.py:510-523, 570-578).
+ */
+int sla2h_complement(const float* Hb, const float* dHb, const float* zb, const float* dzb,
+                     const float* Hall, const float* dHall, const float* zall,
+                     const float* dzall, const int32_t* lut, int B, int H, int Mb,
+                     int Np, int D, int T, void* comp, void* stream);
+
+/*
+ * The fused sparse + linear SLA2 op and its forward-mode JVP, tile-major:
+ *   sparse branch: for each query block m, keys of tiles lut[m,0..T) and the
+ *     n_tail prefix tail blocks; S = int32(q8 . k8^T) * (qs*ks); online softmax
+ *     in exp2 with scale*log2(e); P.V on 16-bit MFMA;
+ *     tangent: dS = (dq.k^T + q.dk^T)*scale, t = p*dS, do_s = (t.V + p.dV)/l
+ *     - (mu/l) o_s (t saturated at +-60000 for fp16 operands);
+ *   linear branch: o_l = phi(q) Hc / den, den = phi(q).zc (+-eps_l, signed);
+ *     do_l by the quotient rule; o = a o_s + (1-a) o_l, a = alpha[h*alpha_stride+m].
+ *   Outputs o, dout (B,H,L,D) fp32.  Tangent inputs/outputs NULL = primal only.
+ *   comp = sla2h_complement records (unused with SLA2H_FLAG_SPARSE_ONLY).
+ * Replaces _cube_fused_jvp_kernel (models/sla2_cube_qat.py:448-602) and,
+ * with SLA2H_FLAG_SPARSE_ONLY, _sla2_cube_jvp_qat_kernel's sparse branch
+ * (models/sla2_cube_qat.py:59-169, 172-207).
+ */
+int sla2h_fwd_jvp(const void* q, const void* k, const void* dq, const void* dk,
+                  const void* vt, const void* dvt, const int8_t* q8, const int8_t* k8,
+                  const float* qs, const float* ks, const void* comp,
+                  const float* alpha, int alpha_stride, const int32_t* lut,
+                  int dtype, int B, int H, int64_t L, int D, int E, int Np, int T,
+                  float scale, float eps_l, int flags,
+                  float* o, float* dout, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* SLA2H_H */

@@ -1,0 +1,372 @@
+"""CPU restatement of the SLA2 INT8 cube-attention hot path (test infrastructure only).
+
+Bit-exact parts (quantisation, pooling, router scores, top-k) are numpy fp32
+with every sum in a fixed sequential order and no fused multiply-add: numpy
+rounds each elementwise fp32 operation separately, exactly as the gfx950
+kernels compiled with -ffp-contract=off do.  Floating-point parts (phi,
+states, attention, linear branch) are torch CPU fp32 following the reference
+kernels operation by operation, including the 16-bit rounding of the MMA
+operands P and t.  Dense fp64 forms at the bottom serve only to pin the
+blockwise restatement on tiny inputs.
+
+All inputs are CPU tensors / arrays holding the fp32 values of the 16-bit
+data (bf16 or fp16), tile-major token order, shape (B, H, L, D).
+"""
+
+import math
+
+import numpy as np
+import torch
+import torch.nn.functional as F
+
+E = 64
+LOG2E = 1.4426950408889634
+EPS_L = 1e-5
+_F32 = np.float32
+
+
+def _np(x):
+    if isinstance(x, torch.Tensor):
+        return x.detach().cpu().float().numpy()
+    return np.asarray(x, dtype=np.float32)
+
+
+def _pad_rows(x, rows):
+    pad = rows - x.shape[-2]
+    if pad == 0:
+        return x
+    z = np.zeros(x.shape[:-2] + (pad, x.shape[-1]), dtype=x.dtype)
+    return np.concatenate([x, z], axis=-2)
+
+
+# ---------------------------------------------------------------------------
+# INT8 block quantisation -- models/sla2_vendor/kernel_sparse_qat.py:128-141
+#   s = max|x| / 127 + 1e-12 (fp32 ops), q = round_half_away(x / s)
+# ---------------------------------------------------------------------------
+def round_half_away(y):
+    """Round to nearest, ties away from zero (libdevice.round), exact in fp32."""
+    a = np.abs(y)
+    f = np.floor(a)
+    r = f + ((a - f) >= _F32(0.5)).astype(np.float32)
+    return np.where(y < 0, -r, r)
+
+
+def quantize_blocks(x, block=E):
+    """x (..., L, D) -> (q int8 (..., L, D), s fp32 (..., ceil(L/block)))."""
+    x = _np(x)
+    L, D = x.shape[-2:]
+    nb = -(-L // block)
+    xb = _pad_rows(x, nb * block).reshape(x.shape[:-2] + (nb, block, D))
+    amax = np.abs(xb).max(axis=(-2, -1))
+    s = (amax / _F32(127.0)).astype(np.float32) + _F32(1e-12)
+    y = xb / s[..., None, None]
+    q = round_half_away(y).astype(np.int8)
+    return q.reshape(x.shape[:-2] + (nb * block, D))[..., :L, :], s.astype(np.float32)
+
+
+# ---------------------------------------------------------------------------
+# Router -- models/mla_video_sparse_jvp.py:506-566 (route_tiles_fast) with the
+# canonical fp32 order: per-channel sequential sum over rows, / count;
+# projections and scores as sequential fp32 dots (mul, then add).
+# ---------------------------------------------------------------------------
+def pool_tiles(x, nblocks, count_len, block=E):
+    """Mean of each of the first `nblocks` blocks over its rows < count_len."""
+    x = _np(x)
+    D = x.shape[-1]
+    out = np.zeros(x.shape[:-2] + (nblocks, D), dtype=np.float32)
+    for b in range(nblocks):
+        cnt = min(block, count_len - b * block)
+        acc = np.zeros(x.shape[:-2] + (D,), dtype=np.float32)
+        for r in range(cnt):
+            acc = acc + x[..., b * block + r, :]
+        out[..., b, :] = acc / _F32(cnt)
+    return out
+
+
+def project_pool(p, proj):
+    """p (..., n, D) @ proj^T with a sequential fp32 dot: out[e] = sum_d p[d] proj[e, d]."""
+    if proj is None:
+        return p
+    proj = _np(proj)
+    acc = np.zeros(p.shape[:-1] + (proj.shape[0],), dtype=np.float32)
+    for d in range(p.shape[-1]):
+        acc = acc + p[..., d:d + 1] * proj[:, d]
+    return acc
+
+
+def route_scores(qp, kp, scale):
+    """pc[..., m, n] = (sum_d qp[m, d] kp[n, d]) * scale, sequential fp32."""
+    acc = np.zeros(qp.shape[:-1] + (kp.shape[-2],), dtype=np.float32)
+    for d in range(qp.shape[-1]):
+        acc = acc + qp[..., :, d:d + 1] * kp[..., None, :, d]
+    return acc * _F32(scale)
+
+
+def score_keys(pc):
+    """Total order of torch.topk on fp32 (NaN largest, -0 == +0), ties to lower index."""
+    u = np.ascontiguousarray(pc, dtype=np.float32).view(np.uint32).copy()
+    u[np.isnan(pc)] = 0x7FC00000
+    u[u == 0x80000000] = 0
+    ordk = np.where(u & 0x80000000, ~u, u | 0x80000000).astype(np.uint64)
+    idx = np.arange(pc.shape[-1], dtype=np.uint64)
+    return (ordk << np.uint64(32)) | (np.uint64(0xFFFFFFFF) - idx)
+
+
+def topk_rows(pc, T):
+    """Indices of the T largest per row, in descending score order (int32)."""
+    keys = score_keys(pc)
+    order = np.argsort(keys, axis=-1, kind="stable")[..., ::-1]
+    return np.ascontiguousarray(order[..., :T]).astype(np.int32)
+
+
+def topk_count(topk_frac, Np):
+    return max(1, min(Np, int(topk_frac * Np)))
+
+
+def route(q, k, topk_frac, Np, prefix_len=0, proj_q=None, proj_k=None, T=None):
+    """Returns (lut int32 (B,H,Mb,T), T, qpool (B,H,Mb,D), kpool (B,H,Np,D))."""
+    q, k = _np(q), _np(k)
+    L, D = q.shape[-2:]
+    Mb = -(-L // E)
+    qp = project_pool(pool_tiles(q, Mb, L), proj_q)
+    kp = project_pool(pool_tiles(k, Np, Np * E), proj_k)
+    pc = route_scores(qp, kp, D ** -0.5)
+    T = topk_count(topk_frac, Np) if T is None else T
+    return topk_rows(pc, T), T, qp, kp
+
+
+# ---------------------------------------------------------------------------
+# Tile permutation -- models/mla_video_sparse_jvp.py:61-91
+# ---------------------------------------------------------------------------
+def tile_permutation(grid, tile, prefix_len):
+    Tg, Hh, Ww = grid
+    tt, th, tw = tile
+    assert Tg % tt == 0 and Hh % th == 0 and Ww % tw == 0
+    idx = np.arange(Tg * Hh * Ww).reshape(Tg // tt, tt, Hh // th, th, Ww // tw, tw)
+    idx = idx.transpose(0, 2, 4, 1, 3, 5).reshape(-1) + prefix_len
+    perm = np.concatenate([idx, np.arange(prefix_len)])
+    inv = np.empty_like(perm)
+    inv[perm] = np.arange(perm.size)
+    return perm, inv, (Tg // tt) * (Hh // th) * (Ww // tw)
+
+
+# ---------------------------------------------------------------------------
+# phi-states -- models/sla2_cube_qat.py:911-958 and the sums at :645-648
+# ---------------------------------------------------------------------------
+def phi_jvp(x, dx=None):
+    """phi = softmax over D (fp32), dphi = phi * (dx - <phi, dx>)."""
+    x = x.float()
+    mx = x.amax(-1, keepdim=True)
+    ex = torch.exp(x - mx)
+    phi = ex / ex.sum(-1, keepdim=True)
+    if dx is None:
+        return phi, None
+    dx = dx.float()
+    return phi, phi * (dx - (phi * dx).sum(-1, keepdim=True))
+
+
+def phi_states(k, v, Np, dk=None, dv=None):
+    """Per-video-tile states and their sums over the Np tiles (fp32)."""
+    B, H, L, D = k.shape
+    kv = k[:, :, :Np * E].float().reshape(B, H, Np, E, D)
+    vv = v[:, :, :Np * E].float().reshape(B, H, Np, E, D)
+    phi, dphi = phi_jvp(kv, None if dk is None else dk[:, :, :Np * E].reshape(B, H, Np, E, D))
+    st = {"Hb": torch.einsum("bhnrd,bhnrv->bhndv", phi, vv), "zb": phi.sum(3)}
+    if dk is not None:
+        dvv = dv[:, :, :Np * E].float().reshape(B, H, Np, E, D)
+        st["dHb"] = (torch.einsum("bhnrd,bhnrv->bhndv", dphi, vv)
+                     + torch.einsum("bhnrd,bhnrv->bhndv", phi, dvv))
+        st["dzb"] = dphi.sum(3)
+    st["Hall"] = st["Hb"].sum(2)
+    st["zall"] = st["zb"].sum(2)
+    if dk is not None:
+        st["dHall"] = st["dHb"].sum(2)
+        st["dzall"] = st["dzb"].sum(2)
+    return st
+
+
+# ---------------------------------------------------------------------------
+# The fused op -- models/sla2_cube_qat.py:448-602 (_cube_fused_jvp_kernel)
+# ---------------------------------------------------------------------------
+def _tiles(x, nb):
+    B, H, L, D = x.shape
+    pad = nb * E - L
+    if pad:
+        x = torch.cat([x, x.new_zeros(B, H, pad, D)], 2)
+    return x.reshape(B, H, nb, E, D)
+
+
+def _gather_tiles(xt, idx):
+    """xt (B,H,nb,E,D), idx (B,H,Mb) -> (B,H,Mb,E,D)."""
+    B, H, Mb = idx.shape
+    ix = idx.long().view(B, H, Mb, 1, 1).expand(B, H, Mb, xt.shape[3], xt.shape[4])
+    return torch.gather(xt, 2, ix)
+
+
+def cube_jvp(q, k, v, dq, dk, dv, alpha, lut, Np, prefix_len, quant=None, states=None,
+             t16=torch.bfloat16, sparse_only=False):
+    """Blockwise restatement of the fused INT8 op and its JVP.
+
+    q..dv: (B,H,L,D) float tensors holding the 16-bit values (dq,dk,dv None =
+    primal only).  alpha (H, Mb) after the sigmoid.  lut (B,H,Mb,T) ids.
+    quant: optional (q8, qs, k8, ks) (numpy or torch); computed when None.
+    t16: the 16-bit type of the MMA operands p and t.
+    Returns (o, do) fp32 (B,H,L,D); do is None for primal only.
+    """
+    B, H, L, D = q.shape
+    nb = -(-L // E)
+    Mb = nb
+    n_tail = nb - Np
+    tan = dq is not None
+    lut = torch.as_tensor(np.asarray(lut)).long()
+    T = lut.shape[-1]
+    if quant is None:
+        q8, qs = quantize_blocks(q)
+        k8, ks = quantize_blocks(k)
+    else:
+        q8, qs, k8, ks = quant
+    q8, k8 = (torch.as_tensor(np.asarray(t)).double() for t in (q8, k8))
+    qs, ks = (torch.as_tensor(np.asarray(t)).float() for t in (qs, ks))
+    scale = float(np.float32(D ** -0.5))
+    c_log2 = float(np.float32(scale) * np.float32(LOG2E))
+    qf, kf, vf = q.float(), k.float(), v.float()
+
+    Qt = _tiles(qf, nb)
+    Q8t = _tiles(q8, nb)
+    K8t, Kt, Vt = _tiles(k8, nb), _tiles(kf, nb), _tiles(vf, nb)
+    if tan:
+        dQt, dKt, dVt = _tiles(dq.float(), nb), _tiles(dk.float(), nb), _tiles(dv.float(), nb)
+
+    m_i = torch.full((B, H, Mb, E), -math.inf)
+    l_i = torch.zeros(B, H, Mb, E)
+    mu = torch.zeros(B, H, Mb, E)
+    acc_o = torch.zeros(B, H, Mb, E, D)
+    acc_do = torch.zeros(B, H, Mb, E, D) if tan else None
+    lin = not sparse_only
+    if lin:
+        if states is None:
+            states = phi_states(k, v, Np, dk, dv)
+        hc = states["Hall"][:, :, None].expand(B, H, Mb, D, D).clone().float()
+        zc = states["zall"][:, :, None].expand(B, H, Mb, D).clone().float()
+        if tan:
+            dhc = states["dHall"][:, :, None].expand(B, H, Mb, D, D).clone().float()
+            dzc = states["dzall"][:, :, None].expand(B, H, Mb, D).clone().float()
+
+    qsb = qs[:, :, :Mb]
+    key_pos = torch.arange(E)
+    for j in range(T + n_tail):
+        if j < T:
+            n = lut[..., j]
+        else:
+            n = torch.full((B, H, Mb), Np + (j - T), dtype=torch.long)
+        k8n = _gather_tiles(K8t, n)
+        s_int = torch.matmul(Q8t, k8n.transpose(-1, -2))       # exact in fp64
+        sk = torch.gather(ks, 2, n)                               # (B,H,Mb)
+        sqk = (qsb * sk)[..., None, None]
+        s2 = (s_int.float() * sqk) * c_log2
+        valid = (n[..., None] * E + key_pos) < L                 # (B,H,Mb,E)
+        s2 = s2.masked_fill(~valid[..., None, :], -math.inf)
+        m_new = torch.maximum(m_i, s2.amax(-1))
+        al = torch.exp2(m_i - m_new)
+        p = torch.exp2(s2 - m_new[..., None])
+        l_i = l_i * al + p.sum(-1)
+        vn = _gather_tiles(Vt, n)
+        pc = p.to(t16).float()
+        acc_o = acc_o * al[..., None] + torch.matmul(pc, vn)
+        if tan:
+            kn, dkn, dvn = _gather_tiles(Kt, n), _gather_tiles(dKt, n), _gather_tiles(dVt, n)
+            ds = (torch.matmul(dQt, kn.transpose(-1, -2))
+                  + torch.matmul(Qt, dkn.transpose(-1, -2))) * scale
+            t = p * ds
+            mu = mu * al + t.sum(-1)
+            tcl = t.clamp(-60000.0, 60000.0) if t16 == torch.float16 else t
+            tc = tcl.to(t16).float()
+            acc_do = acc_do * al[..., None] + torch.matmul(tc, vn) + torch.matmul(pc, dvn)
+        m_i = m_new
+        if lin and j < T:
+            ix4 = n.view(B, H, Mb, 1, 1).expand(B, H, Mb, D, D)
+            ix3 = n.view(B, H, Mb, 1).expand(B, H, Mb, D)
+            hc = hc - torch.gather(states["Hb"].float(), 2, ix4)
+            zc = zc - torch.gather(states["zb"].float(), 2, ix3)
+            if tan:
+                dhc = dhc - torch.gather(states["dHb"].float(), 2, ix4)
+                dzc = dzc - torch.gather(states["dzb"].float(), 2, ix3)
+
+    o = acc_o / l_i[..., None]
+    do = (acc_do / l_i[..., None] - (mu / l_i)[..., None] * o) if tan else None
+    if lin:
+        qphi, dqphi = phi_jvp(Qt, dQt if tan else None)
+        num = torch.matmul(qphi, hc)
+        den = (qphi * zc[..., None, :]).sum(-1)
+        den = torch.where(den >= 0, den + EPS_L, den - EPS_L)
+        o_l = num / den[..., None]
+        a = torch.as_tensor(alpha).float().reshape(1, H, Mb, 1, 1)
+        if tan:
+            dnum = torch.matmul(dqphi, hc) + torch.matmul(qphi, dhc)
+            dden = (dqphi * zc[..., None, :]).sum(-1) + (qphi * dzc[..., None, :]).sum(-1)
+            do_l = (dnum - o_l * dden[..., None]) / den[..., None]
+            do = a * do + (1.0 - a) * do_l
+        o = a * o + (1.0 - a) * o_l
+    o = o.reshape(B, H, Mb * E, D)[:, :, :L]
+    if do is not None:
+        do = do.reshape(B, H, Mb * E, D)[:, :, :L]
+    return o, do
+
+
+# ---------------------------------------------------------------------------
+# Dense fp64 forms (tiny L only) used to pin the blockwise restatement.
+# ---------------------------------------------------------------------------
+def block_mask(lut, Np, L, prefix_len):
+    """(B,H,L,L) {0,1} sparse mask (routed tiles + prefix columns) and complement."""
+    lut = torch.as_tensor(np.asarray(lut)).long()
+    B, H, Mb, T = lut.shape
+    mc = torch.zeros(B, H, Mb, Np, dtype=torch.float64)
+    mc.scatter_(-1, lut, 1.0)
+    m = mc.repeat_interleave(E, dim=-2)[:, :, :L].repeat_interleave(E, dim=-1)
+    m = torch.cat([m, torch.ones(B, H, L, L - Np * E, dtype=torch.float64)], -1)
+    comp = 1.0 - m
+    comp[..., Np * E:] = 0.0
+    return m, comp
+
+
+def dense_op(S, v, q, k, alpha, m, comp, Np, eps=EPS_L):
+    """o = a softmax_m(S) v + (1 - a) [phi(q) phi(k)^T * comp] v / (sum + eps), fp64.
+
+    S is the (already scaled) score matrix.  Mirrors mvs_dense_ref
+    (models/mla_video_sparse_jvp.py:457-498) with S passed in, so that the
+    INT8 primal scores and the straight-through tangent can be fed to
+    torch.func.jvp.
+    """
+    B, H, L, D = v.shape
+    p = torch.softmax(S.masked_fill(m <= 0, -math.inf), dim=-1)
+    o_s = p @ v
+    w = (torch.softmax(q, -1) @ torch.softmax(k, -1).transpose(-1, -2)) * comp
+    o_l = (w @ v) / (w.sum(-1, keepdim=True) + eps)
+    Mb = -(-L // E)
+    reps = torch.tensor([E] * (Mb - 1) + [L - (Mb - 1) * E])
+    a = torch.as_tensor(alpha, dtype=torch.float64).repeat_interleave(reps, -1).view(1, H, L, 1)
+    return a * o_s + (1.0 - a) * o_l
+
+
+def dense_jvp(q, k, v, dq, dk, dv, alpha, lut, Np, prefix_len, quant=None):
+    """fp64 (o, do): primal scores from the dequantised INT8 Q/K, tangent scores
+    (dq k^T + q dk^T) * scale from the unquantised values (straight-through),
+    differentiated by torch.func.jvp through dense_op."""
+    B, H, L, D = q.shape
+    if quant is None:
+        q8, qs = quantize_blocks(q)
+        k8, ks = quantize_blocks(k)
+    else:
+        q8, qs, k8, ks = quant
+    deq = lambda x8, s: (torch.as_tensor(np.asarray(x8)).double()
+                         * torch.as_tensor(np.asarray(s)).double().repeat_interleave(E, -1)[..., :L, None])
+    qd, kd = deq(q8, qs), deq(k8, ks)
+    scale = D ** -0.5
+    qq, kk, vv = q.double(), k.double(), v.double()
+    S = (qd @ kd.transpose(-1, -2)) * scale
+    m, comp = block_mask(lut, Np, L, prefix_len)
+    if dq is None:
+        return dense_op(S, vv, qq, kk, alpha, m, comp, Np), None
+    dS = (dq.double() @ kk.transpose(-1, -2) + qq @ dk.double().transpose(-1, -2)) * scale
+    f = lambda S_, v_, q_, k_: dense_op(S_, v_, q_, k_, alpha, m, comp, Np)
+    return torch.func.jvp(f, (S, vv, qq, kk), (dS, dv.double(), dq.double(), dk.double()))

@@ -1,0 +1,61 @@
+"""The C-ABI library: loads, exports every declared symbol, validates arguments (CPU)."""
+import os
+import re
+
+import pytest
+import torch
+
+from imfvideo_amd import _lib, ops
+
+HEADER = os.path.join(os.path.dirname(os.path.dirname(__file__)), "include", "sla2h.h")
+
+
+def declared_symbols():
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(sla2h_\w+)\s*\(", text)))
+
+
+def test_header_and_binding_agree():
+    names = declared_symbols()
+    assert len(names) >= 8
+    assert names == sorted(_lib.SIGNATURES), "ctypes signatures must mirror include/sla2h.h"
+
+
+def test_library_exports_every_declared_symbol():
+    lib = _lib.load()
+    for name in declared_symbols():
+        assert hasattr(lib, name), name
+    assert lib.sla2h_version() == 1
+    assert lib.sla2h_complement_record_bytes(64) == ops.REC_BYTES
+    assert lib.sla2h_complement_record_bytes(32) == 0
+
+
+def test_invalid_arguments_are_rejected_before_any_launch():
+    lib = _lib.load()
+    bad = 1  # hipErrorInvalidValue
+    assert lib.sla2h_quantize(None, 1, 1, 64, 64, 64, None, None, None) == bad
+    assert lib.sla2h_quantize(1, 1, 1, 64, 32, 64, 1, 1, None) == bad       # D != 64
+    assert lib.sla2h_quantize(1, 7, 1, 64, 64, 64, 1, 1, None) == bad       # dtype
+    assert lib.sla2h_route_topk(1, 1, 1, 1, 4, 5000, 64, 3, 0.125, 1, None, None) == bad  # Np
+    assert lib.sla2h_route_topk(1, 1, 1, 1, 4, 8, 64, 9, 0.125, 1, None, None) == bad     # T > Np
+    assert lib.sla2h_fwd_jvp(1, 1, 1, None, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 128, 64,
+                             64, 2, 1, 0.125, 1e-5, 0, 1, 1, None) == bad  # dq without dk
+    assert lib.sla2h_linear_states(1, None, 1, None, 1, 1, 1, 100, 64, 64, 2, 1, None, 1, None,
+                                   1, None, 1, None, 1, None, None) == bad  # Np*E > L
+
+
+def test_ops_refuse_cpu_tensors():
+    x = torch.zeros(1, 1, 64, 64, dtype=torch.bfloat16)
+    with pytest.raises(RuntimeError, match="GPU only"):
+        ops.quantize(x)
+    from imfvideo_amd.sla2_cube_qat import sla2_cube_qat_jvp_fused
+    with pytest.raises(RuntimeError, match="GPU only"):
+        sla2_cube_qat_jvp_fused(x, x, x, x, x, x, 0.9, 0.5, 1, 64, 0)
+
+
+def test_missing_library_raises(monkeypatch, tmp_path):
+    monkeypatch.setattr(_lib, "LIB_PATH", str(tmp_path / "nope.so"))
+    monkeypatch.setattr(_lib, "_LIB", None)
+    with pytest.raises(RuntimeError, match="build it"):
+        _lib.load()

@@ -1,0 +1,250 @@
+"""Pins the CPU oracle against what the mathematics fixes (CPU only).
+
+The reference ships no golden vectors for this path, so every oracle function
+is checked here against an independent formulation: exact rationals, exact
+small-integer sums, brute-force ordering, fp64 dense attention and
+torch.func.jvp autodiff, finite differences and special cases.
+"""
+import math
+import os
+from fractions import Fraction
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sla2_oracle as O
+from tests.helpers import from_bits16, make_inputs, max_abs, rel_l2
+
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden")
+
+
+# ---------------------------------------------------------------- quantisation
+def _round_half_away_exact(fr):
+    a = abs(fr)
+    f = math.floor(a)
+    r = f + (1 if a - f >= Fraction(1, 2) else 0)
+    return -r if fr < 0 else r
+
+
+def test_quantize_known_answers():
+    # amax = 127 -> s = fl32(127/127) + 1e-12 = 1.0 exactly, so x / s = x.
+    x = np.zeros((1, 64, 64), np.float32)
+    vals = [127.0, 0.5, -0.5, 1.5, -1.5, 2.5, -2.5, 126.5, -126.5, 0.49999997, 3.25, -0.0]
+    x[0, 0, :len(vals)] = vals
+    q, s = O.quantize_blocks(x)
+    assert s.dtype == np.float32 and s[0, 0] == np.float32(1.0)
+    expect = [127, 1, -1, 2, -2, 3, -3, 127, -127, 0, 3, 0]  # ties away from zero
+    assert q[0, 0, :len(vals)].tolist() == expect
+
+
+def test_quantize_zero_tile_and_ragged():
+    x = np.zeros((2, 100, 64), np.float32)
+    x[1, 70, 3] = -2.0  # second block of row 1 is ragged (36 rows)
+    q, s = O.quantize_blocks(x)
+    assert q.shape == (2, 100, 64) and s.shape == (2, 2)
+    assert s[0, 0] == np.float32(1e-12) and not q[0].any()
+    assert q[1, 70, 3] == -127 and s[1, 1] == np.float32(2.0) / np.float32(127) + np.float32(1e-12)
+
+
+def test_quantize_matches_exact_rationals():
+    g = torch.Generator().manual_seed(5)
+    x = (torch.randn(3, 128, 64, generator=g) * 3).to(torch.bfloat16).float().numpy()
+    q, s = O.quantize_blocks(x)
+    for b in range(3):
+        for blk in range(2):
+            tile = x[b, blk * 64:(blk + 1) * 64]
+            amax = Fraction(float(np.abs(tile).max()))
+            sd = np.float32(float(np.abs(tile).max())) / np.float32(127)
+            # fl32(amax / 127) is the correctly rounded quotient
+            ulp = Fraction(float(np.spacing(sd)))
+            assert abs(Fraction(float(sd)) - amax / 127) <= ulp / 2
+            assert s[b, blk] == sd + np.float32(1e-12)
+            sf = Fraction(float(s[b, blk]))
+            qt = q[b, blk * 64:(blk + 1) * 64]
+            flat_x, flat_q = tile.reshape(-1), qt.reshape(-1)
+            for i in range(0, flat_x.size, 37):
+                y32 = np.float32(flat_x[i]) / np.float32(s[b, blk])
+                assert flat_q[i] == _round_half_away_exact(Fraction(float(y32)))
+                assert abs(Fraction(float(flat_x[i])) - flat_q[i] * sf) <= sf / 2 * (1 + Fraction(1, 10**5))
+            assert np.abs(qt).max() == 127
+
+
+# --------------------------------------------------------------------- pooling
+def test_pool_exact_small_integers():
+    g = np.random.default_rng(0)
+    x = (g.integers(-64, 64, size=(2, 3, 200, 64)) / 8.0).astype(np.float32)  # exact sums
+    p = O.pool_tiles(x, 4, 200)
+    for b in range(4):
+        rows = x[..., b * 64:min(200, (b + 1) * 64), :].astype(np.float64)
+        np.testing.assert_array_equal(p[..., b, :], rows.mean(-2).astype(np.float32))
+
+
+def test_pool_and_projection_error_bound():
+    g = np.random.default_rng(1)
+    x = g.standard_normal((2, 256, 64)).astype(np.float32)
+    proj = (np.eye(64) + 0.05 * g.standard_normal((64, 64))).astype(np.float32)
+    p = O.pool_tiles(x, 4, 256)
+    ref = x.astype(np.float64).reshape(2, 4, 64, 64).mean(2)
+    bound = 64 * np.finfo(np.float32).eps * np.abs(x).reshape(2, 4, 64, 64).mean(2)
+    assert (np.abs(p - ref) <= bound).all()
+    pp = O.project_pool(p, proj)
+    ref_pp = p.astype(np.float64) @ proj.astype(np.float64).T
+    bound2 = 64 * np.finfo(np.float32).eps * (np.abs(p) @ np.abs(proj).T)
+    assert (np.abs(pp - ref_pp) <= bound2).all()
+
+
+# ------------------------------------------------------------------------ top-k
+def _brute_topk(row, T):
+    def key(i):
+        v = float(row[i])
+        return (0, 0.0, i) if math.isnan(v) else (1, -v, i)
+    return sorted(range(len(row)), key=key)[:T]
+
+
+def test_topk_brute_force_ties_nan_signed_zero():
+    g = np.random.default_rng(2)
+    for trial in range(40):
+        n = int(g.integers(2, 60))
+        row = g.integers(-4, 5, size=n).astype(np.float32) / 2  # many ties
+        if trial % 5 == 0:
+            row[g.integers(0, n)] = np.nan
+        if trial % 7 == 0:
+            row[row == 0] = -0.0
+        T = int(g.integers(1, n + 1))
+        got = O.topk_rows(row[None], T)[0].tolist()
+        assert got == _brute_topk(row, T), (row, T)
+
+
+def test_topk_matches_torch_values_without_ties():
+    g = torch.Generator().manual_seed(3)
+    pc = torch.randn(4, 6, 468, generator=g)
+    got = O.topk_rows(pc.numpy(), 46)
+    ref = torch.topk(pc, 46, dim=-1).indices.numpy()
+    assert np.array_equal(np.sort(got, -1), np.sort(ref, -1))
+    assert np.array_equal(got, ref)  # descending order, as torch's sorted topk
+
+
+def test_route_matches_fp64_where_gap_allows():
+    B, H, Np, P = 1, 3, 20, 0
+    q, k, _ = make_inputs(4, B, H, Np * 64, tangent=False)
+    lut, T, qp, kp = O.route(q.float(), k.float(), 0.25, Np, P)
+    qd = q.double().reshape(B, H, Np, 64, 64).mean(3)
+    kd = k.double().reshape(B, H, Np, 64, 64).mean(3)
+    pc = (qd @ kd.transpose(-1, -2)).numpy() / 8.0
+    checked = 0
+    for idx in np.ndindex(B, H, Np):
+        srt = np.sort(pc[idx])[::-1]
+        if srt[T - 1] - srt[T] > 1e-5:
+            assert set(lut[idx].tolist()) == set(np.argsort(-pc[idx])[:T].tolist())
+            checked += 1
+    assert checked > Np
+
+
+def test_tile_permutation_round_trip():
+    from imfvideo_amd.mla_video_sparse_jvp import tile_permutation
+    perm, inv, n = tile_permutation((4, 8, 8), (2, 4, 4), 18, torch.device("cpu"))
+    x = torch.randn(274, 5)
+    assert torch.equal(x[perm][inv], x) and n == 8
+    p2, i2, n2 = O.tile_permutation((4, 8, 8), (2, 4, 4), 18)
+    assert np.array_equal(perm.numpy(), p2) and np.array_equal(inv.numpy(), i2) and n2 == 8
+    # first tile = the 2x4x4 cube at the grid origin, prefix tokens last
+    assert perm[:4].tolist() == [18, 19, 20, 21] and perm[16].item() == 18 + 64
+    assert perm[-18:].tolist() == list(range(18))
+
+
+# -------------------------------------------------------------- attention + JVP
+def _case(seed=0, B=2, H=2, Np=4, P=18, topk=0.5, tan=1.0):
+    L = Np * 64 + P
+    q, k, v, dq, dk, dv = (t.float() for t in make_inputs(seed, B, H, L, tan_scale=tan))
+    g = torch.Generator().manual_seed(seed + 7)
+    alpha = torch.rand(H, -(-L // 64), generator=g) * 0.8 + 0.1
+    lut, T, _, _ = O.route(q, k, topk, Np, P)
+    return q, k, v, dq, dk, dv, alpha, lut, Np, P
+
+
+def test_blockwise_matches_dense_fp64_jvp():
+    q, k, v, dq, dk, dv, alpha, lut, Np, P = _case()
+    ro, rdo = O.dense_jvp(q, k, v, dq, dk, dv, alpha, lut, Np, P)
+    o, do = O.cube_jvp(q, k, v, dq, dk, dv, alpha, lut, Np, P, t16=torch.float32)
+    assert rel_l2(o, ro) < 1e-5 and rel_l2(do, rdo) < 1e-5
+    o, do = O.cube_jvp(q, k, v, dq, dk, dv, alpha, lut, Np, P, t16=torch.bfloat16)
+    assert rel_l2(o, ro) < 1e-2 and rel_l2(do, rdo) < 1e-2
+    assert max_abs(o, ro) < 2e-2 and max_abs(do, rdo) < 2e-2
+
+
+def test_dense_jvp_matches_finite_differences():
+    q, k, v, dq, dk, dv, alpha, lut, Np, P = _case(seed=1, B=1, H=1, Np=2, P=5, topk=0.5)
+    L, D = q.shape[-2:]
+    q8, qs = O.quantize_blocks(q)
+    k8, ks = O.quantize_blocks(k)
+    deq = lambda x8, s: torch.as_tensor(x8).double() * torch.as_tensor(s).double().repeat_interleave(64, -1)[..., :L, None]
+    S = deq(q8, qs) @ deq(k8, ks).transpose(-1, -2) * D ** -0.5
+    dS = (dq.double() @ k.double().transpose(-1, -2) + q.double() @ dk.double().transpose(-1, -2)) * D ** -0.5
+    m, comp = O.block_mask(lut, Np, L, P)
+    f = lambda eps: O.dense_op(S + eps * dS, v.double() + eps * dv.double(), q.double() + eps * dq.double(),
+                               k.double() + eps * dk.double(), alpha, m, comp, Np)
+    h = 1e-5
+    fd = (f(h) - f(-h)) / (2 * h)
+    _, do = O.dense_jvp(q, k, v, dq, dk, dv, alpha, lut, Np, P)
+    assert rel_l2(do, fd) < 1e-6
+
+
+def test_alpha_one_is_sparse_only_and_alpha_zero_linear_only():
+    q, k, v, dq, dk, dv, alpha, lut, Np, P = _case(seed=2)
+    H, Mb = alpha.shape
+    ones, zeros = torch.ones(H, Mb), torch.zeros(H, Mb)
+    o1, do1 = O.cube_jvp(q, k, v, dq, dk, dv, ones, lut, Np, P, t16=torch.float32)
+    os_, dos = O.cube_jvp(q, k, v, dq, dk, dv, ones, lut, Np, P, t16=torch.float32, sparse_only=True)
+    assert torch.equal(o1, os_) and torch.equal(do1, dos)
+    # alpha = 0: linear branch only, against the dense fp64 complement form
+    o0, _ = O.cube_jvp(q, k, v, dq, dk, dv, zeros, lut, Np, P, t16=torch.float32)
+    m, comp = O.block_mask(lut, Np, q.shape[2], P)
+    w = (torch.softmax(q.double(), -1) @ torch.softmax(k.double(), -1).transpose(-1, -2)) * comp
+    ref = (w @ v.double()) / (w.sum(-1, keepdim=True) + O.EPS_L)
+    assert rel_l2(o0, ref) < 1e-5
+
+
+def test_all_tiles_routed_is_full_softmax():
+    q, k, v, dq, dk, dv, alpha, _, Np, P = _case(seed=3, Np=3, P=10)
+    B, H, L, D = q.shape
+    lut = np.broadcast_to(np.arange(Np, dtype=np.int32), (B, H, 4, Np)).copy()
+    ones = torch.ones(H, 4)
+    o, _ = O.cube_jvp(q, k, v, dq, dk, dv, ones, lut, Np, P, t16=torch.float32)
+    q8, qs = O.quantize_blocks(q)
+    k8, ks = O.quantize_blocks(k)
+    deq = lambda x8, s: torch.as_tensor(x8).double() * torch.as_tensor(s).double().repeat_interleave(64, -1)[..., :L, None]
+    S = deq(q8, qs) @ deq(k8, ks).transpose(-1, -2) * D ** -0.5
+    ref = torch.softmax(S, -1) @ v.double()
+    assert rel_l2(o, ref) < 1e-5
+    # alpha < 1 with an empty complement stays finite (signed epsilon)
+    o2, do2 = O.cube_jvp(q, k, v, dq, dk, dv, alpha[:, :4], lut, Np, P)
+    assert torch.isfinite(o2).all() and torch.isfinite(do2).all()
+
+
+def test_phi_states_sum_invariant():
+    q, k, v, dq, dk, dv, *_ = _case(seed=4)
+    st = O.phi_states(k, v, 4, dk, dv)
+    assert torch.allclose(st["Hall"], st["Hb"].sum(2)) and torch.allclose(st["dzall"], st["dzb"].sum(2))
+    # zb rows of phi sum to 64 per tile (softmax rows sum to one)
+    assert torch.allclose(st["zb"].sum(-1), torch.full_like(st["zb"].sum(-1), 64.0), atol=1e-4)
+    # dphi rows sum to zero
+    assert st["dzb"].sum(-1).abs().max() < 1e-4
+
+
+# ---------------------------------------------------------------- golden files
+@pytest.mark.parametrize("name", ["ref_geom_bf16", "tiny_f16", "two_tails_bf16"])
+def test_oracle_reproduces_golden(name):
+    z = np.load(os.path.join(GOLDEN, name + ".npz"))
+    dt = getattr(torch, str(z["dtype"]))
+    ins = {n: from_bits16(z[n], dt).float() for n in ("q", "k", "v", "dq", "dk", "dv")}
+    Np, P = int(z["Np"]), int(z["P"])
+    pq = torch.from_numpy(z["proj_q"]) if "proj_q" in z else None
+    pk = torch.from_numpy(z["proj_k"]) if "proj_k" in z else None
+    lut, T, qp, kp = O.route(ins["q"], ins["k"], float(z["topk"]), Np, P, pq, pk)
+    assert np.array_equal(lut, z["lut"]) and np.array_equal(qp, z["qpool"]) and np.array_equal(kp, z["kpool"])
+    q8, qs = O.quantize_blocks(ins["q"])
+    assert np.array_equal(q8, z["q8"]) and np.array_equal(qs, z["qs"])
+    o, do = O.cube_jvp(*(ins[n] for n in ("q", "k", "v", "dq", "dk", "dv")),
+                       torch.from_numpy(z["alpha"]), lut, Np, P, t16=dt)
+    assert max_abs(o, torch.from_numpy(z["o"])) < 1e-5 and max_abs(do, torch.from_numpy(z["do"])) < 1e-4
