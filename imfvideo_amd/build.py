@@ -21,7 +21,8 @@ ARCH = os.environ.get("SLA2H_ARCH", "gfx950")
 SOURCES = {
     "quant_route.hip": ["-ffp-contract=off"],
     "states.hip": [],
-    "attn.hip": [],
+    # accumulators in VGPR-form MFMA: no AGPR round trips across the key loop
+    "attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 COMMON_FLAGS = [

@@ -1,33 +1,43 @@
 // Fused SLA2 sparse + linear attention with forward-mode JVP, gfx950.
 //
-// One workgroup (4 wave64) per (query block m, b, h): 64 query rows.  The key
-// tiles of the block (T routed video tiles + n_tail prefix blocks) are split
-// across the waves by key: wave w owns keys 16w..16w+15 of every tile and runs
-// its own online softmax over them for all 64 queries; the four partial
-// softmax states are merged once at the end through LDS.  Each wave therefore
-// streams only its quarter of every key tile straight from global memory
-// into MFMA operand registers -- no LDS staging, no barriers in the loop.
+// Work unit: 32 query rows (half of a 64-row query block m) of one (b, h),
+// one workgroup of 4 wave64.  The key tiles of the block (T routed video
+// tiles + n_tail prefix blocks) are split across the waves by key: wave w
+// owns keys 16w..16w+15 of every tile and runs its own softmax over them for
+// the 32 queries; the four partial states are merged once at the end through
+// LDS.  Each wave streams its quarter of every key tile straight from global
+// memory into MFMA operand registers (one tile ahead) -- no barriers in the
+// key loop.  Two passes over the tiles: pass 1 takes the exact row maxima of
+// the INT8 scores (i8 MFMAs only), pass 2 accumulates with that fixed
+// maximum, so the loop has no accumulator rescaling and no cross-lane traffic.
 //
 // Scores are computed transposed (S^T = K Q^T) so that a lane holds one query
-// column: the S^T output fragment is directly the B operand of
-// O^T = V^T P^T, and the per-query softmax statistics stay lane-resident.
+// column: the S^T fragment is directly the B operand of O^T = V^T P^T, and the
+// per-query statistics stay lane-resident.
+//
+// Workgroup ids are remapped so that each XCD (ids = x mod 8) processes a
+// contiguous range of work units: both halves of a query block and all query
+// blocks of one head land on the same XCD and share its L2.
 //
 // Reference semantics: models/sla2_cube_qat.py:448-602 (_cube_fused_jvp_kernel),
 // sparse-only variant :59-169 (_sla2_cube_jvp_qat_kernel).
 #include "common.h"
 
+#include <type_traits>
+
 namespace sla2h {
 
 constexpr int kTa = 64;
+constexpr int kQT = 2;  // 16-row query sub-tiles per workgroup
 constexpr size_t kRec = 2 * 16384 + 2 * 256;
+constexpr int kMaxTiles = 1024;  // T + n_tail per query block
 
 struct FwdArgs {
   const uint16_t* q;
   const uint16_t* k;
   const uint16_t* dq;
   const uint16_t* dk;
-  const uint16_t* vt;
-  const uint16_t* dvt;
+  const uint16_t* vt;   // value-operand tiles (V, or V|dV interleaved with tangent)
   const int8_t* q8;
   const int8_t* k8;
   const float* qs;
@@ -38,60 +48,156 @@ struct FwdArgs {
   float* o;
   float* dout;
   int64_t L;
-  int H, Nb, Np, Mb, T, n_tail, alpha_stride;
+  int H, Nb, Np, Mb, T, n_tail, alpha_stride, nwork, per_xcd;
+  int prescale;  // scale is a power of two (folded exactly into bf16 Q-side operands)
   float scale, c_log2, eps_l;
 };
 
-struct KeyRegs {
+// bf16 x 2^k, exact for a power-of-two scale (no bf16 subnormals in range)
+__device__ inline u32x4 scale_bf16x8(u32x4 u, float s) {
+  u32x4 r;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const float lo = bf16_val((uint16_t)(u[e] & 0xffff)) * s;
+    const float hi = bf16_val((uint16_t)(u[e] >> 16)) * s;
+    r[e] = pack2(bf16_bits(lo), bf16_bits(hi));
+  }
+  return r;
+}
+
+struct KeyRegs {   // score-side operands, loaded one tile ahead
   i32x4 k8;      // K8[key 16w + r][16g .. 16g+15]
   u32x4 ka[4];   // ks 0,1: K[key][32ks + 8g ..], ks 2,3: dK[key][32(ks-2) + 8g ..]
-  u32x2 va[4];   // Vt[c = 16ct + r][keys 16w + 4g .. +3]
-  u32x2 dva[4];
-  float sk;
-  int n;
+};
+struct ValRegs {   // value-side operands, loaded at the start of their own tile
+  // per column tile ct: V[keys 16w + 4g .. +3][c = 16ct + r] in .xy and, with
+  // tangent, dV of the same keys in .zw (one 16-byte load)
+  u32x4 v[4];
 };
 
-template <typename T16, bool TAN, bool LINEAR>
-__global__ __launch_bounds__(256, 1) void fwd_jvp_kernel(FwdArgs a) {
-  __shared__ float stat[3][4][4][16];            // [m,l,mu][wave][qt][r]
-  __shared__ __align__(16) float xbuf[4][4][64][4];  // [wave][qt][lane][i]
+template <typename T16, bool TAN, bool LINEAR, bool PRE>
+__global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
+  __shared__ float stat[3][4][kQT][16];  // [m,l,mu][wave][qt][r]
+  // 8 KB: first the [dQ|Q] B-operand fragments [qt][ks][lane] (16 B each),
+  // then, after the key loop, the cross-wave merge buffer [wave][qt][lane][4].
+  __shared__ __align__(16) u32x4 qsh[kQT][4][64];
+  __shared__ __align__(16) i32x4 q8sh[kQT][64];  // INT8 Q B-operand fragments
+  float(*xbuf)[kQT][64][4] = reinterpret_cast<float(*)[kQT][64][4]>(&qsh[0][0][0]);
+  // key tiles of this query block in visiting order: (tile id, key scale)
+  __shared__ int2 tiles[kMaxTiles];
+
+  const int logical = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
+  if (logical >= a.nwork) return;  // whole workgroup: no barrier skipped
+  // integer division runs on the VALU: pin the (uniform) results to SGPRs so
+  // that every pointer and buffer descriptor derived from them stays scalar
+  const int half = logical & 1;
+  const int bh = __builtin_amdgcn_readfirstlane((logical >> 1) / a.Mb);
+  const int m = __builtin_amdgcn_readfirstlane((logical >> 1) - bh * a.Mb);
+  const int h = __builtin_amdgcn_readfirstlane(bh % a.H);
 
   const int tid = threadIdx.x;
   const int w = tid >> 6, l = tid & 63, r = l & 15, g = l >> 4;
-  const int m = blockIdx.x % a.Mb;
-  const int bh = blockIdx.x / a.Mb;
-  const int h = bh % a.H;
   const int64_t L = a.L;
   const int64_t qkbase = (int64_t)bh * L;
+  const int64_t q0 = (int64_t)m * kTa + 32 * half;  // first query row of the unit
 
-  // ---- query-side MFMA B operands for the 4 query sub-tiles ----
-  i32x4 q8b[4];
-  u32x4 qb[4][4];
-#pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
-    const int64_t row = (int64_t)m * kTa + 16 * qt + r;
+  // ---- query side: INT8 B operands in registers; 16-bit [dQ|Q] B operands
+  // staged once in LDS (wave w loads sub-tile w>>1, dQ or Q by w&1).
+  if (w < kQT) {
+    const int64_t row = q0 + 16 * w + r;
+    q8sh[w][l] = row < L ? *reinterpret_cast<const i32x4*>(a.q8 + (qkbase + row) * kTa + 16 * g)
+                         : i32x4{0, 0, 0, 0};
+  }
+  if (TAN) {
+    const int qt = w >> 1;
+    const int64_t row = q0 + 16 * qt + r;
     const bool ok = row < L;
+    const uint16_t* src = (w & 1) ? a.q : a.dq;
     const int64_t ro = (qkbase + row) * kTa;
-    q8b[qt] = ok ? *reinterpret_cast<const i32x4*>(a.q8 + ro + 16 * g) : i32x4{0, 0, 0, 0};
-    if (TAN) {
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        qb[qt][ks] = ok ? *reinterpret_cast<const u32x4*>(a.dq + ro + 32 * ks + 8 * g)
-                        : u32x4{0, 0, 0, 0};
-        qb[qt][ks + 2] = ok ? *reinterpret_cast<const u32x4*>(a.q + ro + 32 * ks + 8 * g)
-                            : u32x4{0, 0, 0, 0};
-      }
+    for (int ks = 0; ks < 2; ++ks) {
+      u32x4 v = ok ? *reinterpret_cast<const u32x4*>(src + ro + 32 * ks + 8 * g) : u32x4{0, 0, 0, 0};
+      if (PRE) v = scale_bf16x8(v, a.scale);
+      qsh[qt][ks + 2 * (w & 1)][l] = v;
     }
   }
+  const int32_t* lrow = a.lut + ((int64_t)bh * a.Mb + m) * a.T;
+  const int J = a.T + a.n_tail;
+  for (int j = tid; j < J; j += 256) {
+    int n = j < a.T ? lrow[j] : a.Np + (j - a.T);
+    n = n < 0 ? 0 : (n >= a.Nb ? a.Nb - 1 : n);  // out-of-range ids are clamped
+    tiles[j] = make_int2(n, __builtin_bit_cast(int, a.ks[(int64_t)bh * a.Nb + n]));
+  }
+  __syncthreads();
   const float sq = a.qs[(int64_t)bh * a.Nb + m];
+  // per-(b,h) buffer resources: key rows past L read as zeros (those keys are
+  // masked; vt/dvt are zero there anyway), 32-bit offsets
+  const auto rk8 = make_rsrc(a.k8 + qkbase * kTa, L * kTa);
+  const auto rk = make_rsrc(a.k + qkbase * kTa, L * kTa * 2);
+  const auto rdk = make_rsrc(TAN ? a.dk + qkbase * kTa : a.k, L * kTa * 2);
+  constexpr int kVtTile = kTa * kTa * 2 * (TAN ? 2 : 1);  // bytes per value-operand tile
+  const auto rvt = make_rsrc(reinterpret_cast<const char*>(a.vt) + (int64_t)bh * a.Nb * kVtTile,
+                             (int64_t)a.Nb * kVtTile);
 
-  float m_i[4], l_i[4], mu_i[4];
-  f32x4 acc_o[4][4], acc_do[4][4];  // [ct][qt]
+  // ---- pass 1: exact per-wave row maxima of the INT8 scores ----
+  // Loads are branch-free (rows past L clamped to L-1: those keys are masked)
+  // so every tile issues the same vector loads and the prefetch one tile
+  // ahead overlaps the current tile.
+  float mref[kQT];
+  {
+    float mrow[kQT];
 #pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
-    m_i[qt] = -INFINITY;
+    for (int qt = 0; qt < kQT; ++qt) mrow[qt] = -INFINITY;
+    const int v8off = (16 * w + r) * kTa + 16 * g;  // per-lane part, tile base in soffset
+    auto load8 = [&](int j) {
+      const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
+      return __builtin_bit_cast(i32x4, buf_load16(rk8, v8off, n * kTa * kTa));
+    };
+    auto tile_max = [&](const i32x4& k8v, int j, auto mask_tag) {
+      constexpr bool MASK = decltype(mask_tag)::value;
+      const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
+      const float sqk = sq * __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(tiles[j].y));
+      const int64_t key0 = (int64_t)n * kTa + 16 * w + 4 * g;
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
+        const i32x4 si = mfma_i8_16x16x64(k8v, q8sh[qt][l], i32x4{0, 0, 0, 0});
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          float s2 = ((float)si[i] * sqk) * a.c_log2;
+          if (MASK && key0 + i >= L) s2 = -INFINITY;
+          mrow[qt] = fmaxf(mrow[qt], s2);
+        }
+      }
+    };
+    i32x4 kA = load8(0), kB;
+    int j = 0;
+    for (; j + 1 < a.T; j += 2) {
+      kB = load8(j + 1);
+      tile_max(kA, j, std::false_type{});
+      kA = load8(j + 2 < J ? j + 2 : J - 1);
+      tile_max(kB, j + 1, std::false_type{});
+    }
+    for (; j < J; ++j) {
+      kB = load8(j + 1 < J ? j + 1 : J - 1);
+      if (j < a.T)
+        tile_max(kA, j, std::false_type{});
+      else
+        tile_max(kA, j, std::true_type{});
+      kA = kB;
+    }
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) mref[qt] = max_over_groups(mrow[qt]);
+  }
+
+  // ---- pass 2: P = exp2(s - m), O^T += V^T P^T, dO^T += [V|dV]^T [T;P]^T ----
+  float l_i[kQT], mu_i[kQT];
+  f32x4 acc_o[4][kQT], acc_do[4][kQT];  // [ct][qt]
+  float moff[kQT];
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) {
     l_i[qt] = 0.f;
     mu_i[qt] = 0.f;
+    moff[qt] = mref[qt] == -INFINITY ? 0.f : mref[qt];  // -inf: the wave saw no key
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       acc_o[ct][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -99,187 +205,202 @@ __global__ __launch_bounds__(256, 1) void fwd_jvp_kernel(FwdArgs a) {
     }
   }
 
-  const int32_t* lrow = a.lut + ((int64_t)bh * a.Mb + m) * a.T;
-  const int J = a.T + a.n_tail;
-
+  // per-lane parts of the operand offsets; the tile base goes to soffset
+  const int k8off = (16 * w + r) * kTa + 16 * g;
+  const int koff = (16 * w + r) * (kTa * 2) + 16 * g;
+  // primal: vt[c][key] (8 B per lane); tangent: vt[c][key/4][V4|dV4] (16 B per lane)
+  const int voff = TAN ? r * (kTa * 4) + 64 * w + 16 * g : r * (kTa * 2) + 32 * w + 8 * g;
   auto load_keys = [&](int j, KeyRegs& kr) {
-    int n = j < a.T ? lrow[j] : a.Np + (j - a.T);
-    if ((unsigned)n >= (unsigned)a.Nb) n = -1;  // corrupt id: skipped
-    kr.n = n;
-    if (n < 0) return;
-    const int64_t krow = (int64_t)n * kTa + 16 * w + r;
-    const bool ok = krow < L;
-    const int64_t ko = (qkbase + krow) * kTa;
-    kr.sk = a.ks[(int64_t)bh * a.Nb + n];
-    kr.k8 = ok ? *reinterpret_cast<const i32x4*>(a.k8 + ko + 16 * g) : i32x4{0, 0, 0, 0};
+    const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
+    kr.k8 = __builtin_bit_cast(i32x4, buf_load16(rk8, k8off, n * kTa * kTa));
     if (TAN) {
+      const int sb = n * kTa * kTa * 2;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        kr.ka[ks] = ok ? *reinterpret_cast<const u32x4*>(a.k + ko + 32 * ks + 8 * g)
-                       : u32x4{0, 0, 0, 0};
-        kr.ka[ks + 2] = ok ? *reinterpret_cast<const u32x4*>(a.dk + ko + 32 * ks + 8 * g)
-                           : u32x4{0, 0, 0, 0};
+        kr.ka[ks] = buf_load16(rk, koff + 64 * ks, sb);
+        kr.ka[ks + 2] = buf_load16(rdk, koff + 64 * ks, sb);
       }
     }
-    const int64_t vo = ((int64_t)bh * a.Nb + n) * kTa * kTa + 16 * w + 4 * g;
+  };
+  auto load_vals = [&](int j, ValRegs& vr) {
+    const int sb = __builtin_amdgcn_readfirstlane(tiles[j].x) * kVtTile;
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
-      kr.va[ct] = *reinterpret_cast<const u32x2*>(a.vt + vo + (16 * ct + r) * kTa);
-      if (TAN) kr.dva[ct] = *reinterpret_cast<const u32x2*>(a.dvt + vo + (16 * ct + r) * kTa);
+      if (TAN) {
+        vr.v[ct] = buf_load16(rvt, voff + ct * 16 * kTa * 4, sb);
+      } else {
+        const u32x2 x = buf_load8(rvt, voff + ct * 16 * kTa * 2, sb);
+        vr.v[ct] = u32x4{x.x, x.y, 0u, 0u};
+      }
     }
   };
 
-  KeyRegs cur, nxt;
-  if (J > 0) load_keys(0, cur);
-  for (int j = 0; j < J; ++j) {
-    if (j + 1 < J) load_keys(j + 1, nxt);
-    if (cur.n >= 0) {
-      const float sqk = sq * cur.sk;
-      const int64_t key0 = (int64_t)cur.n * kTa + 16 * w + 4 * g;
+  // one key tile; MASK only for the ragged prefix tail tiles (j >= T)
+  auto process = [&](const KeyRegs& kr, const ValRegs& vr, int j, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
+    const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
+    const float c = (sq * __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(tiles[j].y))) * a.c_log2;
+    const int64_t key0 = (int64_t)n * kTa + 16 * w + 4 * g;
 #pragma unroll
-      for (int qt = 0; qt < 4; ++qt) {
-        const i32x4 si = mfma_i8_16x16x64(cur.k8, q8b[qt], i32x4{0, 0, 0, 0});
-        float s2[4], p[4], ds[4], t[4];
-        float mx = -INFINITY;
+    for (int qt = 0; qt < kQT; ++qt) {
+      const i32x4 si = mfma_i8_16x16x64(kr.k8, q8sh[qt][l], i32x4{0, 0, 0, 0});
+      float p[4], ds[4], t[4];
+      if (TAN) {
+        f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const float sf = (float)si[i] * sqk;
-          s2[i] = (key0 + i < L) ? sf * a.c_log2 : -INFINITY;
-          mx = fmaxf(mx, s2[i]);
-        }
+        for (int ks = 0; ks < 4; ++ks) d = mfma_16x16x32<T16>(kr.ka[ks], qsh[qt][ks][l], d);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ds[i] = PRE ? d[i] : d[i] * a.scale;
+      }
+      float ps = 0.f, ts = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float e = fmaf((float)si[i], c, -moff[qt]);
+        if (MASK && key0 + i >= L) e = -INFINITY;
+        p[i] = fast_exp2(e);
+        ps += p[i];
         if (TAN) {
-          f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-          for (int ks = 0; ks < 4; ++ks) d = mfma_16x16x32<T16>(cur.ka[ks], qb[qt][ks], d);
-#pragma unroll
-          for (int i = 0; i < 4; ++i) ds[i] = d[i] * a.scale;
-        }
-        mx = max_over_groups(mx);
-        const float m_new = fmaxf(m_i[qt], mx);
-        const bool dead = m_new == -INFINITY;
-        const float al = dead ? 1.f : exp2f(m_i[qt] - m_new);
-        float ps = 0.f, ts = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          p[i] = dead ? 0.f : exp2f(s2[i] - m_new);
-          ps += p[i];
-          if (TAN) {
-            t[i] = p[i] * ds[i];
-            ts += t[i];
-          }
-        }
-        ps = sum_over_groups(ps);
-        l_i[qt] = l_i[qt] * al + ps;
-        if (TAN) {
-          ts = sum_over_groups(ts);
-          mu_i[qt] = mu_i[qt] * al + ts;
-        }
-        m_i[qt] = m_new;
-
-        u32x2 pb;
-        pb.x = pack2(T16::from_f32(p[0]), T16::from_f32(p[1]));
-        pb.y = pack2(T16::from_f32(p[2]), T16::from_f32(p[3]));
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          acc_o[ct][qt] = acc_o[ct][qt] * al;
-          acc_o[ct][qt] = mfma_16x16x16<T16>(cur.va[ct], pb, acc_o[ct][qt]);
-        }
-        if (TAN) {
-          float tc[4];
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            tc[i] = (T16::kDtype == SLA2H_DTYPE_F16) ? fminf(fmaxf(t[i], -60000.f), 60000.f) : t[i];
-          u32x4 bt;
-          bt.x = pack2(T16::from_f32(tc[0]), T16::from_f32(tc[1]));
-          bt.y = pack2(T16::from_f32(tc[2]), T16::from_f32(tc[3]));
-          bt.z = pb.x;
-          bt.w = pb.y;
-#pragma unroll
-          for (int ct = 0; ct < 4; ++ct) {
-            u32x4 av;
-            av.x = cur.va[ct].x;
-            av.y = cur.va[ct].y;
-            av.z = cur.dva[ct].x;
-            av.w = cur.dva[ct].y;
-            acc_do[ct][qt] = acc_do[ct][qt] * al;
-            acc_do[ct][qt] = mfma_16x16x32<T16>(av, bt, acc_do[ct][qt]);
-          }
+          t[i] = p[i] * ds[i];
+          ts += t[i];
         }
       }
+      l_i[qt] += ps;
+      if (TAN) mu_i[qt] += ts;
+
+      u32x2 pb;
+      pb.x = pack_pair<T16>(p[0], p[1]);
+      pb.y = pack_pair<T16>(p[2], p[3]);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+        acc_o[ct][qt] = mfma_16x16x16<T16>(u32x2{vr.v[ct].x, vr.v[ct].y}, pb, acc_o[ct][qt]);
+      if (TAN) {
+        if (T16::kDtype == SLA2H_DTYPE_F16) {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) t[i] = fminf(fmaxf(t[i], -60000.f), 60000.f);
+        }
+        u32x4 bt;
+        bt.x = pack_pair<T16>(t[0], t[1]);
+        bt.y = pack_pair<T16>(t[2], t[3]);
+        bt.z = pb.x;
+        bt.w = pb.y;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct)
+          acc_do[ct][qt] = mfma_16x16x32<T16>(vr.v[ct], bt, acc_do[ct][qt]);
+      }
     }
-    cur = nxt;
+  };
+  // Issue order per tile: value loads of tile j, then the score-side prefetch
+  // of tile j+1 -- the in-order vmcnt lets tile j wait for its own values
+  // while the prefetch stays in flight.
+  auto run = [&](const KeyRegs& kr, int j, KeyRegs& knext, auto mask_tag) {
+    ValRegs vr;
+    load_vals(j, vr);
+    load_keys(j + 1 < J ? j + 1 : J - 1, knext);
+    process(kr, vr, j, mask_tag);
+  };
+
+  // routed video tiles (full, unmasked): two score-side register sets
+  // alternately loaded one tile ahead, one basic block per pair of tiles
+  KeyRegs ka_, kb_;
+  load_keys(0, ka_);
+  int j = 0;
+  for (; j + 1 < a.T; j += 2) {
+    run(ka_, j, kb_, std::false_type{});
+    run(kb_, j + 1, ka_, std::false_type{});
+  }
+  // odd leftover routed tile and the ragged prefix tail tiles
+  for (; j < J; ++j) {
+    if (j < a.T)
+      run(ka_, j, kb_, std::false_type{});
+    else
+      run(ka_, j, kb_, std::true_type{});
+    ka_ = kb_;
+  }
+#pragma unroll
+  for (int qt = 0; qt < kQT; ++qt) {
+    l_i[qt] = sum_over_groups(l_i[qt]);
+    if (TAN) mu_i[qt] = sum_over_groups(mu_i[qt]);
   }
 
-  // ---- merge the four per-wave softmax states (fixed order: exact ties) ----
+  // ---- merge the four per-wave states (fixed order: deterministic) ----
+  __syncthreads();  // every wave is done with the qsh operands
   if (g == 0) {
 #pragma unroll
-    for (int qt = 0; qt < 4; ++qt) {
-      stat[0][w][qt][r] = m_i[qt];
+    for (int qt = 0; qt < kQT; ++qt) {
+      stat[0][w][qt][r] = mref[qt];
       stat[1][w][qt][r] = l_i[qt];
       stat[2][w][qt][r] = mu_i[qt];
     }
   }
   __syncthreads();
-  float fself[4];
+  float fself[kQT];
 #pragma unroll
-  for (int qt = 0; qt < 4; ++qt) {
+  for (int qt = 0; qt < kQT; ++qt) {
     float M = -INFINITY;
 #pragma unroll
     for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, stat[0][ww][qt][r]);
-    fself[qt] = (m_i[qt] == -INFINITY) ? 0.f : exp2f(m_i[qt] - M);
+    fself[qt] = (mref[qt] == -INFINITY) ? 0.f : fast_exp2(mref[qt] - M);
   }
+  // this wave finalises query sub-tile qo = w >> 1, output column tiles cpair, cpair+1
+  const int qo = w >> 1;
+  const int cpair = 2 * (w & 1);
   float Mw = -INFINITY;
 #pragma unroll
-  for (int ww = 0; ww < 4; ++ww) Mw = fmaxf(Mw, stat[0][ww][w][r]);
+  for (int ww = 0; ww < 4; ++ww) Mw = fmaxf(Mw, stat[0][ww][qo][r]);
   float ltot = 0.f, mutot = 0.f;
 #pragma unroll
   for (int ww = 0; ww < 4; ++ww) {
-    const float mw = stat[0][ww][w][r];
-    const float f = (mw == -INFINITY) ? 0.f : exp2f(mw - Mw);
-    ltot += stat[1][ww][w][r] * f;
-    mutot += stat[2][ww][w][r] * f;
+    const float mw = stat[0][ww][qo][r];
+    const float f = (mw == -INFINITY) ? 0.f : fast_exp2(mw - Mw);
+    ltot += stat[1][ww][qo][r] * f;
+    mutot += stat[2][ww][qo][r] * f;
   }
 
-  f32x4 O[4], DO[4];
+  f32x4 O[2], DO[2];
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
+    const bool mine = (ct >> 1) == (w & 1);
 #pragma unroll
-    for (int qt = 0; qt < 4; ++qt)
+    for (int qt = 0; qt < kQT; ++qt)
       *reinterpret_cast<f32x4*>(&xbuf[w][qt][l][0]) = acc_o[ct][qt] * fself[qt];
     __syncthreads();
-    f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+    if (mine) {
+      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-    for (int ww = 0; ww < 4; ++ww) s += *reinterpret_cast<const f32x4*>(&xbuf[ww][w][l][0]);
-    O[ct] = s;
+      for (int ww = 0; ww < 4; ++ww) s += *reinterpret_cast<const f32x4*>(&xbuf[ww][qo][l][0]);
+      O[ct & 1] = s;
+    }
     __syncthreads();
     if (TAN) {
 #pragma unroll
-      for (int qt = 0; qt < 4; ++qt)
+      for (int qt = 0; qt < kQT; ++qt)
         *reinterpret_cast<f32x4*>(&xbuf[w][qt][l][0]) = acc_do[ct][qt] * fself[qt];
       __syncthreads();
-      f32x4 s2 = f32x4{0.f, 0.f, 0.f, 0.f};
+      if (mine) {
+        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int ww = 0; ww < 4; ++ww) s2 += *reinterpret_cast<const f32x4*>(&xbuf[ww][w][l][0]);
-      DO[ct] = s2;
+        for (int ww = 0; ww < 4; ++ww) s += *reinterpret_cast<const f32x4*>(&xbuf[ww][qo][l][0]);
+        DO[ct & 1] = s;
+      }
       __syncthreads();
     }
   }
 
-  // ---- epilogue for queries 16w + r of this block ----
-  const int64_t qrow = (int64_t)m * kTa + 16 * w + r;
+  // ---- epilogue: query q0 + 16 qo + r, output columns 16 (cpair + cc) + 4g + i ----
+  const int64_t qrow = q0 + 16 * qo + r;
   const float inv_mu = mutot / ltot;
-  f32x4 os[4], dos[4];
+  f32x4 os[2], dos[2];
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
+  for (int cc = 0; cc < 2; ++cc) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      os[ct][i] = O[ct][i] / ltot;
-      if (TAN) dos[ct][i] = DO[ct][i] / ltot - inv_mu * os[ct][i];
+      os[cc][i] = O[cc][i] / ltot;
+      if (TAN) dos[cc][i] = DO[cc][i] / ltot - inv_mu * os[cc][i];
     }
   }
 
   if (LINEAR) {
-    // phi(q), dphi(q) for query qrow in B-operand layout: d = 32 ks + 8 g + jj
+    // phi(q), dphi(q) of this lane's query in B-operand layout: d = 32 ks + 8 g + e
     float qv[2][8], dqv[2][8];
     const bool qok = qrow < L;
     const int64_t ro = (qkbase + qrow) * kTa;
@@ -331,23 +452,17 @@ __global__ __launch_bounds__(256, 1) void fwd_jvp_kernel(FwdArgs a) {
     u32x4 ph[2], pl[2], dph[2], dpl[2];
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      uint16_t hi[8], lo[8], dhi[8], dlo[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        hi[e] = bf16_bits(phi[ks][e]);
-        lo[e] = bf16_bits(phi[ks][e] - bf16_val(hi[e]));
-        if (TAN) {
-          dhi[e] = bf16_bits(dphi[ks][e]);
-          dlo[e] = bf16_bits(dphi[ks][e] - bf16_val(dhi[e]));
-        }
-      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        ph[ks][e] = pack2(hi[2 * e], hi[2 * e + 1]);
-        pl[ks][e] = pack2(lo[2 * e], lo[2 * e + 1]);
+        const float a0 = phi[ks][2 * e], a1 = phi[ks][2 * e + 1];
+        ph[ks][e] = pack_pair<BF16>(a0, a1);
+        pl[ks][e] = pack_pair<BF16>(a0 - bf16_val((uint16_t)(ph[ks][e] & 0xffff)),
+                                    a1 - bf16_val((uint16_t)(ph[ks][e] >> 16)));
         if (TAN) {
-          dph[ks][e] = pack2(dhi[2 * e], dhi[2 * e + 1]);
-          dpl[ks][e] = pack2(dlo[2 * e], dlo[2 * e + 1]);
+          const float b0 = dphi[ks][2 * e], b1 = dphi[ks][2 * e + 1];
+          dph[ks][e] = pack_pair<BF16>(b0, b1);
+          dpl[ks][e] = pack_pair<BF16>(b0 - bf16_val((uint16_t)(dph[ks][e] & 0xffff)),
+                                       b1 - bf16_val((uint16_t)(dph[ks][e] >> 16)));
         }
       }
     }
@@ -356,19 +471,28 @@ __global__ __launch_bounds__(256, 1) void fwd_jvp_kernel(FwdArgs a) {
     const float* dzc = reinterpret_cast<const float*>(rec + 33024);
     float dn = 0.f, ddn = 0.f;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
+    for (int ks = 0; ks < 2; ++ks) {
+      const f32x4 z0 = *reinterpret_cast<const f32x4*>(zc + 32 * ks + 8 * g);
+      const f32x4 z1 = *reinterpret_cast<const f32x4*>(zc + 32 * ks + 8 * g + 4);
+      f32x4 dz0 = f32x4{0.f, 0.f, 0.f, 0.f}, dz1 = dz0;
+      if (TAN) {
+        dz0 = *reinterpret_cast<const f32x4*>(dzc + 32 * ks + 8 * g);
+        dz1 = *reinterpret_cast<const f32x4*>(dzc + 32 * ks + 8 * g + 4);
+      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const int d = 32 * ks + 8 * g + e;
-        dn += phi[ks][e] * zc[d];
-        if (TAN) ddn += dphi[ks][e] * zc[d] + phi[ks][e] * dzc[d];
+        const float z = e < 4 ? z0[e] : z1[e - 4];
+        dn += phi[ks][e] * z;
+        if (TAN) ddn += dphi[ks][e] * z + phi[ks][e] * (e < 4 ? dz0[e] : dz1[e - 4]);
       }
+    }
     dn = sum_over_groups(dn);
     dn = dn >= 0.f ? dn + a.eps_l : dn - a.eps_l;
     if (TAN) ddn = sum_over_groups(ddn);
     const float al = a.alpha[(int64_t)h * a.alpha_stride + m];
 #pragma unroll
-    for (int vt_ = 0; vt_ < 4; ++vt_) {
+    for (int cc = 0; cc < 2; ++cc) {
+      const int vt_ = cpair + cc;
       f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f}, dnum = num;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
@@ -392,10 +516,10 @@ __global__ __launch_bounds__(256, 1) void fwd_jvp_kernel(FwdArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float ol = num[i] / dn;
-        os[vt_][i] = al * os[vt_][i] + (1.f - al) * ol;
+        os[cc][i] = al * os[cc][i] + (1.f - al) * ol;
         if (TAN) {
           const float dol = (dnum[i] - ol * ddn) / dn;
-          dos[vt_][i] = al * dos[vt_][i] + (1.f - al) * dol;
+          dos[cc][i] = al * dos[cc][i] + (1.f - al) * dol;
         }
       }
     }
@@ -404,23 +528,23 @@ __global__ __launch_bounds__(256, 1) void fwd_jvp_kernel(FwdArgs a) {
   if (qrow < L) {
     const int64_t oo = (qkbase + qrow) * kTa + 4 * g;
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      *reinterpret_cast<f32x4*>(a.o + oo + 16 * ct) = os[ct];
-      if (TAN) *reinterpret_cast<f32x4*>(a.dout + oo + 16 * ct) = dos[ct];
+    for (int cc = 0; cc < 2; ++cc) {
+      *reinterpret_cast<f32x4*>(a.o + oo + 16 * (cpair + cc)) = os[cc];
+      if (TAN) *reinterpret_cast<f32x4*>(a.dout + oo + 16 * (cpair + cc)) = dos[cc];
     }
   }
 }
 
-template <typename T16>
+template <typename T16, bool PRE>
 static void launch_fwd(const FwdArgs& a, bool tan, bool linear, int nblocks, hipStream_t st) {
   if (tan && linear)
-    fwd_jvp_kernel<T16, true, true><<<nblocks, 256, 0, st>>>(a);
+    fwd_jvp_kernel<T16, true, true, PRE><<<nblocks, 256, 0, st>>>(a);
   else if (tan)
-    fwd_jvp_kernel<T16, true, false><<<nblocks, 256, 0, st>>>(a);
+    fwd_jvp_kernel<T16, true, false, PRE><<<nblocks, 256, 0, st>>>(a);
   else if (linear)
-    fwd_jvp_kernel<T16, false, true><<<nblocks, 256, 0, st>>>(a);
+    fwd_jvp_kernel<T16, false, true, false><<<nblocks, 256, 0, st>>>(a);
   else
-    fwd_jvp_kernel<T16, false, false><<<nblocks, 256, 0, st>>>(a);
+    fwd_jvp_kernel<T16, false, false, false><<<nblocks, 256, 0, st>>>(a);
 }
 
 }  // namespace sla2h
@@ -428,7 +552,7 @@ static void launch_fwd(const FwdArgs& a, bool tan, bool linear, int nblocks, hip
 using namespace sla2h;
 
 extern "C" int sla2h_fwd_jvp(const void* q, const void* k, const void* dq, const void* dk,
-                             const void* vt, const void* dvt, const int8_t* q8, const int8_t* k8,
+                             const void* vt, const int8_t* q8, const int8_t* k8,
                              const float* qs, const float* ks, const void* comp,
                              const float* alpha, int alpha_stride, const int32_t* lut, int dtype,
                              int B, int H, int64_t L, int D, int E, int Np, int T, float scale,
@@ -438,20 +562,22 @@ extern "C" int sla2h_fwd_jvp(const void* q, const void* k, const void* dq, const
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   SLA2H_CHECK_ARG(B > 0 && H > 0 && L > 0 && Np > 0 && (int64_t)Np * E <= L);
   SLA2H_CHECK_ARG(T >= 1 && T <= Np);
+  const int Nb_ = (int)((L + E - 1) / E);
+  SLA2H_CHECK_ARG(T + (Nb_ - Np) <= kMaxTiles);
   const bool tan = dq != nullptr;
-  if (tan) SLA2H_CHECK_ARG(k && dk && dvt && dout);
+  if (tan) SLA2H_CHECK_ARG(k && dk && dout);
   const bool linear = (flags & SLA2H_FLAG_SPARSE_ONLY) == 0;
   if (linear) SLA2H_CHECK_ARG(comp && alpha && alpha_stride >= 0);
   const int Nb = (int)((L + E - 1) / E);
-  const int64_t nblocks = (int64_t)Nb * B * H;
-  SLA2H_CHECK_ARG(nblocks < (1ll << 31));
+  const int64_t nwork = 2ll * Nb * B * H;  // half query blocks
+  const int64_t per_xcd = (nwork + 7) / 8;
+  SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31));
   FwdArgs a;
   a.q = static_cast<const uint16_t*>(q);
   a.k = static_cast<const uint16_t*>(k);
   a.dq = static_cast<const uint16_t*>(dq);
   a.dk = static_cast<const uint16_t*>(dk);
   a.vt = static_cast<const uint16_t*>(vt);
-  a.dvt = static_cast<const uint16_t*>(dvt);
   a.q8 = q8;
   a.k8 = k8;
   a.qs = qs;
@@ -469,13 +595,25 @@ extern "C" int sla2h_fwd_jvp(const void* q, const void* k, const void* dq, const
   a.T = T;
   a.n_tail = Nb - Np;
   a.alpha_stride = alpha_stride;
+  a.nwork = (int)nwork;
+  a.per_xcd = (int)per_xcd;
   a.scale = scale;
+  {
+    int ex;
+    const float fr = frexpf(scale, &ex);
+    a.prescale = (fr == 0.5f && ex > -100 && ex < 100) ? 1 : 0;
+  }
   a.c_log2 = scale * 1.4426950408889634f;
   a.eps_l = eps_l;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  if (dtype == SLA2H_DTYPE_BF16)
-    launch_fwd<BF16>(a, tan, linear, (int)nblocks, st);
-  else
-    launch_fwd<F16>(a, tan, linear, (int)nblocks, st);
+  const int nblocks = (int)(8 * per_xcd);
+  if (dtype == SLA2H_DTYPE_BF16) {
+    if (a.prescale)
+      launch_fwd<BF16, true>(a, tan, linear, nblocks, st);
+    else
+      launch_fwd<BF16, false>(a, tan, linear, nblocks, st);
+  } else {
+    launch_fwd<F16, false>(a, tan, linear, nblocks, st);
+  }
   return (int)hipGetLastError();
 }

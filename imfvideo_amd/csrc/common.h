@@ -92,19 +92,74 @@ __device__ inline uint32_t pack2(uint16_t lo, uint16_t hi) {
   return (uint32_t)lo | ((uint32_t)hi << 16);
 }
 
-// xor-shuffle within the wave64 (ds_bpermute).
-__device__ inline float shfl_xor(float v, int m) { return __shfl_xor(v, m, 64); }
+typedef __attribute__((ext_vector_type(2))) float f32x2;
+typedef __attribute__((ext_vector_type(2))) __bf16 bf16x2;
+typedef __attribute__((ext_vector_type(2))) _Float16 f16x2;
 
-__device__ inline float max_over_groups(float v) {  // over lanes l, l^16, l^32, l^48
-  v = fmaxf(v, shfl_xor(v, 16));
-  v = fmaxf(v, shfl_xor(v, 32));
-  return v;
+// Two fp32 -> one packed pair of 16-bit values (round to nearest even),
+// a single v_cvt_pk_* instruction.
+template <typename T16>
+__device__ inline uint32_t pack_pair(float lo, float hi);
+template <>
+__device__ inline uint32_t pack_pair<BF16>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), bf16x2));
 }
+template <>
+__device__ inline uint32_t pack_pair<F16>(float lo, float hi) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
+}
+
+// Reductions over the four 16-lane rows of a wave64 (lanes l, l^16, l^32,
+// l^48) with the gfx950 row-swap permutes: VALU only, no LDS round trip.
+// permlane16_swap(x, x) yields (x[l & ~16], x[l | 16]) and
+// permlane32_swap(x, x) yields (x[l & ~32], x[l | 32]).
+__device__ inline float2 swap16(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(unsigned, v),
+                                                  __builtin_bit_cast(unsigned, v), false, false);
+  return make_float2(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+__device__ inline float2 swap32(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__builtin_bit_cast(unsigned, v),
+                                                  __builtin_bit_cast(unsigned, v), false, false);
+  return make_float2(__builtin_bit_cast(float, (unsigned)r[0]), __builtin_bit_cast(float, (unsigned)r[1]));
+}
+__device__ inline float max_over_groups(float v) {
+  float2 a = swap16(v);
+  v = fmaxf(a.x, a.y);
+  a = swap32(v);
+  return fmaxf(a.x, a.y);
+}
+// (x0 + x1) + (x2 + x3) with the row pairs in a fixed order: every lane of a
+// column gets the bit-identical sum.
 __device__ inline float sum_over_groups(float v) {
-  v += shfl_xor(v, 16);
-  v += shfl_xor(v, 32);
-  return v;
+  float2 a = swap16(v);
+  v = a.x + a.y;
+  a = swap32(v);
+  return a.x + a.y;
 }
+
+// Raw buffer resources (gfx9 descriptor, stride 0, byte-addressed): loads
+// past num_bytes return zeros, and offsets are 32-bit VGPRs.
+// `base` and `num_bytes` must be wave-uniform; they are pinned to SGPRs here
+// (64-bit products may be computed on the VALU, and a VGPR descriptor would
+// make every load a readfirstlane waterfall loop).
+__device__ inline __amdgpu_buffer_rsrc_t make_rsrc(const void* base, int64_t num_bytes) {
+  const uint64_t v = reinterpret_cast<uint64_t>(base);
+  const uint32_t lo = __builtin_amdgcn_readfirstlane((uint32_t)v);
+  const uint32_t hi = __builtin_amdgcn_readfirstlane((uint32_t)(v >> 32));
+  void* p = reinterpret_cast<void*>(((uint64_t)hi << 32) | lo);
+  return __builtin_amdgcn_make_buffer_rsrc(p, 0, __builtin_amdgcn_readfirstlane((int)num_bytes),
+                                           0x00020000);
+}
+__device__ inline u32x4 buf_load16(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+  return __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rs, voff, soff, 0));
+}
+__device__ inline u32x2 buf_load8(__amdgpu_buffer_rsrc_t rs, int voff, int soff) {
+  return __builtin_bit_cast(u32x2, __builtin_amdgcn_raw_buffer_load_b64(rs, voff, soff, 0));
+}
+
+// 2^x on the hardware exp unit (v_exp_f32); inputs here are <= 0 or -inf.
+__device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 }  // namespace sla2h
 

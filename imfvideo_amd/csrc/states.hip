@@ -14,8 +14,10 @@ constexpr int kT = 64;          // E = D = 64
 constexpr int kLds = kT + 8;    // padded LDS row (16-bit elements)
 constexpr size_t kRecBytes = 2 * 16384 + 2 * 256;
 
-// One tile (b,h,n) per workgroup.  n < Np: phi, states; every n < Nb:
-// transposed value tiles vt/dvt (rows past L are zero).
+// One tile (b,h,n) per workgroup.  n < Np: phi, states; every n < Nb: the
+// value-operand tile vt (rows past L are zero): without tangent the
+// transposed V tile vt[c][r]; with tangent V and dV interleaved in groups of
+// four keys, vt[c][r/4][0:4] = V[r..r+3][c], vt[c][r/4][4:8] = dV[r..r+3][c].
 //
 // Products phi^T V run on 16-bit MFMA with phi split into hi + lo halves of
 // the input's 16-bit type (about 16 significant bits), fp32 accumulate.
@@ -24,7 +26,7 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
     const uint16_t* __restrict__ K, const uint16_t* __restrict__ dK,
     const uint16_t* __restrict__ V, const uint16_t* __restrict__ dV, int64_t L, int Np, int Nb,
     float* __restrict__ Hb, float* __restrict__ dHb, float* __restrict__ zb,
-    float* __restrict__ dzb, uint16_t* __restrict__ vt, uint16_t* __restrict__ dvt) {
+    float* __restrict__ dzb, uint16_t* __restrict__ vt) {
   __shared__ __align__(16) uint16_t phiT[2][kT][kLds];   // [hi/lo][d][r]
   __shared__ __align__(16) uint16_t dphiT[2][kT][kLds];
   __shared__ __align__(16) uint16_t vT[kT][kLds];        // [c][r]
@@ -132,20 +134,27 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
   }
   __syncthreads();
 
-  // transposed value tiles: vt[bh, n, c, r]
+  // value-operand tile
   {
     const int c = tid >> 2;
     const int r0 = (tid & 3) * 16;
-    const int64_t vo = (((int64_t)bh * Nb + n) * kT + c) * kT + r0;
-    const uint4* s = reinterpret_cast<const uint4*>(&vT[c][r0]);
-    uint4* d = reinterpret_cast<uint4*>(vt + vo);
-    d[0] = s[0];
-    d[1] = s[1];
-    if (TAN) {
-      const uint4* s2 = reinterpret_cast<const uint4*>(&dvT[c][r0]);
-      uint4* d2 = reinterpret_cast<uint4*>(dvt + vo);
-      d2[0] = s2[0];
-      d2[1] = s2[1];
+    if (!TAN) {
+      const int64_t vo = (((int64_t)bh * Nb + n) * kT + c) * kT + r0;
+      const uint4* src = reinterpret_cast<const uint4*>(&vT[c][r0]);
+      uint4* d = reinterpret_cast<uint4*>(vt + vo);
+      d[0] = src[0];
+      d[1] = src[1];
+    } else {
+      // 4 key groups of this thread: 4 x (4 V + 4 dV) halves = 64 contiguous bytes
+      const int64_t vo = ((((int64_t)bh * Nb + n) * kT + c) * (kT / 4) + r0 / 4) * 8;
+      const uint2* sv = reinterpret_cast<const uint2*>(&vT[c][r0]);
+      const uint2* sd = reinterpret_cast<const uint2*>(&dvT[c][r0]);
+      uint4* d = reinterpret_cast<uint4*>(vt + vo);
+#pragma unroll
+      for (int kg = 0; kg < 4; ++kg) {
+        const uint2 a = sv[kg], b = sd[kg];
+        d[kg] = make_uint4(a.x, a.y, b.x, b.y);
+      }
     }
   }
   if (!states) return;
@@ -295,7 +304,7 @@ extern "C" size_t sla2h_complement_record_bytes(int D) { return D == kT ? kRecBy
 extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v, const void* dv,
                                    int dtype, int B, int H, int64_t L, int D, int E, int Np,
                                    float* Hb, float* dHb, float* zb, float* dzb, float* Hall,
-                                   float* dHall, float* zall, float* dzall, void* vt, void* dvt,
+                                   float* dHall, float* zall, float* dzall, void* vt,
                                    void* stream) {
   SLA2H_CHECK_ARG(k && v && Hb && zb && Hall && zall && vt);
   SLA2H_CHECK_ARG(D == kT && E == kT);
@@ -303,7 +312,7 @@ extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v,
   SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535);
   SLA2H_CHECK_ARG(Np > 0 && (int64_t)Np * E <= L);
   const bool tan = dk != nullptr;
-  if (tan) SLA2H_CHECK_ARG(dv && dHb && dzb && dHall && dzall && dvt);
+  if (tan) SLA2H_CHECK_ARG(dv && dHb && dzb && dHall && dzall);
   const int Nb = (int)((L + E - 1) / E);
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid(Nb, B * H);
@@ -312,17 +321,16 @@ extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v,
   auto V = static_cast<const uint16_t*>(v);
   auto dV = static_cast<const uint16_t*>(dv);
   auto VT = static_cast<uint16_t*>(vt);
-  auto dVT = static_cast<uint16_t*>(dvt);
   if (dtype == SLA2H_DTYPE_BF16) {
     if (tan)
-      linear_states_kernel<BF16, true><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT, dVT);
+      linear_states_kernel<BF16, true><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT);
     else
-      linear_states_kernel<BF16, false><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT, dVT);
+      linear_states_kernel<BF16, false><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT);
   } else {
     if (tan)
-      linear_states_kernel<F16, true><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT, dVT);
+      linear_states_kernel<F16, true><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT);
     else
-      linear_states_kernel<F16, false><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT, dVT);
+      linear_states_kernel<F16, false><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT);
   }
   int err = (int)hipGetLastError();
   if (err) return err;

@@ -110,8 +110,8 @@ def route_topk(qpool, kpool_t, T, scale, with_mask=False):
 def linear_states(k, v, Np, dk=None, dv=None, E=E_TILE):
     """phi(K)-states of the video tiles, their sums and transposed value tiles.
 
-    Returns a dict with Hb, zb, Hall, zall, vt (and dHb, dzb, dHall, dzall, dvt
-    when dk/dv are given).
+    Returns a dict with Hb, zb, Hall, zall, vt (and dHb, dzb, dHall, dzall
+    when dk/dv are given; vt then interleaves V and dV).
     """
     _need_gpu(k, v, dk, dv)
     k, v = _bhld(k, "k"), _bhld(v, "v")
@@ -126,19 +126,18 @@ def linear_states(k, v, Np, dk=None, dv=None, E=E_TILE):
         "zb": torch.empty(B, H, Np, D, device=dev, dtype=f32),
         "Hall": torch.empty(B, H, D, D, device=dev, dtype=f32),
         "zall": torch.empty(B, H, D, device=dev, dtype=f32),
-        "vt": torch.empty(B, H, nb, D, E, device=dev, dtype=v.dtype),
+        "vt": torch.empty(B, H, nb, D, E * (2 if tan else 1), device=dev, dtype=v.dtype),
     }
     if tan:
         st.update({
             "dHb": torch.empty_like(st["Hb"]), "dzb": torch.empty_like(st["zb"]),
             "dHall": torch.empty_like(st["Hall"]), "dzall": torch.empty_like(st["zall"]),
-            "dvt": torch.empty_like(st["vt"]),
         })
     g = lambda n: _ptr(st.get(n))
     _lib.check(_lib.load().sla2h_linear_states(
         k.data_ptr(), _ptr(dk), v.data_ptr(), _ptr(dv), _dtype_code(k), B, H, L, D, E, Np,
         g("Hb"), g("dHb"), g("zb"), g("dzb"), g("Hall"), g("dHall"), g("zall"), g("dzall"),
-        g("vt"), g("dvt"), _stream(dev)), "sla2h_linear_states")
+        g("vt"), _stream(dev)), "sla2h_linear_states")
     return st
 
 
@@ -161,6 +160,8 @@ def fwd_jvp(q, k, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq=None, dk=None,
     B, H, L, D = q.shape
     T = lut.shape[-1]
     tan = dq is not None
+    if tan != ("dHb" in st):
+        raise ValueError("fwd_jvp: the states must be built with tangents exactly when dq is given")
     scale = D ** -0.5 if scale is None else scale
     o = torch.empty(B, H, L, D, device=q.device, dtype=torch.float32)
     do = torch.empty_like(o) if tan else None
@@ -170,7 +171,7 @@ def fwd_jvp(q, k, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq=None, dk=None,
             alpha = alpha.reshape(H, -1).contiguous()
     _lib.check(_lib.load().sla2h_fwd_jvp(
         q.data_ptr(), k.data_ptr(), _ptr(dq), _ptr(dk), st["vt"].data_ptr(),
-        _ptr(st.get("dvt")) if tan else None, q8.data_ptr(), k8.data_ptr(), qs.data_ptr(),
+        q8.data_ptr(), k8.data_ptr(), qs.data_ptr(),
         ks.data_ptr(), _ptr(comp), _ptr(alpha), 0 if alpha is None else alpha.stride(0),
         lut.contiguous().data_ptr(), _dtype_code(q), B, H, L, D, E_TILE, Np, T, float(scale),
         float(eps_l), 1 if sparse_only else 0, o.data_ptr(), _ptr(do), _stream(q.device)),

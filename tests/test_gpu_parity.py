@@ -87,11 +87,15 @@ def test_linear_states_and_complement():
         r = rel_l2(st[key].cpu(), ref[key])
         print(f"  {key} rel {r:.2e}", flush=True)
         assert r < 1e-4, key
-    # transposed value tiles, zero past L
+    # value-operand tiles, zero past L: V and dV interleaved by groups of 4 keys
     L = ins["v"].shape[2]
     nb = -(-L // 64)
-    vpad = torch.cat([ins["v"], ins["v"].new_zeros(1, 2, nb * 64 - L, 64)], 2)
-    assert torch.equal(st["vt"].cpu(), vpad.view(1, 2, nb, 64, 64).transpose(-1, -2))
+    pad = lambda x: torch.cat([x, x.new_zeros(1, 2, nb * 64 - L, 64)], 2)
+    vT = pad(ins["v"]).view(1, 2, nb, 16, 4, 64).permute(0, 1, 2, 5, 3, 4)   # [n][c][kg][4]
+    dvT = pad(ins["dv"]).view(1, 2, nb, 16, 4, 64).permute(0, 1, 2, 5, 3, 4)
+    assert torch.equal(st["vt"].cpu().view(1, 2, nb, 64, 16, 8), torch.cat([vT, dvT], -1))
+    st0 = ops.linear_states(g["k"], g["v"], Np)
+    assert torch.equal(st0["vt"].cpu(), pad(ins["v"]).view(1, 2, nb, 64, 64).transpose(-1, -2))
     # decode the records: Hc = Hall - sum Hb[lut], bf16 hi + lo
     rec = comp.view(1, 2, nb, -1)
     hc = rec[..., :16384].contiguous().view(torch.int16).view(torch.bfloat16).float()
