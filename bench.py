@@ -122,7 +122,7 @@ def main():
         rec(1)
         lut = ops.route_topk(qpool, kpool_t, T, 0.125)
         rec(2)
-        st = ops.linear_states(k, v, Np, dk, dv)
+        st = ops.linear_states(k, v, Np, dk, dv, with_sums=False)
         rec(3)
         comp = ops.complement(st, lut, Np)
         rec(4)

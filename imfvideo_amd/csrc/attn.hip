@@ -65,6 +65,21 @@ __device__ inline u32x4 scale_bf16x8(u32x4 u, float s) {
   return r;
 }
 
+// A-operand fragment of H^T for numerator MFMAs from a record's fp32 H[d][v]
+// (row-major): 8 consecutive d = 32 ks + 8 g + j at v, split into bf16 hi/lo.
+__device__ inline void load_hfrag(const float* H, int ks, int g, int v, u32x4& hi, u32x4& lo) {
+  float x[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) x[j] = H[(32 * ks + 8 * g + j) * 64 + v];
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t h = pack_pair<BF16>(x[2 * e], x[2 * e + 1]);
+    hi[e] = h;
+    lo[e] = pack_pair<BF16>(x[2 * e] - bf16_val((uint16_t)(h & 0xffff)),
+                            x[2 * e + 1] - bf16_val((uint16_t)(h >> 16)));
+  }
+}
+
 struct KeyRegs {   // score-side operands, loaded one tile ahead
   i32x4 k8;      // K8[key 16w + r][16g .. 16g+15]
   u32x4 ka[4];   // ks 0,1: K[key][32ks + 8g ..], ks 2,3: dK[key][32(ks-2) + 8g ..]
@@ -496,15 +511,15 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
       f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f}, dnum = num;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const unsigned char* hp = rec + ((vt_ * 2 + ks) * 64 + l) * 32;
-        const u32x4 hh = *reinterpret_cast<const u32x4*>(hp);
-        const u32x4 hl = *reinterpret_cast<const u32x4*>(hp + 16);
+        const float* Hc = reinterpret_cast<const float*>(rec);
+        u32x4 hh, hl;
+        load_hfrag(Hc, ks, g, 16 * vt_ + r, hh, hl);
         num = mfma_bf16_16x16x32(hh, ph[ks], num);
         num = mfma_bf16_16x16x32(hh, pl[ks], num);
         num = mfma_bf16_16x16x32(hl, ph[ks], num);
         if (TAN) {
-          const u32x4 dh = *reinterpret_cast<const u32x4*>(hp + 16384);
-          const u32x4 dl = *reinterpret_cast<const u32x4*>(hp + 16384 + 16);
+          u32x4 dh, dl;
+          load_hfrag(Hc + 4096, ks, g, 16 * vt_ + r, dh, dl);
           dnum = mfma_bf16_16x16x32(hh, dph[ks], dnum);
           dnum = mfma_bf16_16x16x32(hh, dpl[ks], dnum);
           dnum = mfma_bf16_16x16x32(hl, dph[ks], dnum);

@@ -243,54 +243,146 @@ __global__ __launch_bounds__(256) void states_sum_kernel(const float* __restrict
   dst[(int64_t)bh * stride + col] = acc;
 }
 
-// Complement record of query block m: Hc = Hall - sum_j Hb[lut[m,j]] in LUT
-// order (fp32), stored as bf16 hi/lo MFMA A-operand fragments:
-//   u16 index (((vt*2 + ks)*64 + lane)*16 + j [+8 for lo]),
-//   v = 16 vt + lane%16, d = 32 ks + 8 (lane/16) + j, value Hc[d][v];
-// then dHc at byte 16384, zc at 32768, dzc at 33024 (fp32).
-__global__ __launch_bounds__(256) void complement_kernel(
+// ---------------------------------------------------------------------------
+// Complement records.  For each query block m of a head:
+//   Hc[m] = sum over the video tiles n NOT routed for m of Hb[n]   (and dHc, zc, dzc)
+// computed as one GEMM per head, C = Mc . S, with Mc[m][n] = 1 - sel(m, n)
+// (Mb x Np, 0/1) and S = [Hb | dHb | zb | dzb] (Np x 8320 columns, fp32).  S
+// is split into bf16 hi + lo halves (about 16 significant bits) and the
+// products accumulate in fp32 on MFMA; the mask is exact in bf16.
+//
+// Record of (b,h,m), kRecBytes bytes, fp32:
+//   [0, 16384) Hc[d][v] row-major, [16384, 32768) dHc, [32768, 33024) zc,
+//   [33024, 33280) dzc.
+// ---------------------------------------------------------------------------
+constexpr int kMaskSub = 32;  // 16-row mask sub-tiles per GEMM workgroup (512 rows)
+
+// Mask operand fragments mfrag[bh][mt][kc][lane][8] (bf16 bits): row
+// m = 16 mt + lane%16, tiles n = 32 kc + 8 (lane/16) + 0..7; value 1 where n < Np
+// is not routed for m (and m < Mb), else 0.
+__global__ __launch_bounds__(256) void comp_mask_kernel(const int32_t* __restrict__ lut, int Mb,
+                                                      int Np, int T, int MT, int NC,
+                                                      uint16_t* __restrict__ mfrag) {
+  extern __shared__ uint32_t selbits[];  // [16][NC]
+  const int mt = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
+  for (int i = tid; i < 16 * NC; i += 256) selbits[i] = 0u;
+  __syncthreads();
+  for (int i = tid; i < 16 * T; i += 256) {
+    const int row = i / T, jj = i % T;
+    const int m = mt * 16 + row;
+    if (m >= Mb) continue;
+    const int n = lut[((int64_t)bh * Mb + m) * T + jj];
+    if ((unsigned)n < (unsigned)Np) atomicOr(&selbits[row * NC + (n >> 5)], 1u << (n & 31));
+  }
+  __syncthreads();
+  for (int i = tid; i < NC * 64; i += 256) {
+    const int kc = i >> 6, lane = i & 63;
+    const int rr = lane & 15, g = lane >> 4;
+    const int m = mt * 16 + rr;
+    const uint32_t bits = selbits[rr * NC + kc] >> (8 * g);
+    uint32_t w[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint32_t pair = 0;
+#pragma unroll
+      for (int h2 = 0; h2 < 2; ++h2) {
+        const int jb = 2 * e + h2;
+        const int n = kc * 32 + 8 * g + jb;
+        const bool on = m < Mb && n < Np && !((bits >> jb) & 1u);
+        pair |= (on ? 0x3F80u : 0u) << (16 * h2);  // bf16 1.0
+      }
+      w[e] = pair;
+    }
+    *reinterpret_cast<uint4*>(mfrag + ((((int64_t)bh * MT + mt) * NC + kc) * 64 + lane) * 8) =
+        make_uint4(w[0], w[1], w[2], w[3]);
+  }
+}
+
+// One workgroup: 32 state columns x up to 512 query blocks of one head.
+template <bool TAN>
+__global__ __launch_bounds__(256) void comp_gemm_kernel(
     const float* __restrict__ Hb, const float* __restrict__ dHb, const float* __restrict__ zb,
-    const float* __restrict__ dzb, const float* __restrict__ Hall,
-    const float* __restrict__ dHall, const float* __restrict__ zall,
-    const float* __restrict__ dzall, const int32_t* __restrict__ lut, int Mb, int Np, int T,
-    unsigned char* __restrict__ comp) {
-  const int m = blockIdx.x;
+    const float* __restrict__ dzb, const uint16_t* __restrict__ mfrag, int Mb, int Np, int MT,
+    int NC, unsigned char* __restrict__ comp) {
+  __shared__ __align__(16) uint16_t st[2][32][40];  // [hi/lo][column][n] (+pad)
+
+  const int tid = threadIdx.x;
+  const int w = tid >> 6, l = tid & 63, r = l & 15, g = l >> 4;
+  const int c0 = blockIdx.x * 32;
   const int bh = blockIdx.y;
-  const int32_t* lrow = lut + ((int64_t)bh * Mb + m) * T;
-  unsigned char* rec = comp + ((int64_t)bh * Mb + m) * kRecBytes;
-  const bool tan = dHb != nullptr;
-  for (int e = threadIdx.x; e < 8320; e += 256) {
-    const float* src;
-    const float* all;
-    int stride, col, part;
-    if (e < 4096) {
-      src = Hb; all = Hall; stride = 4096; col = e; part = 0;
-    } else if (e < 8192) {
-      src = dHb; all = dHall; stride = 4096; col = e - 4096; part = 1;
-    } else if (e < 8256) {
-      src = zb; all = zall; stride = 64; col = e - 8192; part = 2;
-    } else {
-      src = dzb; all = dzall; stride = 64; col = e - 8256; part = 3;
+  const int mt0 = blockIdx.z * kMaskSub;
+
+  // column tile -> source tensor (boundaries are multiples of 32)
+  const float* src;
+  int stride, col0, part;  // part: 0 Hc, 1 dHc, 2 zc, 3 dzc
+  const int zbase = TAN ? 8192 : 4096;
+  if (c0 < 4096) {
+    src = Hb; stride = 4096; col0 = c0; part = 0;
+  } else if (TAN && c0 < 8192) {
+    src = dHb; stride = 4096; col0 = c0 - 4096; part = 1;
+  } else if (c0 < zbase + 64) {
+    src = zb; stride = 64; col0 = c0 - zbase; part = 2;
+  } else {
+    src = dzb; stride = 64; col0 = c0 - zbase - 64; part = 3;
+  }
+  src += (int64_t)bh * Np * stride + col0;
+
+  f32x4 acc[8][2];
+#pragma unroll
+  for (int s = 0; s < 8; ++s) acc[s][0] = acc[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const int ln = tid >> 3, lc = (tid & 7) * 4;  // staging: tile row n, 4 columns
+  auto load_chunk = [&](int kc) {
+    const int n = kc * 32 + ln;
+    return n < Np ? *reinterpret_cast<const float4*>(src + (int64_t)n * stride + lc)
+                  : make_float4(0.f, 0.f, 0.f, 0.f);
+  };
+  float4 x = load_chunk(0);
+  for (int kc = 0; kc < NC; ++kc) {
+    const float xv[4] = {x.x, x.y, x.z, x.w};
+    if (kc + 1 < NC) x = load_chunk(kc + 1);  // prefetch the next chunk
+    __syncthreads();  // previous chunk's operands consumed
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const uint16_t hi = bf16_bits(xv[e]);
+      st[0][lc + e][ln] = hi;
+      st[1][lc + e][ln] = bf16_bits(xv[e] - bf16_val(hi));
     }
-    if (!tan && (part & 1)) continue;
-    float acc = all[(int64_t)bh * stride + col];
-    const float* sb = src + (int64_t)bh * Np * stride + col;
-    for (int j = 0; j < T; ++j) {
-      const int nn = lrow[j];
-      if ((unsigned)nn < (unsigned)Np) acc -= sb[(int64_t)nn * stride];  // ignore corrupt ids
+    __syncthreads();
+    u32x4 bhi[2], blo[2];
+#pragma unroll
+    for (int cs = 0; cs < 2; ++cs) {
+      bhi[cs] = *reinterpret_cast<const u32x4*>(&st[0][cs * 16 + r][8 * g]);
+      blo[cs] = *reinterpret_cast<const u32x4*>(&st[1][cs * 16 + r][8 * g]);
     }
-    if (part >= 2) {
-      reinterpret_cast<float*>(rec + 32768 + (part - 2) * 256)[col] = acc;
-    } else {
-      const int d = col >> 6, v = col & 63;
-      const int vt_ = v >> 4, lr = v & 15, ks = d >> 5, g = (d & 31) >> 3, j = d & 7;
-      const int lane = g * 16 + lr;
-      uint16_t* base = reinterpret_cast<uint16_t*>(rec + part * 16384);
-      const uint16_t hi = bf16_bits(acc);
-      const uint16_t lo = bf16_bits(acc - bf16_val(hi));
-      const int idx = ((vt_ * 2 + ks) * 64 + lane) * 16 + j;
-      base[idx] = hi;
-      base[idx + 8] = lo;
+#pragma unroll
+    for (int s = 0; s < 8; ++s) {
+      const int mt = mt0 + w + 4 * s;
+      if (mt >= MT) break;  // uniform per wave
+      const u32x4 am = *reinterpret_cast<const u32x4*>(
+          mfrag + ((((int64_t)bh * MT + mt) * NC + kc) * 64 + l) * 8);
+#pragma unroll
+      for (int cs = 0; cs < 2; ++cs) {
+        acc[s][cs] = mfma_bf16_16x16x32(am, bhi[cs], acc[s][cs]);
+        acc[s][cs] = mfma_bf16_16x16x32(am, blo[cs], acc[s][cs]);
+      }
+    }
+  }
+
+  // records: lane (g, r) element i = C[16 mt + 4g + i][c0 + 16 cs + r]; 16
+  // consecutive columns of one record per 16 lanes
+  const int pbase = part < 2 ? part * 16384 : 32768 + (part - 2) * 256;
+#pragma unroll
+  for (int s = 0; s < 8; ++s) {
+    const int mt = mt0 + w + 4 * s;
+    if (mt >= MT) break;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int m = mt * 16 + 4 * g + i;
+      if (m >= Mb) continue;
+      float* rec = reinterpret_cast<float*>(comp + ((int64_t)bh * Mb + m) * kRecBytes + pbase);
+#pragma unroll
+      for (int cs = 0; cs < 2; ++cs) rec[col0 + cs * 16 + r] = acc[s][cs][i];
     }
   }
 }
@@ -306,13 +398,15 @@ extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v,
                                    float* Hb, float* dHb, float* zb, float* dzb, float* Hall,
                                    float* dHall, float* zall, float* dzall, void* vt,
                                    void* stream) {
-  SLA2H_CHECK_ARG(k && v && Hb && zb && Hall && zall && vt);
+  SLA2H_CHECK_ARG(k && v && Hb && zb && vt);
+  SLA2H_CHECK_ARG((Hall == nullptr) == (zall == nullptr));
   SLA2H_CHECK_ARG(D == kT && E == kT);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535);
   SLA2H_CHECK_ARG(Np > 0 && (int64_t)Np * E <= L);
   const bool tan = dk != nullptr;
-  if (tan) SLA2H_CHECK_ARG(dv && dHb && dzb && dHall && dzall);
+  if (tan) SLA2H_CHECK_ARG(dv && dHb && dzb);
+  if (tan && Hall) SLA2H_CHECK_ARG(dHall && dzall);
   const int Nb = (int)((L + E - 1) / E);
   hipStream_t st = static_cast<hipStream_t>(stream);
   dim3 grid(Nb, B * H);
@@ -333,24 +427,41 @@ extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v,
       linear_states_kernel<F16, false><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT);
   }
   int err = (int)hipGetLastError();
-  if (err) return err;
+  if (err || Hall == nullptr) return err;
   dim3 g2((8320 + 255) / 256, B * H);
   states_sum_kernel<<<g2, 256, 0, st>>>(Hb, tan ? dHb : nullptr, zb, tan ? dzb : nullptr, Np, Hall,
                                         dHall, zall, dzall);
   return (int)hipGetLastError();
 }
 
+extern "C" size_t sla2h_complement_workspace_bytes(int B, int H, int Mb, int Np) {
+  if (B <= 0 || H <= 0 || Mb <= 0 || Np <= 0) return 0;
+  const size_t MT = (size_t)(Mb + 15) / 16, NC = (size_t)(Np + 31) / 32;
+  return (size_t)B * H * MT * NC * 64 * 8 * 2;
+}
+
 extern "C" int sla2h_complement(const float* Hb, const float* dHb, const float* zb,
-                                const float* dzb, const float* Hall, const float* dHall,
-                                const float* zall, const float* dzall, const int32_t* lut, int B,
-                                int H, int Mb, int Np, int D, int T, void* comp, void* stream) {
-  SLA2H_CHECK_ARG(Hb && zb && Hall && zall && lut && comp);
+                                const float* dzb, const int32_t* lut, int B, int H, int Mb,
+                                int Np, int D, int T, void* workspace, void* comp,
+                                void* stream) {
+  SLA2H_CHECK_ARG(Hb && zb && lut && comp && workspace);
   SLA2H_CHECK_ARG(D == kT);
-  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && Mb > 0 && Np > 0 && T >= 1 && T <= Np);
-  if (dHb) SLA2H_CHECK_ARG(dzb && dHall && dzall);
-  dim3 grid(Mb, B * H);
-  complement_kernel<<<grid, 256, 0, static_cast<hipStream_t>(stream)>>>(
-      Hb, dHb, zb, dzb, Hall, dHall, zall, dzall, lut, Mb, Np, T,
-      static_cast<unsigned char*>(comp));
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && Mb > 0 && Np > 0 && Np <= 4096);
+  SLA2H_CHECK_ARG(T >= 1 && T <= Np);
+  const bool tan = dHb != nullptr;
+  if (tan) SLA2H_CHECK_ARG(dzb);
+  const int MT = (Mb + 15) / 16, NC = (Np + 31) / 32;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto mfrag = static_cast<uint16_t*>(workspace);
+  comp_mask_kernel<<<dim3(MT, B * H), 256, (size_t)16 * NC * 4, st>>>(lut, Mb, Np, T, MT, NC, mfrag);
+  int err = (int)hipGetLastError();
+  if (err) return err;
+  const int ncols = tan ? 8320 : 4160;
+  dim3 grid(ncols / 32, B * H, (MT + kMaskSub - 1) / kMaskSub);
+  auto out = static_cast<unsigned char*>(comp);
+  if (tan)
+    comp_gemm_kernel<true><<<grid, 256, 0, st>>>(Hb, dHb, zb, dzb, mfrag, Mb, Np, MT, NC, out);
+  else
+    comp_gemm_kernel<false><<<grid, 256, 0, st>>>(Hb, nullptr, zb, nullptr, mfrag, Mb, Np, MT, NC, out);
   return (int)hipGetLastError();
 }

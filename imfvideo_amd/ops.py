@@ -107,11 +107,12 @@ def route_topk(qpool, kpool_t, T, scale, with_mask=False):
     return (lut, mask) if with_mask else lut
 
 
-def linear_states(k, v, Np, dk=None, dv=None, E=E_TILE):
-    """phi(K)-states of the video tiles, their sums and transposed value tiles.
+def linear_states(k, v, Np, dk=None, dv=None, E=E_TILE, with_sums=True):
+    """phi(K)-states of the video tiles, their sums and the value-operand tiles.
 
-    Returns a dict with Hb, zb, Hall, zall, vt (and dHb, dzb, dHall, dzall
-    when dk/dv are given; vt then interleaves V and dV).
+    Returns a dict with Hb, zb, vt [, Hall, zall] (and dHb, dzb [, dHall,
+    dzall] when dk/dv are given; vt then interleaves V and dV).  The sums over
+    the tiles are skipped with with_sums=False (the fused op does not need them).
     """
     _need_gpu(k, v, dk, dv)
     k, v = _bhld(k, "k"), _bhld(v, "v")
@@ -124,15 +125,16 @@ def linear_states(k, v, Np, dk=None, dv=None, E=E_TILE):
     st = {
         "Hb": torch.empty(B, H, Np, D, D, device=dev, dtype=f32),
         "zb": torch.empty(B, H, Np, D, device=dev, dtype=f32),
-        "Hall": torch.empty(B, H, D, D, device=dev, dtype=f32),
-        "zall": torch.empty(B, H, D, device=dev, dtype=f32),
         "vt": torch.empty(B, H, nb, D, E * (2 if tan else 1), device=dev, dtype=v.dtype),
     }
     if tan:
-        st.update({
-            "dHb": torch.empty_like(st["Hb"]), "dzb": torch.empty_like(st["zb"]),
-            "dHall": torch.empty_like(st["Hall"]), "dzall": torch.empty_like(st["zall"]),
-        })
+        st.update({"dHb": torch.empty_like(st["Hb"]), "dzb": torch.empty_like(st["zb"])})
+    if with_sums:
+        st.update({"Hall": torch.empty(B, H, D, D, device=dev, dtype=f32),
+                   "zall": torch.empty(B, H, D, device=dev, dtype=f32)})
+        if tan:
+            st.update({"dHall": torch.empty_like(st["Hall"]),
+                       "dzall": torch.empty_like(st["zall"])})
     g = lambda n: _ptr(st.get(n))
     _lib.check(_lib.load().sla2h_linear_states(
         k.data_ptr(), _ptr(dk), v.data_ptr(), _ptr(dv), _dtype_code(k), B, H, L, D, E, Np,
@@ -144,12 +146,14 @@ def linear_states(k, v, Np, dk=None, dv=None, E=E_TILE):
 def complement(st, lut, Np):
     """Per-query-block complement records (uint8 (B,H,Mb,REC_BYTES))."""
     B, H, Mb, T = lut.shape
+    lib = _lib.load()
     comp = torch.empty(B, H, Mb, REC_BYTES, device=lut.device, dtype=torch.uint8)
+    ws = torch.empty(lib.sla2h_complement_workspace_bytes(B, H, Mb, Np), device=lut.device,
+                     dtype=torch.uint8)
     g = lambda n: _ptr(st.get(n))
-    _lib.check(_lib.load().sla2h_complement(
-        g("Hb"), g("dHb"), g("zb"), g("dzb"), g("Hall"), g("dHall"), g("zall"), g("dzall"),
-        lut.contiguous().data_ptr(), B, H, Mb, Np, E_TILE, T, comp.data_ptr(),
-        _stream(lut.device)), "sla2h_complement")
+    _lib.check(lib.sla2h_complement(
+        g("Hb"), g("dHb"), g("zb"), g("dzb"), lut.contiguous().data_ptr(), B, H, Mb, Np,
+        E_TILE, T, ws.data_ptr(), comp.data_ptr(), _stream(lut.device)), "sla2h_complement")
     return comp
 
 
@@ -202,7 +206,7 @@ def cube_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, Np, prefix_len=0, proj_q=Non
     else:
         lut = lut.to(torch.int32).contiguous()
         T = lut.shape[-1]
-    st = linear_states(k, v, Np, dk if tan else None, dv if tan else None, E)
+    st = linear_states(k, v, Np, dk if tan else None, dv if tan else None, E, with_sums=False)
     comp = complement(st, lut, Np)
     o, do = fwd_jvp(q, k, q8, k8, qs, ks, st, comp, alpha, lut, Np,
                     dq if tan else None, dk if tan else None)

@@ -72,7 +72,7 @@ int sla2h_quant_pool_qk(const void* q, const void* k, int dtype, int B, int H,
  * (sequential fp32, no FMA), per row the T largest, ties to the lower index.
  *   lut (B,H,Mb,T) int32, each row ordered by descending score.
  *   mask (B,H,Mb,Np) uint8 or NULL: 1 where selected.
- * Np <= 8192.  Replaces the score GEMM + torch.topk of route_tiles_fast
+ * Np <= 4096.  Replaces the score GEMM + torch.topk of route_tiles_fast
  * (models/mla_video_sparse_jvp.py:563-565) and route_tiles (:292-294).
  */
 int sla2h_route_topk(const float* qpool, const float* kpool_t, int B, int H,
@@ -84,7 +84,8 @@ int sla2h_route_topk(const float* qpool, const float* kpool_t, int B, int H,
  *   Hb  (B,H,Np,D,D) fp32 = phi(K_n)^T V_n
  *   dHb (B,H,Np,D,D) fp32 = dphi(K_n)^T V_n + phi(K_n)^T dV_n
  *   zb, dzb (B,H,Np,D) fp32 = column sums of phi(K_n), dphi(K_n)
- *   Hall,dHall (B,H,D,D), zall,dzall (B,H,D): sums over n (in n order).
+ *   Hall,dHall (B,H,D,D), zall,dzall (B,H,D): sums over n (in n order);
+ *     optional (NULL skips the summation).
  * Also writes the value-operand tiles used by sla2h_fwd_jvp (zero past L):
  *   primal (dv NULL): vt (B,H,Nb,D,E) 16-bit, vt[b,h,n,c,r] = v[b,h,n*E+r,c];
  *   tangent: vt (B,H,Nb,D,E/4,8) 16-bit, V and dV interleaved by 4 keys:
@@ -102,19 +103,24 @@ int sla2h_linear_states(const void* k, const void* dk, const void* v, const void
 /* Bytes of one per-query-block complement record (see sla2h_complement). */
 size_t sla2h_complement_record_bytes(int D);
 
+/* Bytes of the workspace sla2h_complement needs (mask operand fragments). */
+size_t sla2h_complement_workspace_bytes(int B, int H, int Mb, int Np);
+
 /*
- * Complement (non-selected video tiles) linear-branch states per query block:
- *   Hc[m] = Hall - sum_{j<T} Hb[lut[m,j]]   (fp32, subtracted in LUT order)
- *   and dHc, zc, dzc likewise, written as one record of
- *   sla2h_complement_record_bytes(D) bytes per (b,h,m) in the operand layout
- *   that sla2h_fwd_jvp consumes.  Tangent parts skipped when dHb == NULL.
- * Replaces the in-loop state subtraction of _cube_fused_jvp_kernel
- * (models/sla2_cube_qat.py:510-523, 570-578).
+ * Complement (non-routed video tiles) linear-branch states per query block:
+ *   Hc[m] = sum_{n < Np, n not in lut[m,:]} Hb[n], and dHc, zc, dzc likewise,
+ * computed per head as one 0/1-mask GEMM on bf16 MFMA (states split into
+ * bf16 hi + lo, fp32 accumulate) and written as one record of
+ * sla2h_complement_record_bytes(D) bytes per (b,h,m) in the operand layout
+ * that sla2h_fwd_jvp consumes.  Tangent parts skipped when dHb == NULL.
+ * workspace: sla2h_complement_workspace_bytes(B,H,Mb,Np) bytes.  Np <= 4096.
+ * Replaces the in-loop complement-state subtraction of _cube_fused_jvp_kernel
+ * (models/sla2_cube_qat.py:510-523, 570-578), which forms the same sums as
+ * Hall - sum_{j<T} Hb[lut[m,j]].
  */
 int sla2h_complement(const float* Hb, const float* dHb, const float* zb, const float* dzb,
-                     const float* Hall, const float* dHall, const float* zall,
-                     const float* dzall, const int32_t* lut, int B, int H, int Mb,
-                     int Np, int D, int T, void* comp, void* stream);
+                     const int32_t* lut, int B, int H, int Mb, int Np, int D, int T,
+                     void* workspace, void* comp, void* stream);
 
 /*
  * The fused sparse + linear SLA2 op and its forward-mode JVP, tile-major:
