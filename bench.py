@@ -126,7 +126,7 @@ def main():
         rec(3)
         comp = ops.complement(st, lut, Np)
         rec(4)
-        o, do = ops.fwd_jvp(q, k, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq, dk)
+        o, do = ops.fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq)
         rec(5)
         return o, do
 

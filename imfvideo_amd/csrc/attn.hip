@@ -34,10 +34,9 @@ constexpr int kMaxTiles = 1024;  // T + n_tail per query block
 
 struct FwdArgs {
   const uint16_t* q;
-  const uint16_t* k;
   const uint16_t* dq;
-  const uint16_t* dk;
-  const uint16_t* vt;   // value-operand tiles (V, or V|dV interleaved with tangent)
+  const uint16_t* kt;   // key-operand tiles [K|dK] in fragment order (tangent only)
+  const uint16_t* vt;   // value-operand tiles (V, or V|dV with tangent) in fragment order
   const int8_t* q8;
   const int8_t* k8;
   const float* qs;
@@ -148,8 +147,9 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   // per-(b,h) buffer resources: key rows past L read as zeros (those keys are
   // masked; vt/dvt are zero there anyway), 32-bit offsets
   const auto rk8 = make_rsrc(a.k8 + qkbase * kTa, L * kTa);
-  const auto rk = make_rsrc(a.k + qkbase * kTa, L * kTa * 2);
-  const auto rdk = make_rsrc(TAN ? a.dk + qkbase * kTa : a.k, L * kTa * 2);
+  const auto rkt = make_rsrc(TAN ? reinterpret_cast<const char*>(a.kt) + (int64_t)bh * a.Nb * 16384
+                                 : reinterpret_cast<const char*>(a.vt),
+                             (int64_t)a.Nb * 16384);
   constexpr int kVtTile = kTa * kTa * 2 * (TAN ? 2 : 1);  // bytes per value-operand tile
   const auto rvt = make_rsrc(reinterpret_cast<const char*>(a.vt) + (int64_t)bh * a.Nb * kVtTile,
                              (int64_t)a.Nb * kVtTile);
@@ -220,21 +220,17 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     }
   }
 
-  // per-lane parts of the operand offsets; the tile base goes to soffset
+  // per-lane parts of the operand offsets (fragment-ordered tiles: each load
+  // is one contiguous 1 KB per wave); the tile base goes to soffset
   const int k8off = (16 * w + r) * kTa + 16 * g;
-  const int koff = (16 * w + r) * (kTa * 2) + 16 * g;
-  // primal: vt[c][key] (8 B per lane); tangent: vt[c][key/4][V4|dV4] (16 B per lane)
-  const int voff = TAN ? r * (kTa * 4) + 64 * w + 16 * g : r * (kTa * 2) + 32 * w + 8 * g;
+  const int ktoff = w * 4096 + l * 16;
+  const int vtoff = TAN ? w * 1024 + l * 16 : w * 512 + l * 8;
   auto load_keys = [&](int j, KeyRegs& kr) {
     const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
     kr.k8 = __builtin_bit_cast(i32x4, buf_load16(rk8, k8off, n * kTa * kTa));
     if (TAN) {
-      const int sb = n * kTa * kTa * 2;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        kr.ka[ks] = buf_load16(rk, koff + 64 * ks, sb);
-        kr.ka[ks + 2] = buf_load16(rdk, koff + 64 * ks, sb);
-      }
+      for (int ks = 0; ks < 4; ++ks) kr.ka[ks] = buf_load16(rkt, ktoff + ks * 1024, n * 16384);
     }
   };
   auto load_vals = [&](int j, ValRegs& vr) {
@@ -242,9 +238,9 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       if (TAN) {
-        vr.v[ct] = buf_load16(rvt, voff + ct * 16 * kTa * 4, sb);
+        vr.v[ct] = buf_load16(rvt, vtoff + ct * 4096, sb);
       } else {
-        const u32x2 x = buf_load8(rvt, voff + ct * 16 * kTa * 2, sb);
+        const u32x2 x = buf_load8(rvt, vtoff + ct * 2048, sb);
         vr.v[ct] = u32x4{x.x, x.y, 0u, 0u};
       }
     }
@@ -566,8 +562,8 @@ static void launch_fwd(const FwdArgs& a, bool tan, bool linear, int nblocks, hip
 
 using namespace sla2h;
 
-extern "C" int sla2h_fwd_jvp(const void* q, const void* k, const void* dq, const void* dk,
-                             const void* vt, const int8_t* q8, const int8_t* k8,
+extern "C" int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, const void* vt,
+                             const int8_t* q8, const int8_t* k8,
                              const float* qs, const float* ks, const void* comp,
                              const float* alpha, int alpha_stride, const int32_t* lut, int dtype,
                              int B, int H, int64_t L, int D, int E, int Np, int T, float scale,
@@ -580,7 +576,7 @@ extern "C" int sla2h_fwd_jvp(const void* q, const void* k, const void* dq, const
   const int Nb_ = (int)((L + E - 1) / E);
   SLA2H_CHECK_ARG(T + (Nb_ - Np) <= kMaxTiles);
   const bool tan = dq != nullptr;
-  if (tan) SLA2H_CHECK_ARG(k && dk && dout);
+  if (tan) SLA2H_CHECK_ARG(kt && dout);
   const bool linear = (flags & SLA2H_FLAG_SPARSE_ONLY) == 0;
   if (linear) SLA2H_CHECK_ARG(comp && alpha && alpha_stride >= 0);
   const int Nb = (int)((L + E - 1) / E);
@@ -589,9 +585,8 @@ extern "C" int sla2h_fwd_jvp(const void* q, const void* k, const void* dq, const
   SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31));
   FwdArgs a;
   a.q = static_cast<const uint16_t*>(q);
-  a.k = static_cast<const uint16_t*>(k);
   a.dq = static_cast<const uint16_t*>(dq);
-  a.dk = static_cast<const uint16_t*>(dk);
+  a.kt = static_cast<const uint16_t*>(kt);
   a.vt = static_cast<const uint16_t*>(vt);
   a.q8 = q8;
   a.k8 = k8;

@@ -15,9 +15,13 @@ constexpr int kLds = kT + 8;    // padded LDS row (16-bit elements)
 constexpr size_t kRecBytes = 2 * 16384 + 2 * 256;
 
 // One tile (b,h,n) per workgroup.  n < Np: phi, states; every n < Nb: the
-// value-operand tile vt (rows past L are zero): without tangent the
-// transposed V tile vt[c][r]; with tangent V and dV interleaved in groups of
-// four keys, vt[c][r/4][0:4] = V[r..r+3][c], vt[c][r/4][4:8] = dV[r..r+3][c].
+// attention kernel's operand tiles, in MFMA fragment order so that each wave
+// load there is one contiguous 1 KB (rows past L are zero).  With lane
+// (g, r) = (lane/16, lane%16), wave w = keys 16w..16w+15, column tile ct:
+//   vt, tangent: [ct][w][lane] 16 B = V[16w+4g+0..3][16ct+r] | dV[same]
+//   vt, primal:  [ct][w][lane]  8 B = V[16w+4g+0..3][16ct+r]
+//   kt (tangent only): [w][ks][lane] 16 B = K[16w+r][32ks+8g+0..7] for ks 0,1,
+//                      dK[16w+r][32(ks-2)+8g+0..7] for ks 2,3
 //
 // Products phi^T V run on 16-bit MFMA with phi split into hi + lo halves of
 // the input's 16-bit type (about 16 significant bits), fp32 accumulate.
@@ -26,7 +30,7 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
     const uint16_t* __restrict__ K, const uint16_t* __restrict__ dK,
     const uint16_t* __restrict__ V, const uint16_t* __restrict__ dV, int64_t L, int Np, int Nb,
     float* __restrict__ Hb, float* __restrict__ dHb, float* __restrict__ zb,
-    float* __restrict__ dzb, uint16_t* __restrict__ vt) {
+    float* __restrict__ dzb, uint16_t* __restrict__ vt, uint16_t* __restrict__ kt) {
   __shared__ __align__(16) uint16_t phiT[2][kT][kLds];   // [hi/lo][d][r]
   __shared__ __align__(16) uint16_t dphiT[2][kT][kLds];
   __shared__ __align__(16) uint16_t vT[kT][kLds];        // [c][r]
@@ -68,10 +72,27 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
   }
 
   const bool states = n < Np;  // uniform over the workgroup
-  if (states) {
-    uint16_t kb[16], dkb[16];
+  uint16_t kb[16], dkb[16];
+  if (states || TAN) {
     load16(K, kb);
     if (TAN) load16(dK, dkb);
+  }
+  if (TAN) {  // key-operand fragments of this thread's 16 columns: 2 x (K, dK) chunks
+    const int kw = r >> 4, rr = r & 15, ksd = c0 >> 5, g0 = (c0 & 31) >> 3;
+    unsigned char* base = reinterpret_cast<unsigned char*>(kt) + ((int64_t)bh * Nb + n) * 16384;
+#pragma unroll
+    for (int h2 = 0; h2 < 2; ++h2) {
+      const int lane = (g0 + h2) * 16 + rr;
+      uint4 kv, dkv;
+      kv.x = pack2(kb[8 * h2 + 0], kb[8 * h2 + 1]); kv.y = pack2(kb[8 * h2 + 2], kb[8 * h2 + 3]);
+      kv.z = pack2(kb[8 * h2 + 4], kb[8 * h2 + 5]); kv.w = pack2(kb[8 * h2 + 6], kb[8 * h2 + 7]);
+      dkv.x = pack2(dkb[8 * h2 + 0], dkb[8 * h2 + 1]); dkv.y = pack2(dkb[8 * h2 + 2], dkb[8 * h2 + 3]);
+      dkv.z = pack2(dkb[8 * h2 + 4], dkb[8 * h2 + 5]); dkv.w = pack2(dkb[8 * h2 + 6], dkb[8 * h2 + 7]);
+      *reinterpret_cast<uint4*>(base + ((kw * 4 + ksd) * 64 + lane) * 16) = kv;
+      *reinterpret_cast<uint4*>(base + ((kw * 4 + ksd + 2) * 64 + lane) * 16) = dkv;
+    }
+  }
+  if (states) {
     float x[16], phi[16], dphi[16];
     float mx = -INFINITY;
 #pragma unroll
@@ -134,26 +155,22 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
   }
   __syncthreads();
 
-  // value-operand tile
+  // value-operand tile in fragment order: thread -> (ct, w, r), 4 lane groups g
   {
-    const int c = tid >> 2;
-    const int r0 = (tid & 3) * 16;
-    if (!TAN) {
-      const int64_t vo = (((int64_t)bh * Nb + n) * kT + c) * kT + r0;
-      const uint4* src = reinterpret_cast<const uint4*>(&vT[c][r0]);
-      uint4* d = reinterpret_cast<uint4*>(vt + vo);
-      d[0] = src[0];
-      d[1] = src[1];
-    } else {
-      // 4 key groups of this thread: 4 x (4 V + 4 dV) halves = 64 contiguous bytes
-      const int64_t vo = ((((int64_t)bh * Nb + n) * kT + c) * (kT / 4) + r0 / 4) * 8;
-      const uint2* sv = reinterpret_cast<const uint2*>(&vT[c][r0]);
-      const uint2* sd = reinterpret_cast<const uint2*>(&dvT[c][r0]);
-      uint4* d = reinterpret_cast<uint4*>(vt + vo);
+    const int ct = tid >> 6, vw = (tid >> 4) & 3, rr = tid & 15;
+    const int c = 16 * ct + rr;
+    unsigned char* base = reinterpret_cast<unsigned char*>(vt) +
+                          ((int64_t)bh * Nb + n) * (TAN ? 16384 : 8192);
 #pragma unroll
-      for (int kg = 0; kg < 4; ++kg) {
-        const uint2 a = sv[kg], b = sd[kg];
-        d[kg] = make_uint4(a.x, a.y, b.x, b.y);
+    for (int g = 0; g < 4; ++g) {
+      const int lane = g * 16 + rr;
+      const int k0 = 16 * vw + 4 * g;
+      const uint2 a = *reinterpret_cast<const uint2*>(&vT[c][k0]);
+      if (TAN) {
+        const uint2 b = *reinterpret_cast<const uint2*>(&dvT[c][k0]);
+        *reinterpret_cast<uint4*>(base + ((ct * 4 + vw) * 64 + lane) * 16) = make_uint4(a.x, a.y, b.x, b.y);
+      } else {
+        *reinterpret_cast<uint2*>(base + ((ct * 4 + vw) * 64 + lane) * 8) = a;
       }
     }
   }
@@ -396,7 +413,7 @@ extern "C" size_t sla2h_complement_record_bytes(int D) { return D == kT ? kRecBy
 extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v, const void* dv,
                                    int dtype, int B, int H, int64_t L, int D, int E, int Np,
                                    float* Hb, float* dHb, float* zb, float* dzb, float* Hall,
-                                   float* dHall, float* zall, float* dzall, void* vt,
+                                   float* dHall, float* zall, float* dzall, void* vt, void* kt,
                                    void* stream) {
   SLA2H_CHECK_ARG(k && v && Hb && zb && vt);
   SLA2H_CHECK_ARG((Hall == nullptr) == (zall == nullptr));
@@ -405,7 +422,7 @@ extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v,
   SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535);
   SLA2H_CHECK_ARG(Np > 0 && (int64_t)Np * E <= L);
   const bool tan = dk != nullptr;
-  if (tan) SLA2H_CHECK_ARG(dv && dHb && dzb);
+  if (tan) SLA2H_CHECK_ARG(dv && dHb && dzb && kt);
   if (tan && Hall) SLA2H_CHECK_ARG(dHall && dzall);
   const int Nb = (int)((L + E - 1) / E);
   hipStream_t st = static_cast<hipStream_t>(stream);
@@ -415,16 +432,17 @@ extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v,
   auto V = static_cast<const uint16_t*>(v);
   auto dV = static_cast<const uint16_t*>(dv);
   auto VT = static_cast<uint16_t*>(vt);
+  auto KT = static_cast<uint16_t*>(kt);
   if (dtype == SLA2H_DTYPE_BF16) {
     if (tan)
-      linear_states_kernel<BF16, true><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT);
+      linear_states_kernel<BF16, true><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT, KT);
     else
-      linear_states_kernel<BF16, false><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT);
+      linear_states_kernel<BF16, false><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT, KT);
   } else {
     if (tan)
-      linear_states_kernel<F16, true><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT);
+      linear_states_kernel<F16, true><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT, KT);
     else
-      linear_states_kernel<F16, false><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT);
+      linear_states_kernel<F16, false><<<grid, 256, 0, st>>>(K, dK, V, dV, L, Np, Nb, Hb, dHb, zb, dzb, VT, KT);
   }
   int err = (int)hipGetLastError();
   if (err || Hall == nullptr) return err;

@@ -128,7 +128,8 @@ def linear_states(k, v, Np, dk=None, dv=None, E=E_TILE, with_sums=True):
         "vt": torch.empty(B, H, nb, D, E * (2 if tan else 1), device=dev, dtype=v.dtype),
     }
     if tan:
-        st.update({"dHb": torch.empty_like(st["Hb"]), "dzb": torch.empty_like(st["zb"])})
+        st.update({"dHb": torch.empty_like(st["Hb"]), "dzb": torch.empty_like(st["zb"]),
+                   "kt": torch.empty(B, H, nb, D, 2 * E, device=dev, dtype=k.dtype)})
     if with_sums:
         st.update({"Hall": torch.empty(B, H, D, D, device=dev, dtype=f32),
                    "zall": torch.empty(B, H, D, device=dev, dtype=f32)})
@@ -139,7 +140,7 @@ def linear_states(k, v, Np, dk=None, dv=None, E=E_TILE, with_sums=True):
     _lib.check(_lib.load().sla2h_linear_states(
         k.data_ptr(), _ptr(dk), v.data_ptr(), _ptr(dv), _dtype_code(k), B, H, L, D, E, Np,
         g("Hb"), g("dHb"), g("zb"), g("dzb"), g("Hall"), g("dHall"), g("zall"), g("dzall"),
-        g("vt"), _stream(dev)), "sla2h_linear_states")
+        g("vt"), g("kt"), _stream(dev)), "sla2h_linear_states")
     return st
 
 
@@ -157,10 +158,14 @@ def complement(st, lut, Np):
     return comp
 
 
-def fwd_jvp(q, k, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq=None, dk=None,
-            scale=None, eps_l=1e-5, sparse_only=False):
-    """The fused sparse+linear op (and JVP when dq/dk are given) -> (o, do|None) fp32."""
-    _need_gpu(q, k, dq, dk, alpha, lut)
+def fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq=None, scale=None, eps_l=1e-5,
+            sparse_only=False):
+    """The fused sparse+linear op (and JVP when dq is given) -> (o, do|None) fp32.
+
+    The key side comes from k8/ks and the operand tiles of `st`
+    (linear_states with tangents when dq is given).
+    """
+    _need_gpu(q, dq, alpha, lut)
     B, H, L, D = q.shape
     T = lut.shape[-1]
     tan = dq is not None
@@ -174,7 +179,7 @@ def fwd_jvp(q, k, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq=None, dk=None,
         if alpha.dim() != 2 or alpha.stride(1) != 1:
             alpha = alpha.reshape(H, -1).contiguous()
     _lib.check(_lib.load().sla2h_fwd_jvp(
-        q.data_ptr(), k.data_ptr(), _ptr(dq), _ptr(dk), st["vt"].data_ptr(),
+        q.data_ptr(), _ptr(dq), _ptr(st.get("kt")) if tan else None, st["vt"].data_ptr(),
         q8.data_ptr(), k8.data_ptr(), qs.data_ptr(),
         ks.data_ptr(), _ptr(comp), _ptr(alpha), 0 if alpha is None else alpha.stride(0),
         lut.contiguous().data_ptr(), _dtype_code(q), B, H, L, D, E_TILE, Np, T, float(scale),
@@ -208,8 +213,7 @@ def cube_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, Np, prefix_len=0, proj_q=Non
         T = lut.shape[-1]
     st = linear_states(k, v, Np, dk if tan else None, dv if tan else None, E, with_sums=False)
     comp = complement(st, lut, Np)
-    o, do = fwd_jvp(q, k, q8, k8, qs, ks, st, comp, alpha, lut, Np,
-                    dq if tan else None, dk if tan else None)
+    o, do = fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq if tan else None)
     if return_aux:
         aux = dict(q8=q8, qs=qs, k8=k8, ks=ks, qpool=qpool, kpool_t=kpool_t, lut=lut, T=T,
                    comp=comp, **st)

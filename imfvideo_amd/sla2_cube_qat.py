@@ -97,7 +97,7 @@ def _sparse_primal_only(q, k, v, lut, T, Np, E, prefix_len):
     lut = lut.to(torch.int32).contiguous()
     q8, qs, k8, ks, _, _ = ops.quant_pool_qk(qc, kc, Np, E)
     st = ops.linear_states(kc, vc, Np)
-    o, _ = ops.fwd_jvp(qc, kc, q8, k8, qs, ks, st, None, None, lut, Np, sparse_only=True)
+    o, _ = ops.fwd_jvp(qc, q8, k8, qs, ks, st, None, None, lut, Np, sparse_only=True)
     return o
 
 

@@ -86,11 +86,13 @@ int sla2h_route_topk(const float* qpool, const float* kpool_t, int B, int H,
  *   zb, dzb (B,H,Np,D) fp32 = column sums of phi(K_n), dphi(K_n)
  *   Hall,dHall (B,H,D,D), zall,dzall (B,H,D): sums over n (in n order);
  *     optional (NULL skips the summation).
- * Also writes the value-operand tiles used by sla2h_fwd_jvp (zero past L):
- *   primal (dv NULL): vt (B,H,Nb,D,E) 16-bit, vt[b,h,n,c,r] = v[b,h,n*E+r,c];
- *   tangent: vt (B,H,Nb,D,E/4,8) 16-bit, V and dV interleaved by 4 keys:
- *     vt[b,h,n,c,g,0:4] = v[b,h,n*E+4g+0..3,c], vt[b,h,n,c,g,4:8] = dv[...].
- * dk, dv, dHb, dzb, dHall, dzall may all be NULL (primal only).
+ * Also writes the operand tiles of sla2h_fwd_jvp in MFMA fragment order (zero
+ * past L; lane = 16 g + r, wave w = keys 16w..16w+15, column tile ct):
+ *   vt (B,H,Nb,4,4,64,8) 16-bit with tangent: [ct][w][lane] = V[16w+4g+0..3][16ct+r]
+ *      then dV of the same keys; (B,H,Nb,4,4,64,4) = V only without tangent;
+ *   kt (B,H,Nb,4,4,64,8) 16-bit, tangent only: [w][ks][lane] = K[16w+r][32ks+8g+0..7]
+ *      for ks 0,1 and dK[16w+r][32(ks-2)+8g+0..7] for ks 2,3.
+ * dk, dv, dHb, dzb, dHall, dzall, kt may all be NULL (primal only).
  * Replaces _phi_states_kernel + the torch sums of sla2_cube_qat_jvp_fused
  * (models/sla2_cube_qat.py:634-648, 911-958).
  */
@@ -98,7 +100,7 @@ int sla2h_linear_states(const void* k, const void* dk, const void* v, const void
                         int dtype, int B, int H, int64_t L, int D, int E, int Np,
                         float* Hb, float* dHb, float* zb, float* dzb,
                         float* Hall, float* dHall, float* zall, float* dzall,
-                        void* vt, void* stream);
+                        void* vt, void* kt, void* stream);
 
 /* Bytes of one per-query-block complement record (see sla2h_complement). */
 size_t sla2h_complement_record_bytes(int D);
@@ -132,15 +134,15 @@ int sla2h_complement(const float* Hb, const float* dHb, const float* zb, const f
  *   linear branch: o_l = phi(q) Hc / den, den = phi(q).zc (+-eps_l, signed);
  *     do_l by the quotient rule; o = a o_s + (1-a) o_l, a = alpha[h*alpha_stride+m].
  *   Outputs o, dout (B,H,L,D) fp32.  Tangent inputs/outputs NULL = primal only.
- *   vt = the value-operand tiles of sla2h_linear_states (tangent layout when
- *   dq is given).
+ *   vt, kt = the operand tiles of sla2h_linear_states (tangent layouts and kt
+ *   required when dq is given).
  *   comp = sla2h_complement records (unused with SLA2H_FLAG_SPARSE_ONLY).
  * Replaces _cube_fused_jvp_kernel (models/sla2_cube_qat.py:448-602) and,
  * with SLA2H_FLAG_SPARSE_ONLY, _sla2_cube_jvp_qat_kernel's sparse branch
  * (models/sla2_cube_qat.py:59-169, 172-207).
  */
-int sla2h_fwd_jvp(const void* q, const void* k, const void* dq, const void* dk,
-                  const void* vt, const int8_t* q8, const int8_t* k8,
+int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, const void* vt,
+                  const int8_t* q8, const int8_t* k8,
                   const float* qs, const float* ks, const void* comp,
                   const float* alpha, int alpha_stride, const int32_t* lut,
                   int dtype, int B, int H, int64_t L, int D, int E, int Np, int T,

@@ -87,15 +87,20 @@ def test_linear_states_and_complement():
         r = rel_l2(st[key].cpu(), ref[key])
         print(f"  {key} rel {r:.2e}", flush=True)
         assert r < 1e-4, key
-    # value-operand tiles, zero past L: V and dV interleaved by groups of 4 keys
+    # operand tiles in fragment order, zero past L (lane = 16 g + r)
     L = ins["v"].shape[2]
     nb = -(-L // 64)
-    pad = lambda x: torch.cat([x, x.new_zeros(1, 2, nb * 64 - L, 64)], 2)
-    vT = pad(ins["v"]).view(1, 2, nb, 16, 4, 64).permute(0, 1, 2, 5, 3, 4)   # [n][c][kg][4]
-    dvT = pad(ins["dv"]).view(1, 2, nb, 16, 4, 64).permute(0, 1, 2, 5, 3, 4)
-    assert torch.equal(st["vt"].cpu().view(1, 2, nb, 64, 16, 8), torch.cat([vT, dvT], -1))
+    pad = lambda x: torch.cat([x, x.new_zeros(1, 2, nb * 64 - L, 64)], 2).view(1, 2, nb, 64, 64)
+    # vt[ct][w][g][r][i] = V[16w + 4g + i][16ct + r]  (key, column)
+    fragv = lambda x: pad(x).view(1, 2, nb, 4, 4, 4, 4, 16).permute(0, 1, 2, 6, 3, 4, 7, 5)
+    want_vt = torch.cat([fragv(ins["v"]), fragv(ins["dv"])], -1)
+    assert torch.equal(st["vt"].cpu().view(want_vt.shape), want_vt)
+    # kt[w][ks][g][r][j] = K[16w + r][32 ks + 8g + j] (ks 0,1), dK for ks 2,3
+    fragk = lambda x: pad(x).view(1, 2, nb, 4, 16, 2, 4, 8).permute(0, 1, 2, 3, 5, 6, 4, 7)
+    want_kt = torch.cat([fragk(ins["k"]), fragk(ins["dk"])], 4)
+    assert torch.equal(st["kt"].cpu().view(want_kt.shape), want_kt)
     st0 = ops.linear_states(g["k"], g["v"], Np)
-    assert torch.equal(st0["vt"].cpu(), pad(ins["v"]).view(1, 2, nb, 64, 64).transpose(-1, -2))
+    assert torch.equal(st0["vt"].cpu().view(1, 2, nb, 4, 4, 4, 16, 4), fragv(ins["v"]))
     # decode the records: Hc = Hall - sum Hb[lut], bf16 hi + lo
     rec = comp.view(1, 2, nb, -1)
     hc = rec[..., :16384].contiguous().view(torch.float32).view(1, 2, nb, 64, 64)  # [d][v]
