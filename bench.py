@@ -58,7 +58,9 @@ def hbm_bytes(B, H, N, Np, tangent):
     t = B * H * N * 64
     quant = 2 * t * 2 + 2 * t + 2 * B * H * (-(-N // 64)) * 4 + B * H * (-(-N // 64) + Np) * 64 * 4
     n_in = 4 if tangent else 2
-    states = n_in * t * 2 + (2 if tangent else 1) * B * H * Np * (64 * 64 + 64) * 4
+    tiles = B * H * (-(-N // 64)) * 64 * 64 * 2  # one 16-bit (64, 64) operand tile per block
+    states = (n_in * t * 2 + (2 if tangent else 1) * B * H * Np * (64 * 64 + 64) * 4
+              + (4 if tangent else 1) * tiles)  # vt (V|dV) and kt (K|dK) operand tiles
     return quant, states
 
 

@@ -166,7 +166,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     const int v8off = (16 * w + r) * kTa + 16 * g;  // per-lane part, tile base in soffset
     auto load8 = [&](int j) {
       const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
-      return __builtin_bit_cast(i32x4, buf_load16(rk8, v8off, n * kTa * kTa));
+      return __builtin_bit_cast(i32x4, buf_load16(rk8, v8off + n * kTa * kTa, 0));
     };
     auto tile_max = [&](const i32x4& k8v, int j, auto mask_tag) {
       constexpr bool MASK = decltype(mask_tag)::value;
@@ -227,7 +227,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   const int vtoff = TAN ? w * 1024 + l * 16 : w * 512 + l * 8;
   auto load_keys = [&](int j, KeyRegs& kr) {
     const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
-    kr.k8 = __builtin_bit_cast(i32x4, buf_load16(rk8, k8off, n * kTa * kTa));
+    kr.k8 = __builtin_bit_cast(i32x4, buf_load16(rk8, k8off + n * kTa * kTa, 0));
     if (TAN) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) kr.ka[ks] = buf_load16(rkt, ktoff + ks * 1024, n * 16384);

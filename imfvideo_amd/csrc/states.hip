@@ -273,13 +273,13 @@ __global__ __launch_bounds__(256) void states_sum_kernel(const float* __restrict
 //   [33024, 33280) dzc.
 // ---------------------------------------------------------------------------
 constexpr int kMaskSub = 32;  // 16-row mask sub-tiles per GEMM workgroup (512 rows)
+constexpr int kCompCols = 64;  // state columns per GEMM workgroup
 
-// Mask operand fragments mfrag[bh][mt][kc][lane][8] (bf16 bits): row
-// m = 16 mt + lane%16, tiles n = 32 kc + 8 (lane/16) + 0..7; value 1 where n < Np
-// is not routed for m (and m < Mb), else 0.
+// Complement bit masks cbits[bh][kc][m] (m < 16 MT): bit j of word (kc, m) is
+// 1 where tile n = 32 kc + j < Np is not routed for query block m < Mb.
 __global__ __launch_bounds__(256) void comp_mask_kernel(const int32_t* __restrict__ lut, int Mb,
                                                       int Np, int T, int MT, int NC,
-                                                      uint16_t* __restrict__ mfrag) {
+                                                      uint32_t* __restrict__ cbits) {
   extern __shared__ uint32_t selbits[];  // [16][NC]
   const int mt = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
   for (int i = tid; i < 16 * NC; i += 256) selbits[i] = 0u;
@@ -292,44 +292,52 @@ __global__ __launch_bounds__(256) void comp_mask_kernel(const int32_t* __restric
     if ((unsigned)n < (unsigned)Np) atomicOr(&selbits[row * NC + (n >> 5)], 1u << (n & 31));
   }
   __syncthreads();
-  for (int i = tid; i < NC * 64; i += 256) {
-    const int kc = i >> 6, lane = i & 63;
-    const int rr = lane & 15, g = lane >> 4;
-    const int m = mt * 16 + rr;
-    const uint32_t bits = selbits[rr * NC + kc] >> (8 * g);
-    uint32_t w[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      uint32_t pair = 0;
-#pragma unroll
-      for (int h2 = 0; h2 < 2; ++h2) {
-        const int jb = 2 * e + h2;
-        const int n = kc * 32 + 8 * g + jb;
-        const bool on = m < Mb && n < Np && !((bits >> jb) & 1u);
-        pair |= (on ? 0x3F80u : 0u) << (16 * h2);  // bf16 1.0
-      }
-      w[e] = pair;
-    }
-    *reinterpret_cast<uint4*>(mfrag + ((((int64_t)bh * MT + mt) * NC + kc) * 64 + lane) * 8) =
-        make_uint4(w[0], w[1], w[2], w[3]);
+  for (int i = tid; i < NC * 16; i += 256) {
+    const int kc = i >> 4, row = i & 15;
+    const int m = mt * 16 + row;
+    const int nv = Np - 32 * kc;  // real tiles in this word
+    const uint32_t valid = nv >= 32 ? 0xffffffffu : ((1u << nv) - 1u);
+    cbits[((int64_t)bh * NC + kc) * (MT * 16) + m] = m < Mb ? (~selbits[row * NC + kc] & valid) : 0u;
   }
 }
 
-// One workgroup: 32 state columns x up to 512 query blocks of one head.
+// 8 mask bits -> the 8 bf16 A-operand slots (1.0 where set)
+__device__ __forceinline__ u32x4 expand_mask8(uint32_t b) {
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t v = (b >> (2 * e)) & 3u;
+    o[e] = ((v & 1u) | ((v & 2u) << 15)) * 0x3F80u;
+  }
+  return o;
+}
+
+// One workgroup: 64 state columns x up to 512 query blocks of one head; the
+// contraction over video tiles runs in chunks of 32, double-buffered in LDS
+// and prefetched two chunks ahead.  Staging: thread (wave w, column c) loads
+// rows 8w..8w+7 of column c, i.e. exactly one 8-slot B-operand fragment,
+// splits it into bf16 hi + lo and writes each as one 16-byte LDS store.
+// The A operand (0/1 mask) comes from the row's mask byte through a
+// 256-entry expansion table in LDS.
 template <bool TAN>
-__global__ __launch_bounds__(256) void comp_gemm_kernel(
+__global__ __launch_bounds__(256, 2) void comp_gemm_kernel(
     const float* __restrict__ Hb, const float* __restrict__ dHb, const float* __restrict__ zb,
-    const float* __restrict__ dzb, const uint16_t* __restrict__ mfrag, int Mb, int Np, int MT,
+    const float* __restrict__ dzb, const uint32_t* __restrict__ cbits, int Mb, int Np, int MT,
     int NC, unsigned char* __restrict__ comp) {
-  __shared__ __align__(16) uint16_t st[2][32][40];  // [hi/lo][column][n] (+pad)
+  __shared__ __align__(16) uint16_t sb[2][2][kCompCols][40];  // [buf][hi/lo][column][n] (+pad)
+  __shared__ __align__(16) uint32_t mw[2][16 * kMaskSub];    // [buf][local row] mask words
+  __shared__ __align__(16) u32x4 mexp[256];                  // mask byte -> operand slots
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, r = l & 15, g = l >> 4;
-  const int c0 = blockIdx.x * 32;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, r = l & 15, g = l >> 4;
+  const int c0 = blockIdx.x * kCompCols;
   const int bh = blockIdx.y;
   const int mt0 = blockIdx.z * kMaskSub;
+  const int MTp = MT * 16;
+  const int m0 = mt0 * 16;
 
-  // column tile -> source tensor (boundaries are multiples of 32)
+  // column tile -> source tensor (boundaries are multiples of 64)
   const float* src;
   int stride, col0, part;  // part: 0 Hc, 1 dHc, 2 zc, 3 dzc
   const int zbase = TAN ? 8192 : 4096;
@@ -342,51 +350,88 @@ __global__ __launch_bounds__(256) void comp_gemm_kernel(
   } else {
     src = dzb; stride = 64; col0 = c0 - zbase - 64; part = 3;
   }
-  src += (int64_t)bh * Np * stride + col0;
+  // tile rows n >= Np and mask words past the head read as 0 (buffer range check)
+  const auto rs = make_rsrc(src + (int64_t)bh * Np * stride, (int64_t)Np * stride * 4);
+  const auto rb = make_rsrc(cbits + (int64_t)bh * NC * MTp, (int64_t)NC * MTp * 4);
 
-  f32x4 acc[8][2];
+  mexp[tid] = expand_mask8(tid);
+
+  f32x4 acc[8][4];
 #pragma unroll
-  for (int s = 0; s < 8; ++s) acc[s][0] = acc[s][1] = f32x4{0.f, 0.f, 0.f, 0.f};
+  for (int s = 0; s < 8; ++s)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) acc[s][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const int ln = tid >> 3, lc = (tid & 7) * 4;  // staging: tile row n, 4 columns
-  auto load_chunk = [&](int kc) {
-    const int n = kc * 32 + ln;
-    return n < Np ? *reinterpret_cast<const float4*>(src + (int64_t)n * stride + lc)
-                  : make_float4(0.f, 0.f, 0.f, 0.f);
+  struct Chunk {
+    float x[8];
+    uint32_t mk[2];
   };
-  float4 x = load_chunk(0);
-  for (int kc = 0; kc < NC; ++kc) {
-    const float xv[4] = {x.x, x.y, x.z, x.w};
-    if (kc + 1 < NC) x = load_chunk(kc + 1);  // prefetch the next chunk
-    __syncthreads();  // previous chunk's operands consumed
+  const int xoff = (col0 + l) * 4 + 8 * w * stride * 4;
+  auto load_chunk = [&](int kc, Chunk& c) {
+    kc = min(kc, NC - 1);  // past the end: a harmless reload, never stored
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      c.x[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                             rs, xoff + (32 * kc + j) * stride * 4, 0, 0));
+#pragma unroll
+    for (int h = 0; h < 2; ++h)
+      c.mk[h] = __builtin_amdgcn_raw_buffer_load_b32(rb, (kc * MTp + m0 + tid + 256 * h) * 4, 0, 0);
+  };
+  auto store_chunk = [&](int buf, const Chunk& c) {
+    u32x4 hi, lo;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      const uint16_t hi = bf16_bits(xv[e]);
-      st[0][lc + e][ln] = hi;
-      st[1][lc + e][ln] = bf16_bits(xv[e] - bf16_val(hi));
+      const uint32_t h = pack_pair<BF16>(c.x[2 * e], c.x[2 * e + 1]);
+      hi[e] = h;
+      lo[e] = pack_pair<BF16>(c.x[2 * e] - __builtin_bit_cast(float, h << 16),
+                              c.x[2 * e + 1] - __builtin_bit_cast(float, h & 0xffff0000u));
     }
-    __syncthreads();
-    u32x4 bhi[2], blo[2];
+    *reinterpret_cast<u32x4*>(&sb[buf][0][l][8 * w]) = hi;
+    *reinterpret_cast<u32x4*>(&sb[buf][1][l][8 * w]) = lo;
+    mw[buf][tid] = c.mk[0];
+    mw[buf][tid + 256] = c.mk[1];
+  };
+  const unsigned char* mwb = reinterpret_cast<const unsigned char*>(&mw[0][0]);
+  auto compute = [&](int buf) {
+    u32x4 bhi[4], blo[4];
 #pragma unroll
-    for (int cs = 0; cs < 2; ++cs) {
-      bhi[cs] = *reinterpret_cast<const u32x4*>(&st[0][cs * 16 + r][8 * g]);
-      blo[cs] = *reinterpret_cast<const u32x4*>(&st[1][cs * 16 + r][8 * g]);
+    for (int ct = 0; ct < 4; ++ct) {
+      bhi[ct] = *reinterpret_cast<const u32x4*>(&sb[buf][0][ct * 16 + r][8 * g]);
+      blo[ct] = *reinterpret_cast<const u32x4*>(&sb[buf][1][ct * 16 + r][8 * g]);
     }
 #pragma unroll
     for (int s = 0; s < 8; ++s) {
-      const int mt = mt0 + w + 4 * s;
-      if (mt >= MT) break;  // uniform per wave
-      const u32x4 am = *reinterpret_cast<const u32x4*>(
-          mfrag + ((((int64_t)bh * MT + mt) * NC + kc) * 64 + l) * 8);
+      const int lt = w + 4 * s;  // local 16-row tile; uniform per wave
+      if (mt0 + lt < MT) {
+        const u32x4 am = mexp[mwb[(buf * 16 * kMaskSub + lt * 16 + r) * 4 + g]];
 #pragma unroll
-      for (int cs = 0; cs < 2; ++cs) {
-        acc[s][cs] = mfma_bf16_16x16x32(am, bhi[cs], acc[s][cs]);
-        acc[s][cs] = mfma_bf16_16x16x32(am, blo[cs], acc[s][cs]);
+        for (int ct = 0; ct < 4; ++ct) {
+          acc[s][ct] = mfma_bf16_16x16x32(am, bhi[ct], acc[s][ct]);
+          acc[s][ct] = mfma_bf16_16x16x32(am, blo[ct], acc[s][ct]);
+        }
       }
     }
+  };
+
+  Chunk ca, cb;
+  load_chunk(0, ca);
+  load_chunk(1, cb);
+  store_chunk(0, ca);
+  __syncthreads();
+  for (int kc = 0; kc < NC; kc += 2) {
+    // chunk kc in buffer 0, chunk kc+1 in registers cb
+    load_chunk(kc + 2, ca);
+    compute(0);
+    store_chunk(1, cb);  // buffer 1 was last read before the previous barrier
+    __syncthreads();
+    if (kc + 1 >= NC) break;
+    load_chunk(kc + 3, cb);
+    compute(1);
+    store_chunk(0, ca);
+    __syncthreads();
   }
 
-  // records: lane (g, r) element i = C[16 mt + 4g + i][c0 + 16 cs + r]; 16
+  // records: lane (g, r) element i = C[16 mt + 4g + i][c0 + 16 ct + r]; 16
   // consecutive columns of one record per 16 lanes
   const int pbase = part < 2 ? part * 16384 : 32768 + (part - 2) * 256;
 #pragma unroll
@@ -399,7 +444,7 @@ __global__ __launch_bounds__(256) void comp_gemm_kernel(
       if (m >= Mb) continue;
       float* rec = reinterpret_cast<float*>(comp + ((int64_t)bh * Mb + m) * kRecBytes + pbase);
 #pragma unroll
-      for (int cs = 0; cs < 2; ++cs) rec[col0 + cs * 16 + r] = acc[s][cs][i];
+      for (int ct = 0; ct < 4; ++ct) rec[col0 + ct * 16 + r] = acc[s][ct][i];
     }
   }
 }
@@ -455,7 +500,7 @@ extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v,
 extern "C" size_t sla2h_complement_workspace_bytes(int B, int H, int Mb, int Np) {
   if (B <= 0 || H <= 0 || Mb <= 0 || Np <= 0) return 0;
   const size_t MT = (size_t)(Mb + 15) / 16, NC = (size_t)(Np + 31) / 32;
-  return (size_t)B * H * MT * NC * 64 * 8 * 2;
+  return (size_t)B * H * NC * MT * 16 * 4;
 }
 
 extern "C" int sla2h_complement(const float* Hb, const float* dHb, const float* zb,
@@ -470,16 +515,16 @@ extern "C" int sla2h_complement(const float* Hb, const float* dHb, const float* 
   if (tan) SLA2H_CHECK_ARG(dzb);
   const int MT = (Mb + 15) / 16, NC = (Np + 31) / 32;
   hipStream_t st = static_cast<hipStream_t>(stream);
-  auto mfrag = static_cast<uint16_t*>(workspace);
-  comp_mask_kernel<<<dim3(MT, B * H), 256, (size_t)16 * NC * 4, st>>>(lut, Mb, Np, T, MT, NC, mfrag);
+  auto cbits = static_cast<uint32_t*>(workspace);
+  comp_mask_kernel<<<dim3(MT, B * H), 256, (size_t)16 * NC * 4, st>>>(lut, Mb, Np, T, MT, NC, cbits);
   int err = (int)hipGetLastError();
   if (err) return err;
   const int ncols = tan ? 8320 : 4160;
-  dim3 grid(ncols / 32, B * H, (MT + kMaskSub - 1) / kMaskSub);
+  dim3 grid(ncols / kCompCols, B * H, (MT + kMaskSub - 1) / kMaskSub);
   auto out = static_cast<unsigned char*>(comp);
   if (tan)
-    comp_gemm_kernel<true><<<grid, 256, 0, st>>>(Hb, dHb, zb, dzb, mfrag, Mb, Np, MT, NC, out);
+    comp_gemm_kernel<true><<<grid, 256, 0, st>>>(Hb, dHb, zb, dzb, cbits, Mb, Np, MT, NC, out);
   else
-    comp_gemm_kernel<false><<<grid, 256, 0, st>>>(Hb, nullptr, zb, nullptr, mfrag, Mb, Np, MT, NC, out);
+    comp_gemm_kernel<false><<<grid, 256, 0, st>>>(Hb, nullptr, zb, nullptr, cbits, Mb, Np, MT, NC, out);
   return (int)hipGetLastError();
 }

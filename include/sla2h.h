@@ -105,7 +105,7 @@ int sla2h_linear_states(const void* k, const void* dk, const void* v, const void
 /* Bytes of one per-query-block complement record (see sla2h_complement). */
 size_t sla2h_complement_record_bytes(int D);
 
-/* Bytes of the workspace sla2h_complement needs (mask operand fragments). */
+/* Bytes of the workspace sla2h_complement needs (complement bit masks). */
 size_t sla2h_complement_workspace_bytes(int B, int H, int Mb, int Np);
 
 /*
