@@ -92,11 +92,11 @@ struct ValRegs {   // value-side operands, loaded at the start of their own tile
 template <typename T16, bool TAN, bool LINEAR, bool PRE>
 __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   __shared__ float stat[3][4][kQT][16];  // [m,l,mu][wave][qt][r]
-  // 8 KB: first the [dQ|Q] B-operand fragments [qt][ks][lane] (16 B each),
-  // then, after the key loop, the cross-wave merge buffer [wave][qt][lane][4].
+  // [dQ|Q] B-operand fragments [qt][ks][lane] (16 B each)
   __shared__ __align__(16) u32x4 qsh[kQT][4][64];
   __shared__ __align__(16) i32x4 q8sh[kQT][64];  // INT8 Q B-operand fragments
-  float(*xbuf)[kQT][64][4] = reinterpret_cast<float(*)[kQT][64][4]>(&qsh[0][0][0]);
+  // cross-wave merge buffer [wave][column tile of the round x {O, dO}][qt][lane][4]
+  __shared__ __align__(16) float mbuf[4][4][kQT][64][4];
   // key tiles of this query block in visiting order: (tile id, key scale)
   __shared__ int2 tiles[kMaxTiles];
 
@@ -144,6 +144,10 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   }
   __syncthreads();
   const float sq = a.qs[(int64_t)bh * a.Nb + m];
+  // log2-domain score factor of key tile j: (sq * sk_j) * scale * log2(e)
+  auto tile_c = [&](int j) {
+    return (sq * __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(tiles[j].y))) * a.c_log2;
+  };
   // per-(b,h) buffer resources: key rows past L read as zeros (those keys are
   // masked; vt/dvt are zero there anyway), 32-bit offsets
   const auto rk8 = make_rsrc(a.k8 + qkbase * kTa, L * kTa);
@@ -168,19 +172,24 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
       const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
       return __builtin_bit_cast(i32x4, buf_load16(rk8, v8off + n * kTa * kTa, 0));
     };
+    // c > 0 (positive block scales and softmax scale) and rounding is
+    // monotonic, so the maximum of fl(s * c) over a tile is fl(max(s) * c):
+    // the unmasked tiles take the integer maximum first.
     auto tile_max = [&](const i32x4& k8v, int j, auto mask_tag) {
       constexpr bool MASK = decltype(mask_tag)::value;
+      const float c = tile_c(j);
       const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
-      const float sqk = sq * __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(tiles[j].y));
       const int64_t key0 = (int64_t)n * kTa + 16 * w + 4 * g;
 #pragma unroll
       for (int qt = 0; qt < kQT; ++qt) {
         const i32x4 si = mfma_i8_16x16x64(k8v, q8sh[qt][l], i32x4{0, 0, 0, 0});
+        if (MASK) {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          float s2 = ((float)si[i] * sqk) * a.c_log2;
-          if (MASK && key0 + i >= L) s2 = -INFINITY;
-          mrow[qt] = fmaxf(mrow[qt], s2);
+          for (int i = 0; i < 4; ++i)
+            if (key0 + i < L) mrow[qt] = fmaxf(mrow[qt], (float)si[i] * c);
+        } else {
+          const int mx = max(max(si[0], si[1]), max(si[2], si[3]));
+          mrow[qt] = fmaxf(mrow[qt], (float)mx * c);
         }
       }
     };
@@ -246,11 +255,13 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     }
   };
 
-  // one key tile; MASK only for the ragged prefix tail tiles (j >= T)
-  auto process = [&](const KeyRegs& kr, const ValRegs& vr, int j, auto mask_tag) {
+  // One key tile: scores, P (and T = P dS), the row sums and the dO^T update;
+  // returns the P^T fragments for the O^T update (pairs of tiles share one
+  // K = 32 MFMA).  MASK only for the ragged prefix tail tiles (j >= T).
+  auto stage = [&](const KeyRegs& kr, const ValRegs& vr, int j, u32x2 (&pb)[kQT], auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
-    const float c = (sq * __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(tiles[j].y))) * a.c_log2;
+    const float c = tile_c(j);
     const int64_t key0 = (int64_t)n * kTa + 16 * w + 4 * g;
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
@@ -278,12 +289,8 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
       l_i[qt] += ps;
       if (TAN) mu_i[qt] += ts;
 
-      u32x2 pb;
-      pb.x = pack_pair<T16>(p[0], p[1]);
-      pb.y = pack_pair<T16>(p[2], p[3]);
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-        acc_o[ct][qt] = mfma_16x16x16<T16>(u32x2{vr.v[ct].x, vr.v[ct].y}, pb, acc_o[ct][qt]);
+      pb[qt].x = pack_pair<T16>(p[0], p[1]);
+      pb[qt].y = pack_pair<T16>(p[2], p[3]);
       if (TAN) {
         if (T16::kDtype == SLA2H_DTYPE_F16) {
 #pragma unroll
@@ -292,39 +299,63 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
         u32x4 bt;
         bt.x = pack_pair<T16>(t[0], t[1]);
         bt.y = pack_pair<T16>(t[2], t[3]);
-        bt.z = pb.x;
-        bt.w = pb.y;
+        bt.z = pb[qt].x;
+        bt.w = pb[qt].y;
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct)
           acc_do[ct][qt] = mfma_16x16x32<T16>(vr.v[ct], bt, acc_do[ct][qt]);
       }
     }
   };
-  // Issue order per tile: value loads of tile j, then the score-side prefetch
-  // of tile j+1 -- the in-order vmcnt lets tile j wait for its own values
-  // while the prefetch stays in flight.
-  auto run = [&](const KeyRegs& kr, int j, KeyRegs& knext, auto mask_tag) {
-    ValRegs vr;
-    load_vals(j, vr);
-    load_keys(j + 1 < J ? j + 1 : J - 1, knext);
-    process(kr, vr, j, mask_tag);
+  // O^T += V^T P^T for one tile (K = 16) or a pair (K = 32: the A and B
+  // operand slots 4..7 take the second tile's keys 4g..4g+3)
+  auto o_single = [&](const ValRegs& vr, const u32x2 (&pb)[kQT]) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt)
+        acc_o[ct][qt] = mfma_16x16x16<T16>(u32x2{vr.v[ct].x, vr.v[ct].y}, pb[qt], acc_o[ct][qt]);
+  };
+  auto o_pair = [&](const ValRegs& va, const u32x2 (&pa)[kQT], const ValRegs& vb,
+                    const u32x2 (&pbb)[kQT]) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt)
+        acc_o[ct][qt] = mfma_16x16x32<T16>(u32x4{va.v[ct].x, va.v[ct].y, vb.v[ct].x, vb.v[ct].y},
+                                           u32x4{pa[qt].x, pa[qt].y, pbb[qt].x, pbb[qt].y},
+                                           acc_o[ct][qt]);
   };
 
-  // routed video tiles (full, unmasked): two score-side register sets
-  // alternately loaded one tile ahead, one basic block per pair of tiles
+  // Issue order: value loads of a tile, then the score-side prefetch of the
+  // next tile -- the in-order vmcnt lets a tile wait for its own values while
+  // the prefetch stays in flight.
   KeyRegs ka_, kb_;
   load_keys(0, ka_);
   int j = 0;
+  // routed video tiles in pairs (full, unmasked)
   for (; j + 1 < a.T; j += 2) {
-    run(ka_, j, kb_, std::false_type{});
-    run(kb_, j + 1, ka_, std::false_type{});
+    ValRegs va, vb;
+    u32x2 pa[kQT], pbb[kQT];
+    load_vals(j, va);
+    load_keys(j + 1, kb_);
+    stage(ka_, va, j, pa, std::false_type{});
+    load_vals(j + 1, vb);
+    load_keys(j + 2 < J ? j + 2 : J - 1, ka_);
+    stage(kb_, vb, j + 1, pbb, std::false_type{});
+    o_pair(va, pa, vb, pbb);
   }
-  // odd leftover routed tile and the ragged prefix tail tiles
+  // odd leftover routed tile and the ragged prefix tail tiles, one at a time
   for (; j < J; ++j) {
+    ValRegs vr;
+    u32x2 pb[kQT];
+    load_vals(j, vr);
+    load_keys(j + 1 < J ? j + 1 : J - 1, kb_);
     if (j < a.T)
-      run(ka_, j, kb_, std::false_type{});
+      stage(ka_, vr, j, pb, std::false_type{});
     else
-      run(ka_, j, kb_, std::true_type{});
+      stage(ka_, vr, j, pb, std::true_type{});
+    o_single(vr, pb);
     ka_ = kb_;
   }
 #pragma unroll
@@ -367,46 +398,48 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     mutot += stat[2][ww][qo][r] * f;
   }
 
+  // two rounds (column tiles 0-1, then 2-3), O and dO together; round rd
+  // is summed by the waves with (w & 1) == rd
   f32x4 O[2], DO[2];
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
-    const bool mine = (ct >> 1) == (w & 1);
+  for (int rd = 0; rd < 2; ++rd) {
 #pragma unroll
-    for (int qt = 0; qt < kQT; ++qt)
-      *reinterpret_cast<f32x4*>(&xbuf[w][qt][l][0]) = acc_o[ct][qt] * fself[qt];
-    __syncthreads();
-    if (mine) {
-      f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
-      for (int ww = 0; ww < 4; ++ww) s += *reinterpret_cast<const f32x4*>(&xbuf[ww][qo][l][0]);
-      O[ct & 1] = s;
-    }
-    __syncthreads();
-    if (TAN) {
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt)
-        *reinterpret_cast<f32x4*>(&xbuf[w][qt][l][0]) = acc_do[ct][qt] * fself[qt];
-      __syncthreads();
-      if (mine) {
-        f32x4 s = f32x4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int ww = 0; ww < 4; ++ww) s += *reinterpret_cast<const f32x4*>(&xbuf[ww][qo][l][0]);
-        DO[ct & 1] = s;
+      for (int qt = 0; qt < kQT; ++qt) {
+        *reinterpret_cast<f32x4*>(&mbuf[w][2 * cc][qt][l][0]) = acc_o[2 * rd + cc][qt] * fself[qt];
+        if (TAN)
+          *reinterpret_cast<f32x4*>(&mbuf[w][2 * cc + 1][qt][l][0]) =
+              acc_do[2 * rd + cc][qt] * fself[qt];
       }
-      __syncthreads();
+    __syncthreads();
+    if ((w & 1) == rd) {
+#pragma unroll
+      for (int cc = 0; cc < 2; ++cc) {
+        f32x4 so = f32x4{0.f, 0.f, 0.f, 0.f}, sd = so;
+#pragma unroll
+        for (int ww = 0; ww < 4; ++ww) {
+          so += *reinterpret_cast<const f32x4*>(&mbuf[ww][2 * cc][qo][l][0]);
+          if (TAN) sd += *reinterpret_cast<const f32x4*>(&mbuf[ww][2 * cc + 1][qo][l][0]);
+        }
+        O[cc] = so;
+        DO[cc] = sd;
+      }
     }
+    if (rd == 0) __syncthreads();
   }
 
   // ---- epilogue: query q0 + 16 qo + r, output columns 16 (cpair + cc) + 4g + i ----
   const int64_t qrow = q0 + 16 * qo + r;
-  const float inv_mu = mutot / ltot;
+  const float rl = 1.f / ltot;
+  const float inv_mu = mutot * rl;
   f32x4 os[2], dos[2];
 #pragma unroll
   for (int cc = 0; cc < 2; ++cc) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      os[cc][i] = O[cc][i] / ltot;
-      if (TAN) dos[cc][i] = DO[cc][i] / ltot - inv_mu * os[cc][i];
+      os[cc][i] = O[cc][i] * rl;
+      if (TAN) dos[cc][i] = DO[cc][i] * rl - inv_mu * os[cc][i];
     }
   }
 
@@ -444,12 +477,13 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
         den += phi[ks][e];
       }
     den = sum_over_groups(den);
+    const float rden = 1.f / den;
     float qdot = 0.f;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        phi[ks][e] = phi[ks][e] / den;
+        phi[ks][e] = phi[ks][e] * rden;
         qdot += phi[ks][e] * dqv[ks][e];
       }
     if (TAN) {
@@ -499,6 +533,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     }
     dn = sum_over_groups(dn);
     dn = dn >= 0.f ? dn + a.eps_l : dn - a.eps_l;
+    const float rdn = 1.f / dn;
     if (TAN) ddn = sum_over_groups(ddn);
     const float al = a.alpha[(int64_t)h * a.alpha_stride + m];
 #pragma unroll
@@ -526,10 +561,10 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
       }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float ol = num[i] / dn;
+        const float ol = num[i] * rdn;
         os[cc][i] = al * os[cc][i] + (1.f - al) * ol;
         if (TAN) {
-          const float dol = (dnum[i] - ol * ddn) / dn;
+          const float dol = (dnum[i] - ol * ddn) * rdn;
           dos[cc][i] = al * dos[cc][i] + (1.f - al) * dol;
         }
       }
@@ -573,6 +608,7 @@ extern "C" int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, cons
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   SLA2H_CHECK_ARG(B > 0 && H > 0 && L > 0 && Np > 0 && (int64_t)Np * E <= L);
   SLA2H_CHECK_ARG(T >= 1 && T <= Np);
+  SLA2H_CHECK_ARG(scale > 0.f);  // the tile-maximum pass relies on positive score factors
   const int Nb_ = (int)((L + E - 1) / E);
   SLA2H_CHECK_ARG(T + (Nb_ - Np) <= kMaxTiles);
   const bool tan = dq != nullptr;
