@@ -159,9 +159,8 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
                              (int64_t)a.Nb * kVtTile);
 
   // ---- pass 1: exact per-wave row maxima of the INT8 scores ----
-  // Loads are branch-free (rows past L clamped to L-1: those keys are masked)
-  // so every tile issues the same vector loads and the prefetch one tile
-  // ahead overlaps the current tile.
+  // Loads are branch-free (rows past L read as zero: those keys are masked;
+  // past the last tile they repeat it) and run eight tiles ahead.
   float mref[kQT];
   {
     float mrow[kQT];
@@ -193,33 +192,53 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
         }
       }
     };
-    i32x4 kA = load8(0), kB;
+    // eight tiles in flight: register set i holds tile j + i
+    constexpr int kPre = 8;
+    auto clampj = [&](int jj) { return jj < J ? jj : J - 1; };
+    i32x4 kb[kPre];
+#pragma unroll
+    for (int i = 0; i < kPre; ++i) kb[i] = load8(clampj(i));
     int j = 0;
-    for (; j + 1 < a.T; j += 2) {
-      kB = load8(j + 1);
-      tile_max(kA, j, std::false_type{});
-      kA = load8(j + 2 < J ? j + 2 : J - 1);
-      tile_max(kB, j + 1, std::false_type{});
+    for (; j + kPre - 1 < a.T; j += kPre) {
+#pragma unroll
+      for (int i = 0; i < kPre; ++i) {
+        tile_max(kb[i], j + i, std::false_type{});
+        kb[i] = load8(clampj(j + kPre + i));
+        // keep each refill right after its use, or the scheduler batches
+        // the eight uses ahead of all refills (no prefetch left)
+        __builtin_amdgcn_sched_barrier(0);
+      }
     }
-    for (; j < J; ++j) {
-      kB = load8(j + 1 < J ? j + 1 : J - 1);
-      if (j < a.T)
-        tile_max(kA, j, std::false_type{});
-      else
-        tile_max(kA, j, std::true_type{});
-      kA = kB;
+    // fewer than kPre routed tiles left, then the prefix tail tiles
+    for (; j < J; j += kPre) {
+#pragma unroll
+      for (int i = 0; i < kPre; ++i) {
+        if (j + i < a.T)
+          tile_max(kb[i], j + i, std::false_type{});
+        else if (j + i < J)
+          tile_max(kb[i], j + i, std::true_type{});
+        kb[i] = load8(clampj(j + kPre + i));
+      }
     }
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) mref[qt] = max_over_groups(mrow[qt]);
   }
 
   // ---- pass 2: P = exp2(s - m), O^T += V^T P^T, dO^T += [V|dV]^T [T;P]^T ----
-  float l_i[kQT], mu_i[kQT];
+  // Row sum l = sum_k p on the matrix core: acc_lm accumulates an all-ones A
+  // operand times the same P^T fragments as the O^T update (one MFMA per
+  // pair of tiles instead of eight VALU adds per sub-tile and tile).  The
+  // JVP's mu = sum_k p dS stays an fp32 VALU sum: dO subtracts (mu / l) O
+  // from a nearly equal term, so mu keeps the reference's unrounded t.
+  f32x4 acc_lm[kQT];
+  float mu_i[kQT];
   f32x4 acc_o[4][kQT], acc_do[4][kQT];  // [ct][qt]
   float moff[kQT];
+  constexpr uint32_t kOne2 = T16::kDtype == SLA2H_DTYPE_F16 ? 0x3C003C00u : 0x3F803F80u;
+  const u32x4 lm_a = u32x4{kOne2, kOne2, kOne2, kOne2};
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt) {
-    l_i[qt] = 0.f;
+    acc_lm[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     mu_i[qt] = 0.f;
     moff[qt] = mref[qt] == -INFINITY ? 0.f : mref[qt];  // -inf: the wave saw no key
 #pragma unroll
@@ -274,19 +293,17 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) ds[i] = PRE ? d[i] : d[i] * a.scale;
       }
-      float ps = 0.f, ts = 0.f;
+      float ts = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float e = fmaf((float)si[i], c, -moff[qt]);
         if (MASK && key0 + i >= L) e = -INFINITY;
         p[i] = fast_exp2(e);
-        ps += p[i];
         if (TAN) {
           t[i] = p[i] * ds[i];
           ts += t[i];
         }
       }
-      l_i[qt] += ps;
       if (TAN) mu_i[qt] += ts;
 
       pb[qt].x = pack_pair<T16>(p[0], p[1]);
@@ -315,6 +332,9 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
 #pragma unroll
       for (int qt = 0; qt < kQT; ++qt)
         acc_o[ct][qt] = mfma_16x16x16<T16>(u32x2{vr.v[ct].x, vr.v[ct].y}, pb[qt], acc_o[ct][qt]);
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt)
+      acc_lm[qt] = mfma_16x16x16<T16>(u32x2{lm_a.x, lm_a.y}, pb[qt], acc_lm[qt]);
   };
   auto o_pair = [&](const ValRegs& va, const u32x2 (&pa)[kQT], const ValRegs& vb,
                     const u32x2 (&pbb)[kQT]) {
@@ -325,6 +345,10 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
         acc_o[ct][qt] = mfma_16x16x32<T16>(u32x4{va.v[ct].x, va.v[ct].y, vb.v[ct].x, vb.v[ct].y},
                                            u32x4{pa[qt].x, pa[qt].y, pbb[qt].x, pbb[qt].y},
                                            acc_o[ct][qt]);
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt)
+      acc_lm[qt] = mfma_16x16x32<T16>(lm_a, u32x4{pa[qt].x, pa[qt].y, pbb[qt].x, pbb[qt].y},
+                                      acc_lm[qt]);
   };
 
   // Issue order: value loads of a tile, then the score-side prefetch of the
@@ -358,9 +382,10 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     o_single(vr, pb);
     ka_ = kb_;
   }
+  float l_i[kQT];
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt) {
-    l_i[qt] = sum_over_groups(l_i[qt]);
+    l_i[qt] = acc_lm[qt][0];  // every row of the product holds the column sum
     if (TAN) mu_i[qt] = sum_over_groups(mu_i[qt]);
   }
 
@@ -448,17 +473,24 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     float qv[2][8], dqv[2][8];
     const bool qok = qrow < L;
     const int64_t ro = (qkbase + qrow) * kTa;
+    // tangent: the [dQ|Q] operand fragments in LDS are exactly this lane's
+    // row (zero past L), scaled by the power-of-two softmax scale when PRE
+    const float unscale = PRE ? 1.f / a.scale : 1.f;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      u32x4 u = qok ? *reinterpret_cast<const u32x4*>(a.q + ro + 32 * ks + 8 * g) : u32x4{0, 0, 0, 0};
-      u32x4 du = u32x4{0, 0, 0, 0};
-      if (TAN && qok) du = *reinterpret_cast<const u32x4*>(a.dq + ro + 32 * ks + 8 * g);
+      u32x4 u, du = u32x4{0, 0, 0, 0};
+      if (TAN) {
+        u = qsh[qo][2 + ks][l];
+        du = qsh[qo][ks][l];
+      } else {
+        u = qok ? *reinterpret_cast<const u32x4*>(a.q + ro + 32 * ks + 8 * g) : u32x4{0, 0, 0, 0};
+      }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        qv[ks][2 * e] = T16::to_f32((uint16_t)(u[e] & 0xffff));
-        qv[ks][2 * e + 1] = T16::to_f32((uint16_t)(u[e] >> 16));
-        dqv[ks][2 * e] = T16::to_f32((uint16_t)(du[e] & 0xffff));
-        dqv[ks][2 * e + 1] = T16::to_f32((uint16_t)(du[e] >> 16));
+        qv[ks][2 * e] = T16::to_f32((uint16_t)(u[e] & 0xffff)) * unscale;
+        qv[ks][2 * e + 1] = T16::to_f32((uint16_t)(u[e] >> 16)) * unscale;
+        dqv[ks][2 * e] = T16::to_f32((uint16_t)(du[e] & 0xffff)) * unscale;
+        dqv[ks][2 * e + 1] = T16::to_f32((uint16_t)(du[e] >> 16)) * unscale;
       }
     }
     float mx = -INFINITY;
