@@ -10,6 +10,8 @@
 //   scores+top-k  models/mla_video_sparse_jvp.py:563-565, 292-294
 #include "common.h"
 
+#include <type_traits>
+
 namespace sla2h {
 
 constexpr int kTile = 64;  // E = D = 64
@@ -208,6 +210,143 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
   }
 }
 
+// Top-T of each row by wave-wide radix selection (T <= 64): one wave per
+// query block, NK keys per lane (tile n = lane + 64 i), R rows per wave.
+//   1. scores, same sequential fp32 order as route_topk_kernel;
+//   2. s* = the T-th largest order-preserving score word (32-bit binary
+//      search with ballot counts); if several keys share s*, the lowest
+//      indices among them fill up to T (a 12-bit binary search over n);
+//   3. the T winners are compacted through LDS and bitonic-sorted across
+//      the lanes by their 64-bit keys (score word, then lower index first).
+template <int NK, int R>
+__global__ __launch_bounds__(256) void route_select_kernel(const float* __restrict__ qpool,
+                                                           const float* __restrict__ kpool_t,
+                                                           int Mb, int Np, int T, float scale,
+                                                           int32_t* __restrict__ lut,
+                                                           uint8_t* __restrict__ mask) {
+  __shared__ uint64_t win[4][64];
+  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int lane = threadIdx.x & 63;
+  const int bh = blockIdx.y;
+  const int m0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + w) * R);
+  if (m0 >= Mb) return;  // whole wave; no workgroup barrier below
+
+  const float* kt = kpool_t + (int64_t)bh * kTile * Np;
+  float acc[R][NK];
+#pragma unroll
+  for (int rr = 0; rr < R; ++rr)
+#pragma unroll
+    for (int i = 0; i < NK; ++i) acc[rr][i] = 0.f;
+  // lane d holds q[row][d] (broadcast with readlane).  Key slots past Np
+  // need no guard: their scores are never selected (ord = 0 below), and the
+  // buffer range check returns 0 past the end of this head's pooled keys.
+  const float* qrow = qpool + ((int64_t)bh * Mb + m0) * kTile;
+  float qlane[R];
+#pragma unroll
+  for (int rr = 0; rr < R; ++rr) qlane[rr] = (m0 + rr < Mb) ? qrow[rr * kTile + lane] : 0.f;
+  const auto rk = make_rsrc(kt, (int64_t)kTile * Np * 4);
+#pragma unroll 4
+  for (int d = 0; d < kTile; ++d) {
+    float kv[NK];
+#pragma unroll
+    for (int i = 0; i < NK; ++i)
+      kv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                            rk, (d * Np + lane + 64 * i) * 4, 0, 0));
+#pragma unroll
+    for (int rr = 0; rr < R; ++rr) {
+      const float qv = __builtin_bit_cast(
+          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, qlane[rr]), d));
+#pragma unroll
+      for (int i = 0; i < NK; ++i) acc[rr][i] = acc[rr][i] + qv * kv[i];
+    }
+  }
+
+#pragma unroll
+  for (int rr = 0; rr < R; ++rr) {
+    const int m = m0 + rr;
+    if (m >= Mb) break;  // uniform
+    uint32_t ord[NK];
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const int n = lane + 64 * i;
+      ord[i] = n < Np ? (uint32_t)(score_key(acc[rr][i] * scale, n) >> 32) : 0u;  // 0: below all
+    }
+    // wave-wide sum of per-lane counts 0..NK: one ballot per count bit
+    constexpr int kBits = NK == 8 ? 4 : (NK == 16 ? 5 : (NK == 32 ? 6 : 7));
+    auto wave_sum = [&](int cl) {
+      int c = 0;
+#pragma unroll
+      for (int b = 0; b < kBits; ++b) c += __popcll(__ballot((cl >> b) & 1)) << b;
+      return c;
+    };
+    auto count_ge = [&](uint32_t v) {
+      int cl = 0;
+#pragma unroll
+      for (int i = 0; i < NK; ++i) cl += ord[i] >= v ? 1 : 0;
+      return wave_sum(cl);
+    };
+    uint32_t sstar = 0;
+    for (int b = 31; b >= 0; --b) {
+      const uint32_t cand = sstar | (1u << b);
+      if (count_ge(cand) >= T) sstar = cand;
+    }
+    int l_gt = 0, l_eq = 0;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      l_gt += ord[i] > sstar ? 1 : 0;
+      l_eq += ord[i] == sstar ? 1 : 0;
+    }
+    const int c_gt = wave_sum(l_gt), c_eq = wave_sum(l_eq);
+    const int need = T - c_gt;  // 1 <= need <= c_eq
+    uint32_t nstar = 0xffffffffu;  // tie keys with n <= nstar are taken
+    if (need < c_eq) {
+      uint32_t pre = 0;
+      for (int b = 12; b >= 0; --b) {
+        const uint32_t cand = pre | (1u << b);
+        int cl = 0;
+#pragma unroll
+        for (int i = 0; i < NK; ++i) cl += (ord[i] == sstar && (uint32_t)(lane + 64 * i) < cand) ? 1 : 0;
+        if (wave_sum(cl) < need) pre = cand;
+      }
+      nstar = pre;
+    }
+    // compact the T winners (any order), then sort them across the lanes
+    int base = 0;
+#pragma unroll
+    for (int i = 0; i < NK; ++i) {
+      const uint32_t n = lane + 64 * i;
+      const bool sel = ord[i] > sstar || (ord[i] == sstar && n <= nstar);
+      const uint64_t bal = __ballot(sel);
+      if (sel) {
+        const int pos = base + __builtin_amdgcn_mbcnt_hi((uint32_t)(bal >> 32),
+                                                         __builtin_amdgcn_mbcnt_lo((uint32_t)bal, 0u));
+        win[w][pos] = ((uint64_t)ord[i] << 32) | (uint64_t)(0xffffffffu - n);
+      }
+      if (mask != nullptr && (int)n < Np) mask[((int64_t)bh * Mb + m) * Np + n] = sel ? 1 : 0;
+      base += __popcll(bal);
+    }
+    __builtin_amdgcn_wave_barrier();
+    __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+    uint64_t key = lane < T ? win[w][lane] : 0ull;
+    // bitonic sort, descending, over the 64 lanes
+#pragma unroll
+    for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+      for (int j = k >> 1; j > 0; j >>= 1) {
+        const uint32_t lo = __shfl_xor((uint32_t)key, j, 64);
+        const uint32_t hi = __shfl_xor((uint32_t)(key >> 32), j, 64);
+        const uint64_t other = ((uint64_t)hi << 32) | lo;
+        const bool desc = (lane & k) == 0;
+        const bool lower = (lane & j) == 0;  // this lane keeps the larger key in a desc run
+        const bool take = desc == lower ? other > key : other < key;
+        key = take ? other : key;
+      }
+    }
+    if (lane < T) lut[((int64_t)bh * Mb + m) * T + lane] = (int32_t)(0xffffffffu - (uint32_t)key);
+    __builtin_amdgcn_wave_barrier();  // win[w] is reused by the next row
+  }
+}
+
 }  // namespace sla2h
 
 using namespace sla2h;
@@ -283,13 +422,30 @@ extern "C" int sla2h_route_topk(const float* qpool, const float* kpool_t, int B,
   SLA2H_CHECK_ARG(D == kTile);
   SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && Mb > 0);
   SLA2H_CHECK_ARG(Np > 0 && Np <= 4096 && T >= 1 && T <= Np);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (T <= 64) {
+    // one query block per wave: enough waves to hide the load latency
+    auto go = [&](auto nk, auto rows) {
+      constexpr int NK = decltype(nk)::value, R = decltype(rows)::value;
+      dim3 grid((Mb + 4 * R - 1) / (4 * R), B * H);
+      route_select_kernel<NK, R><<<grid, 256, 0, st>>>(qpool, kpool_t, Mb, Np, T, scale, lut, mask);
+    };
+    if (Np <= 512)
+      go(std::integral_constant<int, 8>{}, std::integral_constant<int, 1>{});
+    else if (Np <= 1024)
+      go(std::integral_constant<int, 16>{}, std::integral_constant<int, 1>{});
+    else if (Np <= 2048)
+      go(std::integral_constant<int, 32>{}, std::integral_constant<int, 1>{});
+    else
+      go(std::integral_constant<int, 64>{}, std::integral_constant<int, 1>{});
+    return (int)hipGetLastError();
+  }
   int P2 = 1;
   while (P2 < Np) P2 <<= 1;
   if (P2 < 2) P2 = 2;
   const int rows = P2 <= 512 ? 8 : (P2 <= 1024 ? 4 : (P2 <= 2048 ? 2 : 1));
   const size_t shmem = (size_t)rows * P2 * 8 + (size_t)rows * kTile * 4 + (size_t)rows * P2;
   dim3 grid((Mb + rows - 1) / rows, B * H);
-  hipStream_t st = static_cast<hipStream_t>(stream);
   switch (rows) {
     case 8: route_topk_kernel<8><<<grid, 256, shmem, st>>>(qpool, kpool_t, Mb, Np, T, scale, P2, lut, mask); break;
     case 4: route_topk_kernel<4><<<grid, 256, shmem, st>>>(qpool, kpool_t, Mb, Np, T, scale, P2, lut, mask); break;
