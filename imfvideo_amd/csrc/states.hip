@@ -274,6 +274,7 @@ __global__ __launch_bounds__(256) void states_sum_kernel(const float* __restrict
 // ---------------------------------------------------------------------------
 constexpr int kMaskSub = 32;  // 16-row mask sub-tiles per GEMM workgroup (512 rows)
 constexpr int kCompCols = 64;  // state columns per GEMM workgroup
+constexpr int kCompThreads = 512;  // 8 waves
 
 // Complement bit masks cbits[bh][kc][m] (m < 16 MT): bit j of word (kc, m) is
 // 1 where tile n = 32 kc + j < Np is not routed for query block m < Mb.
@@ -312,15 +313,16 @@ __device__ __forceinline__ u32x4 expand_mask8(uint32_t b) {
   return o;
 }
 
-// One workgroup: 64 state columns x up to 512 query blocks of one head; the
-// contraction over video tiles runs in chunks of 32, double-buffered in LDS
-// and prefetched two chunks ahead.  Staging: thread (wave w, column c) loads
-// rows 8w..8w+7 of column c, i.e. exactly one 8-slot B-operand fragment,
-// splits it into bf16 hi + lo and writes each as one 16-byte LDS store.
-// The A operand (0/1 mask) comes from the row's mask byte through a
-// 256-entry expansion table in LDS.
+// One workgroup of 8 waves: 64 state columns x up to 512 query blocks of one
+// head (wave w owns the 16-row tiles w, w+8, w+16, w+24, so 64 accumulator
+// registers per lane and four waves per SIMD).  The contraction over video
+// tiles runs in chunks of 32, double-buffered in LDS and prefetched two
+// chunks ahead.  Staging: thread (wave w, column c) loads rows 4w..4w+3 of
+// column c, splits them into bf16 hi + lo and writes half a B-operand
+// fragment of each with one 8-byte LDS store.  The A operand (0/1 mask)
+// comes from the row's mask byte through a 256-entry expansion table in LDS.
 template <bool TAN>
-__global__ __launch_bounds__(256, 2) void comp_gemm_kernel(
+__global__ __launch_bounds__(kCompThreads, 4) void comp_gemm_kernel(
     const float* __restrict__ Hb, const float* __restrict__ dHb, const float* __restrict__ zb,
     const float* __restrict__ dzb, const uint32_t* __restrict__ cbits, int Mb, int Np, int MT,
     int NC, unsigned char* __restrict__ comp) {
@@ -354,42 +356,39 @@ __global__ __launch_bounds__(256, 2) void comp_gemm_kernel(
   const auto rs = make_rsrc(src + (int64_t)bh * Np * stride, (int64_t)Np * stride * 4);
   const auto rb = make_rsrc(cbits + (int64_t)bh * NC * MTp, (int64_t)NC * MTp * 4);
 
-  mexp[tid] = expand_mask8(tid);
+  if (tid < 256) mexp[tid] = expand_mask8(tid);
 
-  f32x4 acc[8][4];
+  f32x4 acc[4][4];
 #pragma unroll
-  for (int s = 0; s < 8; ++s)
+  for (int s = 0; s < 4; ++s)
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) acc[s][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   struct Chunk {
-    float x[8];
-    uint32_t mk[2];
+    float x[4];
+    uint32_t mk;
   };
-  const int xoff = (col0 + l) * 4 + 8 * w * stride * 4;
+  const int xoff = (col0 + l) * 4 + 4 * w * stride * 4;
   auto load_chunk = [&](int kc, Chunk& c) {
     kc = min(kc, NC - 1);  // past the end: a harmless reload, never stored
 #pragma unroll
-    for (int j = 0; j < 8; ++j)
+    for (int j = 0; j < 4; ++j)
       c.x[j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
                                              rs, xoff + (32 * kc + j) * stride * 4, 0, 0));
-#pragma unroll
-    for (int h = 0; h < 2; ++h)
-      c.mk[h] = __builtin_amdgcn_raw_buffer_load_b32(rb, (kc * MTp + m0 + tid + 256 * h) * 4, 0, 0);
+    c.mk = __builtin_amdgcn_raw_buffer_load_b32(rb, (kc * MTp + m0 + tid) * 4, 0, 0);
   };
   auto store_chunk = [&](int buf, const Chunk& c) {
-    u32x4 hi, lo;
+    u32x2 hi, lo;
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
+    for (int e = 0; e < 2; ++e) {
       const uint32_t h = pack_pair<BF16>(c.x[2 * e], c.x[2 * e + 1]);
       hi[e] = h;
       lo[e] = pack_pair<BF16>(c.x[2 * e] - __builtin_bit_cast(float, h << 16),
                               c.x[2 * e + 1] - __builtin_bit_cast(float, h & 0xffff0000u));
     }
-    *reinterpret_cast<u32x4*>(&sb[buf][0][l][8 * w]) = hi;
-    *reinterpret_cast<u32x4*>(&sb[buf][1][l][8 * w]) = lo;
-    mw[buf][tid] = c.mk[0];
-    mw[buf][tid + 256] = c.mk[1];
+    *reinterpret_cast<u32x2*>(&sb[buf][0][l][4 * w]) = hi;
+    *reinterpret_cast<u32x2*>(&sb[buf][1][l][4 * w]) = lo;
+    mw[buf][tid] = c.mk;
   };
   const unsigned char* mwb = reinterpret_cast<const unsigned char*>(&mw[0][0]);
   auto compute = [&](int buf) {
@@ -400,8 +399,8 @@ __global__ __launch_bounds__(256, 2) void comp_gemm_kernel(
       blo[ct] = *reinterpret_cast<const u32x4*>(&sb[buf][1][ct * 16 + r][8 * g]);
     }
 #pragma unroll
-    for (int s = 0; s < 8; ++s) {
-      const int lt = w + 4 * s;  // local 16-row tile; uniform per wave
+    for (int s = 0; s < 4; ++s) {
+      const int lt = w + 8 * s;  // local 16-row tile; uniform per wave
       if (mt0 + lt < MT) {
         const u32x4 am = mexp[mwb[(buf * 16 * kMaskSub + lt * 16 + r) * 4 + g]];
 #pragma unroll
@@ -435,8 +434,8 @@ __global__ __launch_bounds__(256, 2) void comp_gemm_kernel(
   // consecutive columns of one record per 16 lanes
   const int pbase = part < 2 ? part * 16384 : 32768 + (part - 2) * 256;
 #pragma unroll
-  for (int s = 0; s < 8; ++s) {
-    const int mt = mt0 + w + 4 * s;
+  for (int s = 0; s < 4; ++s) {
+    const int mt = mt0 + w + 8 * s;
     if (mt >= MT) break;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -523,8 +522,8 @@ extern "C" int sla2h_complement(const float* Hb, const float* dHb, const float* 
   dim3 grid(ncols / kCompCols, B * H, (MT + kMaskSub - 1) / kMaskSub);
   auto out = static_cast<unsigned char*>(comp);
   if (tan)
-    comp_gemm_kernel<true><<<grid, 256, 0, st>>>(Hb, dHb, zb, dzb, cbits, Mb, Np, MT, NC, out);
+    comp_gemm_kernel<true><<<grid, kCompThreads, 0, st>>>(Hb, dHb, zb, dzb, cbits, Mb, Np, MT, NC, out);
   else
-    comp_gemm_kernel<false><<<grid, 256, 0, st>>>(Hb, nullptr, zb, nullptr, cbits, Mb, Np, MT, NC, out);
+    comp_gemm_kernel<false><<<grid, kCompThreads, 0, st>>>(Hb, nullptr, zb, nullptr, cbits, Mb, Np, MT, NC, out);
   return (int)hipGetLastError();
 }
