@@ -7,9 +7,9 @@
 // the 32 queries; the four partial states are merged once at the end through
 // LDS.  Each wave streams its quarter of every key tile straight from global
 // memory into MFMA operand registers (one tile ahead) -- no barriers in the
-// key loop.  Two passes over the tiles: pass 1 takes the exact row maxima of
-// the INT8 scores (i8 MFMAs only), pass 2 accumulates with that fixed
-// maximum, so the loop has no accumulator rescaling and no cross-lane traffic.
+// key loop.  One pass over the tiles with a lazy running maximum: it moves
+// only when a tile exceeds it by a margin (one wave ballot per tile), so the
+// accumulators are rescaled about once per row.
 //
 // Scores are computed transposed (S^T = K Q^T) so that a lane holds one query
 // column: the S^T fragment is directly the B operand of O^T = V^T P^T, and the
@@ -23,6 +23,7 @@
 // sparse-only variant :59-169 (_sla2_cube_jvp_qat_kernel).
 #include "common.h"
 
+#include <climits>
 #include <type_traits>
 
 namespace sla2h {
@@ -158,73 +159,15 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   const auto rvt = make_rsrc(reinterpret_cast<const char*>(a.vt) + (int64_t)bh * a.Nb * kVtTile,
                              (int64_t)a.Nb * kVtTile);
 
-  // ---- pass 1: exact per-wave row maxima of the INT8 scores ----
-  // Loads are branch-free (rows past L read as zero: those keys are masked;
-  // past the last tile they repeat it) and run eight tiles ahead.
-  float mref[kQT];
-  {
-    float mrow[kQT];
-#pragma unroll
-    for (int qt = 0; qt < kQT; ++qt) mrow[qt] = -INFINITY;
-    const int v8off = (16 * w + r) * kTa + 16 * g;  // per-lane part, tile base in soffset
-    auto load8 = [&](int j) {
-      const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
-      return __builtin_bit_cast(i32x4, buf_load16(rk8, v8off + n * kTa * kTa, 0));
-    };
-    // c > 0 (positive block scales and softmax scale) and rounding is
-    // monotonic, so the maximum of fl(s * c) over a tile is fl(max(s) * c):
-    // the unmasked tiles take the integer maximum first.
-    auto tile_max = [&](const i32x4& k8v, int j, auto mask_tag) {
-      constexpr bool MASK = decltype(mask_tag)::value;
-      const float c = tile_c(j);
-      const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
-      const int64_t key0 = (int64_t)n * kTa + 16 * w + 4 * g;
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
-        const i32x4 si = mfma_i8_16x16x64(k8v, q8sh[qt][l], i32x4{0, 0, 0, 0});
-        if (MASK) {
-#pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (key0 + i < L) mrow[qt] = fmaxf(mrow[qt], (float)si[i] * c);
-        } else {
-          const int mx = max(max(si[0], si[1]), max(si[2], si[3]));
-          mrow[qt] = fmaxf(mrow[qt], (float)mx * c);
-        }
-      }
-    };
-    // eight tiles in flight: register set i holds tile j + i
-    constexpr int kPre = 8;
-    auto clampj = [&](int jj) { return jj < J ? jj : J - 1; };
-    i32x4 kb[kPre];
-#pragma unroll
-    for (int i = 0; i < kPre; ++i) kb[i] = load8(clampj(i));
-    int j = 0;
-    for (; j + kPre - 1 < a.T; j += kPre) {
-#pragma unroll
-      for (int i = 0; i < kPre; ++i) {
-        tile_max(kb[i], j + i, std::false_type{});
-        kb[i] = load8(clampj(j + kPre + i));
-        // keep each refill right after its use, or the scheduler batches
-        // the eight uses ahead of all refills (no prefetch left)
-        __builtin_amdgcn_sched_barrier(0);
-      }
-    }
-    // fewer than kPre routed tiles left, then the prefix tail tiles
-    for (; j < J; j += kPre) {
-#pragma unroll
-      for (int i = 0; i < kPre; ++i) {
-        if (j + i < a.T)
-          tile_max(kb[i], j + i, std::false_type{});
-        else if (j + i < J)
-          tile_max(kb[i], j + i, std::true_type{});
-        kb[i] = load8(clampj(j + kPre + i));
-      }
-    }
-#pragma unroll
-    for (int qt = 0; qt < kQT; ++qt) mref[qt] = max_over_groups(mrow[qt]);
-  }
-
-  // ---- pass 2: P = exp2(s - m), O^T += V^T P^T, dO^T += [V|dV]^T [T;P]^T ----
+  // ---- one pass: P = exp2(s - m), O^T += V^T P^T, dO^T += [V|dV]^T [T;P]^T ----
+  // Lazy running maximum: m only moves when a tile's row maximum exceeds it
+  // by more than kThr (log2 units), so P <= 2^kThr and a rescale of the
+  // accumulators is rare (every row's first tile, then hardly ever).  fp16
+  // operands keep kThr = 0 (P <= 1 and the +-60000 clamp of T act as in the
+  // reference's per-block online softmax).  The check is one ballot per
+  // sub-tile and tile: c > 0 and rounding is monotonic, so the maximum of
+  // fl(s * c) over a tile is fl(max(s) * c) from the integer maximum.
+  constexpr float kThr = T16::kDtype == SLA2H_DTYPE_F16 ? 0.f : 8.f;
   // Row sum l = sum_k p on the matrix core: acc_lm accumulates an all-ones A
   // operand times the same P^T fragments as the O^T update (one MFMA per
   // pair of tiles instead of eight VALU adds per sub-tile and tile).  The
@@ -233,14 +176,15 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   f32x4 acc_lm[kQT];
   float mu_i[kQT];
   f32x4 acc_o[4][kQT], acc_do[4][kQT];  // [ct][qt]
-  float moff[kQT];
+  float mrun[kQT], mthr[kQT];  // running maximum (uniform per query column), + kThr
   constexpr uint32_t kOne2 = T16::kDtype == SLA2H_DTYPE_F16 ? 0x3C003C00u : 0x3F803F80u;
   const u32x4 lm_a = u32x4{kOne2, kOne2, kOne2, kOne2};
 #pragma unroll
   for (int qt = 0; qt < kQT; ++qt) {
     acc_lm[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
     mu_i[qt] = 0.f;
-    moff[qt] = mref[qt] == -INFINITY ? 0.f : mref[qt];  // -inf: the wave saw no key
+    mrun[qt] = -INFINITY;
+    mthr[qt] = -INFINITY;
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       acc_o[ct][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -274,10 +218,38 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     }
   };
 
-  // One key tile: scores, P (and T = P dS), the row sums and the dO^T update;
-  // returns the P^T fragments for the O^T update (pairs of tiles share one
-  // K = 32 MFMA).  MASK only for the ragged prefix tail tiles (j >= T).
-  auto stage = [&](const KeyRegs& kr, const ValRegs& vr, int j, u32x2 (&pb)[kQT], auto mask_tag) {
+  // rescale sub-tile qt to the new running maximum max(mrun, mt) of each
+  // query column; `pend` holds the previous tile's P^T fragments of a pair,
+  // still to be accumulated at the old maximum
+  auto rescale = [&](int qt, float mt, u32x2* pend) {
+    const float mn = max_over_groups(fmaxf(mrun[qt], mt));
+    const float f = mrun[qt] == -INFINITY ? 0.f : fast_exp2(mrun[qt] - mn);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      acc_o[ct][qt] *= f;
+      if (TAN) acc_do[ct][qt] *= f;
+    }
+    acc_lm[qt] *= f;
+    mu_i[qt] *= f;
+    if (pend != nullptr) {
+      u32x2& pp = pend[qt];
+#pragma unroll
+      for (int e = 0; e < 2; ++e) {
+        const float lo = T16::to_f32((uint16_t)(pp[e] & 0xffff)) * f;
+        const float hi = T16::to_f32((uint16_t)(pp[e] >> 16)) * f;
+        pp[e] = pack_pair<T16>(lo, hi);
+      }
+    }
+    mrun[qt] = mn;
+    mthr[qt] = mn + kThr;
+  };
+
+  // One key tile: scores, the running-maximum check, P (and T = P dS), the
+  // mu sums and the dO^T update; returns the P^T fragments for the O^T update
+  // (pairs of tiles share one K = 32 MFMA).  MASK only for the ragged prefix
+  // tail tiles (j >= T).
+  auto stage = [&](const KeyRegs& kr, const ValRegs& vr, int j, u32x2 (&pb)[kQT], u32x2* pend,
+                   auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
     const float c = tile_c(j);
@@ -285,6 +257,17 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
       const i32x4 si = mfma_i8_16x16x64(kr.k8, q8sh[qt][l], i32x4{0, 0, 0, 0});
+      int mx;
+      if (MASK) {
+        mx = INT_MIN;
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+          if (key0 + i < L) mx = max(mx, si[i]);
+      } else {
+        mx = max(max(si[0], si[1]), max(si[2], si[3]));
+      }
+      const float mt = mx == INT_MIN ? -INFINITY : (float)mx * c;
+      if (__builtin_amdgcn_ballot_w64(mt > mthr[qt]) != 0) rescale(qt, mt, pend);
       float p[4], ds[4], t[4];
       if (TAN) {
         f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -293,10 +276,11 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) ds[i] = PRE ? d[i] : d[i] * a.scale;
       }
+      const float moff = mrun[qt];
       float ts = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float e = fmaf((float)si[i], c, -moff[qt]);
+        float e = fmaf((float)si[i], c, -moff);
         if (MASK && key0 + i >= L) e = -INFINITY;
         p[i] = fast_exp2(e);
         if (TAN) {
@@ -363,10 +347,10 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     u32x2 pa[kQT], pbb[kQT];
     load_vals(j, va);
     load_keys(j + 1, kb_);
-    stage(ka_, va, j, pa, std::false_type{});
+    stage(ka_, va, j, pa, nullptr, std::false_type{});
     load_vals(j + 1, vb);
     load_keys(j + 2 < J ? j + 2 : J - 1, ka_);
-    stage(kb_, vb, j + 1, pbb, std::false_type{});
+    stage(kb_, vb, j + 1, pbb, pa, std::false_type{});
     o_pair(va, pa, vb, pbb);
   }
   // odd leftover routed tile and the ragged prefix tail tiles, one at a time
@@ -376,9 +360,9 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     load_vals(j, vr);
     load_keys(j + 1 < J ? j + 1 : J - 1, kb_);
     if (j < a.T)
-      stage(ka_, vr, j, pb, std::false_type{});
+      stage(ka_, vr, j, pb, nullptr, std::false_type{});
     else
-      stage(ka_, vr, j, pb, std::true_type{});
+      stage(ka_, vr, j, pb, nullptr, std::true_type{});
     o_single(vr, pb);
     ka_ = kb_;
   }
@@ -394,7 +378,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   if (g == 0) {
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
-      stat[0][w][qt][r] = mref[qt];
+      stat[0][w][qt][r] = mrun[qt];
       stat[1][w][qt][r] = l_i[qt];
       stat[2][w][qt][r] = mu_i[qt];
     }
@@ -406,7 +390,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     float M = -INFINITY;
 #pragma unroll
     for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, stat[0][ww][qt][r]);
-    fself[qt] = (mref[qt] == -INFINITY) ? 0.f : fast_exp2(mref[qt] - M);
+    fself[qt] = (mrun[qt] == -INFINITY) ? 0.f : fast_exp2(mrun[qt] - M);
   }
   // this wave finalises query sub-tile qo = w >> 1, output column tiles cpair, cpair+1
   const int qo = w >> 1;
