@@ -47,6 +47,17 @@ def make_config(cfg):
     return dict(B=B, H=H, N=N, Np=Np, qkv=qkv, tan=tan, alpha=alpha, topk=0.1)
 
 
+def measured_traffic(cfg, tangent):
+    """HBM bytes per fwd_jvp launch from the committed rocprofv3 FETCH_SIZE /
+    WRITE_SIZE passes (scaled by the same counters on a plain copy kernel),
+    for the Config 3 tangent workload only; None otherwise."""
+    path = os.path.join(ROOT, "profiles", "fwd_jvp_config3_traffic.json")
+    if cfg != 3 or not tangent or not os.path.exists(path):
+        return None
+    with open(path) as f:
+        return int(json.load(f)["bytes_per_launch"])
+
+
 def roofline_work(B, H, Mb, T, n_tail, tangent):
     pairs = B * H * Mb * (T + n_tail)
     ops_i8 = pairs * 2 * 64 ** 3
@@ -99,7 +110,18 @@ def main():
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3])
     ap.add_argument("--cpu-baseline", type=int, default=1)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 256 MiB fp32 copy kernel (torch.mul by 1) three times: "
+                         "the reference reading for the FETCH_SIZE / WRITE_SIZE counters")
     args = ap.parse_args()
+    if args.copy_calibration:
+        x = torch.randn(64 * 1024 * 1024, device="cuda")
+        y = torch.empty_like(x)
+        for _ in range(3):
+            torch.mul(x, 1.0, out=y)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration": "256 MiB read + 256 MiB written per dispatch"}))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the op shards by head with no exchange, see DESIGN.md", file=sys.stderr)
@@ -173,7 +195,7 @@ def main():
         "roofline": {"bound": "mfma", "kernel": "fwd_jvp",
                      "achieved": round(achieved, 2), "peak": PEAK_BF16_TFLOPS,
                      "unit": "TFLOP/s", "frac": round(achieved / PEAK_BF16_TFLOPS, 4),
-                     "traffic": None,
+                     "traffic": measured_traffic(args.config, tangent),
                      "work": {"int8_ops": ops_i8, "bf16_flops": flops16,
                               "note": "achieved = (int8_ops/2 + bf16_flops) / t: int8 counted "
                                       "at its 2x peak, so frac = t_roofline / t"}},
