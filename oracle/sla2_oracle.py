@@ -370,3 +370,110 @@ def dense_jvp(q, k, v, dq, dk, dv, alpha, lut, Np, prefix_len, quant=None):
     dS = (dq.double() @ kk.transpose(-1, -2) + qq @ dk.double().transpose(-1, -2)) * scale
     f = lambda S_, v_, q_, k_: dense_op(S_, v_, q_, k_, alpha, m, comp, Np)
     return torch.func.jvp(f, (S, vv, qq, kk), (dS, dv.double(), dq.double(), dk.double()))
+
+
+# ---------------------------------------------------------------------------
+# Training-forward semantics (b): _CubeQATFunction.forward
+# (models/sla2_cube_qat.py:696-751) = _attn_fwd_qat (kernel_sparse_qat.py:28-117)
+# + kphi / _precompute_global (kernel_linear.py:305-313) + _lin_fwd2 state
+# form (kernel_linear.py:205-302) + the alpha mix in 16-bit.
+# ---------------------------------------------------------------------------
+def quantize_blocks_trunc(x, block=E):
+    """In-kernel quantisation of _attn_fwd_qat (kernel_sparse_qat.py:56-58, 88-90,
+    106-107): s = max|x|/127 + 1e-12, q = int(fl32(fl32(x / s) + 0.5*sign(x)))
+    truncated toward zero (sign(+-0) = +1).  x (..., L, D) -> (q int8, s fp32)."""
+    x = _np(x)
+    L, D = x.shape[-2:]
+    nb = -(-L // block)
+    xb = _pad_rows(x, nb * block).reshape(x.shape[:-2] + (nb, block, D))
+    amax = np.abs(xb).max(axis=(-2, -1))
+    s = (amax / _F32(127.0)).astype(np.float32) + _F32(1e-12)
+    y = (xb / s[..., None, None]).astype(np.float32)
+    y = (y + np.where(xb >= 0, _F32(0.5), _F32(-0.5))).astype(np.float32)
+    q = np.trunc(y).astype(np.int8)
+    return q.reshape(x.shape[:-2] + (nb * block, D))[..., :L, :], s.astype(np.float32)
+
+
+def _round16(x, t16):
+    return x.to(t16).float()
+
+
+def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L):
+    """Training-forward semantics (b), blockwise, CPU.
+
+    q, k, v: (B,H,L,D) float tensors holding 16-bit values.  alpha: (H, Mb)
+    after the sigmoid.  lut: (B,H,Mb,T) routed video tiles; the n_tail prefix
+    blocks are appended (lut_aug).  Returns dict with o (16-bit values, the
+    module output), o_s, o_l (16-bit values), lse (fp32, log2 domain), qphi.
+    """
+    B, H, L, D = q.shape
+    nb = -(-L // E)
+    Mb = nb
+    n_tail = nb - Np
+    lut = torch.as_tensor(np.asarray(lut)).long()
+    tails = torch.arange(Np, Np + n_tail).view(1, 1, 1, -1).expand(B, H, Mb, n_tail)
+    lut_aug = torch.cat([lut, tails], -1)
+    J = lut_aug.shape[-1]
+    q8, qs = quantize_blocks_trunc(q)
+    k8, ks = quantize_blocks_trunc(k)
+    v8, vs = quantize_blocks_trunc(v)
+    q8t = _tiles(torch.as_tensor(q8).double(), nb)
+    k8t = _tiles(torch.as_tensor(k8).double(), nb)
+    v8t = _tiles(torch.as_tensor(v8).double(), nb)
+    qs, ks, vs = (torch.as_tensor(t).float() for t in (qs, ks, vs))
+    scale = float(np.float32(D ** -0.5))
+    c2 = float(np.float32(scale * LOG2E))
+    rows = torch.arange(nb * E).view(nb, E)
+    m_i = torch.full((B, H, Mb, E), -math.inf)
+    l_i = torch.zeros(B, H, Mb, E)
+    o_s = torch.zeros(B, H, Mb, E, D)
+    for j in range(J):
+        n = lut_aug[..., j]                                   # (B,H,Mb)
+        kt = _gather_tiles(k8t, n)                            # (B,H,Mb,E,D)
+        vt = _gather_tiles(v8t, n)
+        skn = torch.gather(ks, 2, n)                          # (B,H,Mb)
+        svn = torch.gather(vs, 2, n)
+        si = torch.matmul(q8t[:, :, :Mb], kt.transpose(-1, -2)).float()  # exact ints
+        qk = si * (qs[:, :, :Mb] * skn)[..., None, None]
+        qk = qk * c2
+        valid = (rows[n] < L)                                 # (B,H,Mb,E) key rows
+        qk = qk.masked_fill(~valid[..., None, :], -math.inf)
+        local_m = qk.amax(-1)
+        new_m = torch.maximum(m_i, local_m)
+        p = torch.exp2(qk - new_m[..., None])
+        l_ij = p.sum(-1)
+        al = torch.exp2(m_i - new_m)
+        o_s = o_s * al[..., None]
+        p8 = torch.trunc(p * 127.0 + 0.5)
+        pv = torch.matmul(p8.double(), vt).float()
+        o_s = o_s + pv * (svn / 127.0)[..., None, None]
+        l_i = l_i * al + l_ij
+        m_i = new_m
+    o_s = o_s / l_i[..., None]
+    lse = m_i + torch.log2(l_i)
+    o_s = o_s.reshape(B, H, Mb * E, D)[:, :, :L]
+    lse = lse.reshape(B, H, Mb * E)[:, :, :L]
+    o_s16 = _round16(o_s, t16)
+    qphi = _round16(torch.softmax(q.float(), -1), t16)
+    kphi = _round16(torch.softmax(k.float(), -1), t16)
+    vf = v.float()
+    htot = _round16(kphi.transpose(-1, -2) @ vf, t16)          # (B,H,D,D)
+    ztot = kphi.sum(-2)                                        # (B,H,D)
+    kpt, vvt = _tiles(kphi, nb), _tiles(vf, nb)
+    qpt = _tiles(qphi, nb)
+    hi = htot[:, :, None].expand(B, H, Mb, D, D).clone()
+    zi = ztot[:, :, None].expand(B, H, Mb, D).clone()
+    for j in range(J):
+        n = lut_aug[..., j]
+        kp, vv = _gather_tiles(kpt, n), _gather_tiles(vvt, n)
+        hi = hi - kp.transpose(-1, -2) @ vv
+        zi = zi - kp.sum(-2)
+    num = qpt[:, :, :Mb] @ _round16(hi, t16)                  # (B,H,Mb,E,D)
+    den = (qpt[:, :, :Mb] * zi[..., None, :]).sum(-1)
+    den = torch.where(den >= 0, den + eps, den - eps)
+    o_l = (num / den[..., None]).reshape(B, H, Mb * E, D)[:, :, :L]
+    o_l16 = _round16(o_l, t16)
+    a = _round16(alpha.float()[None, :, :, None, None].expand(B, H, Mb, E, 1)
+                 .reshape(B, H, Mb * E, 1)[:, :, :L], t16)
+    o = _round16(_round16(a * o_s16, t16) + _round16(_round16(1.0 - a, t16) * o_l16, t16), t16)
+    return {"o": o, "o_s": o_s16, "o_l": o_l16, "lse": lse, "qphi": qphi}

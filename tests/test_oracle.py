@@ -248,3 +248,83 @@ def test_oracle_reproduces_golden(name):
     o, do = O.cube_jvp(*(ins[n] for n in ("q", "k", "v", "dq", "dk", "dv")),
                        torch.from_numpy(z["alpha"]), lut, Np, P, t16=dt)
     assert max_abs(o, torch.from_numpy(z["o"])) < 1e-5 and max_abs(do, torch.from_numpy(z["do"])) < 1e-4
+
+
+# ------------------------------------------------ training forward, semantics (b)
+def test_quantize_trunc_known_answers():
+    # amax = 127 -> s = 1 exactly (1e-12 vanishes in fp32): q = trunc(fl(x + 0.5 sign x))
+    x = np.zeros((64, 64), np.float32)
+    x[0, 0] = 127.0
+    x[0, 1] = np.float32(0.49999997)   # + 0.5 rounds (to even) to 1.0 in fp32 -> 1
+    x[0, 2] = -np.float32(0.49999997)  # -> -1
+    x[0, 3] = 2.5
+    x[0, 4] = -2.5
+    x[0, 5] = -0.0
+    x[0, 6] = np.float32(2.4999998)    # + 0.5 = 2.9999998 exactly -> 2
+    q, s = O.quantize_blocks_trunc(x)
+    assert s[0] == np.float32(1.0)
+    assert q[0, :7].tolist() == [127, 1, -1, 3, -3, 0, 2]
+    # round-half-away (the JVP path's quantiser) differs exactly on the first pair
+    qa, _ = O.quantize_blocks(x)
+    assert qa[0, :7].tolist() == [127, 0, 0, 3, -3, 0, 2]
+
+
+def _train_case(seed=5, B=1, H=2, Np=4, P=18, topk=0.5):
+    L = Np * 64 + P
+    q, k, v, *_ = (t.float() for t in make_inputs(seed, B, H, L))
+    g = torch.Generator().manual_seed(seed + 7)
+    alpha = torch.rand(H, -(-L // 64), generator=g) * 0.8 + 0.1
+    lut, T, _, _ = O.route(q, k, topk, Np, P)
+    return q, k, v, alpha, lut, Np, P
+
+
+def _dense_quantized_scores(q, k):
+    """log2-domain scores from the (b) INT8 integers, dense, fp64."""
+    L, D = q.shape[-2:]
+    q8, qs = O.quantize_blocks_trunc(q)
+    k8, ks = O.quantize_blocks_trunc(k)
+    rep = lambda s: torch.as_tensor(s).double().repeat_interleave(64, -1)[..., :L]
+    si = torch.as_tensor(q8).double() @ torch.as_tensor(k8).double().transpose(-1, -2)
+    c2 = float(np.float32(np.float32(D ** -0.5) * O.LOG2E))
+    return si * rep(qs)[..., :, None] * rep(ks)[..., None, :] * c2
+
+
+def test_train_fwd_lse_is_dense_log2sumexp2():
+    q, k, v, alpha, lut, Np, P = _train_case()
+    r = O.train_fwd(q, k, v, alpha, lut, Np, P, t16=torch.float32)
+    S = _dense_quantized_scores(q, k)
+    m, _ = O.block_mask(lut, Np, q.shape[2], P)
+    S = S.masked_fill(m == 0, -math.inf)
+    ref = torch.logsumexp(S * math.log(2.0), -1) / math.log(2.0)
+    assert (r["lse"].double() - ref).abs().max() < 1e-4
+
+
+def test_train_fwd_sparse_branch_within_int8_p_bound():
+    q, k, v, alpha, lut, Np, P = _train_case(seed=6)
+    L = q.shape[2]
+    r = O.train_fwd(q, k, v, alpha, lut, Np, P, t16=torch.float32)
+    S = _dense_quantized_scores(q, k)
+    m, _ = O.block_mask(lut, Np, L, P)
+    Pm = torch.softmax((S * math.log(2.0)).masked_fill(m == 0, -math.inf), -1)
+    v8, vs = O.quantize_blocks_trunc(v)
+    vdq = torch.as_tensor(v8).double() * torch.as_tensor(vs).double().repeat_interleave(64, -1)[..., :L, None]
+    ref = Pm @ vdq
+    # P enters as trunc(127 p + 0.5) / 127 against the running maximum: a few per cent
+    assert rel_l2(r["o_s"], ref) < 3e-2
+    # a wrong scale, rescale or V factor is an O(1) error
+    assert rel_l2(r["o_s"] * 1.1, ref) > 5e-2
+
+
+def test_train_fwd_linear_branch_and_mix_endpoints():
+    q, k, v, alpha, lut, Np, P = _train_case(seed=7)
+    H, Mb = alpha.shape
+    r1 = O.train_fwd(q, k, v, torch.ones(H, Mb), lut, Np, P, t16=torch.float32)
+    r0 = O.train_fwd(q, k, v, torch.zeros(H, Mb), lut, Np, P, t16=torch.float32)
+    assert torch.equal(r1["o"], r1["o_s"]) and torch.equal(r0["o"], r0["o_l"])
+    # the linear branch is the (a) path's (pinned by its dense complement form)
+    ol_a, _ = O.cube_jvp(q, k, v, None, None, None, torch.zeros(H, Mb), lut, Np, P, t16=torch.float32)
+    assert rel_l2(r0["o_l"], ol_a) < 1e-5
+    # 16-bit rounding of phi, the states and the outputs stays at bf16 level
+    rb = O.train_fwd(q, k, v, alpha, lut, Np, P, t16=torch.bfloat16)
+    rf = O.train_fwd(q, k, v, alpha, lut, Np, P, t16=torch.float32)
+    assert rel_l2(rb["o"], rf["o"]) < 1e-2
