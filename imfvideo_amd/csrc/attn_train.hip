@@ -1,0 +1,374 @@
+// Sparse branch of the SLA2 cube attention in the training-forward semantics
+// of _attn_fwd_qat (models/sla2_vendor/kernel_sparse_qat.py:28-117, with
+// USE_INT8, BLOCK_N = 64, PHI_OUT), gfx950:
+//   S = int32(Q8 . K8^T) * (sq * sk) * scale * log2(e), keys past L masked;
+//   running maximum m per block of keys (exact), P = exp2(S - m),
+//   P8 = (int) fl(127 P + 0.5), O += int32(P8 . V8) * (sv / 127) after the
+//   rescale of O and l by exp2(m_old - m); o_s = O / l (16-bit),
+//   lse = m + log2(l) (fp32), and phi(Q) = softmax_D(Q) (16-bit).
+// Q8, K8, V8 and their per-tile scales come from sla2h_quant_train (the
+// reference quantises in-kernel with the same law; the result is the same).
+//
+// Work unit: one 64-row query block of one (b, h), one workgroup of 4 wave64;
+// wave w owns queries 16w..16w+15 and all 64 keys of every tile.  Scores are
+// computed transposed (S^T = K8 Q8^T, four 16-key blocks): a lane holds 16
+// keys of one query, which is directly the B operand of the INT8 MFMA
+// O^T = V8^T P8^T (K = 64 keys; V8 is stored in the matching fragment order).
+// Key and value fragments are loaded one tile ahead.
+#include "common.h"
+
+#include <climits>
+
+namespace sla2h {
+
+namespace {
+
+constexpr int kT = 64;
+constexpr int kMaxJ = 1024;
+
+struct TrainArgs {
+  const uint16_t* q;
+  const int8_t* q8;
+  const int8_t* k8;
+  const int8_t* v8f;
+  const float* qs;
+  const float* ks;
+  const float* vs;
+  const int32_t* lut;
+  uint16_t* os;
+  float* lse;
+  uint16_t* qphi;
+  int64_t L;
+  int Nb, Np, Mb, T, n_tail, nwork, per_xcd;
+  float c2;  // fl32(scale * log2(e))
+};
+
+template <typename T16>
+__global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
+  __shared__ int2 tiles[kMaxJ];  // (tile id, bits of sk)
+  __shared__ float vsc[kMaxJ];   // sv / 127 of each visited tile
+
+  const int logical = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
+  if (logical >= a.nwork) return;
+  const int bh = __builtin_amdgcn_readfirstlane(logical / a.Mb);
+  const int m = __builtin_amdgcn_readfirstlane(logical - bh * a.Mb);
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, r = l & 15, g = l >> 4;
+  const int64_t L = a.L;
+  const int64_t qkbase = (int64_t)bh * L;
+  const int64_t qrow = (int64_t)m * kT + 16 * w + r;  // this lane's query
+  const bool qok = qrow < L;
+
+  const int J = a.T + a.n_tail;
+  const int32_t* lrow = a.lut + ((int64_t)bh * a.Mb + m) * a.T;
+  for (int j = tid; j < J; j += 256) {
+    int n = j < a.T ? lrow[j] : a.Np + (j - a.T);
+    n = n < 0 ? 0 : (n >= a.Nb ? a.Nb - 1 : n);
+    tiles[j] = make_int2(n, __builtin_bit_cast(int, a.ks[(int64_t)bh * a.Nb + n]));
+    vsc[j] = a.vs[(int64_t)bh * a.Nb + n] / 127.0f;
+  }
+
+  // phi(Q) of this lane's 16 channels 16g..16g+15 (row max / sum over the
+  // four lane groups), written as 16-bit
+  {
+    float x[16];
+    uint4 u0 = make_uint4(0, 0, 0, 0), u1 = u0;
+    if (qok) {
+      const uint4* src = reinterpret_cast<const uint4*>(a.q + (qkbase + qrow) * kT + 16 * g);
+      u0 = src[0];
+      u1 = src[1];
+    }
+    const uint32_t wd[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[2 * i] = T16::to_f32((uint16_t)(wd[i] & 0xffff));
+      x[2 * i + 1] = T16::to_f32((uint16_t)(wd[i] >> 16));
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, x[i]);
+    mx = max_over_groups(mx);
+    float den = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x[i] = __expf(x[i] - mx);
+      den += x[i];
+    }
+    den = sum_over_groups(den);
+    const float rd = 1.f / den;
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = pack_pair<T16>(x[2 * i] * rd, x[2 * i + 1] * rd);
+    if (qok) {
+      uint4* dst = reinterpret_cast<uint4*>(a.qphi + (qkbase + qrow) * kT + 16 * g);
+      dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+      dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+  }
+  __syncthreads();
+
+  // INT8 Q B operand: this lane's query, channels 16g..16g+15
+  const i32x4 q8f = qok ? *reinterpret_cast<const i32x4*>(a.q8 + (qkbase + qrow) * kT + 16 * g)
+                        : i32x4{0, 0, 0, 0};
+  const float sq = a.qs[(int64_t)bh * a.Nb + m];
+  const auto rk8 = make_rsrc(a.k8 + qkbase * kT, L * kT);  // key rows past L read as 0
+  const auto rv8 = make_rsrc(a.v8f + (int64_t)bh * a.Nb * 4096, (int64_t)a.Nb * 4096);
+  const int k8off = r * kT + 16 * g;  // + 16 kb rows + tile base
+
+  struct Frags {
+    i32x4 k[4];  // K8[16kb + r][16g ..]
+    i32x4 v[4];  // V8 fragments of column tile ct
+  };
+  auto load = [&](int j, Frags& f) {
+    const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+      f.k[kb] = __builtin_bit_cast(i32x4, buf_load16(rk8, k8off + (n * kT + 16 * kb) * kT, 0));
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+      f.v[ct] = __builtin_bit_cast(i32x4, buf_load16(rv8, ct * 1024 + l * 16, n * 4096));
+  };
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_i = -INFINITY, l_i = 0.f;  // l_i: this lane's 16 keys per tile, reduced at the end
+
+  auto tile = [&](const Frags& f, int j) {
+    const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
+    const float sqk = sq * __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(tiles[j].y));
+    const int64_t key0 = (int64_t)n * kT + 4 * g;
+    float s[16];
+    float lm = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      const i32x4 si = mfma_i8_16x16x64(f.k[kb], q8f, i32x4{0, 0, 0, 0});
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float x = ((float)si[i] * sqk) * a.c2;
+        if (key0 + 16 * kb + i >= L) x = -INFINITY;
+        s[4 * kb + i] = x;
+        lm = fmaxf(lm, x);
+      }
+    }
+    lm = max_over_groups(lm);
+    const float mn = fmaxf(m_i, lm);
+    const float alpha = fast_exp2(m_i - mn);  // 0 on the first tile (m_i = -inf)
+    float ls = 0.f;
+    uint32_t pk[4];
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      uint32_t wd = 0;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float p = fast_exp2(s[4 * kb + i] - mn);
+        ls += p;
+        wd |= ((uint32_t)(int)fmaf(p, 127.f, 0.5f)) << (8 * i);  // p in [0, 1]: 0..127
+      }
+      pk[kb] = wd;
+    }
+    l_i = l_i * alpha + ls;
+    m_i = mn;
+    const i32x4 p8 = i32x4{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
+    const float sv = vsc[j];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const i32x4 pv = mfma_i8_16x16x64(f.v[ct], p8, i32x4{0, 0, 0, 0});
+#pragma unroll
+      for (int i = 0; i < 4; ++i) acc[ct][i] = fmaf((float)pv[i], sv, acc[ct][i] * alpha);
+    }
+  };
+
+  Frags fa, fb;
+  load(0, fa);
+  int j = 0;
+  for (; j + 1 < J; j += 2) {
+    load(j + 1, fb);
+    tile(fa, j);
+    load(j + 2 < J ? j + 2 : J - 1, fa);
+    tile(fb, j + 1);
+  }
+  if (j < J) tile(fa, j);
+
+  const float lt = sum_over_groups(l_i);
+  const float rl = 1.f / lt;
+  // lane (g, r) holds O^T[16 ct + 4g + i][query r]
+  if (qok) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const uint32_t lo = pack_pair<T16>(acc[ct][0] * rl, acc[ct][1] * rl);
+      const uint32_t hi = pack_pair<T16>(acc[ct][2] * rl, acc[ct][3] * rl);
+      *reinterpret_cast<uint2*>(a.os + (qkbase + qrow) * kT + 16 * ct + 4 * g) = make_uint2(lo, hi);
+    }
+    if (g == 0) a.lse[qkbase + qrow] = m_i + __log2f(lt);
+  }
+}
+
+// Linear branch and mix of the training forward (_lin_fwd2 in its state form,
+// models/sla2_vendor/kernel_linear.py:274-304, and the mix at
+// models/sla2_cube_qat.py:742-744), one 64-row query block per workgroup:
+//   H_i = htot16 - sum_{j in lut_aug(i)} phi(K_j)^T V_j, rounded to 16 bits,
+//   num = phi(Q) H_i (16-bit MFMA, fp32 accumulate), den = phi(Q) . z_i +- eps,
+//   o_l = num / den, o = a o_s + (1 - a) o_l with every product, difference
+//   and sum rounded to the 16-bit type as the reference's half-precision
+//   tensor arithmetic does.
+// The complement record holds sum over the tiles NOT in lut_aug of
+// phi(K_j)^T V_j; H_i = record + (htot16 - htot) with htot = sum over all tiles
+// (the same sum, in another fp32 order).  Wave w owns queries 16w..16w+15;
+// lane (g, r) holds query r, output channels 16 ct + 4g + i.
+constexpr int kRecH = 0, kRecZ = 32768, kRecBytes = 33280;
+
+template <typename T16>
+__global__ __launch_bounds__(256) void linear_mix_qat_kernel(
+    const uint16_t* __restrict__ qphi, const unsigned char* __restrict__ comp,
+    const float* __restrict__ Hall, const uint16_t* __restrict__ o_s,
+    const float* __restrict__ alpha, int alpha_stride, int64_t L, int Mb, int H, float eps_l,
+    uint16_t* __restrict__ o, uint16_t* __restrict__ o_l, float* __restrict__ den_out) {
+  __shared__ __align__(16) uint16_t hT[kT][kT + 8];  // [value channel][key channel]
+  __shared__ float zs[kT];
+
+  const int m = blockIdx.x, bh = blockIdx.y, h = bh % H;
+  const int tid = threadIdx.x;
+  const unsigned char* rec = comp + ((int64_t)bh * Mb + m) * kRecBytes;
+  {
+    const int d = tid >> 2, v0 = (tid & 3) * 16;
+    const f32x4* hr = reinterpret_cast<const f32x4*>(rec + kRecH) + (d * kT + v0) / 4;
+    const f32x4* ha = reinterpret_cast<const f32x4*>(Hall + (int64_t)bh * kT * kT + d * kT + v0);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const f32x4 x = hr[c], t = ha[c];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float t16 = T16::to_f32(T16::from_f32(t[i]));
+        hT[v0 + 4 * c + i][d] = T16::from_f32(x[i] + (t16 - t[i]));
+      }
+    }
+    if (tid < kT) zs[tid] = reinterpret_cast<const float*>(rec + kRecZ)[tid];
+  }
+  __syncthreads();
+
+  const int w = tid >> 6, l = tid & 63, r = l & 15, g = l >> 4;
+  const int64_t qrow = (int64_t)m * kT + 16 * w + r;
+  const bool qok = qrow < L;
+  const int64_t rowoff = ((int64_t)bh * L + qrow) * kT;
+  u32x4 qb[2];
+  float dn = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    qb[ks] = qok ? *reinterpret_cast<const u32x4*>(qphi + rowoff + 32 * ks + 8 * g)
+                 : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      dn += T16::to_f32((uint16_t)(qb[ks][e] & 0xffff)) * zs[32 * ks + 8 * g + 2 * e];
+      dn += T16::to_f32((uint16_t)(qb[ks][e] >> 16)) * zs[32 * ks + 8 * g + 2 * e + 1];
+    }
+  }
+  dn = sum_over_groups(dn);
+  dn = dn >= 0.f ? dn + eps_l : dn - eps_l;
+  const float rdn = 1.f / dn;
+  const float a16 = T16::to_f32(T16::from_f32(alpha[(int64_t)h * alpha_stride + m]));
+  const float b16 = T16::to_f32(T16::from_f32(1.f - a16));
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const u32x4 av = *reinterpret_cast<const u32x4*>(&hT[16 * ct + r][32 * ks + 8 * g]);
+      num = mfma_16x16x32<T16>(av, qb[ks], num);
+    }
+    if (qok) {
+      const int64_t oo = rowoff + 16 * ct + 4 * g;
+      const uint2 sv = *reinterpret_cast<const uint2*>(o_s + oo);
+      const uint32_t sw[2] = {sv.x, sv.y};
+      float ol[4], ov[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        ol[i] = T16::to_f32(T16::from_f32(num[i] * rdn));
+        const float os16 = T16::to_f32((uint16_t)(sw[i >> 1] >> (16 * (i & 1))));
+        const float x = T16::to_f32(T16::from_f32(a16 * os16));
+        const float y = T16::to_f32(T16::from_f32(b16 * ol[i]));
+        ov[i] = x + y;
+      }
+      *reinterpret_cast<uint2*>(o + oo) =
+          make_uint2(pack_pair<T16>(ov[0], ov[1]), pack_pair<T16>(ov[2], ov[3]));
+      *reinterpret_cast<uint2*>(o_l + oo) =
+          make_uint2(pack_pair<T16>(ol[0], ol[1]), pack_pair<T16>(ol[2], ol[3]));
+    }
+  }
+  if (qok && g == 0) den_out[(int64_t)bh * L + qrow] = dn;
+}
+
+}  // namespace
+
+}  // namespace sla2h
+
+using namespace sla2h;
+
+extern "C" int sla2h_sparse_fwd_qat(const void* q, const int8_t* q8, const float* qs,
+                                    const int8_t* k8, const float* ks, const int8_t* v8f,
+                                    const float* vs, const int32_t* lut, int dtype, int B, int H,
+                                    int64_t L, int D, int E, int Np, int T, float scale,
+                                    void* o_s, float* lse, void* qphi, void* stream) {
+  SLA2H_CHECK_ARG(q && q8 && qs && k8 && ks && v8f && vs && lut && o_s && lse && qphi);
+  SLA2H_CHECK_ARG(D == kT && E == kT);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && L > 0 && Np > 0 && (int64_t)Np * E <= L);
+  SLA2H_CHECK_ARG(T >= 1 && T <= Np);
+  const int Nb = (int)((L + E - 1) / E);
+  SLA2H_CHECK_ARG(T + (Nb - Np) <= kMaxJ);
+  const int64_t nwork = (int64_t)Nb * B * H;
+  const int64_t per_xcd = (nwork + 7) / 8;
+  SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31));
+  TrainArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q8 = q8;
+  a.k8 = k8;
+  a.v8f = v8f;
+  a.qs = qs;
+  a.ks = ks;
+  a.vs = vs;
+  a.lut = lut;
+  a.os = static_cast<uint16_t*>(o_s);
+  a.lse = lse;
+  a.qphi = static_cast<uint16_t*>(qphi);
+  a.L = L;
+  a.Nb = Nb;
+  a.Np = Np;
+  a.Mb = Nb;
+  a.T = T;
+  a.n_tail = Nb - Np;
+  a.nwork = (int)nwork;
+  a.per_xcd = (int)per_xcd;
+  a.c2 = scale * 1.4426950408889634f;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nblocks = (int)(8 * per_xcd);
+  if (dtype == SLA2H_DTYPE_BF16)
+    sparse_fwd_qat_kernel<BF16><<<nblocks, 256, 0, st>>>(a);
+  else
+    sparse_fwd_qat_kernel<F16><<<nblocks, 256, 0, st>>>(a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_linear_mix_qat(const void* qphi, const void* comp, const float* Hall,
+                                    const void* o_s, const float* alpha, int alpha_stride,
+                                    int dtype, int B, int H, int64_t L, int D, int E, float eps_l,
+                                    void* o, void* o_l, float* den, void* stream) {
+  SLA2H_CHECK_ARG(qphi && comp && Hall && o_s && alpha && o && o_l && den);
+  SLA2H_CHECK_ARG(D == kT && E == kT && alpha_stride >= 0);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && L > 0);
+  const int Mb = (int)((L + E - 1) / E);
+  dim3 grid(Mb, B * H);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto QP = static_cast<const uint16_t*>(qphi);
+  auto C = static_cast<const unsigned char*>(comp);
+  auto OS = static_cast<const uint16_t*>(o_s);
+  auto O = static_cast<uint16_t*>(o);
+  auto OL = static_cast<uint16_t*>(o_l);
+  if (dtype == SLA2H_DTYPE_BF16)
+    linear_mix_qat_kernel<BF16><<<grid, 256, 0, st>>>(QP, C, Hall, OS, alpha, alpha_stride, L, Mb, H, eps_l, O, OL, den);
+  else
+    linear_mix_qat_kernel<F16><<<grid, 256, 0, st>>>(QP, C, Hall, OS, alpha, alpha_stride, L, Mb, H, eps_l, O, OL, den);
+  return (int)hipGetLastError();
+}

@@ -119,6 +119,95 @@ __global__ __launch_bounds__(256) void quant_pool_kernel(QuantPoolArgs a) {
   }
 }
 
+// Training-forward quantisation (semantics of the in-kernel quantisation of
+// _attn_fwd_qat, models/sla2_vendor/kernel_sparse_qat.py:56-58, 88-90,
+// 106-107): s = max|x| / 127 + 1e-12 per 64 x 64 tile, q = (int) fl(fl(x / s)
+// + 0.5 sign(x)) truncated toward zero (sign(+-0) = +1).  Q and K keep the
+// row-major (BH, L, 64) int8 layout; V is written as INT8 MFMA A-operand
+// fragments of O^T = V8^T P8^T: per tile [ct][lane][16 B], byte s of lane
+// (g, rr) of column tile ct = V8[16 (s >> 2) + 4 g + (s & 3)][16 ct + rr].
+struct QuantTrainArgs {
+  const uint16_t* x[3];  // q, k, v (BH, L, 64)
+  int8_t* xq[3];         // q8, k8 (BH, L, 64); v8f (BH, Nb, 4096)
+  float* xs[3];          // (BH, Nb)
+  int BH;
+  int64_t L;
+  int Nb;
+};
+
+template <typename T16>
+__global__ __launch_bounds__(256) void quant_train_kernel(QuantTrainArgs a) {
+  __shared__ float red[4];
+  __shared__ __align__(16) int8_t q8t[kTile][kTile + 16];
+
+  const int tid = threadIdx.x;
+  const int blk = blockIdx.x;
+  const int t = blockIdx.y / a.BH;
+  const int bh = blockIdx.y % a.BH;
+  const int r = tid >> 2;
+  const int c0 = (tid & 3) * 16;
+  const int64_t row = (int64_t)blk * kTile + r;
+  const bool valid = row < a.L;
+  const int64_t off = ((int64_t)bh * a.L + row) * kTile + c0;
+
+  float xv[16];
+  if (valid) {
+    const uint4* src = reinterpret_cast<const uint4*>(a.x[t] + off);
+    uint4 u0 = src[0], u1 = src[1];
+    uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      xv[2 * i] = T16::to_f32((uint16_t)(w[i] & 0xffff));
+      xv[2 * i + 1] = T16::to_f32((uint16_t)(w[i] >> 16));
+    }
+  } else {
+#pragma unroll
+    for (int i = 0; i < 16; ++i) xv[i] = 0.f;
+  }
+  float am = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) am = fmaxf(am, fabsf(xv[i]));
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) am = fmaxf(am, __shfl_xor(am, m, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = am;
+  __syncthreads();
+  am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = am / 127.0f + 1e-12f;
+
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    uint32_t acc = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const float x = xv[4 * i + b];
+      const float y = x / s + (x >= 0.f ? 0.5f : -0.5f);  // two roundings (no contraction)
+      acc |= ((uint32_t)((int)y & 0xff)) << (8 * b);
+    }
+    w[i] = acc;
+  }
+  if (tid == 0) a.xs[t][(int64_t)bh * a.Nb + blk] = s;
+  if (t < 2) {
+    if (valid) *reinterpret_cast<uint4*>(a.xq[t] + off) = make_uint4(w[0], w[1], w[2], w[3]);
+    return;
+  }
+  // V: transpose to the fragment order through LDS (rows past L are zero)
+  *reinterpret_cast<uint4*>(&q8t[r][c0]) = make_uint4(w[0], w[1], w[2], w[3]);
+  __syncthreads();
+  const int ct = tid >> 6, lane = tid & 63, g = lane >> 4, rr = lane & 15;
+  uint32_t f[4];
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb) {
+    uint32_t acc = 0;
+#pragma unroll
+    for (int i = 0; i < 4; ++i)
+      acc |= ((uint32_t)(uint8_t)q8t[16 * kb + 4 * g + i][16 * ct + rr]) << (8 * i);
+    f[kb] = acc;
+  }
+  *reinterpret_cast<uint4*>(a.xq[2] + ((int64_t)bh * a.Nb + blk) * 4096 + tid * 16) =
+      make_uint4(f[0], f[1], f[2], f[3]);
+}
+
 // Orderable 64-bit key: high word = monotone map of the fp32 score
 // (NaN -> +NaN, the largest, as torch.topk orders; -0 -> +0), low word =
 // ~index so that equal scores rank the lower index first.
@@ -364,6 +453,35 @@ extern "C" int sla2h_version(void) { return 1; }
 
 extern "C" const char* sla2h_error_string(int code) {
   return hipGetErrorString((hipError_t)code);
+}
+
+extern "C" int sla2h_quant_train(const void* q, const void* k, const void* v, int dtype, int B,
+                                 int H, int64_t L, int D, int E, int8_t* q8, float* qs, int8_t* k8,
+                                 float* ks, int8_t* v8f, float* vs, void* stream) {
+  SLA2H_CHECK_ARG(q && k && v && q8 && qs && k8 && ks && v8f && vs);
+  SLA2H_CHECK_ARG(D == kTile && E == kTile);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && 3 * B * H <= 65535 && L > 0);
+  QuantTrainArgs a;
+  a.x[0] = static_cast<const uint16_t*>(q);
+  a.x[1] = static_cast<const uint16_t*>(k);
+  a.x[2] = static_cast<const uint16_t*>(v);
+  a.xq[0] = q8;
+  a.xq[1] = k8;
+  a.xq[2] = v8f;
+  a.xs[0] = qs;
+  a.xs[1] = ks;
+  a.xs[2] = vs;
+  a.BH = B * H;
+  a.L = L;
+  a.Nb = (int)((L + E - 1) / E);
+  dim3 grid(a.Nb, 3 * a.BH);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SLA2H_DTYPE_BF16)
+    quant_train_kernel<BF16><<<grid, 256, 0, st>>>(a);
+  else
+    quant_train_kernel<F16><<<grid, 256, 0, st>>>(a);
+  return (int)hipGetLastError();
 }
 
 extern "C" int sla2h_quantize(const void* x, int dtype, int64_t BH, int64_t L, int D, int E,

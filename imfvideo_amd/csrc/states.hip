@@ -25,7 +25,10 @@ constexpr size_t kRecBytes = 2 * 16384 + 2 * 256;
 //
 // Products phi^T V run on 16-bit MFMA with phi split into hi + lo halves of
 // the input's 16-bit type (about 16 significant bits), fp32 accumulate.
-template <typename T16, bool TAN>
+// ROUND (training forward): phi is rounded to the 16-bit type first, as the
+// reference's softmax(K).to(dtype) (models/sla2_cube_qat.py:728), the lo half
+// vanishes, and no operand tiles are written.
+template <typename T16, bool TAN, bool ROUND = false>
 __global__ __launch_bounds__(256) void linear_states_kernel(
     const uint16_t* __restrict__ K, const uint16_t* __restrict__ dK,
     const uint16_t* __restrict__ V, const uint16_t* __restrict__ dV, int64_t L, int Np, int Nb,
@@ -121,9 +124,13 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
 #pragma unroll
       for (int i = 0; i < 16; ++i) dphi[i] = phi[i] * (T16::to_f32(dkb[i]) - dot);
     }
-    if (!valid) {  // cannot happen for video tiles; keeps padding rows inert
+    if (!valid) {  // padding rows of a ragged last tile stay inert
 #pragma unroll
       for (int i = 0; i < 16; ++i) phi[i] = dphi[i] = 0.f;
+    }
+    if (ROUND) {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) phi[i] = T16::to_f32(T16::from_f32(phi[i]));
     }
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -156,7 +163,7 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
   __syncthreads();
 
   // value-operand tile in fragment order: thread -> (ct, w, r), 4 lane groups g
-  {
+  if (!ROUND) {
     const int ct = tid >> 6, vw = (tid >> 4) & 3, rr = tid & 15;
     const int c = 16 * ct + rr;
     unsigned char* base = reinterpret_cast<unsigned char*>(vt) +
@@ -205,7 +212,7 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
     for (int vt_ = 0; vt_ < 4; ++vt_) {
       const u32x4 bv = *reinterpret_cast<const u32x4*>(&vT[16 * vt_ + lr][k0]);
       acc[vt_] = mfma_16x16x32<T16>(ah, bv, acc[vt_]);
-      acc[vt_] = mfma_16x16x32<T16>(al, bv, acc[vt_]);
+      if (!ROUND) acc[vt_] = mfma_16x16x32<T16>(al, bv, acc[vt_]);
       if (TAN) {
         const u32x4 bdv = *reinterpret_cast<const u32x4*>(&dvT[16 * vt_ + lr][k0]);
         dacc[vt_] = mfma_16x16x32<T16>(dah, bv, dacc[vt_]);
@@ -493,6 +500,29 @@ extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v,
   dim3 g2((8320 + 255) / 256, B * H);
   states_sum_kernel<<<g2, 256, 0, st>>>(Hb, tan ? dHb : nullptr, zb, tan ? dzb : nullptr, Np, Hall,
                                         dHall, zall, dzall);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_linear_states_qat(const void* k, const void* v, int dtype, int B, int H,
+                                       int64_t L, int D, int E, float* Hb, float* zb, float* Hall,
+                                       float* zall, void* stream) {
+  SLA2H_CHECK_ARG(k && v && Hb && zb && Hall && zall);
+  SLA2H_CHECK_ARG(D == kT && E == kT);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && L > 0);
+  const int Nb = (int)((L + E - 1) / E);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(Nb, B * H);
+  auto K = static_cast<const uint16_t*>(k);
+  auto V = static_cast<const uint16_t*>(v);
+  if (dtype == SLA2H_DTYPE_BF16)
+    linear_states_kernel<BF16, false, true><<<grid, 256, 0, st>>>(K, nullptr, V, nullptr, L, Nb, Nb, Hb, nullptr, zb, nullptr, nullptr, nullptr);
+  else
+    linear_states_kernel<F16, false, true><<<grid, 256, 0, st>>>(K, nullptr, V, nullptr, L, Nb, Nb, Hb, nullptr, zb, nullptr, nullptr, nullptr);
+  int err = (int)hipGetLastError();
+  if (err) return err;
+  dim3 g2((8320 + 255) / 256, B * H);
+  states_sum_kernel<<<g2, 256, 0, st>>>(Hb, nullptr, zb, nullptr, Nb, Hall, nullptr, zall, nullptr);
   return (int)hipGetLastError();
 }
 

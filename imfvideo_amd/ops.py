@@ -47,6 +47,22 @@ def _bhld(t, name):
     return t.contiguous()
 
 
+def _check_lut(lut, B, H, L):
+    Mb = -(-L // E_TILE)
+    if lut.dim() != 4 or tuple(lut.shape[:3]) != (B, H, Mb):
+        raise ValueError(f"lut: expected (B, H, Mb, T) = ({B}, {H}, {Mb}, T), got {tuple(lut.shape)}")
+
+
+def _alpha_rows(alpha, H, Mb, device):
+    """(H, Mb) fp32 with unit column stride (the kernels read alpha[h * stride + m])."""
+    alpha = alpha.detach().to(device, torch.float32)
+    if alpha.dim() != 2:
+        alpha = alpha.reshape(H, -1)
+    if tuple(alpha.shape) != (H, Mb):
+        raise ValueError(f"alpha: expected (H, Mb) = ({H}, {Mb}), got {tuple(alpha.shape)}")
+    return alpha if alpha.stride(1) == 1 else alpha.contiguous()
+
+
 def quantize(x, E=E_TILE):
     """x (B,H,L,D) 16-bit -> (xq int8 (B,H,L,D), xs fp32 (B,H,ceil(L/E)))."""
     _need_gpu(x)
@@ -174,10 +190,9 @@ def fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq=None, scale=None, ep
     scale = D ** -0.5 if scale is None else scale
     o = torch.empty(B, H, L, D, device=q.device, dtype=torch.float32)
     do = torch.empty_like(o) if tan else None
+    _check_lut(lut, B, H, L)
     if alpha is not None:
-        alpha = alpha.detach().to(q.device, torch.float32)
-        if alpha.dim() != 2 or alpha.stride(1) != 1:
-            alpha = alpha.reshape(H, -1).contiguous()
+        alpha = _alpha_rows(alpha, H, -(-L // E_TILE), q.device)
     _lib.check(_lib.load().sla2h_fwd_jvp(
         q.data_ptr(), _ptr(dq), _ptr(st.get("kt")) if tan else None, st["vt"].data_ptr(),
         q8.data_ptr(), k8.data_ptr(), qs.data_ptr(),
@@ -219,3 +234,117 @@ def cube_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, Np, prefix_len=0, proj_q=Non
                    comp=comp, **st)
         return o, do, aux
     return o, do
+
+
+# ---------------------------------------------------------------------------
+# Training forward (_CubeQATFunction.forward, models/sla2_cube_qat.py:703-752)
+# ---------------------------------------------------------------------------
+
+def quant_train(q, k, v, E=E_TILE):
+    """Truncating INT8 quantisation of Q, K, V (the training kernel's law).
+
+    -> dict(q8, qs, k8, ks, v8f, vs); v8f (B,H,Nb,4096) int8 in fragment order.
+    """
+    _need_gpu(q, k, v)
+    q, k, v = (_bhld(t, n) for t, n in ((q, "q"), (k, "k"), (v, "v")))
+    if not (q.shape == k.shape == v.shape and q.dtype == k.dtype == v.dtype):
+        raise ValueError("quant_train: q, k, v must share shape and dtype")
+    B, H, L, D = q.shape
+    nb = -(-L // E)
+    dev = q.device
+    out = dict(q8=torch.empty_like(q, dtype=torch.int8), k8=torch.empty_like(k, dtype=torch.int8),
+               v8f=torch.empty(B, H, nb, 4096, device=dev, dtype=torch.int8))
+    for n in ("qs", "ks", "vs"):
+        out[n] = torch.empty(B, H, nb, device=dev, dtype=torch.float32)
+    _lib.check(_lib.load().sla2h_quant_train(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), _dtype_code(q), B, H, L, D, E,
+        out["q8"].data_ptr(), out["qs"].data_ptr(), out["k8"].data_ptr(), out["ks"].data_ptr(),
+        out["v8f"].data_ptr(), out["vs"].data_ptr(), _stream(dev)), "sla2h_quant_train")
+    return out
+
+
+def sparse_fwd_qat(q, qz, lut, Np, scale=None):
+    """Sparse branch of the training forward -> (o_s 16-bit, lse fp32, qphi 16-bit)."""
+    _need_gpu(q, lut)
+    B, H, L, D = q.shape
+    T = lut.shape[-1]
+    _check_lut(lut, B, H, L)
+    scale = D ** -0.5 if scale is None else scale
+    o_s = torch.empty_like(q)
+    qphi = torch.empty_like(q)
+    lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
+    _lib.check(_lib.load().sla2h_sparse_fwd_qat(
+        q.data_ptr(), qz["q8"].data_ptr(), qz["qs"].data_ptr(), qz["k8"].data_ptr(),
+        qz["ks"].data_ptr(), qz["v8f"].data_ptr(), qz["vs"].data_ptr(),
+        lut.to(torch.int32).contiguous().data_ptr(), _dtype_code(q), B, H, L, D, E_TILE, Np, T,
+        float(scale), o_s.data_ptr(), lse.data_ptr(), qphi.data_ptr(), _stream(q.device)),
+        "sla2h_sparse_fwd_qat")
+    return o_s, lse, qphi
+
+
+def linear_states_qat(k, v):
+    """States of all Nb tiles with 16-bit-rounded phi(K) -> dict(Hb, zb, Hall, zall)."""
+    _need_gpu(k, v)
+    k, v = _bhld(k, "k"), _bhld(v, "v")
+    B, H, L, D = k.shape
+    nb = -(-L // E_TILE)
+    dev = k.device
+    st = dict(Hb=torch.empty(B, H, nb, D, D, device=dev), zb=torch.empty(B, H, nb, D, device=dev),
+              Hall=torch.empty(B, H, D, D, device=dev), zall=torch.empty(B, H, D, device=dev))
+    _lib.check(_lib.load().sla2h_linear_states_qat(
+        k.data_ptr(), v.data_ptr(), _dtype_code(k), B, H, L, D, E_TILE, st["Hb"].data_ptr(),
+        st["zb"].data_ptr(), st["Hall"].data_ptr(), st["zall"].data_ptr(), _stream(dev)),
+        "sla2h_linear_states_qat")
+    return st
+
+
+def linear_mix_qat(qphi, comp, Hall, o_s, alpha, eps_l=1e-5):
+    """Linear branch + alpha mix of the training forward -> (o, o_l 16-bit, den fp32)."""
+    _need_gpu(qphi, comp, Hall, o_s, alpha)
+    B, H, L, D = qphi.shape
+    Mb = -(-L // E_TILE)
+    if tuple(comp.shape) != (B, H, Mb, REC_BYTES) or tuple(Hall.shape) != (B, H, D, D):
+        raise ValueError("linear_mix_qat: comp / Hall shapes do not match qphi")
+    alpha = _alpha_rows(alpha, H, Mb, qphi.device)
+    o = torch.empty_like(o_s)
+    o_l = torch.empty_like(o_s)
+    den = torch.empty(B, H, L, device=qphi.device, dtype=torch.float32)
+    _lib.check(_lib.load().sla2h_linear_mix_qat(
+        qphi.data_ptr(), comp.data_ptr(), Hall.contiguous().data_ptr(), o_s.data_ptr(),
+        alpha.data_ptr(), alpha.stride(0), _dtype_code(qphi), B, H, L, D, E_TILE,
+        float(eps_l), o.data_ptr(), o_l.data_ptr(), den.data_ptr(), _stream(qphi.device)),
+        "sla2h_linear_mix_qat")
+    return o, o_l, den
+
+
+def augment_lut(lut, Np, n_tail):
+    """lut (B,H,Mb,T) -> lut_aug (B,H,Mb,T+n_tail) int32 with the prefix tail blocks appended."""
+    B, H, Mb, _ = lut.shape
+    tail = torch.arange(Np, Np + n_tail, device=lut.device, dtype=torch.int32)
+    return torch.cat([lut.to(torch.int32), tail.view(1, 1, 1, -1).expand(B, H, Mb, n_tail)],
+                     -1).contiguous()
+
+
+def train_fwd(q, k, v, alpha, lut, Np, eps_l=1e-5):
+    """Training forward of the cube-QAT op on given routing.
+
+    q, k, v: (B,H,L,64) 16-bit, tile-major.  alpha: (H, Mb) after the sigmoid.
+    lut: (B,H,Mb,T) routed video tiles.  Returns a dict with the module output
+    o and the tensors the reference saves for its backward: o_s, o_l, lse, den,
+    qphi, htot (rounded to 16 bits, held in fp32), ztot, lut_aug, and the
+    quantised operands.
+    """
+    q, k, v = (t.contiguous() for t in (q, k, v))
+    B, H, L, D = q.shape
+    nb = -(-L // E_TILE)
+    n_tail = nb - Np
+    lut = lut.to(torch.int32).contiguous()
+    qz = quant_train(q, k, v)
+    o_s, lse, qphi = sparse_fwd_qat(q, qz, lut, Np)
+    st = linear_states_qat(k, v)
+    lut_aug = augment_lut(lut, Np, n_tail)
+    comp = complement(st, lut_aug, nb)
+    o, o_l, den = linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha, eps_l)
+    htot = st["Hall"].to(q.dtype).float()
+    return dict(o=o, o_s=o_s, o_l=o_l, lse=lse, den=den, qphi=qphi, htot=htot,
+                ztot=st["zall"], lut_aug=lut_aug, **qz)

@@ -115,9 +115,12 @@ class SLA2CubeQATAttentionImpl(nn.Module):
         use_int8: INT8 primal scores (the only mode of this build).
         pre_permuted: tokens are already tile-major.
 
-    The forward runs the fused INT8 primal kernel (the JVP kernel's INT8
-    semantics).  The autograd backward of the training path is not part of
-    this build yet: calling the module with gradients required raises.
+    The forward follows the reference module: tokens permuted tile-major and
+    cast to fp16, routed, then the training-forward kernels (INT8 sparse
+    branch with truncating quantisation and INT8 P.V, 16-bit state-form
+    linear branch, 16-bit mix; ``ops.train_fwd``), which the reference also
+    runs under no_grad.  The autograd backward of the training path is not
+    part of this build yet: calling the module with gradients required raises.
     """
 
     TILE_MAJOR = True
@@ -160,14 +163,13 @@ class SLA2CubeQATAttentionImpl(nn.Module):
             x = x.permute(0, 2, 1, 3)
             if not self.pre_permuted:
                 x = x[:, :, self.perm]
-            return _c16(x)
+            return x.half().contiguous()
 
-        qh, kh, vh = tm(q), tm(k), tm(v.to(q.dtype))
+        qh, kh, vh = tm(q), tm(k), tm(v)
         lut, T = route_tiles_fast(qh, kh, self.topk_frac, self.Np, self.E, self.prefix_len,
                                   proj_q=self.proj_q, proj_k=self.proj_k)
         a = torch.sigmoid(self.alpha_logit.detach().float())
-        o, _ = ops.cube_jvp(qh, kh, vh, None, None, None, a, self.topk_frac, self.Np,
-                            self.prefix_len, lut=lut, T=T)
+        o = ops.train_fwd(qh, kh, vh, a, lut, self.Np)["o"]
         if self.pre_permuted:
             return o.permute(0, 2, 1, 3).to(q.dtype)
         return o[:, :, self.inv].permute(0, 2, 1, 3).to(q.dtype)

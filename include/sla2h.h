@@ -149,6 +149,71 @@ int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, const void* vt,
                   float scale, float eps_l, int flags,
                   float* o, float* dout, void* stream);
 
+/* ---- training forward (the module's autograd forward) ------------------ */
+
+/*
+ * Per-(b,h,64-token block) INT8 quantisation of Q, K and V with the
+ * training kernel's law: s = fl32(max|x| / 127) + 1e-12,
+ * x8 = trunc(fl32(fl32(x / s) + 0.5 sign(x))) (toward zero; sign(+-0) = +1).
+ *   q8,k8 (B,H,L,D) int8; qs,ks,vs (B,H,Nb) fp32;
+ *   v8f (B,H,Nb,4,64,16) int8, the value tile in INT8 MFMA fragment order:
+ *     [ct][lane][s] = V8[16(s>>2) + 4g + (s&3)][16ct + r], lane = 16g + r,
+ *     rows past L zero.
+ * 3*B*H <= 65535.  Replaces the in-kernel quantisation of _attn_fwd_qat
+ * (models/sla2_vendor/kernel_sparse_qat.py:56-58, 88-90, 106-107).
+ */
+int sla2h_quant_train(const void* q, const void* k, const void* v, int dtype, int B, int H,
+                      int64_t L, int D, int E, int8_t* q8, float* qs, int8_t* k8, float* ks,
+                      int8_t* v8f, float* vs, void* stream);
+
+/*
+ * Sparse branch of the training forward over the augmented LUT (lut[m,0..T)
+ * then the Nb-Np prefix tail blocks):
+ *   S = int32(q8 . k8^T) * (qs*ks) * fl32(scale*log2 e), keys past L masked;
+ *   exact running max per 64-key tile, P = exp2(S - m),
+ *   P8 = (int) fl(127 P + 0.5), O += int32(P8 . V8) * (vs/127);
+ *   o_s = O / l (B,H,L,D) 16-bit, lse = m + log2 l (B,H,L) fp32 (log2 domain),
+ *   qphi = softmax_D(q) (B,H,L,D) 16-bit.
+ * Inputs from sla2h_quant_train.  T + (Nb - Np) <= 1024.  Replaces
+ * _attn_fwd_qat with USE_INT8 and PHI_OUT
+ * (models/sla2_vendor/kernel_sparse_qat.py:28-117) as launched by
+ * _CubeQATFunction.forward (models/sla2_cube_qat.py:717-722).
+ */
+int sla2h_sparse_fwd_qat(const void* q, const int8_t* q8, const float* qs, const int8_t* k8,
+                         const float* ks, const int8_t* v8f, const float* vs,
+                         const int32_t* lut, int dtype, int B, int H, int64_t L, int D, int E,
+                         int Np, int T, float scale, void* o_s, float* lse, void* qphi,
+                         void* stream);
+
+/*
+ * Linear-branch states of ALL Nb tiles with phi(K) rounded to the 16-bit type
+ * first (softmax(K).to(dtype)), rows past L zero:
+ *   Hb (B,H,Nb,D,D), zb (B,H,Nb,D) fp32 per tile; Hall (B,H,D,D), zall (B,H,D)
+ *   fp32 sums over the tiles in n order (= htot and ztot before rounding).
+ * Feed Hb/zb to sla2h_complement with Np = Nb and the augmented LUT.
+ * Replaces kphi = softmax(kh).to(dtype) and _precompute_global
+ * (models/sla2_cube_qat.py:728-730; models/sla2_vendor/kernel_linear.py:305-313).
+ */
+int sla2h_linear_states_qat(const void* k, const void* v, int dtype, int B, int H, int64_t L,
+                            int D, int E, float* Hb, float* zb, float* Hall, float* zall,
+                            void* stream);
+
+/*
+ * Linear branch (state form) and alpha mix of the training forward:
+ *   H_m = round16(comp.Hc[m] + (round16(Hall) - Hall)), z_m = comp.zc[m];
+ *   den = qphi . z_m (+-eps_l, signed) (B,H,L) fp32;
+ *   o_l = round16(qphi H_m / den) (B,H,L,D) 16-bit;
+ *   o = round16(round16(a o_s) + round16(round16(1 - a) o_l)), a =
+ *   round16(alpha[h*alpha_stride + m]) (B,H,L,D) 16-bit.
+ * comp = sla2h_complement records over the augmented LUT.  Replaces _lin_fwd2
+ * without SCORE_FORM (models/sla2_vendor/kernel_linear.py:206-304) and the mix
+ * of _CubeQATFunction.forward (models/sla2_cube_qat.py:733-744).
+ */
+int sla2h_linear_mix_qat(const void* qphi, const void* comp, const float* Hall,
+                         const void* o_s, const float* alpha, int alpha_stride, int dtype,
+                         int B, int H, int64_t L, int D, int E, float eps_l, void* o,
+                         void* o_l, float* den, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

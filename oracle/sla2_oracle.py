@@ -404,7 +404,8 @@ def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L
     q, k, v: (B,H,L,D) float tensors holding 16-bit values.  alpha: (H, Mb)
     after the sigmoid.  lut: (B,H,Mb,T) routed video tiles; the n_tail prefix
     blocks are appended (lut_aug).  Returns dict with o (16-bit values, the
-    module output), o_s, o_l (16-bit values), lse (fp32, log2 domain), qphi.
+    module output), o_s, o_l (16-bit values), lse (fp32, log2 domain), qphi,
+    den (the signed-epsilon denominator), htot (16-bit values), ztot.
     """
     B, H, L, D = q.shape
     nb = -(-L // E)
@@ -472,8 +473,10 @@ def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L
     den = (qpt[:, :, :Mb] * zi[..., None, :]).sum(-1)
     den = torch.where(den >= 0, den + eps, den - eps)
     o_l = (num / den[..., None]).reshape(B, H, Mb * E, D)[:, :, :L]
+    den = den.reshape(B, H, Mb * E)[:, :, :L]
     o_l16 = _round16(o_l, t16)
     a = _round16(alpha.float()[None, :, :, None, None].expand(B, H, Mb, E, 1)
                  .reshape(B, H, Mb * E, 1)[:, :, :L], t16)
     o = _round16(_round16(a * o_s16, t16) + _round16(_round16(1.0 - a, t16) * o_l16, t16), t16)
-    return {"o": o, "o_s": o_s16, "o_l": o_l16, "lse": lse, "qphi": qphi}
+    return {"o": o, "o_s": o_s16, "o_l": o_l16, "lse": lse, "qphi": qphi, "den": den,
+            "htot": htot, "ztot": ztot}

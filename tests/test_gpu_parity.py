@@ -248,11 +248,12 @@ def test_module_forward_no_grad():
     with torch.no_grad():
         out = mod(cuda(x), cuda(x * 0.9), cuda(x * 1.1)).cpu()
     assert out.shape == x.shape and torch.isfinite(out).all()
-    tm = lambda t: t.permute(0, 2, 1, 3)[:, :, mod.perm.cpu()].to(torch.bfloat16).float()
+    # the reference module: fp16 tile-major operands, training-forward semantics
+    tm = lambda t: t.permute(0, 2, 1, 3)[:, :, mod.perm.cpu()].half().float()
     qh, kh, vh = tm(x), tm(x * 0.9), tm(x * 1.1)
     lut, T, _, _ = O.route(qh, kh, 0.5, mod.Np, mod.prefix_len, torch.eye(64), torch.eye(64))
     a = torch.sigmoid(mod.alpha_logit.detach().cpu())
-    eo, _ = O.cube_jvp(qh, kh, vh, None, None, None, a, lut, mod.Np, mod.prefix_len)
+    eo = O.train_fwd(qh, kh, vh, a, lut, mod.Np, mod.prefix_len, t16=torch.float16)["o"]
     eo = eo[:, :, mod.inv.cpu()].permute(0, 2, 1, 3)
     assert max_abs(out, eo) < TOL_MAX and rel_l2(out, eo) < TOL_REL
     with pytest.raises(NotImplementedError):

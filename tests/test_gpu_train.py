@@ -1,0 +1,143 @@
+"""GPU parity of the training forward (semantics of _CubeQATFunction.forward,
+models/sla2_cube_qat.py:703-752) against the CPU oracle's train_fwd (marked gpu).
+
+Quantised operands and scales bit-exact; 16-bit outputs (o, o_s, o_l, qphi)
+within max-abs 2e-2 and rel-L2 1e-2; lse (log2 domain) within 1e-3 absolute;
+den and htot relative 1e-3.
+"""
+import numpy as np
+import pytest
+import torch
+
+from oracle import sla2_oracle as O
+from tests.helpers import make_inputs, max_abs, rel_l2
+from tests.test_gpu_parity import TOL_MAX, TOL_REL, config_inputs, cuda, golden, say
+
+pytestmark = pytest.mark.gpu
+
+
+def expected_v8f(v8, L):
+    """V8 (B,H,L,64) -> (B,H,Nb,4096) with [ct][lane=16g+r][s=4kb+i] = V8[16kb+4g+i][16ct+r]."""
+    B, H = v8.shape[:2]
+    nb = -(-L // 64)
+    x = torch.zeros(B, H, nb * 64, 64, dtype=torch.int8)
+    x[:, :, :L] = torch.as_tensor(v8)
+    x = x.view(B, H, nb, 4, 4, 4, 4, 16)        # [kb][g][i][ct][r]
+    return x.permute(0, 1, 2, 6, 4, 7, 3, 5).reshape(B, H, nb, 4096)
+
+
+def check_quant(qz, f, L):
+    for n in ("q", "k", "v"):
+        x8, xs = O.quantize_blocks_trunc(f[n])
+        assert np.array_equal(qz[n + "s"].cpu().numpy(), xs), n
+        if n == "v":
+            assert torch.equal(qz["v8f"].cpu(), expected_v8f(x8, L))
+        else:
+            assert np.array_equal(qz[n + "8"].cpu().numpy(), x8), n
+
+
+def compare(out, ref, tag=""):
+    for n in ("o", "o_s", "o_l", "qphi"):
+        got = out[n].cpu().float()
+        print(f"  {tag}{n} max {max_abs(got, ref[n]):.2e} rel {rel_l2(got, ref[n]):.2e}", flush=True)
+        assert max_abs(got, ref[n]) < TOL_MAX and rel_l2(got, ref[n]) < TOL_REL, n
+    lse = out["lse"].cpu()
+    print(f"  {tag}lse max {max_abs(lse, ref['lse']):.2e}", flush=True)
+    assert max_abs(lse, ref["lse"]) < 1e-3
+    assert rel_l2(out["den"].cpu(), ref["den"]) < 1e-3
+    assert rel_l2(out["htot"].cpu(), ref["htot"]) < 1e-3
+    assert rel_l2(out["ztot"].cpu(), ref["ztot"]) < 1e-5
+
+
+def run_train(ins, alpha, lut, Np):
+    from imfvideo_amd import ops
+    g = {n: cuda(ins[n]) for n in ("q", "k", "v")}
+    out = ops.train_fwd(g["q"], g["k"], g["v"], cuda(alpha), cuda(torch.as_tensor(lut)), Np)
+    torch.cuda.synchronize()
+    return out
+
+
+@pytest.mark.parametrize("name", ["ref_geom_bf16", "tiny_f16", "two_tails_bf16"])
+def test_train_fwd_golden(name):
+    say("train_fwd golden", name)
+    z, dt, ins = golden(name)
+    Np, P = int(z["Np"]), int(z["P"])
+    alpha = torch.from_numpy(z["alpha"])
+    out = run_train(ins, alpha, z["lut"], Np)
+    f = {n: t.float() for n, t in ins.items()}
+    check_quant(out, f, f["q"].shape[2])
+    ref = O.train_fwd(f["q"], f["k"], f["v"], alpha, z["lut"], Np, P, t16=dt)
+    compare(out, ref)
+
+
+def test_train_fwd_config1_and_determinism():
+    say("train_fwd config1 (1,4,4096)")
+    ins, Np, P = config_inputs(1)
+    f = {n: t.float() for n, t in ins.items()}
+    lut, T, _, _ = O.route(f["q"], f["k"], 0.1, Np, P)
+    g = torch.Generator().manual_seed(5)
+    alpha = torch.rand(4, Np, generator=g) * 0.8 + 0.1
+    out = run_train(ins, alpha, lut, Np)
+    check_quant(out, f, 4096)
+    compare(out, O.train_fwd(f["q"], f["k"], f["v"], alpha, lut, Np, P))
+    again = run_train(ins, alpha, lut, Np)
+    for n in ("o", "lse", "den"):
+        assert torch.equal(out[n], again[n]), n
+
+
+def test_train_fwd_ragged_fp16_and_alpha_endpoints():
+    say("train_fwd ragged prefix fp16, alpha 0 / 1")
+    B, H, Np, P = 2, 2, 5, 37
+    L = Np * 64 + P
+    q, k, v = make_inputs(31, B, H, L, dtype=torch.float16, tangent=False)
+    ins = dict(q=q, k=k, v=v)
+    f = {n: t.float() for n, t in ins.items()}
+    lut, T, _, _ = O.route(f["q"], f["k"], 0.4, Np, P)
+    for a in (0.0, 1.0, 0.3):
+        alpha = torch.full((H, Np + 1), a)
+        out = run_train(ins, alpha, lut, Np)
+        ref = O.train_fwd(f["q"], f["k"], f["v"], alpha, lut, Np, P, t16=torch.float16)
+        compare(out, ref, f"a={a} ")
+        if a == 1.0:
+            assert torch.equal(out["o"], out["o_s"])
+        if a == 0.0:
+            assert torch.equal(out["o"], out["o_l"])
+
+
+def test_train_fwd_all_tiles_routed_and_zero_tiles():
+    say("train_fwd T = Np, zero tiles")
+    B, H, Np, P = 1, 2, 3, 10
+    L = Np * 64 + P
+    q, k, v = make_inputs(21, B, H, L, tangent=False)
+    q[:, :, 64:128] = 0
+    k[:, 1, :64] = 0
+    ins = dict(q=q, k=k, v=v)
+    lut = np.broadcast_to(np.arange(Np, dtype=np.int32), (B, H, 4, Np)).copy()
+    alpha = torch.full((H, 4), 0.5)
+    out = run_train(ins, alpha, lut, Np)
+    f = {n: t.float() for n, t in ins.items()}
+    check_quant(out, f, L)
+    ref = O.train_fwd(f["q"], f["k"], f["v"], alpha, lut, Np, P)
+    # the complement is empty: o_l = qphi . 0 / (+-eps) -> the 16-bit rounding of
+    # (htot16 - htot) / eps; compare the sparse side and the finite output only
+    for n in ("o_s", "qphi"):
+        assert max_abs(out[n].cpu().float(), ref[n]) < TOL_MAX, n
+    assert max_abs(out["lse"].cpu(), ref["lse"]) < 1e-3
+    assert torch.isfinite(out["o"].float()).all()
+
+
+def test_train_fwd_config3_full_size():
+    say("train_fwd config3 full size (1,8,29952,64)")
+    ins, Np, P = config_inputs(3)
+    f = {n: t.float() for n, t in ins.items() if n in ("q", "k", "v")}
+    lut, T, _, _ = O.route(f["q"], f["k"], 0.1, Np, P)
+    alpha = torch.full((8, Np), 0.9)
+    out = run_train(ins, alpha, lut, Np)
+    assert torch.isfinite(out["o"].float()).all() and torch.isfinite(out["lse"]).all()
+    check_quant(out, f, 29952)
+    for h in (0, 5):
+        sl = slice(h, h + 1)
+        ref = O.train_fwd(f["q"][:, sl], f["k"][:, sl], f["v"][:, sl], alpha[sl], lut[:, sl],
+                          Np, P)
+        compare({n: (t[:, sl] if torch.is_tensor(t) and t.dim() >= 3 and t.shape[1] == 8 else t)
+                 for n, t in out.items()}, ref, f"h{h} ")

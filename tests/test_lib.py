@@ -48,6 +48,18 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     # tangent states without the key operand tiles
     assert lib.sla2h_linear_states(1, 1, 1, 1, 1, 1, 1, 128, 64, 64, 2, 1, 1, 1, 1,
                                    None, None, None, None, 1, None, None) == bad
+    # training forward: q, k, v, dtype, B, H, L, D, E, q8, qs, k8, ks, v8f, vs, stream
+    assert lib.sla2h_quant_train(1, 1, 1, 1, 1, 30000, 128, 64, 64, 1, 1, 1, 1, 1, 1, None) == bad
+    assert lib.sla2h_quant_train(1, 1, None, 1, 1, 1, 128, 64, 64, 1, 1, 1, 1, 1, 1, None) == bad
+    # q, q8, qs, k8, ks, v8f, vs, lut, dtype, B, H, L, D, E, Np, T, scale, o_s, lse, qphi
+    assert lib.sla2h_sparse_fwd_qat(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 128, 64, 64, 2, 3, 0.125,
+                                    1, 1, 1, None) == bad                   # T > Np
+    assert lib.sla2h_sparse_fwd_qat(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 100000, 64, 64, 1, 1,
+                                    0.125, 1, 1, 1, None) == bad            # tail > 1024 tiles
+    assert lib.sla2h_linear_states_qat(1, 1, 1, 1, 1, 128, 64, 64, 1, 1, None, 1, None) == bad
+    # qphi, comp, Hall, o_s, alpha, alpha_stride, dtype, B, H, L, D, E, eps, o, o_l, den
+    assert lib.sla2h_linear_mix_qat(1, 1, 1, 1, 1, -1, 1, 1, 1, 128, 64, 64, 1e-5, 1, 1, 1,
+                                    None) == bad
 
 
 def test_ops_refuse_cpu_tensors():
