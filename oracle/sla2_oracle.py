@@ -480,3 +480,148 @@ def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L
     o = _round16(_round16(a * o_s16, t16) + _round16(_round16(1.0 - a, t16) * o_l16, t16), t16)
     return {"o": o, "o_s": o_s16, "o_l": o_l16, "lse": lse, "qphi": qphi, "den": den,
             "htot": htot, "ztot": ztot}
+
+
+def train_bwd(q, k, v, alpha, lut, Np, prefix_len, fwd, do, t16=torch.bfloat16):
+    """Training backward (straight-through estimator), blockwise, CPU.
+
+    Restates _CubeQATFunction.backward (models/sla2_cube_qat.py:753-832) and its
+    kernels: _bwd_split_kernel (:838-872), _attn_bwd_preprocess / _attn_bwd_dq
+    (models/sla2_vendor/sla_kernel.py:89-184), _sparse_bwd_dkdv_lut
+    (models/sla2_cube_qat.py:986-1042), _lin_bwd_dq
+    (models/sla2_vendor/kernel_linear.py:85-138), _lin_bwd_dkdv_lut
+    (models/sla2_cube_qat.py:1045-1104), _phi_chain_add_kernel (:875-904).
+
+    The sparse branch is re-differentiated with the UNQUANTISED q, k, v in
+    16-bit, p = exp2(min(q.k * scale*log2e - lse, 4)) with the INT8 forward's
+    lse, delta = rowsum(o_s * do_s); 16-bit rounding of ds, p (for dv), the
+    stored dq_s/dk_s/dv_s; saturation at +-60000 where the reference clamps.
+    fwd: the train_fwd dict (o_s, o_l, lse, den, qphi, htot, ztot); do (B,H,L,D)
+    the output gradient; alpha (H, Mb) after the sigmoid.
+    t16=None: exact mode (float64, no rounding, no clamps), in which the result
+    is the exact gradient of the op whose forward quantities fwd holds.
+    Returns dict dq, dk, dv (B,H,L,D), d_alpha (H, Mb; the gradient with respect
+    to the alpha LOGITS) and the intermediates dq_s, dk_s, dv_s, dqphi, dkphi,
+    dv_l, delta.  LUT rows are assumed free of duplicates (top-k rows are).
+    """
+    exact = t16 is None
+    dt = torch.float64 if exact else torch.float32
+    r16 = (lambda x: x) if exact else (lambda x: x.to(t16).to(dt))
+    sat = (lambda x: x) if exact else (lambda x: x.clamp(-60000.0, 60000.0))
+    B, H, L, D = q.shape
+    nb = -(-L // E)
+    Mb = nb
+    n_tail = nb - Np
+    lut = torch.as_tensor(np.asarray(lut)).long()
+    tails = torch.arange(Np, Np + n_tail).view(1, 1, 1, -1).expand(B, H, Mb, n_tail)
+    lut_aug = torch.cat([lut, tails], -1)
+    J = lut_aug.shape[-1]
+    cv = lambda x: torch.as_tensor(x).to(dt)
+    q, k, v, do = cv(q), cv(k), cv(v), cv(do)
+    o_s, o_l, lse, den, qphi = (cv(fwd[n]) for n in ("o_s", "o_l", "lse", "den", "qphi"))
+    htot, ztot = cv(fwd["htot"]), cv(fwd["ztot"])
+    a_blk = cv(alpha)                                          # (H, Mb)
+    rows = torch.arange(nb * E)
+    a_rows = a_blk[:, (rows[:L] // E)].view(1, H, L, 1)
+    do_s, do_l = r16(do * a_rows), r16(do * (1.0 - a_rows))
+    segr = (do * (o_s - o_l)).sum(-1)                          # (B,H,L)
+    seg = _tiles(segr[..., None], nb).sum((-2, -1)).sum(0)     # (H, Mb)
+    d_alpha = seg * a_blk * (1.0 - a_blk)
+    delta = (o_s * do_s).sum(-1)
+    scale = D ** -0.5
+    c = scale * LOG2E if exact else float(np.float32(scale * LOG2E))
+    qt, kt, vt, dost = (_tiles(x, nb) for x in (q, k, v, do_s))
+    pad1 = lambda x, val: torch.cat([x, x.new_full((B, H, nb * E - L), val)], -1).view(B, H, nb, E)
+    lse_t, delta_t = pad1(lse, math.inf), pad1(delta, 0.0)
+    key_rows = rows.view(nb, E)
+    dq_acc = torch.zeros(B, H, Mb, E, D, dtype=dt)
+    dk_acc = torch.zeros(B, H, nb, E, D, dtype=dt)
+    dv_acc = torch.zeros(B, H, nb, E, D, dtype=dt)
+    ix = lambda n: n.view(B, H, Mb, 1, 1).expand(B, H, Mb, E, D)
+    for j in range(J):
+        n = lut_aug[..., j]
+        kn, vn = _gather_tiles(kt, n), _gather_tiles(vt, n)
+        x = (qt @ kn.transpose(-1, -2)) * c - lse_t[..., None]
+        p = torch.exp2(x if exact else torch.clamp(x, max=4.0))
+        p = p.masked_fill(~(key_rows[n] < L)[..., None, :], 0.0)
+        dp = dost @ vn.transpose(-1, -2)
+        ds16 = r16(sat(p * (dp - delta_t[..., None])))
+        dq_acc += ds16 @ kn
+        dk_acc.scatter_add_(2, ix(n), ds16.transpose(-1, -2) @ qt)
+        dv_acc.scatter_add_(2, ix(n), r16(p).transpose(-1, -2) @ dost)
+    untile = lambda x: x.reshape(B, H, nb * E, -1)[:, :, :L]
+    dq_s = r16(untile(dq_acc) * scale)
+    dk_s = r16(untile(dk_acc) * scale)
+    dv_s = r16(untile(dv_acc))
+
+    # linear branch
+    g = do_l / den[..., None]
+    s = (do_l * o_l).sum(-1) / den
+    dhtot = qphi.transpose(-1, -2) @ g                         # (B,H,D,D)
+    dztot = -(qphi * s[..., None]).sum(-2)                     # (B,H,D)
+    kphi = torch.softmax(k, -1) if exact else r16(torch.softmax(k.float(), -1).to(dt))
+    kpt, vvt = _tiles(kphi, nb), _tiles(v, nb)
+    hi = htot[:, :, None].expand(B, H, Mb, D, D).clone()
+    zi = ztot[:, :, None].expand(B, H, Mb, D).clone()
+    for j in range(J):
+        n = lut_aug[..., j]
+        kp, vv = _gather_tiles(kpt, n), _gather_tiles(vvt, n)
+        hi -= kp.transpose(-1, -2) @ vv
+        zi -= kp.sum(-2)
+    g16 = r16(sat(g))
+    g16t, st, qpt = _tiles(g16, nb), pad1(s, 0.0), _tiles(qphi, nb)
+    dqphi = g16t @ r16(hi).transpose(-1, -2) - st[..., None] * zi[..., None, :]
+    dqphi = untile(dqphi)
+    pm = qpt.transpose(-1, -2) @ g16t                          # (B,H,Mb,D,D)
+    pz = (qpt * st[..., None]).sum(-2)                         # (B,H,Mb,D)
+    dh = dhtot[:, :, None].expand(B, H, nb, D, D).clone()
+    dz = dztot[:, :, None].expand(B, H, nb, D).clone()
+    for j in range(J):
+        n = lut_aug[..., j]
+        dh.scatter_add_(2, ix(n)[..., :D, :], -pm)
+        dz.scatter_add_(2, n.view(B, H, Mb, 1).expand(B, H, Mb, D), pz)
+    dh16 = r16(sat(dh))
+    dkphi = untile(vvt @ dh16.transpose(-1, -2) + dz[..., None, :])
+    dv_l = untile(kpt @ dh16)
+
+    chain = lambda phi, dphi: phi * (dphi - (phi * dphi).sum(-1, keepdim=True))
+    dq = r16(sat(dq_s + chain(qphi, dqphi)))
+    dk = r16(sat(dk_s + chain(kphi, dkphi)))
+    dv = r16(sat(dv_s + dv_l))
+    return {"dq": dq, "dk": dk, "dv": dv, "d_alpha": d_alpha, "dq_s": dq_s, "dk_s": dk_s,
+            "dv_s": dv_s, "dqphi": dqphi, "dkphi": dkphi, "dv_l": dv_l, "delta": delta}
+
+
+def train_dense_f64(q, k, v, alpha_logit, lut, Np, prefix_len, eps=EPS_L):
+    """Differentiable float64 restatement of the training op WITHOUT quantisation
+    (the straight-through view): masked softmax over the augmented-LUT tiles,
+    complement linear attention over the other video tiles, sigmoid mix.
+
+    Returns (o, fwd) where fwd holds the forward quantities train_bwd consumes
+    (o_s, o_l, lse in log2, den, qphi, htot, ztot), detached.  Dense O(L^2):
+    tiny inputs only.
+    """
+    B, H, L, D = q.shape
+    nb = -(-L // E)
+    n_tail = nb - Np
+    lut = torch.as_tensor(np.asarray(lut)).long()
+    tails = torch.arange(Np, Np + n_tail).view(1, 1, 1, -1).expand(B, H, nb, n_tail)
+    lut_aug = torch.cat([lut, tails], -1)
+    sel = torch.zeros(B, H, nb, nb, dtype=torch.bool)
+    sel.scatter_(3, lut_aug, True)
+    blk = torch.arange(L) // E
+    allowed = sel[:, :, blk][:, :, :, blk]                     # (B,H,L,L)
+    s = (q @ k.transpose(-1, -2)) * D ** -0.5
+    s = s.masked_fill(~allowed, -math.inf)
+    o_s = torch.softmax(s, -1) @ v
+    lse = torch.logsumexp(s, -1) * LOG2E
+    qphi, kphi = torch.softmax(q, -1), torch.softmax(k, -1)
+    w = (qphi @ kphi.transpose(-1, -2)) * (~allowed)
+    den0 = w.sum(-1)
+    den = torch.where(den0 >= 0, den0 + eps, den0 - eps)
+    o_l = (w @ v) / den[..., None]
+    a = torch.sigmoid(alpha_logit)[:, blk].view(1, H, L, 1)
+    o = a * o_s + (1 - a) * o_l
+    fwd = {"o_s": o_s, "o_l": o_l, "lse": lse, "den": den, "qphi": qphi,
+           "htot": kphi.transpose(-1, -2) @ v, "ztot": kphi.sum(-2)}
+    return o, {n: t.detach() for n, t in fwd.items()}

@@ -328,3 +328,59 @@ def test_train_fwd_linear_branch_and_mix_endpoints():
     rb = O.train_fwd(q, k, v, alpha, lut, Np, P, t16=torch.bfloat16)
     rf = O.train_fwd(q, k, v, alpha, lut, Np, P, t16=torch.float32)
     assert rel_l2(rb["o"], rf["o"]) < 1e-2
+
+
+def _bwd_case(seed, B=1, H=2, Np=3, P=10, T=2, dtype=torch.float64):
+    g = torch.Generator().manual_seed(seed)
+    L = Np * 64 + P
+    nb = -(-L // 64)
+    q, k, v, do = (torch.randn(B, H, L, 64, generator=g, dtype=torch.float64) for _ in range(4))
+    q, k = q * 1.5, k * 1.5
+    logit = torch.randn(H, nb, generator=g, dtype=torch.float64)
+    lut = torch.stack([torch.randperm(Np, generator=g)[:T] for _ in range(B * H * nb)])
+    lut = lut.view(B, H, nb, T).int().numpy()
+    return q, k, v, do, logit, lut, Np, P
+
+
+def test_train_bwd_exact_mode_is_the_autograd_gradient():
+    # exact mode of the STE backward, fed the exact forward quantities, must be
+    # the float64 autograd gradient of the unquantised op: pins every sign,
+    # index and transpose of the sparse, linear, mix and phi-chain terms
+    for seed in (0, 1):
+        q, k, v, do, logit, lut, Np, P = _bwd_case(seed)
+        xs = [t.clone().requires_grad_() for t in (q, k, v, logit)]
+        o, fwd = O.train_dense_f64(*xs[:3], xs[3], lut, Np, P)
+        want = torch.autograd.grad((o * do).sum(), xs)
+        got = O.train_bwd(q, k, v, torch.sigmoid(logit), lut, Np, P, fwd, do, t16=None)
+        for name, w in zip(("dq", "dk", "dv", "d_alpha"), want):
+            err = ((got[name] - w).norm() / w.norm()).item()
+            assert err < 1e-10, (seed, name, err)
+
+
+def test_train_bwd_exact_mode_detects_a_planted_error():
+    q, k, v, do, logit, lut, Np, P = _bwd_case(2)
+    xs = [t.clone().requires_grad_() for t in (q, k, v, logit)]
+    o, fwd = O.train_dense_f64(*xs[:3], xs[3], lut, Np, P)
+    want = torch.autograd.grad((o * do).sum(), xs)
+    bad = dict(fwd, ztot=fwd["ztot"] * 1.001)   # a perturbed linear-branch global
+    got = O.train_bwd(q, k, v, torch.sigmoid(logit), lut, Np, P, bad, do, t16=None)
+    err = ((got["dq"] - want[0]).norm() / want[0].norm()).item()
+    assert err > 1e-6
+
+
+def test_train_bwd_rounded_mode_near_exact_gradient():
+    # 16-bit inputs, INT8 forward, 16-bit roundings and the STE: close to the
+    # exact gradient of the unquantised op, at the INT8 level
+    q, k, v, do, logit, lut, Np, P = _bwd_case(3)
+    q16, k16, v16 = (t.to(torch.bfloat16).double() for t in (q, k, v))
+    do16 = (do * 0.1).to(torch.bfloat16).double()
+    xs = [t.clone().requires_grad_() for t in (q16, k16, v16, logit)]
+    o, _ = O.train_dense_f64(*xs[:3], xs[3], lut, Np, P)
+    want = torch.autograd.grad((o * do16).sum(), xs)
+    a = torch.sigmoid(logit).float()
+    f = [t.float() for t in (q16, k16, v16)]
+    fwd = O.train_fwd(*f, a, lut, Np, P)
+    got = O.train_bwd(*f, a, lut, Np, P, fwd, do16.float(), t16=torch.bfloat16)
+    for name, w in zip(("dq", "dk", "dv", "d_alpha"), want):
+        err = ((got[name].double() - w).norm() / w.norm()).item()
+        assert err < 5e-2, (name, err)
