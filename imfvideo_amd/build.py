@@ -24,6 +24,7 @@ SOURCES = {
     # accumulators in VGPR-form MFMA: no AGPR round trips across the key loop
     "attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "attn_train.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "attn_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
 }
 
 COMMON_FLAGS = [

@@ -1,0 +1,807 @@
+// Backward of the SLA2 cube attention's training forward through the
+// straight-through estimator, gfx950 (_CubeQATFunction.backward,
+// models/sla2_cube_qat.py:753-832):
+//   sparse branch  re-differentiated in 16-bit from the UNQUANTISED q, k, v:
+//                  p = exp2(min(q.k scale log2e - lse, 4)) with the INT8
+//                  forward's lse, ds = p (do_s . v - delta), saturated at
+//                  +-60000 and rounded to 16 bits before the dq / dk products,
+//                  p rounded to 16 bits for dv (sla_kernel.py:117-184,
+//                  models/sla2_cube_qat.py:986-1042);
+//   linear branch  dqphi = g16 H16^T - s z^T per query block
+//                  (kernel_linear.py:85-138), dh = complement sum of
+//                  qphi^T g over the query blocks NOT routing a tile, then
+//                  dkphi = v dh16^T + dz, dv_l = kphi dh16
+//                  (models/sla2_cube_qat.py:1045-1104);
+//   phi chains     dx = x_s + phi (dphi - <phi, dphi>), saturated
+//                  (models/sla2_cube_qat.py:875-904).
+//
+// Kernels: bwd_prep (per 64-row block: gradient split, delta, g, s, the alpha
+// segment sums, the per-block partial states P = qphi^T g and Pz = qphi^T s,
+// and the transposed operand fragments of q, k and do_s), then the dq kernel
+// (per query block, key-split waves) and the dk/dv kernel (per key tile,
+// query-split waves).  The complement GEMM of the partial states lives with
+// the forward's complement (states.hip).
+//
+// Transposed operand fragments (16-bit, per 64-row block, 8 KB):
+//   tf[ct][p][lane][s] = X[16 (2p + (s>>2)) + 4g + (s&3)][16 ct + r],
+//   lane = 16 g + r; rows past L are zero.  A wave that owns rows
+//   16w..16w+15 reads the 8-byte half s = 4 (w&1) .. 4 (w&1) + 3 of chunk
+//   (ct, p = w>>1): the A operand of a 16x16x16 MFMA that contracts over those
+//   16 rows.
+#include "common.h"
+
+#include <climits>
+
+namespace sla2h {
+
+namespace {
+
+constexpr int kT = 64;
+constexpr int kMaxJ = 1024;
+constexpr int kRecH = 0, kRecZ = 32768, kRecBytes = 33280;
+constexpr float kSat = 60000.f;
+
+__device__ inline float sat(float x) { return fminf(fmaxf(x, -kSat), kSat); }
+
+__device__ inline f32x4 mfma_f32_16x16x4(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+template <typename T16>
+__device__ inline float r16(float x) {
+  return T16::to_f32(T16::from_f32(x));
+}
+
+template <typename T16>
+__device__ inline u32x2 pack4(float a, float b, float c, float d) {
+  return u32x2{pack_pair<T16>(a, b), pack_pair<T16>(c, d)};
+}
+
+// ---------------------------------------------------------------------------
+// bwd_prep: one 64-row block b of one (b, h) per workgroup.
+// ---------------------------------------------------------------------------
+struct PrepArgs {
+  const uint16_t* dout;
+  const uint16_t* o_s;
+  const uint16_t* o_l;
+  const float* den;
+  const uint16_t* qphi;
+  const uint16_t* q;
+  const uint16_t* k;
+  const float* alpha;
+  uint16_t* dos;
+  float* delta;
+  uint16_t* g16;
+  float* s;
+  float* seg;
+  float* P;
+  float* Pz;
+  uint16_t* qtf;
+  uint16_t* ktf;
+  uint16_t* dotf;
+  int64_t L;
+  int Nb, H, alpha_stride;
+};
+
+template <typename T16>
+__global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
+  __shared__ float qps[kT][kT + 1];  // qphi [row][d]
+  __shared__ float gs[kT][kT + 1];   // saturated g [row][e]
+  __shared__ float ss[kT];
+  __shared__ __align__(16) uint16_t xs[3][kT][kT + 8];  // q, k, do_s rows
+  __shared__ float red[4];
+
+  const int blk = blockIdx.x, bh = blockIdx.y, h = bh % a.H;
+  const int tid = threadIdx.x, r = tid >> 2, c0 = (tid & 3) * 16;
+  const int64_t row = (int64_t)blk * kT + r;
+  const bool valid = row < a.L;
+  const int64_t off = ((int64_t)bh * a.L + row) * kT + c0;
+
+  auto ld = [&](const uint16_t* src, uint16_t* x) {
+    if (valid) {
+      const uint4* p = reinterpret_cast<const uint4*>(src + off);
+      const uint4 u0 = p[0], u1 = p[1];
+      const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+      for (int i = 0; i < 8; ++i) {
+        x[2 * i] = (uint16_t)(w[i] & 0xffff);
+        x[2 * i + 1] = (uint16_t)(w[i] >> 16);
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 16; ++i) x[i] = 0;
+    }
+  };
+  auto st16 = [&](uint16_t* dst, const uint16_t* x) {
+    uint32_t w[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) w[i] = pack2(x[2 * i], x[2 * i + 1]);
+    uint4* p = reinterpret_cast<uint4*>(dst + off);
+    p[0] = make_uint4(w[0], w[1], w[2], w[3]);
+    p[1] = make_uint4(w[4], w[5], w[6], w[7]);
+  };
+
+  uint16_t dob[16], osb[16], olb[16], qpb[16], xb[16], g16b[16], dsb[16];
+  ld(a.dout, dob);
+  ld(a.o_s, osb);
+  ld(a.o_l, olb);
+  ld(a.qphi, qpb);
+  const float al = a.alpha[(int64_t)h * a.alpha_stride + blk];
+  const float den = valid ? a.den[(int64_t)bh * a.L + row] : 1.f;
+  float dsum = 0.f, segp = 0.f, ssum = 0.f;
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const float d = T16::to_f32(dob[i]);
+    const float os = T16::to_f32(osb[i]), ol = T16::to_f32(olb[i]);
+    dsb[i] = T16::from_f32(d * al);
+    const float dl = r16<T16>(d * (1.f - al));
+    dsum += os * T16::to_f32(dsb[i]);
+    segp += d * (os - ol);
+    ssum += dl * ol;
+    const float g = sat(dl / den);
+    gs[r][c0 + i] = g;
+    g16b[i] = T16::from_f32(g);
+    qps[r][c0 + i] = T16::to_f32(qpb[i]);
+    xs[2][r][c0 + i] = dsb[i];
+  }
+  dsum += __shfl_xor(dsum, 1, 64);
+  dsum += __shfl_xor(dsum, 2, 64);
+  ssum += __shfl_xor(ssum, 1, 64);
+  ssum += __shfl_xor(ssum, 2, 64);
+  const float srow = valid ? ssum / den : 0.f;
+  if ((tid & 3) == 0) ss[r] = srow;
+  if (valid) {
+    st16(a.dos, dsb);
+    st16(a.g16, g16b);
+    if ((tid & 3) == 0) {
+      a.delta[(int64_t)bh * a.L + row] = dsum;
+      a.s[(int64_t)bh * a.L + row] = srow;
+    }
+  }
+  ld(a.q, xb);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) xs[0][r][c0 + i] = xb[i];
+  ld(a.k, xb);
+#pragma unroll
+  for (int i = 0; i < 16; ++i) xs[1][r][c0 + i] = xb[i];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) segp += __shfl_xor(segp, m, 64);
+  if ((tid & 63) == 0) red[tid >> 6] = segp;
+  __syncthreads();
+  if (tid == 0) atomicAdd(a.seg + (int64_t)h * a.Nb + blk, (red[0] + red[1]) + (red[2] + red[3]));
+
+  // P[d][e] = sum_rows qphi[row][d] g[row][e] on fp32 MFMA: wave w owns d rows 16w..16w+15
+  {
+    const int w = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
+    f32x4 acc[4];
+#pragma unroll
+    for (int et = 0; et < 4; ++et) acc[et] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll 4
+    for (int kk = 0; kk < 16; ++kk) {
+      const int rw = 4 * kk + lg;
+      const float av = qps[rw][16 * w + lr];
+#pragma unroll
+      for (int et = 0; et < 4; ++et) acc[et] = mfma_f32_16x16x4(av, gs[rw][16 * et + lr], acc[et]);
+    }
+    float* P = a.P + ((int64_t)bh * a.Nb + blk) * (kT * kT);
+#pragma unroll
+    for (int et = 0; et < 4; ++et)
+#pragma unroll
+      for (int i = 0; i < 4; ++i) P[(16 * w + 4 * lg + i) * kT + 16 * et + lr] = acc[et][i];
+  }
+  if (tid < kT) {
+    float z = 0.f;
+    for (int rw = 0; rw < kT; ++rw) z += qps[rw][tid] * ss[rw];
+    a.Pz[((int64_t)bh * a.Nb + blk) * kT + tid] = z;
+  }
+
+  // transposed operand fragments of q, k, do_s
+  uint16_t* tfs[3] = {a.qtf, a.ktf, a.dotf};
+#pragma unroll
+  for (int x = 0; x < 3; ++x) {
+#pragma unroll
+    for (int half = 0; half < 2; ++half) {
+      const int cc = tid + 256 * half;
+      const int ct = cc >> 7, p = (cc >> 6) & 1, lane = cc & 63, gg = lane >> 4, rr = lane & 15;
+      uint16_t v[8];
+#pragma unroll
+      for (int s8 = 0; s8 < 8; ++s8) v[s8] = xs[x][16 * (2 * p + (s8 >> 2)) + 4 * gg + (s8 & 3)][16 * ct + rr];
+      *reinterpret_cast<uint4*>(tfs[x] + ((int64_t)bh * a.Nb + blk) * 4096 + cc * 8) =
+          make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dq: one 64-row query block per workgroup; wave w owns keys 16w..16w+15 of
+// every tile of the augmented LUT and all 64 queries.  Per tile and query
+// group qb: S^T = K Q^T and dP^T = V do_s^T (16-bit MFMA, lane (g, r) holds
+// keys 16w+4g+i of query 16qb+r), ds, then dq^T += K^T ds^T over the wave's 16
+// keys.  The four key-split partials are summed through LDS, then wave w
+// finishes queries 16w..16w+15: dq_s, the linear dqphi from the forward's
+// complement record, and the phi chain.
+// ---------------------------------------------------------------------------
+struct DqArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* dos;
+  const uint16_t* ktf;
+  const uint16_t* g16;
+  const uint16_t* qphi;
+  const float* lse;
+  const float* delta;
+  const float* s;
+  const float* Hall;
+  const unsigned char* comp;
+  const int32_t* lut;
+  uint16_t* dq;
+  int64_t L;
+  int Nb, J, nwork, per_xcd;
+  float c, scale;
+};
+
+template <typename T16>
+__global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
+  __shared__ int tiles[kMaxJ];
+  __shared__ __align__(16) f32x4 mb[2][4][2][4][64];  // [round-robin][src wave][qb sel][ct][lane]
+
+  const int logical = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
+  if (logical >= a.nwork) return;
+  const int bh = __builtin_amdgcn_readfirstlane(logical / a.Nb);
+  const int m = __builtin_amdgcn_readfirstlane(logical - bh * a.Nb);
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, r = l & 15, g = l >> 4;
+  const int64_t L = a.L;
+  const int64_t base = (int64_t)bh * L;
+
+  const int32_t* lrow = a.lut + ((int64_t)bh * a.Nb + m) * a.J;
+  for (int j = tid; j < a.J; j += 256) {
+    const int n = lrow[j];
+    tiles[j] = n < 0 ? 0 : (n >= a.Nb ? a.Nb - 1 : n);
+  }
+
+  // resident B operands: Q and do_s rows 16qb + r, channels 32ks + 8g .. +7
+  u32x4 qf[4][2], df[4][2];
+  float lse_r[4], del_r[4];
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) {
+    const int64_t row = (int64_t)m * kT + 16 * qb + r;
+    const bool ok = row < L;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      qf[qb][ks] = ok ? *reinterpret_cast<const u32x4*>(a.q + (base + row) * kT + 32 * ks + 8 * g)
+                      : u32x4{0, 0, 0, 0};
+      df[qb][ks] = ok ? *reinterpret_cast<const u32x4*>(a.dos + (base + row) * kT + 32 * ks + 8 * g)
+                      : u32x4{0, 0, 0, 0};
+    }
+    lse_r[qb] = ok ? a.lse[base + row] : INFINITY;
+    del_r[qb] = ok ? a.delta[base + row] : 0.f;
+  }
+  __syncthreads();
+
+  const auto rk = make_rsrc(a.k + base * kT, L * kT * 2);  // key rows past L read as 0
+  const auto rv = make_rsrc(a.v + base * kT, L * kT * 2);
+  const int rowoff = ((16 * w + r) * kT + 8 * g) * 2;
+  const int tfoff = (((w >> 1) * 64 + l) * 8 + 4 * (w & 1)) * 2;  // + ct * 2048 B
+  const unsigned char* ktf = reinterpret_cast<const unsigned char*>(a.ktf) + (int64_t)bh * a.Nb * 8192;
+
+  struct Frags {
+    u32x4 k[2], v[2];
+    u32x2 kt[4];
+  };
+  auto load = [&](int j, Frags& f) {
+    const int n = __builtin_amdgcn_readfirstlane(tiles[j]);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {  // tile offset in voffset: range-checked, rows past L read 0
+      f.k[ks] = buf_load16(rk, n * kT * kT * 2 + rowoff + 64 * ks, 0);
+      f.v[ks] = buf_load16(rv, n * kT * kT * 2 + rowoff + 64 * ks, 0);
+    }
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+      f.kt[ct] = *reinterpret_cast<const u32x2*>(ktf + (int64_t)n * 8192 + ct * 2048 + tfoff);
+  };
+
+  f32x4 acc[4][4];
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb)
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) acc[qb][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  auto tile = [&](const Frags& f, int j) {
+    const int n = __builtin_amdgcn_readfirstlane(tiles[j]);
+    const int64_t key0 = (int64_t)n * kT + 16 * w + 4 * g;
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb) {
+      f32x4 sc = mfma_16x16x32<T16>(f.k[0], qf[qb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+      sc = mfma_16x16x32<T16>(f.k[1], qf[qb][1], sc);
+      f32x4 dp = mfma_16x16x32<T16>(f.v[0], df[qb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+      dp = mfma_16x16x32<T16>(f.v[1], df[qb][1], dp);
+      float ds[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float p = fast_exp2(fminf(sc[i] * a.c - lse_r[qb], 4.f));
+        if (key0 + i >= L) p = 0.f;
+        ds[i] = sat(p * (dp[i] - del_r[qb]));
+      }
+      const u32x2 dsp = pack4<T16>(ds[0], ds[1], ds[2], ds[3]);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) acc[qb][ct] = mfma_16x16x16<T16>(f.kt[ct], dsp, acc[qb][ct]);
+    }
+  };
+
+  const int J = a.J;
+  Frags fa, fb;
+  load(0, fa);
+  int j = 0;
+  for (; j + 1 < J; j += 2) {
+    load(j + 1, fb);
+    tile(fa, j);
+    load(j + 2 < J ? j + 2 : J - 1, fa);
+    tile(fb, j + 1);
+  }
+  if (j < J) tile(fa, j);
+
+  // sum the key-split partials: round t moves query groups 2t, 2t+1
+  f32x4 tot[4];
+#pragma unroll
+  for (int t = 0; t < 2; ++t) {
+#pragma unroll
+    for (int qs = 0; qs < 2; ++qs)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) mb[t][w][qs][ct][l] = acc[2 * t + qs][ct];
+  }
+  __syncthreads();
+  {
+    const int t = w >> 1, qs = w & 1;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+      tot[ct] = (mb[t][0][qs][ct][l] + mb[t][1][qs][ct][l]) + (mb[t][2][qs][ct][l] + mb[t][3][qs][ct][l]);
+  }
+
+  // epilogue: query row 64m + 16w + r, channels 16ct + 4g + i
+  const int64_t row = (int64_t)m * kT + 16 * w + r;
+  const bool ok = row < L;
+  const unsigned char* rec = a.comp + ((int64_t)bh * a.Nb + m) * kRecBytes;
+  const float* Hc = reinterpret_cast<const float*>(rec + kRecH);
+  const float* zc = reinterpret_cast<const float*>(rec + kRecZ);
+  const float* Ha = a.Hall + (int64_t)bh * kT * kT;
+  u32x4 gb[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+    gb[ks] = ok ? *reinterpret_cast<const u32x4*>(a.g16 + (base + row) * kT + 32 * ks + 8 * g)
+                : u32x4{0, 0, 0, 0};
+  const float srow = ok ? a.s[base + row] : 0.f;
+  float dqphi[4][4], qp[4][4];
+  float dot = 0.f;
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      // A: H16[d = 16ct + r][e = 32ks + 8g .. +7] = round16(Hc + (round16(Hall) - Hall))
+      const int e0 = (16 * ct + r) * kT + 32 * ks + 8 * g;
+      const f32x4 h0 = *reinterpret_cast<const f32x4*>(Hc + e0);
+      const f32x4 h1 = *reinterpret_cast<const f32x4*>(Hc + e0 + 4);
+      const f32x4 t0 = *reinterpret_cast<const f32x4*>(Ha + e0);
+      const f32x4 t1 = *reinterpret_cast<const f32x4*>(Ha + e0 + 4);
+      float hv[8];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        hv[i] = h0[i] + (r16<T16>(t0[i]) - t0[i]);
+        hv[4 + i] = h1[i] + (r16<T16>(t1[i]) - t1[i]);
+      }
+      const u32x4 av = u32x4{pack_pair<T16>(hv[0], hv[1]), pack_pair<T16>(hv[2], hv[3]),
+                             pack_pair<T16>(hv[4], hv[5]), pack_pair<T16>(hv[6], hv[7])};
+      num = mfma_16x16x32<T16>(av, gb[ks], num);
+    }
+    const f32x4 z = *reinterpret_cast<const f32x4*>(zc + 16 * ct + 4 * g);
+    const uint2 qv = ok ? *reinterpret_cast<const uint2*>(a.qphi + (base + row) * kT + 16 * ct + 4 * g)
+                        : make_uint2(0, 0);
+    const uint32_t qw[2] = {qv.x, qv.y};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      dqphi[ct][i] = num[i] - srow * z[i];
+      qp[ct][i] = T16::to_f32((uint16_t)(qw[i >> 1] >> (16 * (i & 1))));
+      dot += qp[ct][i] * dqphi[ct][i];
+    }
+  }
+  dot = sum_over_groups(dot);
+  if (ok) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      float o[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float dqs = r16<T16>(tot[ct][i] * a.scale);
+        o[i] = sat(dqs + qp[ct][i] * (dqphi[ct][i] - dot));
+      }
+      const u32x2 pk = pack4<T16>(o[0], o[1], o[2], o[3]);
+      *reinterpret_cast<u32x2*>(a.dq + (base + row) * kT + 16 * ct + 4 * g) = pk;
+    }
+  }
+}
+
+// ---------------------------------------------------------------------------
+// dk, dv: one key tile per workgroup; wave w owns queries 16w..16w+15 of each
+// query block that routes the tile (ascending block order), all 64 keys.  K
+// and V rows sit in LDS.  Per block and key group kb: S^T = Q K^T and
+// dP = do_s V^T (lane (g, r) holds queries 16w+4g+i of key 16kb+r), p and
+// ds, then dv^T += do_s^T p and dk^T += Q^T ds over the wave's 16 queries.
+// The query-split partials are summed through LDS; wave w finishes keys
+// 16w..16w+15: dk_s, dv_s, the linear dkphi / dv_l from the backward
+// complement record, and the phi chain of K.
+// ---------------------------------------------------------------------------
+struct DkdvArgs {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* v;
+  const uint16_t* dos;
+  const uint16_t* qtf;
+  const uint16_t* dotf;
+  const float* lse;
+  const float* delta;
+  const uint32_t* sel;
+  const unsigned char* compb;
+  uint16_t* dk;
+  uint16_t* dv;
+  int64_t L;
+  int Nb, NCq, nwork, per_xcd;
+  float c, scale;
+};
+
+template <typename T16>
+__global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
+  __shared__ __align__(16) uint16_t kv[2][kT][kT + 8];   // K, V rows of the tile
+  __shared__ __align__(16) uint16_t dhs[2][kT][kT + 8];  // dh16 [d][e], dh16^T [e][d]
+  __shared__ __align__(16) f32x4 mb[4][2][4][64];        // [src wave][kb sel][ct][lane]
+  __shared__ float dzs[kT];
+
+  const int logical = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
+  if (logical >= a.nwork) return;
+  const int bh = __builtin_amdgcn_readfirstlane(logical / a.Nb);
+  const int n = __builtin_amdgcn_readfirstlane(logical - bh * a.Nb);
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, r = l & 15, g = l >> 4;
+  const int64_t L = a.L;
+  const int64_t base = (int64_t)bh * L;
+
+  {  // stage K, V rows (zero past L) and the complement state dh (saturated, 16-bit)
+    const int rr = tid >> 2, c0 = (tid & 3) * 16;
+    const int64_t row = (int64_t)n * kT + rr;
+    const bool ok = row < L;
+#pragma unroll
+    for (int x = 0; x < 2; ++x) {
+      const uint16_t* src = (x == 0 ? a.k : a.v) + (base + row) * kT + c0;
+      uint4 u0 = make_uint4(0, 0, 0, 0), u1 = u0;
+      if (ok) {
+        u0 = reinterpret_cast<const uint4*>(src)[0];
+        u1 = reinterpret_cast<const uint4*>(src)[1];
+      }
+      *reinterpret_cast<uint4*>(&kv[x][rr][c0]) = u0;
+      *reinterpret_cast<uint4*>(&kv[x][rr][c0 + 8]) = u1;
+    }
+    const unsigned char* rec = a.compb + ((int64_t)bh * a.Nb + n) * kRecBytes;
+    const f32x4* hr = reinterpret_cast<const f32x4*>(rec + kRecH) + (rr * kT + c0) / 4;
+#pragma unroll
+    for (int cq = 0; cq < 4; ++cq) {
+      const f32x4 x = hr[cq];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const uint16_t hb = T16::from_f32(sat(x[i]));
+        dhs[0][rr][c0 + 4 * cq + i] = hb;
+        dhs[1][c0 + 4 * cq + i][rr] = hb;
+      }
+    }
+    if (tid < kT) dzs[tid] = -reinterpret_cast<const float*>(rec + kRecZ)[tid];
+  }
+  __syncthreads();
+
+  f32x4 dkT[4][4], dvT[4][4];  // [ct][kb]
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) dkT[ct][kb] = dvT[ct][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+  const uint32_t* selrow = a.sel + ((int64_t)bh * a.Nb + n) * a.NCq;
+  const int tfoff = (((w >> 1) * 64 + l) * 8 + 4 * (w & 1));  // 16-bit elements, + ct * 1024
+  const int64_t keyb = (int64_t)n * kT;
+
+  for (int kc = 0; kc < a.NCq; ++kc) {
+    uint32_t bits = __builtin_amdgcn_readfirstlane(selrow[kc]);
+    while (bits) {
+      const int m = 32 * kc + __builtin_ctz(bits);
+      bits &= bits - 1u;
+      const int64_t row = (int64_t)m * kT + 16 * w + r;  // A-operand row of this lane
+      const bool ok = row < L;
+      u32x4 qa[2], da[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        qa[ks] = ok ? *reinterpret_cast<const u32x4*>(a.q + (base + row) * kT + 32 * ks + 8 * g)
+                    : u32x4{0, 0, 0, 0};
+        da[ks] = ok ? *reinterpret_cast<const u32x4*>(a.dos + (base + row) * kT + 32 * ks + 8 * g)
+                    : u32x4{0, 0, 0, 0};
+      }
+      const uint16_t* qt = a.qtf + ((int64_t)bh * a.Nb + m) * 4096 + tfoff;
+      const uint16_t* dt = a.dotf + ((int64_t)bh * a.Nb + m) * 4096 + tfoff;
+      u32x2 qT[4], dT[4];
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        qT[ct] = *reinterpret_cast<const u32x2*>(qt + ct * 1024);
+        dT[ct] = *reinterpret_cast<const u32x2*>(dt + ct * 1024);
+      }
+      // lse, delta of queries 16w + 4g + i
+      const int64_t q0 = (int64_t)m * kT + 16 * w + 4 * g;
+      float lse4[4], del4[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const bool qok = q0 + i < L;
+        lse4[i] = qok ? a.lse[base + q0 + i] : INFINITY;
+        del4[i] = qok ? a.delta[base + q0 + i] : 0.f;
+      }
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f}, dp = sc;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const u32x4 kbv = *reinterpret_cast<const u32x4*>(&kv[0][16 * kb + r][32 * ks + 8 * g]);
+          const u32x4 vbv = *reinterpret_cast<const u32x4*>(&kv[1][16 * kb + r][32 * ks + 8 * g]);
+          sc = mfma_16x16x32<T16>(qa[ks], kbv, sc);
+          dp = mfma_16x16x32<T16>(da[ks], vbv, dp);
+        }
+        const bool kok = keyb + 16 * kb + r < L;
+        float p[4], ds[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          p[i] = kok ? fast_exp2(fminf(sc[i] * a.c - lse4[i], 4.f)) : 0.f;
+          ds[i] = sat(p[i] * (dp[i] - del4[i]));
+        }
+        const u32x2 pp = pack4<T16>(p[0], p[1], p[2], p[3]);
+        const u32x2 dsp = pack4<T16>(ds[0], ds[1], ds[2], ds[3]);
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          dvT[ct][kb] = mfma_16x16x16<T16>(dT[ct], pp, dvT[ct][kb]);
+          dkT[ct][kb] = mfma_16x16x16<T16>(qT[ct], dsp, dkT[ct][kb]);
+        }
+      }
+    }
+  }
+
+  // sum the query-split partials: wave w keeps key group kb = w
+  f32x4 dkt[4], dvt[4];
+#pragma unroll
+  for (int x = 0; x < 2; ++x) {
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      __syncthreads();
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) mb[w][ks][ct][l] = x == 0 ? dkT[ct][2 * t + ks] : dvT[ct][2 * t + ks];
+      __syncthreads();
+      if ((w >> 1) == t) {
+        const int ks = w & 1;
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          const f32x4 sum = (mb[0][ks][ct][l] + mb[1][ks][ct][l]) + (mb[2][ks][ct][l] + mb[3][ks][ct][l]);
+          if (x == 0)
+            dkt[ct] = sum;
+          else
+            dvt[ct] = sum;
+        }
+      }
+    }
+  }
+
+  // epilogue: key row 64n + 16w + r, channels 16ct + 4g + i
+  const int kr = 16 * w + r;
+  // phi(K) row statistics from this lane's channels 32ks + 8g .. +7
+  float kx[2][8];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    const u32x4 u = *reinterpret_cast<const u32x4*>(&kv[0][kr][32 * ks + 8 * g]);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      kx[ks][2 * e] = T16::to_f32((uint16_t)(u[e] & 0xffff));
+      kx[ks][2 * e + 1] = T16::to_f32((uint16_t)(u[e] >> 16));
+    }
+  }
+  float mx = -INFINITY;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, kx[ks][e]);
+  mx = max_over_groups(mx);
+  float den = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      kx[ks][e] = __expf(kx[ks][e] - mx);
+      den += kx[ks][e];
+    }
+  den = sum_over_groups(den);
+  u32x4 kpb[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+    for (int e = 0; e < 4; ++e) kpb[ks][e] = pack_pair<T16>(kx[ks][2 * e] / den, kx[ks][2 * e + 1] / den);
+
+  float dkphi[4][4], dvl[4][4], kp[4][4];
+  float dot = 0.f;
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    f32x4 x1 = f32x4{0.f, 0.f, 0.f, 0.f}, x2 = x1;
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const u32x4 vb = *reinterpret_cast<const u32x4*>(&kv[1][kr][32 * ks + 8 * g]);
+      const u32x4 ha = *reinterpret_cast<const u32x4*>(&dhs[0][16 * ct + r][32 * ks + 8 * g]);
+      const u32x4 hta = *reinterpret_cast<const u32x4*>(&dhs[1][16 * ct + r][32 * ks + 8 * g]);
+      x1 = mfma_16x16x32<T16>(ha, vb, x1);    // dkphi^T[d][key] = sum_e dh[d][e] V[key][e]
+      x2 = mfma_16x16x32<T16>(hta, kpb[ks], x2);  // dv_l^T[e][key] = sum_d dh[d][e] kphi[key][d]
+    }
+    const uint2 kvv = *reinterpret_cast<const uint2*>(&kv[0][kr][16 * ct + 4 * g]);
+    const uint32_t kw[2] = {kvv.x, kvv.y};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      dkphi[ct][i] = x1[i] + dzs[16 * ct + 4 * g + i];
+      dvl[ct][i] = x2[i];
+      const float kxv = T16::to_f32((uint16_t)(kw[i >> 1] >> (16 * (i & 1))));
+      kp[ct][i] = r16<T16>(__expf(kxv - mx) / den);
+      dot += kp[ct][i] * dkphi[ct][i];
+    }
+  }
+  dot = sum_over_groups(dot);
+  const int64_t row = (int64_t)n * kT + kr;
+  if (row < L) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      float ok_[4], ov[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float dks = r16<T16>(dkt[ct][i] * a.scale);
+        ok_[i] = sat(dks + kp[ct][i] * (dkphi[ct][i] - dot));
+        ov[i] = sat(r16<T16>(dvt[ct][i]) + dvl[ct][i]);
+      }
+      *reinterpret_cast<u32x2*>(a.dk + (base + row) * kT + 16 * ct + 4 * g) = pack4<T16>(ok_[0], ok_[1], ok_[2], ok_[3]);
+      *reinterpret_cast<u32x2*>(a.dv + (base + row) * kT + 16 * ct + 4 * g) = pack4<T16>(ov[0], ov[1], ov[2], ov[3]);
+    }
+  }
+}
+
+}  // namespace
+
+}  // namespace sla2h
+
+using namespace sla2h;
+
+extern "C" int sla2h_bwd_prep(const void* dout, const void* o_s, const void* o_l, const float* den,
+                              const void* qphi, const void* q, const void* k, const float* alpha,
+                              int alpha_stride, int dtype, int B, int H, int64_t L, int D, int E,
+                              void* dos, float* delta, void* g16, float* s, float* seg, float* P,
+                              float* Pz, void* qtf, void* ktf, void* dotf, void* stream) {
+  SLA2H_CHECK_ARG(dout && o_s && o_l && den && qphi && q && k && alpha && dos && delta && g16 &&
+                  s && seg && P && Pz && qtf && ktf && dotf);
+  SLA2H_CHECK_ARG(D == kT && E == kT && alpha_stride >= 0);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && L > 0);
+  PrepArgs a;
+  a.dout = static_cast<const uint16_t*>(dout);
+  a.o_s = static_cast<const uint16_t*>(o_s);
+  a.o_l = static_cast<const uint16_t*>(o_l);
+  a.den = den;
+  a.qphi = static_cast<const uint16_t*>(qphi);
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.alpha = alpha;
+  a.dos = static_cast<uint16_t*>(dos);
+  a.delta = delta;
+  a.g16 = static_cast<uint16_t*>(g16);
+  a.s = s;
+  a.seg = seg;
+  a.P = P;
+  a.Pz = Pz;
+  a.qtf = static_cast<uint16_t*>(qtf);
+  a.ktf = static_cast<uint16_t*>(ktf);
+  a.dotf = static_cast<uint16_t*>(dotf);
+  a.L = L;
+  a.Nb = (int)((L + E - 1) / E);
+  a.H = H;
+  a.alpha_stride = alpha_stride;
+  dim3 grid(a.Nb, B * H);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SLA2H_DTYPE_BF16)
+    bwd_prep_kernel<BF16><<<grid, 256, 0, st>>>(a);
+  else
+    bwd_prep_kernel<F16><<<grid, 256, 0, st>>>(a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_bwd_dq(const void* q, const void* k, const void* v, const void* dos,
+                            const float* lse, const float* delta, const void* ktf,
+                            const void* g16, const float* s, const void* comp, const float* Hall,
+                            const void* qphi, const int32_t* lut_aug, int dtype, int B, int H,
+                            int64_t L, int D, int E, int J, float scale, void* dq, void* stream) {
+  SLA2H_CHECK_ARG(q && k && v && dos && lse && delta && ktf && g16 && s && comp && Hall && qphi &&
+                  lut_aug && dq);
+  SLA2H_CHECK_ARG(D == kT && E == kT && scale > 0.f);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && L > 0 && J >= 1 && J <= kMaxJ);
+  const int Nb = (int)((L + E - 1) / E);
+  const int64_t nwork = (int64_t)Nb * B * H;
+  const int64_t per_xcd = (nwork + 7) / 8;
+  SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31) && L * kT * 2 < (1ll << 31));
+  DqArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.dos = static_cast<const uint16_t*>(dos);
+  a.ktf = static_cast<const uint16_t*>(ktf);
+  a.g16 = static_cast<const uint16_t*>(g16);
+  a.qphi = static_cast<const uint16_t*>(qphi);
+  a.lse = lse;
+  a.delta = delta;
+  a.s = s;
+  a.Hall = Hall;
+  a.comp = static_cast<const unsigned char*>(comp);
+  a.lut = lut_aug;
+  a.dq = static_cast<uint16_t*>(dq);
+  a.L = L;
+  a.Nb = Nb;
+  a.J = J;
+  a.nwork = (int)nwork;
+  a.per_xcd = (int)per_xcd;
+  a.c = scale * 1.4426950408889634f;
+  a.scale = scale;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nblocks = (int)(8 * per_xcd);
+  if (dtype == SLA2H_DTYPE_BF16)
+    bwd_dq_kernel<BF16><<<nblocks, 256, 0, st>>>(a);
+  else
+    bwd_dq_kernel<F16><<<nblocks, 256, 0, st>>>(a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_bwd_dkdv(const void* q, const void* k, const void* v, const void* dos,
+                              const float* lse, const float* delta, const void* qtf,
+                              const void* dotf, const uint32_t* sel, const void* comp_bwd,
+                              int dtype, int B, int H, int64_t L, int D, int E, float scale,
+                              void* dk, void* dv, void* stream) {
+  SLA2H_CHECK_ARG(q && k && v && dos && lse && delta && qtf && dotf && sel && comp_bwd && dk && dv);
+  SLA2H_CHECK_ARG(D == kT && E == kT && scale > 0.f);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && L > 0);
+  const int Nb = (int)((L + E - 1) / E);
+  const int64_t nwork = (int64_t)Nb * B * H;
+  const int64_t per_xcd = (nwork + 7) / 8;
+  SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31));
+  DkdvArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.v = static_cast<const uint16_t*>(v);
+  a.dos = static_cast<const uint16_t*>(dos);
+  a.qtf = static_cast<const uint16_t*>(qtf);
+  a.dotf = static_cast<const uint16_t*>(dotf);
+  a.lse = lse;
+  a.delta = delta;
+  a.sel = sel;
+  a.compb = static_cast<const unsigned char*>(comp_bwd);
+  a.dk = static_cast<uint16_t*>(dk);
+  a.dv = static_cast<uint16_t*>(dv);
+  a.L = L;
+  a.Nb = Nb;
+  a.NCq = (Nb + 31) / 32;
+  a.nwork = (int)nwork;
+  a.per_xcd = (int)per_xcd;
+  a.c = scale * 1.4426950408889634f;
+  a.scale = scale;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nblocks = (int)(8 * per_xcd);
+  if (dtype == SLA2H_DTYPE_BF16)
+    bwd_dkdv_kernel<BF16><<<nblocks, 256, 0, st>>>(a);
+  else
+    bwd_dkdv_kernel<F16><<<nblocks, 256, 0, st>>>(a);
+  return (int)hipGetLastError();
+}

@@ -526,6 +526,64 @@ extern "C" int sla2h_linear_states_qat(const void* k, const void* v, int dtype, 
   return (int)hipGetLastError();
 }
 
+// Backward complement.  sel[bh][n][kc] bit j = 1 where query block
+// m = 32 kc + j routes tile n (augmented LUT); the GEMM above then runs with
+// the roles swapped: rows = tiles n, contraction over query blocks m, mask
+// = NOT sel, operands = the per-query-block partials [P | Pz].
+__global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p, int64_t n) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i < n) p[i] = 0u;
+}
+
+__global__ __launch_bounds__(256) void sel_scatter_kernel(const int32_t* __restrict__ lut, int Mb,
+                                                         int J, int NCq,
+                                                         uint32_t* __restrict__ sel) {
+  const int bh = blockIdx.y;
+  const int idx = blockIdx.x * 256 + threadIdx.x;
+  if (idx >= Mb * J) return;
+  const int m = idx / J;
+  const int n = lut[(int64_t)bh * Mb * J + idx];
+  if ((unsigned)n < (unsigned)Mb)
+    atomicOr(&sel[((int64_t)bh * Mb + n) * NCq + (m >> 5)], 1u << (m & 31));
+}
+
+__global__ __launch_bounds__(256) void sel_complement_kernel(const uint32_t* __restrict__ sel,
+                                                            int Mb, int NCq, int MTp,
+                                                            uint32_t* __restrict__ cbits) {
+  const int bh = blockIdx.y;
+  const int idx = blockIdx.x * 256 + threadIdx.x;  // over NCq * MTp
+  if (idx >= NCq * MTp) return;
+  const int kc = idx / MTp, n = idx - kc * MTp;
+  uint32_t wd = 0u;
+  if (n < Mb) {
+    const int nv = Mb - 32 * kc;
+    const uint32_t valid = nv >= 32 ? 0xffffffffu : ((1u << nv) - 1u);
+    wd = ~sel[((int64_t)bh * Mb + n) * NCq + kc] & valid;
+  }
+  cbits[(int64_t)bh * NCq * MTp + idx] = wd;
+}
+
+extern "C" int sla2h_complement_bwd(const float* P, const float* Pz, const int32_t* lut_aug,
+                                    int B, int H, int Mb, int J, void* workspace, uint32_t* sel,
+                                    void* comp, void* stream) {
+  SLA2H_CHECK_ARG(P && Pz && lut_aug && workspace && sel && comp);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && Mb > 0 && Mb <= 4096 && J >= 1);
+  const int MT = (Mb + 15) / 16, NC = (Mb + 31) / 32;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int64_t nsel = (int64_t)B * H * Mb * NC;
+  fill_u32_kernel<<<(unsigned)((nsel + 255) / 256), 256, 0, st>>>(sel, nsel);
+  sel_scatter_kernel<<<dim3((Mb * J + 255) / 256, B * H), 256, 0, st>>>(lut_aug, Mb, J, NC, sel);
+  auto cbits = static_cast<uint32_t*>(workspace);
+  sel_complement_kernel<<<dim3((NC * MT * 16 + 255) / 256, B * H), 256, 0, st>>>(sel, Mb, NC,
+                                                                               MT * 16, cbits);
+  int err = (int)hipGetLastError();
+  if (err) return err;
+  dim3 grid(4160 / kCompCols, B * H, (MT + kMaskSub - 1) / kMaskSub);
+  comp_gemm_kernel<false><<<grid, kCompThreads, 0, st>>>(P, nullptr, Pz, nullptr, cbits, Mb, Mb,
+                                                         MT, NC, static_cast<unsigned char*>(comp));
+  return (int)hipGetLastError();
+}
+
 extern "C" size_t sla2h_complement_workspace_bytes(int B, int H, int Mb, int Np) {
   if (B <= 0 || H <= 0 || Mb <= 0 || Np <= 0) return 0;
   const size_t MT = (size_t)(Mb + 15) / 16, NC = (size_t)(Np + 31) / 32;

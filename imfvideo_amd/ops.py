@@ -347,4 +347,62 @@ def train_fwd(q, k, v, alpha, lut, Np, eps_l=1e-5):
     o, o_l, den = linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha, eps_l)
     htot = st["Hall"].to(q.dtype).float()
     return dict(o=o, o_s=o_s, o_l=o_l, lse=lse, den=den, qphi=qphi, htot=htot,
-                ztot=st["zall"], lut_aug=lut_aug, **qz)
+                ztot=st["zall"], Hall=st["Hall"], comp=comp, lut_aug=lut_aug, **qz)
+
+
+def train_bwd(q, k, v, alpha, fwd, do, scale=None):
+    """Straight-through backward of train_fwd.
+
+    q, k, v: the forward's 16-bit inputs; alpha (H, Mb) after the sigmoid;
+    fwd: the train_fwd dict; do: (B,H,L,D) output gradient.  Returns
+    (dq, dk, dv) 16-bit and d_alpha (H, Mb) fp32, the gradient with respect to
+    the alpha logits.
+    """
+    _need_gpu(q, k, v, do)
+    q, k, v = (t.contiguous() for t in (q, k, v))
+    B, H, L, D = q.shape
+    nb = -(-L // E_TILE)
+    dev = q.device
+    scale = D ** -0.5 if scale is None else scale
+    do = do.to(q.dtype).contiguous()
+    alpha = _alpha_rows(alpha, H, nb, dev)
+    lib = _lib.load()
+    f16 = lambda: torch.empty_like(q)
+    dos, g16 = f16(), f16()
+    delta = torch.empty(B, H, L, device=dev)
+    srow = torch.empty(B, H, L, device=dev)
+    seg = torch.zeros(H, nb, device=dev)
+    P = torch.empty(B, H, nb, D, D, device=dev)
+    Pz = torch.empty(B, H, nb, D, device=dev)
+    tf = lambda: torch.empty(B, H, nb, 4096, device=dev, dtype=q.dtype)
+    qtf, ktf, dotf = tf(), tf(), tf()
+    dc = _dtype_code(q)
+    st = _stream(dev)
+    _lib.check(lib.sla2h_bwd_prep(
+        do.data_ptr(), fwd["o_s"].data_ptr(), fwd["o_l"].data_ptr(), fwd["den"].data_ptr(),
+        fwd["qphi"].data_ptr(), q.data_ptr(), k.data_ptr(), alpha.data_ptr(), alpha.stride(0), dc,
+        B, H, L, D, E_TILE, dos.data_ptr(), delta.data_ptr(), g16.data_ptr(), srow.data_ptr(),
+        seg.data_ptr(), P.data_ptr(), Pz.data_ptr(), qtf.data_ptr(), ktf.data_ptr(),
+        dotf.data_ptr(), st), "sla2h_bwd_prep")
+    lut_aug = fwd["lut_aug"]
+    J = lut_aug.shape[-1]
+    ncq = -(-nb // 32)
+    sel = torch.empty(B, H, nb, ncq, device=dev, dtype=torch.int32)
+    ws = torch.empty(lib.sla2h_complement_workspace_bytes(B, H, nb, nb), device=dev,
+                     dtype=torch.uint8)
+    compb = torch.empty(B, H, nb, REC_BYTES, device=dev, dtype=torch.uint8)
+    _lib.check(lib.sla2h_complement_bwd(P.data_ptr(), Pz.data_ptr(), lut_aug.data_ptr(), B, H,
+                                        nb, J, ws.data_ptr(), sel.data_ptr(), compb.data_ptr(),
+                                        st), "sla2h_complement_bwd")
+    dq, dk, dv = f16(), f16(), f16()
+    _lib.check(lib.sla2h_bwd_dq(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), dos.data_ptr(), fwd["lse"].data_ptr(),
+        delta.data_ptr(), ktf.data_ptr(), g16.data_ptr(), srow.data_ptr(), fwd["comp"].data_ptr(),
+        fwd["Hall"].data_ptr(), fwd["qphi"].data_ptr(), lut_aug.data_ptr(), dc, B, H, L, D, E_TILE,
+        J, float(scale), dq.data_ptr(), st), "sla2h_bwd_dq")
+    _lib.check(lib.sla2h_bwd_dkdv(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), dos.data_ptr(), fwd["lse"].data_ptr(),
+        delta.data_ptr(), qtf.data_ptr(), dotf.data_ptr(), sel.data_ptr(), compb.data_ptr(), dc,
+        B, H, L, D, E_TILE, float(scale), dk.data_ptr(), dv.data_ptr(), st), "sla2h_bwd_dkdv")
+    d_alpha = seg * alpha * (1.0 - alpha)
+    return dq, dk, dv, d_alpha

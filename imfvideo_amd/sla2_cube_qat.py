@@ -101,6 +101,40 @@ def _sparse_primal_only(q, k, v, lut, T, Np, E, prefix_len):
     return o
 
 
+class _CubeQATFunction(torch.autograd.Function):
+    """Training op with the straight-through backward (reference :696-832).
+
+    Same argument list as the reference.  ``mask`` and ``a_index`` are
+    accepted and unused: the kernels derive the per-tile selection from
+    ``lut_aug`` on the device, and the alpha of a row is that of its 64-row
+    block.  ``use_int8`` must be true (the only mode of this build).
+    """
+
+    @staticmethod
+    def forward(ctx, qh, kh, vh, alpha_logit, lut, lut_aug, mask, T, E, use_int8, a_index,
+                n_tail=1, stats_out=None):
+        if not use_int8:
+            raise NotImplementedError("_CubeQATFunction: only the INT8 training forward is built")
+        assert E == ops.E_TILE, f"E must be {ops.E_TILE}, got {E}"
+        B, H, L, D = qh.shape
+        Np = -(-L // E) - n_tail
+        a = torch.sigmoid(alpha_logit.detach().float())
+        out = ops.train_fwd(qh, kh, vh, a, lut, Np)
+        if stats_out is not None:
+            stats_out.copy_(out["lse"].amax(dim=(0, 2)))
+        ctx.save_for_backward(qh, kh, vh, a, out["o_s"], out["o_l"], out["lse"], out["den"],
+                              out["qphi"], out["Hall"], out["comp"], out["lut_aug"])
+        return out["o"]
+
+    @staticmethod
+    def backward(ctx, do):
+        qh, kh, vh, a, o_s, o_l, lse, den, qphi, Hall, comp, lut_aug = ctx.saved_tensors
+        fwd = dict(o_s=o_s, o_l=o_l, lse=lse, den=den, qphi=qphi, Hall=Hall, comp=comp,
+                   lut_aug=lut_aug)
+        dq, dk, dv, d_alpha = ops.train_bwd(qh, kh, vh, a, fwd, do)
+        return (dq, dk, dv, d_alpha, None, None, None, None, None, None, None, None, None)
+
+
 class SLA2CubeQATAttentionImpl(nn.Module):
     """attn_impl: cube-block sparse-linear attention with INT8 QAT (reference :295-439).
 
@@ -116,11 +150,13 @@ class SLA2CubeQATAttentionImpl(nn.Module):
         pre_permuted: tokens are already tile-major.
 
     The forward follows the reference module: tokens permuted tile-major and
-    cast to fp16, routed, then the training-forward kernels (INT8 sparse
-    branch with truncating quantisation and INT8 P.V, 16-bit state-form
-    linear branch, 16-bit mix; ``ops.train_fwd``), which the reference also
-    runs under no_grad.  The autograd backward of the training path is not
-    part of this build yet: calling the module with gradients required raises.
+    cast to fp16, routed (no gradient reaches proj_q / proj_k), then the
+    training-forward kernels (INT8 sparse branch with truncating quantisation
+    and INT8 P.V, 16-bit state-form linear branch, 16-bit mix;
+    ``ops.train_fwd``), which the reference also runs under no_grad.  With
+    gradients required it goes through ``_CubeQATFunction`` (straight-through
+    backward) and refreshes ``logit_max_log2`` (H,), the per-head maximum of
+    the sparse branch's lse.
     """
 
     TILE_MAJOR = True
@@ -150,13 +186,6 @@ class SLA2CubeQATAttentionImpl(nn.Module):
 
     def forward(self, q, k, v):
         """q, k, v: (b, l, H, hd) -> (b, l, H, hd) attention output in q.dtype."""
-        needs_grad = torch.is_grad_enabled() and (
-            q.requires_grad or k.requires_grad or v.requires_grad
-            or self.alpha_logit.requires_grad)
-        if needs_grad:
-            raise NotImplementedError(
-                "SLA2CubeQATAttentionImpl: the INT8 training backward is not implemented in "
-                "this build; call under torch.no_grad() or use sla2_cube_qat_jvp_fused")
         B, L, H, D = q.shape
 
         def tm(x):
@@ -166,10 +195,22 @@ class SLA2CubeQATAttentionImpl(nn.Module):
             return x.half().contiguous()
 
         qh, kh, vh = tm(q), tm(k), tm(v)
-        lut, T = route_tiles_fast(qh, kh, self.topk_frac, self.Np, self.E, self.prefix_len,
-                                  proj_q=self.proj_q, proj_k=self.proj_k)
-        a = torch.sigmoid(self.alpha_logit.detach().float())
-        o = ops.train_fwd(qh, kh, vh, a, lut, self.Np)["o"]
+        with torch.no_grad():
+            lut, T = route_tiles_fast(qh, kh, self.topk_frac, self.Np, self.E, self.prefix_len,
+                                      proj_q=self.proj_q, proj_k=self.proj_k)
+        needs_grad = torch.is_grad_enabled() and (
+            q.requires_grad or k.requires_grad or v.requires_grad
+            or self.alpha_logit.requires_grad)
+        if needs_grad:
+            if not hasattr(self, "logit_max_log2"):
+                self.logit_max_log2 = torch.zeros(H, device=q.device, dtype=torch.float32)
+            lut_aug = ops.augment_lut(lut, self.Np, self.n_tail)
+            o = _CubeQATFunction.apply(qh, kh, vh, self.alpha_logit, lut, lut_aug, None, T,
+                                       self.E, self.use_int8, self.a_index, self.n_tail,
+                                       self.logit_max_log2)
+        else:
+            a = torch.sigmoid(self.alpha_logit.detach().float())
+            o = ops.train_fwd(qh, kh, vh, a, lut, self.Np)["o"]
         if self.pre_permuted:
             return o.permute(0, 2, 1, 3).to(q.dtype)
         return o[:, :, self.inv].permute(0, 2, 1, 3).to(q.dtype)

@@ -214,6 +214,78 @@ int sla2h_linear_mix_qat(const void* qphi, const void* comp, const float* Hall,
                          int B, int H, int64_t L, int D, int E, float eps_l, void* o,
                          void* o_l, float* den, void* stream);
 
+/* ---- training backward (straight-through estimator) --------------------- */
+
+/*
+ * Per 64-row block: the gradient split and the row statistics of the
+ * backward, plus the operands the dq and dk/dv kernels share.
+ *   dos = round16(dout * a), do_l = round16(dout * (1 - a)), a = alpha[h,m] fp32;
+ *   delta = sum_d o_s * dos (B,H,L) fp32;
+ *   g16 = round16(sat(do_l / den)) (B,H,L,D) 16-bit, s = sum_d do_l o_l / den (B,H,L);
+ *   seg (H,Mb) fp32 += sum over the block of dout * (o_s - o_l) (atomic over b;
+ *     zero it first), so d(alpha logit) = seg * a * (1 - a);
+ *   P = qphi^T sat(g) (B,H,Mb,D,D) fp32, Pz = qphi^T s (B,H,Mb,D) fp32;
+ *   qtf, ktf, dotf (B,H,Nb,4096) 16-bit: q, k, dos in the transposed fragment
+ *     order [ct][p][lane][s] = X[16(2p + (s>>2)) + 4g + (s&3)][16ct + r].
+ * sat(x) = clamp(x, -60000, 60000).  Replaces _bwd_split_kernel
+ * (models/sla2_cube_qat.py:838-872), _attn_bwd_preprocess
+ * (models/sla2_vendor/sla_kernel.py:89-114) and the g, s, dhtot, dztot torch
+ * lines of _CubeQATFunction.backward (models/sla2_cube_qat.py:765-797).
+ */
+int sla2h_bwd_prep(const void* dout, const void* o_s, const void* o_l, const float* den,
+                   const void* qphi, const void* q, const void* k, const float* alpha,
+                   int alpha_stride, int dtype, int B, int H, int64_t L, int D, int E,
+                   void* dos, float* delta, void* g16, float* s, float* seg, float* P,
+                   float* Pz, void* qtf, void* ktf, void* dotf, void* stream);
+
+/*
+ * Backward complement over the augmented LUT lut_aug (B,H,Mb,J) int32:
+ *   sel (B,H,Mb,ceil(Mb/32)) uint32: bit j of word kc of tile n = 1 where query
+ *     block 32kc + j routes tile n;
+ *   comp records (B,H,Mb, sla2h_complement_record_bytes(64) bytes), fp32:
+ *     Hc[n] = sum_{m not routing n} P[m] (the complement dh), zc[n] = sum Pz[m].
+ * workspace: sla2h_complement_workspace_bytes(B,H,Mb,Mb) bytes.  Mb <= 4096
+ * (query blocks = key tiles).  Replaces _invert_lut and the dhtot/dztot minus
+ * selected-blocks loop of _lin_bwd_dkdv_lut (models/sla2_cube_qat.py:966-983,
+ * 1045-1095).
+ */
+int sla2h_complement_bwd(const float* P, const float* Pz, const int32_t* lut_aug, int B, int H,
+                         int Mb, int J, void* workspace, uint32_t* sel, void* comp,
+                         void* stream);
+
+/*
+ * dq = round16(sat(dq_s + qphi (dqphi - <qphi, dqphi>))) (B,H,L,D) 16-bit, with
+ *   dq_s = round16(scale sum_tiles round16(sat(p (dos.v - delta))) k),
+ *   p = exp2(min(q.k scale log2e - lse, 4)) on the unquantised 16-bit q, k;
+ *   dqphi = g16 H16^T - s z^T, H16 = round16(comp.Hc + (round16(Hall) - Hall)),
+ *   z = comp.zc (comp, Hall, lse, qphi from the training forward).
+ * J = columns of lut_aug <= 1024.  Replaces _attn_bwd_dq
+ * (models/sla2_vendor/sla_kernel.py:117-184), _lin_bwd_dq
+ * (models/sla2_vendor/kernel_linear.py:85-138) and the Q-side
+ * _phi_chain_add_kernel (models/sla2_cube_qat.py:875-904, 814-818).
+ */
+int sla2h_bwd_dq(const void* q, const void* k, const void* v, const void* dos, const float* lse,
+                 const float* delta, const void* ktf, const void* g16, const float* s,
+                 const void* comp, const float* Hall, const void* qphi, const int32_t* lut_aug,
+                 int dtype, int B, int H, int64_t L, int D, int E, int J, float scale, void* dq,
+                 void* stream);
+
+/*
+ * dk = round16(sat(dk_s + kphi (dkphi - <kphi, dkphi>))), dv = round16(sat(dv_s + dv_l))
+ * (B,H,L,D) 16-bit, over the query blocks that route each key tile (sel):
+ *   dk_s = round16(scale sum round16(sat(p (dos.v - delta)))^T q),
+ *   dv_s = round16(sum round16(p)^T dos);
+ *   dkphi = v dh16^T + dz, dv_l = kphi dh16, dh16 = round16(sat(comp_bwd.Hc)),
+ *   dz = -comp_bwd.zc, kphi = round16(softmax_D(k)).
+ * Replaces _sparse_bwd_dkdv_lut (models/sla2_cube_qat.py:986-1042),
+ * _lin_bwd_dkdv_lut (:1045-1104), the K-side _phi_chain_add_kernel and the dv
+ * sum (:819-830).
+ */
+int sla2h_bwd_dkdv(const void* q, const void* k, const void* v, const void* dos, const float* lse,
+                   const float* delta, const void* qtf, const void* dotf, const uint32_t* sel,
+                   const void* comp_bwd, int dtype, int B, int H, int64_t L, int D, int E,
+                   float scale, void* dk, void* dv, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

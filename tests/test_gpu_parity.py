@@ -256,5 +256,39 @@ def test_module_forward_no_grad():
     eo = O.train_fwd(qh, kh, vh, a, lut, mod.Np, mod.prefix_len, t16=torch.float16)["o"]
     eo = eo[:, :, mod.inv.cpu()].permute(0, 2, 1, 3)
     assert max_abs(out, eo) < TOL_MAX and rel_l2(out, eo) < TOL_REL
-    with pytest.raises(NotImplementedError):
-        mod(cuda(x).requires_grad_(), cuda(x), cuda(x))
+
+
+def test_module_training_step_gradients():
+    say("SLA2CubeQATAttentionImpl forward + backward")
+    from imfvideo_amd.sla2_cube_qat import SLA2CubeQATAttentionImpl
+    torch.manual_seed(1)
+    mod = SLA2CubeQATAttentionImpl(head_dim=64, seq_len=274, num_heads=2, grid=(4, 8, 8),
+                                   tile=(4, 4, 4), topk=0.5, alpha_init=0.9).cuda()
+    with torch.no_grad():
+        mod.alpha_logit.add_(torch.linspace(-1, 1, mod.alpha_logit.numel(),
+                                            device="cuda").view_as(mod.alpha_logit))
+    g = torch.Generator().manual_seed(9)
+    x = [torch.randn(2, 274, 2, 64, generator=g) for _ in range(4)]
+    xs = [cuda(t).requires_grad_() for t in x[:3]]
+    out = mod(*xs)
+    (out * cuda(x[3])).sum().backward()
+    grads = [t.grad.cpu() for t in xs] + [mod.alpha_logit.grad.cpu()]
+    assert mod.proj_q.grad is None and mod.proj_k.grad is None
+    assert mod.logit_max_log2.shape == (2,) and torch.isfinite(mod.logit_max_log2).all()
+    # oracle: the same tile-major fp16 pipeline
+    perm, inv = mod.perm.cpu(), mod.inv.cpu()
+    tm = lambda t: t.permute(0, 2, 1, 3)[:, :, perm].half().float()
+    qh, kh, vh, doh = (tm(t) for t in x)
+    lut, T, _, _ = O.route(qh, kh, 0.5, mod.Np, mod.prefix_len, torch.eye(64), torch.eye(64))
+    a = torch.sigmoid(mod.alpha_logit.detach().cpu())
+    fwd = O.train_fwd(qh, kh, vh, a, lut, mod.Np, mod.prefix_len, t16=torch.float16)
+    eo = fwd["o"][:, :, inv].permute(0, 2, 1, 3)
+    assert max_abs(out.detach().cpu(), eo) < TOL_MAX
+    assert torch.allclose(mod.logit_max_log2.cpu(), fwd["lse"].amax(dim=(0, 2)), atol=1e-3)
+    ref = O.train_bwd(qh, kh, vh, a, lut, mod.Np, mod.prefix_len, fwd, doh, t16=torch.float16)
+    back = lambda t: t[:, :, inv].permute(0, 2, 1, 3)
+    for got, name in zip(grads[:3], ("dq", "dk", "dv")):
+        want = back(ref[name])
+        print(f"  {name} max {max_abs(got, want):.2e} rel {rel_l2(got, want):.2e}", flush=True)
+        assert rel_l2(got, want) < TOL_REL and max_abs(got, want) < TOL_MAX * max(1, want.abs().max())
+    assert rel_l2(grads[3], ref["d_alpha"]) < 1e-3

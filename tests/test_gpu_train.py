@@ -141,3 +141,91 @@ def test_train_fwd_config3_full_size():
                           Np, P)
         compare({n: (t[:, sl] if torch.is_tensor(t) and t.dim() >= 3 and t.shape[1] == 8 else t)
                  for n, t in out.items()}, ref, f"h{h} ")
+
+
+# ---------------------------------------------------------------------------
+# Backward (straight-through estimator) against O.train_bwd, fed the GPU
+# forward's saved tensors.  16-bit gradients: rel-L2 1e-2, max-abs 2e-2 of
+# max(1, max|ref|); d_alpha (fp32, atomics over b): rel-L2 1e-3.
+# ---------------------------------------------------------------------------
+def run_bwd(ins, alpha, lut, Np, P, seed=7, dscale=1.0):
+    from imfvideo_amd import ops
+    dt = ins["q"].dtype
+    out = run_train(ins, alpha, lut, Np)
+    g = torch.Generator().manual_seed(seed)
+    do = (torch.randn(ins["q"].shape, generator=g) * dscale).to(dt)
+    gq = {n: cuda(ins[n]) for n in ("q", "k", "v")}
+    dq, dk, dv, da = ops.train_bwd(gq["q"], gq["k"], gq["v"], cuda(alpha), out, cuda(do))
+    torch.cuda.synchronize()
+    f = {n: ins[n].float() for n in ("q", "k", "v")}
+    fwd = {n: out[n].cpu().float() for n in ("o_s", "o_l", "lse", "den", "qphi", "htot", "ztot")}
+    ref = O.train_bwd(f["q"], f["k"], f["v"], alpha, lut, Np, P, fwd, do.float(), t16=dt)
+    return dict(dq=dq.cpu().float(), dk=dk.cpu().float(), dv=dv.cpu().float(),
+                d_alpha=da.cpu()), ref
+
+
+def compare_bwd(got, ref, tag="", sl=slice(None)):
+    for n in ("dq", "dk", "dv"):
+        a, b = got[n][:, sl], ref[n]
+        bound = TOL_MAX * max(1.0, b.abs().max().item())
+        print(f"  {tag}{n} max {max_abs(a, b):.2e} (bound {bound:.2e}) rel {rel_l2(a, b):.2e}",
+              flush=True)
+        assert max_abs(a, b) < bound and rel_l2(a, b) < TOL_REL, n
+    da = got["d_alpha"][sl]
+    print(f"  {tag}d_alpha rel {rel_l2(da, ref['d_alpha']):.2e}", flush=True)
+    assert rel_l2(da, ref["d_alpha"]) < 1e-3
+
+
+@pytest.mark.parametrize("name", ["ref_geom_bf16", "tiny_f16", "two_tails_bf16"])
+def test_train_bwd_golden(name):
+    say("train_bwd golden", name)
+    z, dt, ins = golden(name)
+    Np, P = int(z["Np"]), int(z["P"])
+    got, ref = run_bwd(ins, torch.from_numpy(z["alpha"]), z["lut"], Np, P)
+    compare_bwd(got, ref)
+
+
+def test_train_bwd_config1_ragged_fp16():
+    say("train_bwd config1 and a ragged fp16 case")
+    ins, Np, P = config_inputs(1)
+    f = {n: t.float() for n, t in ins.items()}
+    lut, T, _, _ = O.route(f["q"], f["k"], 0.1, Np, P)
+    g = torch.Generator().manual_seed(5)
+    alpha = torch.rand(4, Np, generator=g) * 0.8 + 0.1
+    ins = {n: ins[n] for n in ("q", "k", "v")}
+    got, ref = run_bwd(ins, alpha, lut, Np, P)
+    compare_bwd(got, ref, "c1 ")
+    B, H, Np, P = 2, 2, 5, 37
+    L = Np * 64 + P
+    q, k, v = make_inputs(31, B, H, L, dtype=torch.float16, tangent=False)
+    ins = dict(q=q, k=k, v=v)
+    f = {n: t.float() for n, t in ins.items()}
+    lut, T, _, _ = O.route(f["q"], f["k"], 0.4, Np, P)
+    alpha = torch.full((H, Np + 1), 0.3)
+    got, ref = run_bwd(ins, alpha, lut, Np, P, dscale=0.5)
+    compare_bwd(got, ref, "ragged ")
+
+
+def test_train_bwd_config3_full_size():
+    say("train_bwd config3 full size (1,8,29952,64)")
+    ins, Np, P = config_inputs(3)
+    ins = {n: ins[n] for n in ("q", "k", "v")}
+    f = {n: t.float() for n, t in ins.items()}
+    lut, T, _, _ = O.route(f["q"], f["k"], 0.1, Np, P)
+    alpha = torch.full((8, Np), 0.9)
+    from imfvideo_amd import ops
+    out = run_train(ins, alpha, lut, Np)
+    g = torch.Generator().manual_seed(7)
+    do = torch.randn(ins["q"].shape, generator=g).to(torch.bfloat16)
+    gq = {n: cuda(ins[n]) for n in ("q", "k", "v")}
+    dq, dk, dv, da = ops.train_bwd(gq["q"], gq["k"], gq["v"], cuda(alpha), out, cuda(do))
+    torch.cuda.synchronize()
+    got = dict(dq=dq.cpu().float(), dk=dk.cpu().float(), dv=dv.cpu().float(), d_alpha=da.cpu())
+    for n in ("dq", "dk", "dv"):
+        assert torch.isfinite(got[n]).all(), n
+    for h in (0, 5):
+        sl = slice(h, h + 1)
+        fwd = {n: out[n][:, sl].cpu().float() for n in ("o_s", "o_l", "lse", "den", "qphi", "htot", "ztot")}
+        ref = O.train_bwd(f["q"][:, sl], f["k"][:, sl], f["v"][:, sl], alpha[sl], lut[:, sl], Np, P,
+                          fwd, do[:, sl].float())
+        compare_bwd(got, ref, f"h{h} ", sl)
