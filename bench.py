@@ -103,12 +103,99 @@ def cpu_baseline(cfg_d, tangent):
                       f"scaled x{cfg_d['H']} (heads are independent)"}
 
 
+TRAIN_STAGES = ["route", "quant_train", "sparse_fwd_qat", "linear_states_qat", "complement",
+                "linear_mix_qat", "bwd_prep", "complement_bwd", "bwd_dq", "bwd_dkdv"]
+
+
+def train_bench(args):
+    """Config 5's attention op as one training step: routing, the training
+    forward and the straight-through backward (B=2, H=8, N=29,952, fp16 as
+    the reference module casts).  Not the headline metric: prints its own line."""
+    from imfvideo_amd import ops
+
+    B, H, N, Np, topk = 2, 8, 29952, 468, 0.1
+    g = torch.Generator().manual_seed(5)
+    x = [torch.randn(B, H, N, 64, generator=g) for _ in range(4)]
+    for i in (0, 1):
+        x[i] = x[i] * torch.rsqrt(x[i].pow(2).mean(-1, keepdim=True) + 1e-6)
+    dev = torch.device("cuda:0")
+    q, k, v, do = (t.to(torch.float16).to(dev) for t in x)
+    alpha = torch.full((H, Np), 0.9, device=dev)
+    T = ops.topk_count(topk, Np)
+    nb = -(-N // 64)
+    lib = ops._lib.load()
+
+    def step(ev=None):
+        rec = (lambda i: ev[i].record()) if ev is not None else (lambda i: None)
+        rec(0)
+        _, _, _, _, qpool, kpool_t = ops.quant_pool_qk(q, k, Np)
+        lut = ops.route_topk(qpool, kpool_t, T, 0.125)
+        rec(1)
+        qz = ops.quant_train(q, k, v)
+        rec(2)
+        o_s, lse, qphi = ops.sparse_fwd_qat(q, qz, lut, Np)
+        rec(3)
+        st = ops.linear_states_qat(k, v)
+        rec(4)
+        lut_aug = ops.augment_lut(lut, Np, nb - Np)
+        comp = ops.complement(st, lut_aug, nb)
+        rec(5)
+        o, o_l, den = ops.linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha)
+        rec(6)
+        fwd = dict(o_s=o_s, o_l=o_l, lse=lse, den=den, qphi=qphi, Hall=st["Hall"], comp=comp,
+                   lut_aug=lut_aug)
+        grads = ops.train_bwd(q, k, v, alpha, fwd, do, stage_events=(
+            None if ev is None else ev[6:10]))
+        rec(10)
+        return o, grads
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(11)] for _ in range(args.steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        step(evs[i])
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    stage_us = {name: statistics.mean(e[si].elapsed_time(e[si + 1]) for e in evs) * 1e3
+                for si, name in enumerate(TRAIN_STAGES)}
+    pairs = B * H * nb * T  # n_tail = 0 at this shape
+    gemm = 2 * 64 ** 3
+    work = {"sparse_fwd_qat": ("int8", pairs * 2 * gemm), "bwd_dq": ("bf16", pairs * 3 * gemm),
+            "bwd_dkdv": ("bf16", pairs * 4 * gemm)}
+    roof = {}
+    for kname, (kind, w) in work.items():
+        peak = PEAK_I8_TOPS if kind == "int8" else PEAK_BF16_TFLOPS
+        ach = w / (stage_us[kname] * 1e-6) / 1e12
+        roof[kname] = {"bound": "mfma", "achieved": round(ach, 2), "peak": peak,
+                       "unit": "TOP/s" if kind == "int8" else "TFLOP/s",
+                       "frac": round(ach / peak, 4), "work": w}
+    out = {
+        "metric": "ms per SLA2 INT8 attn training step (fwd + straight-through bwd), "
+                  "Config 5 attention shape, 1 MI355X",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "int8+fp16",
+        "data": "synthetic (CPU-seeded N(0,1); q,k per-token RMS-normalised; do N(0,1))",
+        "config": {"workload": "SLA2 INT8 cube attention training step (BASELINE Config 5 "
+                               "attention op)", "B": B, "H": H, "N": N, "D": 64, "E": 64,
+                   "topk": topk, "T": T, "pairs": pairs},
+        "roofline": roof,
+        "kernels_us": {k_: round(v_, 2) for k_, v_ in stage_us.items()},
+    }
+    print(json.dumps(out), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3])
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 5],
+                    help="5: the attention op's training step at Config 5's shape (own line)")
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB fp32 copy kernel (torch.mul by 1) three times: "
@@ -126,6 +213,10 @@ def main():
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
               "the op shards by head with no exchange, see DESIGN.md", file=sys.stderr)
         sys.exit(1)
+
+    if args.config == 5:
+        train_bench(args)
+        return
 
     from imfvideo_amd import ops
 

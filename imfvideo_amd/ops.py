@@ -350,7 +350,7 @@ def train_fwd(q, k, v, alpha, lut, Np, eps_l=1e-5):
                 ztot=st["zall"], Hall=st["Hall"], comp=comp, lut_aug=lut_aug, **qz)
 
 
-def train_bwd(q, k, v, alpha, fwd, do, scale=None):
+def train_bwd(q, k, v, alpha, fwd, do, scale=None, stage_events=None):
     """Straight-through backward of train_fwd.
 
     q, k, v: the forward's 16-bit inputs; alpha (H, Mb) after the sigmoid;
@@ -378,6 +378,8 @@ def train_bwd(q, k, v, alpha, fwd, do, scale=None):
     qtf, ktf, dotf = tf(), tf(), tf()
     dc = _dtype_code(q)
     st = _stream(dev)
+    rec = (lambda i: stage_events[i].record()) if stage_events else (lambda i: None)
+    rec(0)
     _lib.check(lib.sla2h_bwd_prep(
         do.data_ptr(), fwd["o_s"].data_ptr(), fwd["o_l"].data_ptr(), fwd["den"].data_ptr(),
         fwd["qphi"].data_ptr(), q.data_ptr(), k.data_ptr(), alpha.data_ptr(), alpha.stride(0), dc,
@@ -391,15 +393,18 @@ def train_bwd(q, k, v, alpha, fwd, do, scale=None):
     ws = torch.empty(lib.sla2h_complement_workspace_bytes(B, H, nb, nb), device=dev,
                      dtype=torch.uint8)
     compb = torch.empty(B, H, nb, REC_BYTES, device=dev, dtype=torch.uint8)
+    rec(1)
     _lib.check(lib.sla2h_complement_bwd(P.data_ptr(), Pz.data_ptr(), lut_aug.data_ptr(), B, H,
                                         nb, J, ws.data_ptr(), sel.data_ptr(), compb.data_ptr(),
                                         st), "sla2h_complement_bwd")
     dq, dk, dv = f16(), f16(), f16()
+    rec(2)
     _lib.check(lib.sla2h_bwd_dq(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), dos.data_ptr(), fwd["lse"].data_ptr(),
         delta.data_ptr(), ktf.data_ptr(), g16.data_ptr(), srow.data_ptr(), fwd["comp"].data_ptr(),
         fwd["Hall"].data_ptr(), fwd["qphi"].data_ptr(), lut_aug.data_ptr(), dc, B, H, L, D, E_TILE,
         J, float(scale), dq.data_ptr(), st), "sla2h_bwd_dq")
+    rec(3)
     _lib.check(lib.sla2h_bwd_dkdv(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), dos.data_ptr(), fwd["lse"].data_ptr(),
         delta.data_ptr(), qtf.data_ptr(), dotf.data_ptr(), sel.data_ptr(), compb.data_ptr(), dc,
