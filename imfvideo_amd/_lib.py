@@ -35,6 +35,11 @@ SIGNATURES = {
     "sla2h_fwd_jvp": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _c_int, _p,
                                _c_int, _c_int, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int,
                                _c_f, _c_f, _c_int, _p, _p, _p]),
+    "sla2h_pool_blocks": (_c_int, [_p, _c_int, _c_i64, _c_i64, _c_int, _c_int, _p, _c_int, _p,
+                                   _p]),
+    "sla2h_fwd_jvp_1d": (_c_int, [_p, _p, _p, _p, _p, _p, _c_int, _p, _c_int, _c_int, _c_int,
+                                  _c_i64, _c_int, _c_int, _c_int, _c_int, _c_f, _c_f, _p, _p,
+                                  _p]),
     "sla2h_quant_train": (_c_int, [_p, _p, _p, _c_int, _c_int, _c_int, _c_i64, _c_int, _c_int,
                                    _p, _p, _p, _p, _p, _p, _p]),
     "sla2h_sparse_fwd_qat": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int,

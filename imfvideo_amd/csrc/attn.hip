@@ -50,7 +50,11 @@ struct FwdArgs {
   int64_t L;
   int H, Nb, Np, Mb, T, n_tail, alpha_stride, nwork, per_xcd;
   int prescale;  // scale is a power of two (folded exactly into bf16 Q-side operands)
+  int qshift;    // LUT rows, alpha and records per query block of 64 << qshift rows
+  int Mq;        // LUT rows per (b, h)
+  int ragged;    // id of a partial key tile that routed lists may hold, or -1
   float scale, c_log2, eps_l;
+  float c16;     // log2-domain factor of the 16-bit primal scores
 };
 
 // bf16 x 2^k, exact for a power-of-two scale (no bf16 subnormals in range)
@@ -90,7 +94,9 @@ struct ValRegs {   // value-side operands, loaded at the start of their own tile
   u32x4 v[4];
 };
 
-template <typename T16, bool TAN, bool LINEAR, bool PRE>
+// S16: primal scores from the 16-bit K Q^T (the K half of the kt operands and
+// the Q half of the [dQ|Q] operands) instead of INT8 (the 1-D SLA2 JVP).
+template <typename T16, bool TAN, bool LINEAR, bool PRE, bool S16>
 __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   __shared__ float stat[3][4][kQT][16];  // [m,l,mu][wave][qt][r]
   // [dQ|Q] B-operand fragments [qt][ks][lane] (16 B each)
@@ -100,6 +106,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   __shared__ __align__(16) float mbuf[4][4][kQT][64][4];
   // key tiles of this query block in visiting order: (tile id, key scale)
   __shared__ int2 tiles[kMaxTiles];
+  __shared__ int ragged_last;  // the partial key tile was moved to the end of the routed list
 
   const int logical = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
   if (logical >= a.nwork) return;  // whole workgroup: no barrier skipped
@@ -118,7 +125,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
 
   // ---- query side: INT8 B operands in registers; 16-bit [dQ|Q] B operands
   // staged once in LDS (wave w loads sub-tile w>>1, dQ or Q by w&1).
-  if (w < kQT) {
+  if (!S16 && w < kQT) {
     const int64_t row = q0 + 16 * w + r;
     q8sh[w][l] = row < L ? *reinterpret_cast<const i32x4*>(a.q8 + (qkbase + row) * kTa + 16 * g)
                          : i32x4{0, 0, 0, 0};
@@ -136,17 +143,39 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
       qsh[qt][ks + 2 * (w & 1)][l] = v;
     }
   }
-  const int32_t* lrow = a.lut + ((int64_t)bh * a.Mb + m) * a.T;
+  const int mq = m >> a.qshift;  // LUT row, alpha and record of this query block
+  const int32_t* lrow = a.lut + ((int64_t)bh * a.Mq + mq) * a.T;
   const int J = a.T + a.n_tail;
   for (int j = tid; j < J; j += 256) {
     int n = j < a.T ? lrow[j] : a.Np + (j - a.T);
     n = n < 0 ? 0 : (n >= a.Nb ? a.Nb - 1 : n);  // out-of-range ids are clamped
-    tiles[j] = make_int2(n, __builtin_bit_cast(int, a.ks[(int64_t)bh * a.Nb + n]));
+    tiles[j] = make_int2(n, S16 ? 0 : __builtin_bit_cast(int, a.ks[(int64_t)bh * a.Nb + n]));
   }
   __syncthreads();
-  const float sq = a.qs[(int64_t)bh * a.Nb + m];
+  // A partial key tile (1-D blocks over a ragged L) can sit anywhere in a routed
+  // list: move it to the end, where the masked one-tile path handles it.
+  int Tu = a.T;
+  if (a.ragged >= 0) {
+    if (tid == 0) {
+      int found = 0;
+      for (int j = 0; j < a.T; ++j) {
+        if (tiles[j].x == a.ragged) {
+          const int2 t = tiles[j];
+          tiles[j] = tiles[a.T - 1];
+          tiles[a.T - 1] = t;
+          found = 1;
+          break;
+        }
+      }
+      ragged_last = found;
+    }
+    __syncthreads();
+    Tu = a.T - ragged_last;
+  }
+  const float sq = S16 ? 1.f : a.qs[(int64_t)bh * a.Nb + m];
   // log2-domain score factor of key tile j: (sq * sk_j) * scale * log2(e)
   auto tile_c = [&](int j) {
+    if (S16) return a.c16;
     return (sq * __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(tiles[j].y))) * a.c_log2;
   };
   // per-(b,h) buffer resources: key rows past L read as zeros (those keys are
@@ -199,7 +228,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   const int vtoff = TAN ? w * 1024 + l * 16 : w * 512 + l * 8;
   auto load_keys = [&](int j, KeyRegs& kr) {
     const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
-    kr.k8 = __builtin_bit_cast(i32x4, buf_load16(rk8, k8off + n * kTa * kTa, 0));
+    if (!S16) kr.k8 = __builtin_bit_cast(i32x4, buf_load16(rk8, k8off + n * kTa * kTa, 0));
     if (TAN) {
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) kr.ka[ks] = buf_load16(rkt, ktoff + ks * 1024, n * 16384);
@@ -256,17 +285,33 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     const int64_t key0 = (int64_t)n * kTa + 16 * w + 4 * g;
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
-      const i32x4 si = mfma_i8_16x16x64(kr.k8, q8sh[qt][l], i32x4{0, 0, 0, 0});
-      int mx;
-      if (MASK) {
-        mx = INT_MIN;
+      float sv[4];  // raw scores (integer-valued for INT8)
+      float mt;
+      if (S16) {
+        f32x4 s16 = mfma_16x16x32<T16>(kr.ka[0], qsh[qt][2][l], f32x4{0.f, 0.f, 0.f, 0.f});
+        s16 = mfma_16x16x32<T16>(kr.ka[1], qsh[qt][3][l], s16);
+        float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (key0 + i < L) mx = max(mx, si[i]);
+        for (int i = 0; i < 4; ++i) {
+          sv[i] = s16[i];
+          if (!MASK || key0 + i < L) mx = fmaxf(mx, sv[i]);
+        }
+        mt = mx * c;
       } else {
-        mx = max(max(si[0], si[1]), max(si[2], si[3]));
+        const i32x4 si = mfma_i8_16x16x64(kr.k8, q8sh[qt][l], i32x4{0, 0, 0, 0});
+        int mx;
+        if (MASK) {
+          mx = INT_MIN;
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            if (key0 + i < L) mx = max(mx, si[i]);
+        } else {
+          mx = max(max(si[0], si[1]), max(si[2], si[3]));
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) sv[i] = (float)si[i];
+        mt = mx == INT_MIN ? -INFINITY : (float)mx * c;
       }
-      const float mt = mx == INT_MIN ? -INFINITY : (float)mx * c;
       if (__builtin_amdgcn_ballot_w64(mt > mthr[qt]) != 0) rescale(qt, mt, pend);
       float p[4], ds[4], t[4];
       if (TAN) {
@@ -280,7 +325,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
       float ts = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float e = fmaf((float)si[i], c, -moff);
+        float e = fmaf(sv[i], c, -moff);
         if (MASK && key0 + i >= L) e = -INFINITY;
         p[i] = fast_exp2(e);
         if (TAN) {
@@ -342,7 +387,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   load_keys(0, ka_);
   int j = 0;
   // routed video tiles in pairs (full, unmasked)
-  for (; j + 1 < a.T; j += 2) {
+  for (; j + 1 < Tu; j += 2) {
     ValRegs va, vb;
     u32x2 pa[kQT], pbb[kQT];
     load_vals(j, va);
@@ -359,7 +404,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     u32x2 pb[kQT];
     load_vals(j, vr);
     load_keys(j + 1 < J ? j + 1 : J - 1, kb_);
-    if (j < a.T)
+    if (j < Tu)
       stage(ka_, vr, j, pb, nullptr, std::false_type{});
     else
       stage(ka_, vr, j, pb, nullptr, std::true_type{});
@@ -527,7 +572,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
         }
       }
     }
-    const unsigned char* rec = a.comp + ((int64_t)bh * a.Mb + m) * kRec;
+    const unsigned char* rec = a.comp + ((int64_t)bh * a.Mq + mq) * kRec;
     const float* zc = reinterpret_cast<const float*>(rec + 32768);
     const float* dzc = reinterpret_cast<const float*>(rec + 33024);
     float dn = 0.f, ddn = 0.f;
@@ -551,7 +596,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     dn = dn >= 0.f ? dn + a.eps_l : dn - a.eps_l;
     const float rdn = 1.f / dn;
     if (TAN) ddn = sum_over_groups(ddn);
-    const float al = a.alpha[(int64_t)h * a.alpha_stride + m];
+    const float al = a.alpha[(int64_t)h * a.alpha_stride + mq];
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
       const int vt_ = cpair + cc;
@@ -600,13 +645,13 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
 template <typename T16, bool PRE>
 static void launch_fwd(const FwdArgs& a, bool tan, bool linear, int nblocks, hipStream_t st) {
   if (tan && linear)
-    fwd_jvp_kernel<T16, true, true, PRE><<<nblocks, 256, 0, st>>>(a);
+    fwd_jvp_kernel<T16, true, true, PRE, false><<<nblocks, 256, 0, st>>>(a);
   else if (tan)
-    fwd_jvp_kernel<T16, true, false, PRE><<<nblocks, 256, 0, st>>>(a);
+    fwd_jvp_kernel<T16, true, false, PRE, false><<<nblocks, 256, 0, st>>>(a);
   else if (linear)
-    fwd_jvp_kernel<T16, false, true, false><<<nblocks, 256, 0, st>>>(a);
+    fwd_jvp_kernel<T16, false, true, false, false><<<nblocks, 256, 0, st>>>(a);
   else
-    fwd_jvp_kernel<T16, false, false, false><<<nblocks, 256, 0, st>>>(a);
+    fwd_jvp_kernel<T16, false, false, false, false><<<nblocks, 256, 0, st>>>(a);
 }
 
 }  // namespace sla2h
@@ -666,7 +711,11 @@ extern "C" int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, cons
     a.prescale = (fr == 0.5f && ex > -100 && ex < 100) ? 1 : 0;
   }
   a.c_log2 = scale * 1.4426950408889634f;
+  a.c16 = a.c_log2;
   a.eps_l = eps_l;
+  a.qshift = 0;
+  a.Mq = Nb;
+  a.ragged = -1;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int nblocks = (int)(8 * per_xcd);
   if (dtype == SLA2H_DTYPE_BF16) {
@@ -676,6 +725,67 @@ extern "C" int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, cons
       launch_fwd<BF16, false>(a, tan, linear, nblocks, st);
   } else {
     launch_fwd<F16, false>(a, tan, linear, nblocks, st);
+  }
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_fwd_jvp_1d(const void* q, const void* dq, const void* kt, const void* vt,
+                                const void* comp, const float* alpha, int alpha_stride,
+                                const int32_t* lut, int dtype, int B, int H, int64_t L, int D,
+                                int bq, int bk, int T, float scale, float eps_l, float* o,
+                                float* dout, void* stream) {
+  SLA2H_CHECK_ARG(q && dq && kt && vt && comp && alpha && lut && o && dout);
+  SLA2H_CHECK_ARG(D == kTa && bk == kTa && alpha_stride >= 0);
+  SLA2H_CHECK_ARG(bq == 64 || bq == 128 || bq == 256);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && L > 0 && scale > 0.f);
+  const int Nb = (int)((L + bk - 1) / bk);
+  SLA2H_CHECK_ARG(T >= 1 && T <= Nb && T <= kMaxTiles);
+  const int64_t nwork = 2ll * Nb * B * H;
+  const int64_t per_xcd = (nwork + 7) / 8;
+  SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31));
+  FwdArgs a = {};
+  a.q = static_cast<const uint16_t*>(q);
+  a.dq = static_cast<const uint16_t*>(dq);
+  a.kt = static_cast<const uint16_t*>(kt);
+  a.vt = static_cast<const uint16_t*>(vt);
+  a.comp = static_cast<const unsigned char*>(comp);
+  a.alpha = alpha;
+  a.lut = lut;
+  a.o = o;
+  a.dout = dout;
+  a.L = L;
+  a.H = H;
+  a.Nb = Nb;
+  a.Np = Nb;
+  a.Mb = Nb;
+  a.T = T;
+  a.n_tail = 0;
+  a.alpha_stride = alpha_stride;
+  a.nwork = (int)nwork;
+  a.per_xcd = (int)per_xcd;
+  a.scale = scale;
+  {
+    int ex;
+    const float fr = frexpf(scale, &ex);
+    a.prescale = (fr == 0.5f && ex > -100 && ex < 100) ? 1 : 0;
+  }
+  a.c_log2 = scale * 1.4426950408889634f;
+  a.eps_l = eps_l;
+  a.qshift = bq == 64 ? 0 : (bq == 128 ? 1 : 2);
+  a.Mq = (int)((L + bq - 1) / bq);
+  a.ragged = (L % kTa) ? Nb - 1 : -1;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nblocks = (int)(8 * per_xcd);
+  if (dtype == SLA2H_DTYPE_BF16 && a.prescale) {
+    a.c16 = 1.4426950408889634f;  // the Q operands carry the scale
+    fwd_jvp_kernel<BF16, true, true, true, true><<<nblocks, 256, 0, st>>>(a);
+  } else if (dtype == SLA2H_DTYPE_BF16) {
+    a.c16 = a.c_log2;
+    fwd_jvp_kernel<BF16, true, true, false, true><<<nblocks, 256, 0, st>>>(a);
+  } else {
+    a.c16 = a.c_log2;
+    fwd_jvp_kernel<F16, true, true, false, true><<<nblocks, 256, 0, st>>>(a);
   }
   return (int)hipGetLastError();
 }

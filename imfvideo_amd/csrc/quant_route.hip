@@ -449,6 +449,55 @@ static int launch_quant_pool(const QuantPoolArgs& a, int ntens, int dtype, hipSt
   return (int)hipGetLastError();
 }
 
+// Block means for the 1-D router (blocks of blk rows, the last one ragged):
+// one block of one (b, h) per workgroup, one thread per channel, sequential
+// fp32 sum over the block's real rows, then / count, then the optional
+// projection out[e] = sum_d mean[d] proj[e][d] (sequential, no contraction).
+template <typename T16>
+__global__ __launch_bounds__(64) void pool_blocks_kernel(const uint16_t* __restrict__ x, int64_t L,
+                                                        int blk, int nblk,
+                                                        const float* __restrict__ proj,
+                                                        int transposed, float* __restrict__ out) {
+  __shared__ float vec[kTile];
+  const int j = blockIdx.x, bh = blockIdx.y, d = threadIdx.x;
+  const int64_t r0 = (int64_t)j * blk;
+  const int cnt = (int)((L - r0) < blk ? (L - r0) : blk);
+  const uint16_t* src = x + ((int64_t)bh * L + r0) * kTile + d;
+  float acc = 0.f;
+  for (int rr = 0; rr < cnt; ++rr) acc = acc + T16::to_f32(src[(int64_t)rr * kTile]);
+  vec[d] = acc / (float)cnt;
+  __syncthreads();
+  float outv = vec[d];
+  if (proj != nullptr) {
+    const float* pr = proj + d * kTile;
+    float p = 0.f;
+    for (int e = 0; e < kTile; ++e) p = p + vec[e] * pr[e];
+    outv = p;
+  }
+  if (transposed)
+    out[((int64_t)bh * kTile + d) * nblk + j] = outv;
+  else
+    out[((int64_t)bh * nblk + j) * kTile + d] = outv;
+}
+
+extern "C" int sla2h_pool_blocks(const void* x, int dtype, int64_t BH, int64_t L, int D, int blk,
+                                 const float* proj, int transposed, float* out, void* stream) {
+  SLA2H_CHECK_ARG(x && out);
+  SLA2H_CHECK_ARG(D == kTile && blk >= 1 && blk <= 4096);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(BH > 0 && BH <= 65535 && L > 0);
+  const int64_t nblk = (L + blk - 1) / blk;
+  SLA2H_CHECK_ARG(nblk < (1ll << 31));
+  dim3 grid((unsigned)nblk, (unsigned)BH);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto X = static_cast<const uint16_t*>(x);
+  if (dtype == SLA2H_DTYPE_BF16)
+    pool_blocks_kernel<BF16><<<grid, kTile, 0, st>>>(X, L, blk, (int)nblk, proj, transposed, out);
+  else
+    pool_blocks_kernel<F16><<<grid, kTile, 0, st>>>(X, L, blk, (int)nblk, proj, transposed, out);
+  return (int)hipGetLastError();
+}
+
 extern "C" int sla2h_version(void) { return 1; }
 
 extern "C" const char* sla2h_error_string(int code) {

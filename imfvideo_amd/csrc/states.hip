@@ -471,7 +471,9 @@ extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v,
   SLA2H_CHECK_ARG(D == kT && E == kT);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535);
-  SLA2H_CHECK_ARG(Np > 0 && (int64_t)Np * E <= L);
+  // Np * E <= L for cube video tiles; Np = Nb (every tile, the last one
+  // possibly partial) for 1-D key blocks
+  SLA2H_CHECK_ARG(Np > 0 && (int64_t)(Np - 1) * E < L);
   const bool tan = dk != nullptr;
   if (tan) SLA2H_CHECK_ARG(dv && dHb && dzb && kt);
   if (tan && Hall) SLA2H_CHECK_ARG(dHall && dzall);

@@ -411,3 +411,63 @@ def train_bwd(q, k, v, alpha, fwd, do, scale=None, stage_events=None):
         B, H, L, D, E_TILE, float(scale), dk.data_ptr(), dv.data_ptr(), st), "sla2h_bwd_dkdv")
     d_alpha = seg * alpha * (1.0 - alpha)
     return dq, dk, dv, d_alpha
+
+
+# ---------------------------------------------------------------------------
+# 1-D SLA2 blocks: query blocks of bq rows, key blocks of 64 rows
+# ---------------------------------------------------------------------------
+
+def pool_blocks(x, blk, proj=None, transposed=False):
+    """Block means of x (B,H,L,64) 16-bit over blk rows (+ projection) -> fp32
+    (B,H,nblk,64), or (B,H,64,nblk) when transposed."""
+    _need_gpu(x, proj)
+    x = _bhld(x, "x")
+    B, H, L, D = x.shape
+    nblk = -(-L // blk)
+    shape = (B, H, D, nblk) if transposed else (B, H, nblk, D)
+    out = torch.empty(shape, device=x.device, dtype=torch.float32)
+    if proj is not None:
+        proj = proj.detach().to(x.device, torch.float32).contiguous()
+    _lib.check(_lib.load().sla2h_pool_blocks(
+        x.data_ptr(), _dtype_code(x), B * H, L, D, blk, _ptr(proj), 1 if transposed else 0,
+        out.data_ptr(), _stream(x.device)), "sla2h_pool_blocks")
+    return out
+
+
+def route_1d(q, k, topk_frac, bq, bk=E_TILE, proj_q=None, proj_k=None):
+    """1-D router: pooled-score hard top-k -> (lut (B,H,ceil(L/bq),T) int32, T)."""
+    if bk != E_TILE:
+        raise ValueError(f"key blocks must be {E_TILE} rows, got {bk}")
+    B, H, L, D = q.shape
+    nb = -(-L // bk)
+    T = max(1, min(nb, int(topk_frac * nb)))
+    qpool = pool_blocks(q, bq, proj_q)
+    kpool_t = pool_blocks(k, bk, proj_k, transposed=True)
+    return route_topk(qpool, kpool_t, T, D ** -0.5), T
+
+
+def jvp_1d(q, k, v, dq, dk, dv, alpha, lut, bq, scale=None, eps_l=1e-5, return_aux=False):
+    """1-D SLA2 attention and its JVP on given routing -> (o, do) fp32."""
+    _need_gpu(q, k, v, dq, dk, dv, lut)
+    q, k, v, dq, dk, dv = (_bhld(t, "qkv") for t in (q, k, v, dq, dk, dv))
+    B, H, L, D = q.shape
+    nb = -(-L // E_TILE)
+    mq = -(-L // bq)
+    lut = lut.to(torch.int32).contiguous()
+    if lut.dim() != 4 or tuple(lut.shape[:3]) != (B, H, mq):
+        raise ValueError(f"lut: expected (B, H, {mq}, T), got {tuple(lut.shape)}")
+    T = lut.shape[-1]
+    alpha = _alpha_rows(alpha, H, mq, q.device)
+    scale = D ** -0.5 if scale is None else scale
+    st = linear_states(k, v, nb, dk, dv, with_sums=False)
+    comp = complement(st, lut, nb)
+    o = torch.empty(B, H, L, D, device=q.device, dtype=torch.float32)
+    do = torch.empty_like(o)
+    _lib.check(_lib.load().sla2h_fwd_jvp_1d(
+        q.data_ptr(), dq.data_ptr(), st["kt"].data_ptr(), st["vt"].data_ptr(), comp.data_ptr(),
+        alpha.data_ptr(), alpha.stride(0), lut.data_ptr(), _dtype_code(q), B, H, L, D, bq,
+        E_TILE, T, float(scale), float(eps_l), o.data_ptr(), do.data_ptr(), _stream(q.device)),
+        "sla2h_fwd_jvp_1d")
+    if return_aux:
+        return o, do, dict(comp=comp, **st)
+    return o, do

@@ -149,6 +149,40 @@ int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, const void* vt,
                   float scale, float eps_l, int flags,
                   float* o, float* dout, void* stream);
 
+/* ---- 1-D SLA2 blocks (query blocks of bq rows, key blocks of 64) -------- */
+
+/*
+ * Block means for the 1-D router: out[bh][j][d] (or [bh][d][j] when
+ * transposed) = sum over the real rows t of block j (blk rows, the last block
+ * ragged) of x[bh][t][d] / count, sequential fp32 in row order; then, when
+ * proj (D,D) fp32 is given, out[e] = sum_d mean[d] proj[e][d] (sequential, no
+ * contraction).  Replaces _block_pool + projections of route_blocks
+ * (models/sla2_mla_jvp.py:51-99) and mean_pool_smooth + proj_q/proj_k of the
+ * SLA2 Router (models/sla2_vendor/kernel_router.py:373-404,
+ * models/sla2_vendor/router.py:66-75); the smooth-k shift is a per-row
+ * constant of the scores and leaves the top-k selection unchanged.
+ * Feed the pooled queries and the transposed pooled keys to sla2h_route_topk
+ * with Mb = ceil(L/bq) and Np = ceil(L/64).
+ */
+int sla2h_pool_blocks(const void* x, int dtype, int64_t BH, int64_t L, int D, int blk,
+                      const float* proj, int transposed, float* out, void* stream);
+
+/*
+ * 1-D SLA2 attention with forward-mode JVP (sla2_mla_jvp): as sla2h_fwd_jvp but
+ * with 16-bit primal scores S = q.k^T (fp32 accumulate; no INT8), query blocks
+ * of bq rows (bq = 64, 128 or 256; lut (B,H,ceil(L/bq),T), alpha (H,
+ * ceil(L/bq)) and comp records per query block), every key block routable
+ * (Np = Nb, the last one partial when 64 does not divide L) and no prefix
+ * tail.  kt, vt from sla2h_linear_states(Np = Nb) with tangents; comp from
+ * sla2h_complement(Mb = ceil(L/bq), Np = Nb).  Tangents are required.
+ * Replaces _sla2_sparse_jvp_kernel + _linear_jvp + the mix of sla2_mla_jvp
+ * (models/sla2_mla_jvp.py:108-237, 258-342, 348-385).
+ */
+int sla2h_fwd_jvp_1d(const void* q, const void* dq, const void* kt, const void* vt,
+                     const void* comp, const float* alpha, int alpha_stride, const int32_t* lut,
+                     int dtype, int B, int H, int64_t L, int D, int bq, int bk, int T,
+                     float scale, float eps_l, float* o, float* dout, void* stream);
+
 /* ---- training forward (the module's autograd forward) ------------------ */
 
 /*

@@ -625,3 +625,130 @@ def train_dense_f64(q, k, v, alpha_logit, lut, Np, prefix_len, eps=EPS_L):
     fwd = {"o_s": o_s, "o_l": o_l, "lse": lse, "den": den, "qphi": qphi,
            "htot": kphi.transpose(-1, -2) @ v, "ztot": kphi.sum(-2)}
     return o, {n: t.detach() for n, t in fwd.items()}
+
+
+# ---------------------------------------------------------------------------
+# 1-D SLA2 blocks (query blocks of bq rows, key blocks of bk = 64 rows):
+# route_blocks and sla2_mla_jvp (models/sla2_mla_jvp.py:51-99, 108-385).
+# ---------------------------------------------------------------------------
+def route_1d(q, k, topk_frac, bq, bk=E, proj_q=None, proj_k=None):
+    """route_blocks with the canonical fp32 order (no smooth-k: the per-(b,h)
+    key-mean shift adds a per-row constant to the scores).  Returns (lut, T)."""
+    q, k = _np(q), _np(k)
+    L, D = q.shape[-2:]
+    mq, nb = -(-L // bq), -(-L // bk)
+    qp = project_pool(pool_tiles(q, mq, L, block=bq), proj_q)
+    kp = project_pool(pool_tiles(k, nb, L, block=bk), proj_k)
+    pc = route_scores(qp, kp, D ** -0.5)
+    T = topk_count(topk_frac, nb)
+    return topk_rows(pc, T), T
+
+
+def jvp_1d(q, k, v, dq, dk, dv, alpha, lut, bq, bk=E, t16=torch.float16, eps=EPS_L):
+    """Blockwise restatement of sla2_mla_jvp (models/sla2_mla_jvp.py:348-385):
+    _sla2_sparse_jvp_kernel (:108-197) over the routed key blocks -- 16-bit
+    score operands, exact running maximum, P and T = P dS rounded to t16 for
+    the P.V, T.V, P.dV products, l and mu from the unrounded P, T (products
+    accumulated in fp32; the reference accumulates these dots in fp16) -- and
+    _linear_jvp (:258-342): fp32 phi, per-key-block states, complement
+    H_all - sum over the routed blocks, den + eps (unsigned), quotient rule;
+    o = a o_s + (1-a) o_l per query block.  t16=None: no rounding (exact mode).
+    Returns (o, do) fp32 (B,H,L,D)."""
+    B, H, L, D = q.shape
+    nb, mq = -(-L // bk), -(-L // bq)
+    lut = torch.as_tensor(np.asarray(lut)).long()
+    T = lut.shape[-1]
+    dt = torch.float64 if t16 is None else torch.float32
+    r16 = (lambda x: x) if t16 is None else (lambda x: x.to(t16).to(dt))
+    f = lambda x: torch.as_tensor(x).to(dt)
+    q, k, v, dq, dk, dv = (f(t) for t in (q, k, v, dq, dk, dv))
+    scale = D ** -0.5
+    c = scale * LOG2E if t16 is None else float(np.float32(np.float32(scale) * np.float32(LOG2E)))
+
+    def qblocks(x):
+        pad = mq * bq - L
+        if pad:
+            x = torch.cat([x, x.new_zeros(B, H, pad, x.shape[-1])], 2)
+        return x.reshape(B, H, mq, bq, x.shape[-1])
+
+    def kblocks(x):
+        pad = nb * bk - L
+        if pad:
+            x = torch.cat([x, x.new_zeros(B, H, pad, x.shape[-1])], 2)
+        return x.reshape(B, H, nb, bk, x.shape[-1])
+
+    Qb, dQb = qblocks(q), qblocks(dq)
+    Kb, dKb, Vb, dVb = kblocks(k), kblocks(dk), kblocks(v), kblocks(dv)
+    gat = lambda xb, n: torch.gather(xb, 2, n.view(B, H, mq, 1, 1).expand(B, H, mq, bk, D))
+    m_i = torch.full((B, H, mq, bq), -math.inf, dtype=dt)
+    l_i = torch.zeros(B, H, mq, bq, dtype=dt)
+    mu = torch.zeros(B, H, mq, bq, dtype=dt)
+    acc_o = torch.zeros(B, H, mq, bq, D, dtype=dt)
+    acc_do = torch.zeros(B, H, mq, bq, D, dtype=dt)
+    key_pos = torch.arange(bk)
+    for j in range(T):
+        n = lut[..., j]
+        kn, dkn, vn, dvn = gat(Kb, n), gat(dKb, n), gat(Vb, n), gat(dVb, n)
+        s_f = Qb @ kn.transpose(-1, -2)
+        ds = (dQb @ kn.transpose(-1, -2) + Qb @ dkn.transpose(-1, -2)) * scale
+        valid = (n[..., None] * bk + key_pos) < L
+        s2 = (s_f * c).masked_fill(~valid[..., None, :], -math.inf)
+        m_new = torch.maximum(m_i, s2.amax(-1))
+        al = torch.exp2(m_i - m_new)
+        p = torch.exp2(s2 - m_new[..., None])
+        t = p * ds
+        l_i = l_i * al + p.sum(-1)
+        mu = mu * al + t.sum(-1)
+        pc, tc = r16(p), r16(t)
+        acc_o = acc_o * al[..., None] + pc @ vn
+        acc_do = acc_do * al[..., None] + tc @ vn + pc @ dvn
+        m_i = m_new
+    o_s = acc_o / l_i[..., None]
+    do_s = acc_do / l_i[..., None] - (mu / l_i)[..., None] * o_s
+
+    qphi, dqphi = phi_jvp(q, dq)
+    kphi, dkphi = phi_jvp(k, dk)
+    if t16 is None:
+        qphi, dqphi, kphi, dkphi = (x.double() for x in (qphi, dqphi, kphi, dkphi))
+    kb, dkb = kblocks(kphi), kblocks(dkphi)
+    Hb = kb.transpose(-1, -2) @ Vb
+    dHb = dkb.transpose(-1, -2) @ Vb + kb.transpose(-1, -2) @ dVb
+    zb, dzb = kb.sum(3), dkb.sum(3)
+    gat4 = lambda x: torch.gather(x, 2, lut.view(B, H, mq * T, 1, 1).expand(B, H, mq * T, D, D)
+                                  ).view(B, H, mq, T, D, D).sum(3)
+    gat3 = lambda x: torch.gather(x, 2, lut.view(B, H, mq * T, 1).expand(B, H, mq * T, D)
+                                  ).view(B, H, mq, T, D).sum(3)
+    Hc = Hb.sum(2)[:, :, None] - gat4(Hb)
+    dHc = dHb.sum(2)[:, :, None] - gat4(dHb)
+    zc = zb.sum(2)[:, :, None] - gat3(zb)
+    dzc = dzb.sum(2)[:, :, None] - gat3(dzb)
+    qg, dqg = qblocks(qphi), qblocks(dqphi)
+    num = qg @ Hc
+    dnum = dqg @ Hc + qg @ dHc
+    den = (qg * zc[..., None, :]).sum(-1) + eps
+    dden = (dqg * zc[..., None, :]).sum(-1) + (qg * dzc[..., None, :]).sum(-1)
+    o_l = num / den[..., None]
+    do_l = (dnum - o_l * dden[..., None]) / den[..., None]
+    a = torch.as_tensor(alpha).to(dt).reshape(1, H, mq, 1, 1)
+    o = a * o_s + (1.0 - a) * o_l
+    do = a * do_s + (1.0 - a) * do_l
+    return (o.reshape(B, H, mq * bq, D)[:, :, :L].float(),
+            do.reshape(B, H, mq * bq, D)[:, :, :L].float())
+
+
+def dense_1d_f64(q, k, v, lut, alpha, bq, bk=E, eps=EPS_L):
+    """sla2_dense_ref (models/sla2_mla_jvp.py:388-418) in float64: masked softmax
+    over the routed key blocks plus the complement linear branch, per-block alpha."""
+    B, H, L, D = q.shape
+    lut = torch.as_tensor(np.asarray(lut)).long()
+    nb = -(-L // bk)
+    mc = torch.zeros(B, H, lut.shape[2], nb, dtype=torch.float64)
+    mc.scatter_(-1, lut, 1.0)
+    m = mc.repeat_interleave(bq, dim=-2).repeat_interleave(bk, dim=-1)[..., :L, :L]
+    s = (q @ k.transpose(-1, -2)) * D ** -0.5
+    o_s = torch.softmax(s.masked_fill(m <= 0, -math.inf), dim=-1) @ v
+    w = (torch.softmax(q, -1) @ torch.softmax(k, -1).transpose(-1, -2)) * (1.0 - m)
+    o_l = (w @ v) / (w.sum(-1, keepdim=True) + eps)
+    a = torch.as_tensor(alpha, dtype=torch.float64).repeat_interleave(bq, dim=-1)[:, :L]
+    a = a.view(1, H, L, 1)
+    return a * o_s + (1.0 - a) * o_l

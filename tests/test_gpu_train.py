@@ -229,3 +229,48 @@ def test_train_bwd_config3_full_size():
         ref = O.train_bwd(f["q"][:, sl], f["k"][:, sl], f["v"][:, sl], alpha[sl], lut[:, sl], Np, P,
                           fwd, do[:, sl].float())
         compare_bwd(got, ref, f"h{h} ", sl)
+
+
+# ---------------------------------------------------------------------------
+# 1-D SLA2 JVP (sla2_mla_jvp): bit-exact routing, outputs against O.jvp_1d
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("L,bq,dt", [(512, 128, torch.float16), (583, 128, torch.float16),
+                                      (640, 64, torch.bfloat16), (583, 256, torch.bfloat16)])
+def test_sla2_mla_jvp_small(L, bq, dt):
+    say("sla2_mla_jvp", L, bq, dt)
+    from imfvideo_amd.sla2_mla_jvp import route_blocks, sla2_mla_jvp
+    B, H = 2, 2
+    g = torch.Generator().manual_seed(L + bq)
+    x = [torch.randn(B, H, L, 64, generator=g).to(dt) for _ in range(3)]
+    d = [(torch.randn(B, H, L, 64, generator=g) * 0.1).to(dt) for _ in range(3)]
+    pq = torch.eye(64) + 0.05 * torch.randn(64, 64, generator=g)
+    lut, T = route_blocks(cuda(x[0]), cuda(x[1]), 0.3, bq, 64, proj_q=cuda(pq))
+    elut, eT = O.route_1d(x[0].float(), x[1].float(), 0.3, bq, proj_q=pq)
+    assert T == eT and np.array_equal(lut.cpu().numpy(), elut)
+    mq = -(-L // bq)
+    alpha = torch.rand(H, mq, generator=g) * 0.8 + 0.1
+    o, do = sla2_mla_jvp(*(cuda(t) for t in x + d), cuda(alpha), 0.3, bq, 64, lut=lut, T=T)
+    eo, edo = O.jvp_1d(*(t.float() for t in x + d), alpha, elut, bq, t16=dt)
+    o, do = o.cpu(), do.cpu()
+    print(f"  o max {max_abs(o, eo):.2e} rel {rel_l2(o, eo):.2e}  do max {max_abs(do, edo):.2e} "
+          f"rel {rel_l2(do, edo):.2e}", flush=True)
+    assert max_abs(o, eo) < TOL_MAX and rel_l2(o, eo) < TOL_REL
+    assert max_abs(do, edo) < TOL_MAX and rel_l2(do, edo) < TOL_REL
+
+
+def test_sla2_mla_jvp_config4_shape():
+    say("sla2_mla_jvp (1,8,29952,64) bq=128")
+    from imfvideo_amd.sla2_mla_jvp import sla2_mla_jvp
+    ins, Np, P = config_inputs(3)
+    x = [ins[n].half() for n in ("q", "k", "v", "dq", "dk", "dv")]
+    o, do = sla2_mla_jvp(*(cuda(t) for t in x), 0.9, 0.1, 128, 64)
+    o, do = o.cpu(), do.cpu()
+    assert torch.isfinite(o).all() and torch.isfinite(do).all()
+    for h in (0, 5):
+        sl = slice(h, h + 1)
+        xs = [t[:, sl].float() for t in x]
+        lut, T = O.route_1d(xs[0], xs[1], 0.1, 128)
+        eo, edo = O.jvp_1d(*xs, torch.full((1, 234), 0.9), lut, 128)
+        print(f"  h{h} o rel {rel_l2(o[:, sl], eo):.2e} do rel {rel_l2(do[:, sl], edo):.2e}", flush=True)
+        assert max_abs(o[:, sl], eo) < TOL_MAX and rel_l2(o[:, sl], eo) < TOL_REL
+        assert max_abs(do[:, sl], edo) < TOL_MAX and rel_l2(do[:, sl], edo) < TOL_REL

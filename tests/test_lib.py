@@ -43,8 +43,8 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     # D, E, Np, T, scale, eps_l, flags, o, dout, stream: dq without the key operand tiles
     assert lib.sla2h_fwd_jvp(1, 1, None, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 128, 64,
                              64, 2, 1, 0.125, 1e-5, 0, 1, 1, None) == bad
-    assert lib.sla2h_linear_states(1, None, 1, None, 1, 1, 1, 100, 64, 64, 2, 1, None, 1, None,
-                                   1, None, 1, None, 1, None, None) == bad  # Np*E > L
+    assert lib.sla2h_linear_states(1, None, 1, None, 1, 1, 1, 100, 64, 64, 3, 1, None, 1, None,
+                                   1, None, 1, None, 1, None, None) == bad  # Np > ceil(L/E)
     # tangent states without the key operand tiles
     assert lib.sla2h_linear_states(1, 1, 1, 1, 1, 1, 1, 128, 64, 64, 2, 1, 1, 1, 1,
                                    None, None, None, None, 1, None, None) == bad

@@ -384,3 +384,56 @@ def test_train_bwd_rounded_mode_near_exact_gradient():
     for name, w in zip(("dq", "dk", "dv", "d_alpha"), want):
         err = ((got[name].double() - w).norm() / w.norm()).item()
         assert err < 5e-2, (name, err)
+
+
+def _case_1d(seed, L, B=1, H=2, bq=128, frac=0.3):
+    g = torch.Generator().manual_seed(seed)
+    x = [torch.randn(B, H, L, 64, generator=g, dtype=torch.float64) for _ in range(3)]
+    d = [torch.randn(B, H, L, 64, generator=g, dtype=torch.float64) * 0.1 for _ in range(3)]
+    lut, T = O.route_1d(x[0].float(), x[1].float(), frac, bq)
+    mq = -(-L // bq)
+    alpha = torch.rand(H, mq, generator=g, dtype=torch.float64) * 0.8 + 0.1
+    return x, d, lut, alpha
+
+
+def test_jvp_1d_exact_mode_matches_dense_jvp():
+    # the reference's own dense oracle (sla2_dense_ref) and torch.func.jvp of it
+    for L, bq in ((512, 128), (583, 128), (640, 64)):
+        x, d, lut, alpha = _case_1d(L, L, bq=bq)
+        f = lambda q_, k_, v_: O.dense_1d_f64(q_, k_, v_, lut, alpha, bq)
+        eo, edo = torch.func.jvp(f, tuple(x), tuple(d))
+        o, do = O.jvp_1d(*x, *d, alpha, lut, bq, t16=None)
+        assert ((o.double() - eo).norm() / eo.norm()).item() < 1e-6, L
+        assert ((do.double() - edo).norm() / edo.norm()).item() < 1e-6, L
+
+
+def test_jvp_1d_rounded_within_reference_fp16_tolerance():
+    # tests/test_sla2_jvp.py:41-42 bounds for fp16 operands: o 2e-2, do 5e-2
+    x, d, lut, alpha = _case_1d(3, 583)
+    x16 = [t.half().double() for t in x]
+    d16 = [t.half().double() for t in d]
+    f = lambda q_, k_, v_: O.dense_1d_f64(q_, k_, v_, lut, alpha, 128)
+    eo, edo = torch.func.jvp(f, tuple(x16), tuple(d16))
+    o, do = O.jvp_1d(*[t.float() for t in x16], *[t.float() for t in d16], alpha.float(), lut, 128)
+    ro = ((o.double() - eo).norm() / eo.norm()).item()
+    rdo = ((do.double() - edo).norm() / edo.norm()).item()
+    assert ro < 2e-2 and rdo < 5e-2, (ro, rdo)
+    assert ro > 1e-6  # the 16-bit roundings are in effect
+
+
+def test_route_1d_matches_brute_force_block_scores():
+    g = torch.Generator().manual_seed(4)
+    q = torch.randn(1, 2, 583, 64, generator=g).half().float()
+    k = torch.randn(1, 2, 583, 64, generator=g).half().float()
+    lut, T = O.route_1d(q, k, 0.3, 128)
+    assert lut.shape == (1, 2, 5, 3) and T == 3
+    # fp64 block means and scores: the selection agrees wherever the gap is clear
+    qb = torch.stack([q[:, :, i:i + 128].double().mean(2) for i in range(0, 583, 128)], 2)
+    kb = torch.stack([k[:, :, i:i + 64].double().mean(2) for i in range(0, 583, 64)], 2)
+    kb = kb - kb.mean(2, keepdim=True)   # smooth-k: a per-row constant shift of the scores
+    pc = (qb @ kb.transpose(-1, -2)) * 0.125
+    want = torch.topk(pc, T, -1).indices.sort(-1).values
+    got = torch.from_numpy(lut).long().sort(-1).values
+    srt = pc.sort(-1, descending=True).values
+    clear = (srt[..., T - 1] - srt[..., T]) > 1e-5
+    assert clear.any() and torch.equal(got[clear], want[clear])
