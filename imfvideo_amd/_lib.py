@@ -46,14 +46,16 @@ SIGNATURES = {
                                       _c_i64, _c_int, _c_int, _c_int, _c_int, _c_f, _p, _p, _p,
                                       _p]),
     "sla2h_linear_states_qat": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _c_i64, _c_int, _c_int,
-                                         _p, _p, _p, _p, _p]),
+                                         _p, _p, _p, _p, _p, _p]),
+    "sla2h_sparse_fwd_1d": (_c_int, [_p, _p, _p, _p, _c_int, _c_int, _c_int, _c_i64, _c_int,
+                                     _c_int, _c_int, _c_int, _c_f, _p, _p, _p, _p]),
     "sla2h_linear_mix_qat": (_c_int, [_p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int,
                                       _c_i64, _c_int, _c_int, _c_f, _p, _p, _p, _p]),
     "sla2h_bwd_prep": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int,
                                 _c_i64, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                 _p]),
-    "sla2h_complement_bwd": (_c_int, [_p, _p, _p, _c_int, _c_int, _c_int, _c_int, _p, _p, _p,
-                                      _p]),
+    "sla2h_complement_bwd": (_c_int, [_p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p,
+                                      _p, _p, _p]),
     "sla2h_bwd_dq": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _c_int, _c_int,
                               _c_int, _c_i64, _c_int, _c_int, _c_int, _c_f, _p, _p]),
     "sla2h_bwd_dkdv": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int,

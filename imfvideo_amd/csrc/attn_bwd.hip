@@ -81,6 +81,7 @@ struct PrepArgs {
   uint16_t* dotf;
   int64_t L;
   int Nb, H, alpha_stride;
+  int Mq, qshift;  // alpha rows / seg: query blocks of 64 << qshift rows
 };
 
 template <typename T16>
@@ -126,7 +127,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
   ld(a.o_s, osb);
   ld(a.o_l, olb);
   ld(a.qphi, qpb);
-  const float al = a.alpha[(int64_t)h * a.alpha_stride + blk];
+  const float al = a.alpha[(int64_t)h * a.alpha_stride + (blk >> a.qshift)];
   const float den = valid ? a.den[(int64_t)bh * a.L + row] : 1.f;
   float dsum = 0.f, segp = 0.f, ssum = 0.f;
 #pragma unroll
@@ -168,7 +169,8 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
   for (int m = 32; m >= 1; m >>= 1) segp += __shfl_xor(segp, m, 64);
   if ((tid & 63) == 0) red[tid >> 6] = segp;
   __syncthreads();
-  if (tid == 0) atomicAdd(a.seg + (int64_t)h * a.Nb + blk, (red[0] + red[1]) + (red[2] + red[3]));
+  if (tid == 0)
+    atomicAdd(a.seg + (int64_t)h * a.Mq + (blk >> a.qshift), (red[0] + red[1]) + (red[2] + red[3]));
 
   // P[d][e] = sum_rows qphi[row][d] g[row][e] on fp32 MFMA: wave w owns d rows 16w..16w+15
   {
@@ -238,6 +240,7 @@ struct DqArgs {
   uint16_t* dq;
   int64_t L;
   int Nb, J, nwork, per_xcd;
+  int Mq, qshift;  // LUT rows and forward records per query block of 64 << qshift rows
   float c, scale;
 };
 
@@ -256,7 +259,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
   const int64_t L = a.L;
   const int64_t base = (int64_t)bh * L;
 
-  const int32_t* lrow = a.lut + ((int64_t)bh * a.Nb + m) * a.J;
+  const int mq = m >> a.qshift;
+  const int32_t* lrow = a.lut + ((int64_t)bh * a.Mq + mq) * a.J;
   for (int j = tid; j < a.J; j += 256) {
     const int n = lrow[j];
     tiles[j] = n < 0 ? 0 : (n >= a.Nb ? a.Nb - 1 : n);
@@ -363,7 +367,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
   // epilogue: query row 64m + 16w + r, channels 16ct + 4g + i
   const int64_t row = (int64_t)m * kT + 16 * w + r;
   const bool ok = row < L;
-  const unsigned char* rec = a.comp + ((int64_t)bh * a.Nb + m) * kRecBytes;
+  const unsigned char* rec = a.comp + ((int64_t)bh * a.Mq + mq) * kRecBytes;
   const float* Hc = reinterpret_cast<const float*>(rec + kRecH);
   const float* zc = reinterpret_cast<const float*>(rec + kRecZ);
   const float* Ha = a.Hall + (int64_t)bh * kT * kT;
@@ -684,10 +688,12 @@ extern "C" int sla2h_bwd_prep(const void* dout, const void* o_s, const void* o_l
                               float* Pz, void* qtf, void* ktf, void* dotf, void* stream) {
   SLA2H_CHECK_ARG(dout && o_s && o_l && den && qphi && q && k && alpha && dos && delta && g16 &&
                   s && seg && P && Pz && qtf && ktf && dotf);
-  SLA2H_CHECK_ARG(D == kT && E == kT && alpha_stride >= 0);
+  SLA2H_CHECK_ARG(D == kT && (E == 64 || E == 128 || E == 256) && alpha_stride >= 0);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && L > 0);
   PrepArgs a;
+  a.qshift = E == 64 ? 0 : (E == 128 ? 1 : 2);
+  a.Mq = (int)((L + E - 1) / E);
   a.dout = static_cast<const uint16_t*>(dout);
   a.o_s = static_cast<const uint16_t*>(o_s);
   a.o_l = static_cast<const uint16_t*>(o_l);
@@ -707,7 +713,7 @@ extern "C" int sla2h_bwd_prep(const void* dout, const void* o_s, const void* o_l
   a.ktf = static_cast<uint16_t*>(ktf);
   a.dotf = static_cast<uint16_t*>(dotf);
   a.L = L;
-  a.Nb = (int)((L + E - 1) / E);
+  a.Nb = (int)((L + kT - 1) / kT);
   a.H = H;
   a.alpha_stride = alpha_stride;
   dim3 grid(a.Nb, B * H);
@@ -726,10 +732,10 @@ extern "C" int sla2h_bwd_dq(const void* q, const void* k, const void* v, const v
                             int64_t L, int D, int E, int J, float scale, void* dq, void* stream) {
   SLA2H_CHECK_ARG(q && k && v && dos && lse && delta && ktf && g16 && s && comp && Hall && qphi &&
                   lut_aug && dq);
-  SLA2H_CHECK_ARG(D == kT && E == kT && scale > 0.f);
+  SLA2H_CHECK_ARG(D == kT && (E == 64 || E == 128 || E == 256) && scale > 0.f);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   SLA2H_CHECK_ARG(B > 0 && H > 0 && L > 0 && J >= 1 && J <= kMaxJ);
-  const int Nb = (int)((L + E - 1) / E);
+  const int Nb = (int)((L + kT - 1) / kT);
   const int64_t nwork = (int64_t)Nb * B * H;
   const int64_t per_xcd = (nwork + 7) / 8;
   SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31) && L * kT * 2 < (1ll << 31));
@@ -751,6 +757,8 @@ extern "C" int sla2h_bwd_dq(const void* q, const void* k, const void* v, const v
   a.L = L;
   a.Nb = Nb;
   a.J = J;
+  a.qshift = E == 64 ? 0 : (E == 128 ? 1 : 2);
+  a.Mq = (int)((L + E - 1) / E);
   a.nwork = (int)nwork;
   a.per_xcd = (int)per_xcd;
   a.c = scale * 1.4426950408889634f;

@@ -205,6 +205,187 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
   }
 }
 
+// 16-bit variant of the same recurrence (_attn_fwd_qat without USE_INT8,
+// kernel_sparse_qat.py:28-117, as run by the 1-D SLA2 module): S = q.k^T on
+// 16-bit MFMA (fp32 accumulate) * scale * log2(e), exact running maximum,
+// O += round16(P) . V.  Query blocks of 64 << qshift rows share one LUT row;
+// every key block is routable (the last one possibly partial).  Wave w owns
+// queries 16w..16w+15 and all 64 keys of a tile: S^T = K Q^T leaves a lane
+// with 16 keys of one query, which packed in pairs of 16-key groups is the B
+// operand of O^T = V^T P^T on 16x16x32 (V^T from the primal vt operand tiles).
+struct Fwd16Args {
+  const uint16_t* q;
+  const uint16_t* k;
+  const uint16_t* vt;
+  const int32_t* lut;
+  uint16_t* os;
+  float* lse;
+  uint16_t* qphi;
+  int64_t L;
+  int Nb, Mq, qshift, T, nwork, per_xcd;
+  float c;  // fl32(scale * log2(e))
+};
+
+template <typename T16>
+__global__ __launch_bounds__(256, 2) void sparse_fwd16_kernel(Fwd16Args a) {
+  __shared__ int tiles[kMaxJ];
+
+  const int logical = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
+  if (logical >= a.nwork) return;
+  const int bh = __builtin_amdgcn_readfirstlane(logical / a.Nb);
+  const int m = __builtin_amdgcn_readfirstlane(logical - bh * a.Nb);
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = tid & 63, r = l & 15, g = l >> 4;
+  const int64_t L = a.L;
+  const int64_t qkbase = (int64_t)bh * L;
+  const int64_t qrow = (int64_t)m * kT + 16 * w + r;
+  const bool qok = qrow < L;
+
+  const int32_t* lrow = a.lut + ((int64_t)bh * a.Mq + (m >> a.qshift)) * a.T;
+  for (int j = tid; j < a.T; j += 256) {
+    const int n = lrow[j];
+    tiles[j] = n < 0 ? 0 : (n >= a.Nb ? a.Nb - 1 : n);
+  }
+
+  // phi(Q) of this lane's 16 channels 16g..16g+15, written as 16-bit
+  {
+    float x[16];
+    uint4 u0 = make_uint4(0, 0, 0, 0), u1 = u0;
+    if (qok) {
+      const uint4* src = reinterpret_cast<const uint4*>(a.q + (qkbase + qrow) * kT + 16 * g);
+      u0 = src[0];
+      u1 = src[1];
+    }
+    const uint32_t wd[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      x[2 * i] = T16::to_f32((uint16_t)(wd[i] & 0xffff));
+      x[2 * i + 1] = T16::to_f32((uint16_t)(wd[i] >> 16));
+    }
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) mx = fmaxf(mx, x[i]);
+    mx = max_over_groups(mx);
+    float den = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x[i] = __expf(x[i] - mx);
+      den += x[i];
+    }
+    den = sum_over_groups(den);
+    const float rd = 1.f / den;
+    uint32_t o[8];
+#pragma unroll
+    for (int i = 0; i < 8; ++i) o[i] = pack_pair<T16>(x[2 * i] * rd, x[2 * i + 1] * rd);
+    if (qok) {
+      uint4* dst = reinterpret_cast<uint4*>(a.qphi + (qkbase + qrow) * kT + 16 * g);
+      dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
+      dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
+    }
+  }
+  // 16-bit Q B operand: this lane's query, channels 32ks + 8g .. +7
+  u32x4 qf[2];
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks)
+    qf[ks] = qok ? *reinterpret_cast<const u32x4*>(a.q + (qkbase + qrow) * kT + 32 * ks + 8 * g)
+                 : u32x4{0, 0, 0, 0};
+  __syncthreads();
+
+  const auto rk = make_rsrc(a.k + qkbase * kT, L * kT * 2);  // key rows past L read as 0
+  const auto rv = make_rsrc(a.vt + (int64_t)bh * a.Nb * 4096, (int64_t)a.Nb * 8192);
+  struct Frags {
+    u32x4 k[4][2];  // K[16kb + r][32ks + 8g ..]
+    u32x2 v[4][4];  // [ct][w'] = V[16w' + 4g + 0..3][16ct + r]
+  };
+  auto load = [&](int j, Frags& f) {
+    const int n = __builtin_amdgcn_readfirstlane(tiles[j]);
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+        f.k[kb][ks] = buf_load16(rk, n * 8192 + ((16 * kb + r) * kT + 32 * ks + 8 * g) * 2, 0);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+      for (int ww = 0; ww < 4; ++ww) f.v[ct][ww] = buf_load8(rv, ((ct * 4 + ww) * 64 + l) * 8, n * 8192);
+  };
+
+  f32x4 acc[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+  float m_i = -INFINITY, l_i = 0.f;
+
+  auto tile = [&](const Frags& f, int j) {
+    const int n = __builtin_amdgcn_readfirstlane(tiles[j]);
+    const int64_t key0 = (int64_t)n * kT + 4 * g;
+    float s[16];
+    float lm = -INFINITY;
+#pragma unroll
+    for (int kb = 0; kb < 4; ++kb) {
+      f32x4 sc = mfma_16x16x32<T16>(f.k[kb][0], qf[0], f32x4{0.f, 0.f, 0.f, 0.f});
+      sc = mfma_16x16x32<T16>(f.k[kb][1], qf[1], sc);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        float x = sc[i] * a.c;
+        if (key0 + 16 * kb + i >= L) x = -INFINITY;
+        s[4 * kb + i] = x;
+        lm = fmaxf(lm, x);
+      }
+    }
+    lm = max_over_groups(lm);
+    const float mn = fmaxf(m_i, lm);
+    const float alpha = fast_exp2(m_i - mn);
+    float ls = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      s[i] = fast_exp2(s[i] - mn);
+      ls += s[i];
+    }
+    l_i = l_i * alpha + ls;
+    m_i = mn;
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) acc[ct] *= alpha;
+#pragma unroll
+    for (int pp = 0; pp < 2; ++pp) {
+      const u32x4 pb = u32x4{pack_pair<T16>(s[8 * pp], s[8 * pp + 1]),
+                             pack_pair<T16>(s[8 * pp + 2], s[8 * pp + 3]),
+                             pack_pair<T16>(s[8 * pp + 4], s[8 * pp + 5]),
+                             pack_pair<T16>(s[8 * pp + 6], s[8 * pp + 7])};
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const u32x4 av = u32x4{f.v[ct][2 * pp].x, f.v[ct][2 * pp].y, f.v[ct][2 * pp + 1].x,
+                               f.v[ct][2 * pp + 1].y};
+        acc[ct] = mfma_16x16x32<T16>(av, pb, acc[ct]);
+      }
+    }
+  };
+
+  const int J = a.T;
+  Frags fa, fb;
+  load(0, fa);
+  int j = 0;
+  for (; j + 1 < J; j += 2) {
+    load(j + 1, fb);
+    tile(fa, j);
+    load(j + 2 < J ? j + 2 : J - 1, fa);
+    tile(fb, j + 1);
+  }
+  if (j < J) tile(fa, j);
+
+  const float lt = sum_over_groups(l_i);
+  const float rl = 1.f / lt;
+  if (qok) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const uint32_t lo = pack_pair<T16>(acc[ct][0] * rl, acc[ct][1] * rl);
+      const uint32_t hi = pack_pair<T16>(acc[ct][2] * rl, acc[ct][3] * rl);
+      *reinterpret_cast<uint2*>(a.os + (qkbase + qrow) * kT + 16 * ct + 4 * g) = make_uint2(lo, hi);
+    }
+    if (g == 0) a.lse[qkbase + qrow] = m_i + __log2f(lt);
+  }
+}
+
 // Linear branch and mix of the training forward (_lin_fwd2 in its state form,
 // models/sla2_vendor/kernel_linear.py:274-304, and the mix at
 // models/sla2_cube_qat.py:742-744), one 64-row query block per workgroup:
@@ -223,14 +404,15 @@ template <typename T16>
 __global__ __launch_bounds__(256) void linear_mix_qat_kernel(
     const uint16_t* __restrict__ qphi, const unsigned char* __restrict__ comp,
     const float* __restrict__ Hall, const uint16_t* __restrict__ o_s,
-    const float* __restrict__ alpha, int alpha_stride, int64_t L, int Mb, int H, float eps_l,
-    uint16_t* __restrict__ o, uint16_t* __restrict__ o_l, float* __restrict__ den_out) {
+    const float* __restrict__ alpha, int alpha_stride, int64_t L, int Mq, int qshift, int H,
+    float eps_l, uint16_t* __restrict__ o, uint16_t* __restrict__ o_l, float* __restrict__ den_out) {
   __shared__ __align__(16) uint16_t hT[kT][kT + 8];  // [value channel][key channel]
   __shared__ float zs[kT];
 
   const int m = blockIdx.x, bh = blockIdx.y, h = bh % H;
+  const int mq = m >> qshift;  // record and alpha of this 64-row block's query block
   const int tid = threadIdx.x;
-  const unsigned char* rec = comp + ((int64_t)bh * Mb + m) * kRecBytes;
+  const unsigned char* rec = comp + ((int64_t)bh * Mq + mq) * kRecBytes;
   {
     const int d = tid >> 2, v0 = (tid & 3) * 16;
     const f32x4* hr = reinterpret_cast<const f32x4*>(rec + kRecH) + (d * kT + v0) / 4;
@@ -267,7 +449,7 @@ __global__ __launch_bounds__(256) void linear_mix_qat_kernel(
   dn = sum_over_groups(dn);
   dn = dn >= 0.f ? dn + eps_l : dn - eps_l;
   const float rdn = 1.f / dn;
-  const float a16 = T16::to_f32(T16::from_f32(alpha[(int64_t)h * alpha_stride + m]));
+  const float a16 = T16::to_f32(T16::from_f32(alpha[(int64_t)h * alpha_stride + mq]));
   const float b16 = T16::to_f32(T16::from_f32(1.f - a16));
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
@@ -355,10 +537,12 @@ extern "C" int sla2h_linear_mix_qat(const void* qphi, const void* comp, const fl
                                     int dtype, int B, int H, int64_t L, int D, int E, float eps_l,
                                     void* o, void* o_l, float* den, void* stream) {
   SLA2H_CHECK_ARG(qphi && comp && Hall && o_s && alpha && o && o_l && den);
-  SLA2H_CHECK_ARG(D == kT && E == kT && alpha_stride >= 0);
+  SLA2H_CHECK_ARG(D == kT && (E == 64 || E == 128 || E == 256) && alpha_stride >= 0);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && L > 0);
-  const int Mb = (int)((L + E - 1) / E);
+  const int Mb = (int)((L + kT - 1) / kT);  // 64-row blocks
+  const int Mq = (int)((L + E - 1) / E);     // query blocks of E rows (records, alpha)
+  const int qshift = E == 64 ? 0 : (E == 128 ? 1 : 2);
   dim3 grid(Mb, B * H);
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto QP = static_cast<const uint16_t*>(qphi);
@@ -367,8 +551,46 @@ extern "C" int sla2h_linear_mix_qat(const void* qphi, const void* comp, const fl
   auto O = static_cast<uint16_t*>(o);
   auto OL = static_cast<uint16_t*>(o_l);
   if (dtype == SLA2H_DTYPE_BF16)
-    linear_mix_qat_kernel<BF16><<<grid, 256, 0, st>>>(QP, C, Hall, OS, alpha, alpha_stride, L, Mb, H, eps_l, O, OL, den);
+    linear_mix_qat_kernel<BF16><<<grid, 256, 0, st>>>(QP, C, Hall, OS, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, OL, den);
   else
-    linear_mix_qat_kernel<F16><<<grid, 256, 0, st>>>(QP, C, Hall, OS, alpha, alpha_stride, L, Mb, H, eps_l, O, OL, den);
+    linear_mix_qat_kernel<F16><<<grid, 256, 0, st>>>(QP, C, Hall, OS, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, OL, den);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_sparse_fwd_1d(const void* q, const void* k, const void* vt, const int32_t* lut,
+                                   int dtype, int B, int H, int64_t L, int D, int bq, int bk,
+                                   int T, float scale, void* o_s, float* lse, void* qphi,
+                                   void* stream) {
+  SLA2H_CHECK_ARG(q && k && vt && lut && o_s && lse && qphi);
+  SLA2H_CHECK_ARG(D == kT && bk == kT && (bq == 64 || bq == 128 || bq == 256));
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && L > 0 && L * kT * 2 < (1ll << 31));
+  const int Nb = (int)((L + kT - 1) / kT);
+  SLA2H_CHECK_ARG(T >= 1 && T <= Nb && T <= kMaxJ);
+  const int64_t nwork = (int64_t)Nb * B * H;
+  const int64_t per_xcd = (nwork + 7) / 8;
+  SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31));
+  Fwd16Args a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.k = static_cast<const uint16_t*>(k);
+  a.vt = static_cast<const uint16_t*>(vt);
+  a.lut = lut;
+  a.os = static_cast<uint16_t*>(o_s);
+  a.lse = lse;
+  a.qphi = static_cast<uint16_t*>(qphi);
+  a.L = L;
+  a.Nb = Nb;
+  a.Mq = (int)((L + bq - 1) / bq);
+  a.qshift = bq == 64 ? 0 : (bq == 128 ? 1 : 2);
+  a.T = T;
+  a.nwork = (int)nwork;
+  a.per_xcd = (int)per_xcd;
+  a.c = scale * 1.4426950408889634f;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nblocks = (int)(8 * per_xcd);
+  if (dtype == SLA2H_DTYPE_BF16)
+    sparse_fwd16_kernel<BF16><<<nblocks, 256, 0, st>>>(a);
+  else
+    sparse_fwd16_kernel<F16><<<nblocks, 256, 0, st>>>(a);
   return (int)hipGetLastError();
 }

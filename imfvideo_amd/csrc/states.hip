@@ -26,8 +26,8 @@ constexpr size_t kRecBytes = 2 * 16384 + 2 * 256;
 // Products phi^T V run on 16-bit MFMA with phi split into hi + lo halves of
 // the input's 16-bit type (about 16 significant bits), fp32 accumulate.
 // ROUND (training forward): phi is rounded to the 16-bit type first, as the
-// reference's softmax(K).to(dtype) (models/sla2_cube_qat.py:728), the lo half
-// vanishes, and no operand tiles are written.
+// reference's softmax(K).to(dtype) (models/sla2_cube_qat.py:728), and the lo
+// half vanishes.  The value operand tiles are written when vt is not NULL.
 template <typename T16, bool TAN, bool ROUND = false>
 __global__ __launch_bounds__(256) void linear_states_kernel(
     const uint16_t* __restrict__ K, const uint16_t* __restrict__ dK,
@@ -163,7 +163,7 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
   __syncthreads();
 
   // value-operand tile in fragment order: thread -> (ct, w, r), 4 lane groups g
-  if (!ROUND) {
+  if (vt != nullptr) {
     const int ct = tid >> 6, vw = (tid >> 4) & 3, rr = tid & 15;
     const int c = 16 * ct + rr;
     unsigned char* base = reinterpret_cast<unsigned char*>(vt) +
@@ -507,7 +507,7 @@ extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v,
 
 extern "C" int sla2h_linear_states_qat(const void* k, const void* v, int dtype, int B, int H,
                                        int64_t L, int D, int E, float* Hb, float* zb, float* Hall,
-                                       float* zall, void* stream) {
+                                       float* zall, void* vt, void* stream) {
   SLA2H_CHECK_ARG(k && v && Hb && zb && Hall && zall);
   SLA2H_CHECK_ARG(D == kT && E == kT);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
@@ -518,9 +518,9 @@ extern "C" int sla2h_linear_states_qat(const void* k, const void* v, int dtype, 
   auto K = static_cast<const uint16_t*>(k);
   auto V = static_cast<const uint16_t*>(v);
   if (dtype == SLA2H_DTYPE_BF16)
-    linear_states_kernel<BF16, false, true><<<grid, 256, 0, st>>>(K, nullptr, V, nullptr, L, Nb, Nb, Hb, nullptr, zb, nullptr, nullptr, nullptr);
+    linear_states_kernel<BF16, false, true><<<grid, 256, 0, st>>>(K, nullptr, V, nullptr, L, Nb, Nb, Hb, nullptr, zb, nullptr, static_cast<uint16_t*>(vt), nullptr);
   else
-    linear_states_kernel<F16, false, true><<<grid, 256, 0, st>>>(K, nullptr, V, nullptr, L, Nb, Nb, Hb, nullptr, zb, nullptr, nullptr, nullptr);
+    linear_states_kernel<F16, false, true><<<grid, 256, 0, st>>>(K, nullptr, V, nullptr, L, Nb, Nb, Hb, nullptr, zb, nullptr, static_cast<uint16_t*>(vt), nullptr);
   int err = (int)hipGetLastError();
   if (err) return err;
   dim3 g2((8320 + 255) / 256, B * H);
@@ -538,13 +538,13 @@ __global__ __launch_bounds__(256) void fill_u32_kernel(uint32_t* __restrict__ p,
 }
 
 __global__ __launch_bounds__(256) void sel_scatter_kernel(const int32_t* __restrict__ lut, int Mb,
-                                                         int J, int NCq,
+                                                         int Mq, int qshift, int J, int NCq,
                                                          uint32_t* __restrict__ sel) {
   const int bh = blockIdx.y;
-  const int idx = blockIdx.x * 256 + threadIdx.x;
+  const int idx = blockIdx.x * 256 + threadIdx.x;  // over 64-row query blocks x J
   if (idx >= Mb * J) return;
   const int m = idx / J;
-  const int n = lut[(int64_t)bh * Mb * J + idx];
+  const int n = lut[((int64_t)bh * Mq + (m >> qshift)) * J + (idx - m * J)];
   if ((unsigned)n < (unsigned)Mb)
     atomicOr(&sel[((int64_t)bh * Mb + n) * NCq + (m >> 5)], 1u << (m & 31));
 }
@@ -566,15 +566,19 @@ __global__ __launch_bounds__(256) void sel_complement_kernel(const uint32_t* __r
 }
 
 extern "C" int sla2h_complement_bwd(const float* P, const float* Pz, const int32_t* lut_aug,
-                                    int B, int H, int Mb, int J, void* workspace, uint32_t* sel,
-                                    void* comp, void* stream) {
+                                    int B, int H, int Mb, int bq, int J, void* workspace,
+                                    uint32_t* sel, void* comp, void* stream) {
   SLA2H_CHECK_ARG(P && Pz && lut_aug && workspace && sel && comp);
   SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && Mb > 0 && Mb <= 4096 && J >= 1);
+  SLA2H_CHECK_ARG(bq == 64 || bq == 128 || bq == 256);
+  const int qshift = bq == 64 ? 0 : (bq == 128 ? 1 : 2);
+  const int Mq = (Mb + (1 << qshift) - 1) >> qshift;
   const int MT = (Mb + 15) / 16, NC = (Mb + 31) / 32;
   hipStream_t st = static_cast<hipStream_t>(stream);
   const int64_t nsel = (int64_t)B * H * Mb * NC;
   fill_u32_kernel<<<(unsigned)((nsel + 255) / 256), 256, 0, st>>>(sel, nsel);
-  sel_scatter_kernel<<<dim3((Mb * J + 255) / 256, B * H), 256, 0, st>>>(lut_aug, Mb, J, NC, sel);
+  sel_scatter_kernel<<<dim3((Mb * J + 255) / 256, B * H), 256, 0, st>>>(lut_aug, Mb, Mq, qshift, J,
+                                                                       NC, sel);
   auto cbits = static_cast<uint32_t*>(workspace);
   sel_complement_kernel<<<dim3((NC * MT * 16 + 255) / 256, B * H), 256, 0, st>>>(sel, Mb, NC,
                                                                                MT * 16, cbits);

@@ -282,8 +282,8 @@ def sparse_fwd_qat(q, qz, lut, Np, scale=None):
     return o_s, lse, qphi
 
 
-def linear_states_qat(k, v):
-    """States of all Nb tiles with 16-bit-rounded phi(K) -> dict(Hb, zb, Hall, zall)."""
+def linear_states_qat(k, v, with_vt=False):
+    """States of all Nb tiles with 16-bit-rounded phi(K) -> dict(Hb, zb, Hall, zall[, vt])."""
     _need_gpu(k, v)
     k, v = _bhld(k, "k"), _bhld(v, "v")
     B, H, L, D = k.shape
@@ -291,27 +291,30 @@ def linear_states_qat(k, v):
     dev = k.device
     st = dict(Hb=torch.empty(B, H, nb, D, D, device=dev), zb=torch.empty(B, H, nb, D, device=dev),
               Hall=torch.empty(B, H, D, D, device=dev), zall=torch.empty(B, H, D, device=dev))
+    if with_vt:
+        st["vt"] = torch.empty(B, H, nb, D, E_TILE, device=dev, dtype=v.dtype)
     _lib.check(_lib.load().sla2h_linear_states_qat(
         k.data_ptr(), v.data_ptr(), _dtype_code(k), B, H, L, D, E_TILE, st["Hb"].data_ptr(),
-        st["zb"].data_ptr(), st["Hall"].data_ptr(), st["zall"].data_ptr(), _stream(dev)),
-        "sla2h_linear_states_qat")
+        st["zb"].data_ptr(), st["Hall"].data_ptr(), st["zall"].data_ptr(), _ptr(st.get("vt")),
+        _stream(dev)), "sla2h_linear_states_qat")
     return st
 
 
-def linear_mix_qat(qphi, comp, Hall, o_s, alpha, eps_l=1e-5):
-    """Linear branch + alpha mix of the training forward -> (o, o_l 16-bit, den fp32)."""
+def linear_mix_qat(qphi, comp, Hall, o_s, alpha, eps_l=1e-5, bq=E_TILE):
+    """Linear branch + alpha mix of the training forward -> (o, o_l 16-bit, den fp32).
+    comp and alpha are per query block of bq rows."""
     _need_gpu(qphi, comp, Hall, o_s, alpha)
     B, H, L, D = qphi.shape
-    Mb = -(-L // E_TILE)
-    if tuple(comp.shape) != (B, H, Mb, REC_BYTES) or tuple(Hall.shape) != (B, H, D, D):
+    Mq = -(-L // bq)
+    if tuple(comp.shape) != (B, H, Mq, REC_BYTES) or tuple(Hall.shape) != (B, H, D, D):
         raise ValueError("linear_mix_qat: comp / Hall shapes do not match qphi")
-    alpha = _alpha_rows(alpha, H, Mb, qphi.device)
+    alpha = _alpha_rows(alpha, H, Mq, qphi.device)
     o = torch.empty_like(o_s)
     o_l = torch.empty_like(o_s)
     den = torch.empty(B, H, L, device=qphi.device, dtype=torch.float32)
     _lib.check(_lib.load().sla2h_linear_mix_qat(
         qphi.data_ptr(), comp.data_ptr(), Hall.contiguous().data_ptr(), o_s.data_ptr(),
-        alpha.data_ptr(), alpha.stride(0), _dtype_code(qphi), B, H, L, D, E_TILE,
+        alpha.data_ptr(), alpha.stride(0), _dtype_code(qphi), B, H, L, D, bq,
         float(eps_l), o.data_ptr(), o_l.data_ptr(), den.data_ptr(), _stream(qphi.device)),
         "sla2h_linear_mix_qat")
     return o, o_l, den
@@ -350,13 +353,13 @@ def train_fwd(q, k, v, alpha, lut, Np, eps_l=1e-5):
                 ztot=st["zall"], Hall=st["Hall"], comp=comp, lut_aug=lut_aug, **qz)
 
 
-def train_bwd(q, k, v, alpha, fwd, do, scale=None, stage_events=None):
-    """Straight-through backward of train_fwd.
+def train_bwd(q, k, v, alpha, fwd, do, scale=None, stage_events=None, bq=E_TILE):
+    """Straight-through backward of train_fwd (bq = 64) or train_fwd_1d.
 
-    q, k, v: the forward's 16-bit inputs; alpha (H, Mb) after the sigmoid;
-    fwd: the train_fwd dict; do: (B,H,L,D) output gradient.  Returns
-    (dq, dk, dv) 16-bit and d_alpha (H, Mb) fp32, the gradient with respect to
-    the alpha logits.
+    q, k, v: the forward's 16-bit inputs; alpha (H, Mq) after the sigmoid, one
+    column per query block of bq rows; fwd: the forward's dict; do: (B,H,L,D)
+    output gradient.  Returns (dq, dk, dv) 16-bit and d_alpha (H, Mq) fp32,
+    the gradient with respect to the alpha logits.
     """
     _need_gpu(q, k, v, do)
     q, k, v = (t.contiguous() for t in (q, k, v))
@@ -365,13 +368,14 @@ def train_bwd(q, k, v, alpha, fwd, do, scale=None, stage_events=None):
     dev = q.device
     scale = D ** -0.5 if scale is None else scale
     do = do.to(q.dtype).contiguous()
-    alpha = _alpha_rows(alpha, H, nb, dev)
+    mq = -(-L // bq)
+    alpha = _alpha_rows(alpha, H, mq, dev)
     lib = _lib.load()
     f16 = lambda: torch.empty_like(q)
     dos, g16 = f16(), f16()
     delta = torch.empty(B, H, L, device=dev)
     srow = torch.empty(B, H, L, device=dev)
-    seg = torch.zeros(H, nb, device=dev)
+    seg = torch.zeros(H, mq, device=dev)
     P = torch.empty(B, H, nb, D, D, device=dev)
     Pz = torch.empty(B, H, nb, D, device=dev)
     tf = lambda: torch.empty(B, H, nb, 4096, device=dev, dtype=q.dtype)
@@ -383,7 +387,7 @@ def train_bwd(q, k, v, alpha, fwd, do, scale=None, stage_events=None):
     _lib.check(lib.sla2h_bwd_prep(
         do.data_ptr(), fwd["o_s"].data_ptr(), fwd["o_l"].data_ptr(), fwd["den"].data_ptr(),
         fwd["qphi"].data_ptr(), q.data_ptr(), k.data_ptr(), alpha.data_ptr(), alpha.stride(0), dc,
-        B, H, L, D, E_TILE, dos.data_ptr(), delta.data_ptr(), g16.data_ptr(), srow.data_ptr(),
+        B, H, L, D, bq, dos.data_ptr(), delta.data_ptr(), g16.data_ptr(), srow.data_ptr(),
         seg.data_ptr(), P.data_ptr(), Pz.data_ptr(), qtf.data_ptr(), ktf.data_ptr(),
         dotf.data_ptr(), st), "sla2h_bwd_prep")
     lut_aug = fwd["lut_aug"]
@@ -395,14 +399,14 @@ def train_bwd(q, k, v, alpha, fwd, do, scale=None, stage_events=None):
     compb = torch.empty(B, H, nb, REC_BYTES, device=dev, dtype=torch.uint8)
     rec(1)
     _lib.check(lib.sla2h_complement_bwd(P.data_ptr(), Pz.data_ptr(), lut_aug.data_ptr(), B, H,
-                                        nb, J, ws.data_ptr(), sel.data_ptr(), compb.data_ptr(),
-                                        st), "sla2h_complement_bwd")
+                                        nb, bq, J, ws.data_ptr(), sel.data_ptr(),
+                                        compb.data_ptr(), st), "sla2h_complement_bwd")
     dq, dk, dv = f16(), f16(), f16()
     rec(2)
     _lib.check(lib.sla2h_bwd_dq(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), dos.data_ptr(), fwd["lse"].data_ptr(),
         delta.data_ptr(), ktf.data_ptr(), g16.data_ptr(), srow.data_ptr(), fwd["comp"].data_ptr(),
-        fwd["Hall"].data_ptr(), fwd["qphi"].data_ptr(), lut_aug.data_ptr(), dc, B, H, L, D, E_TILE,
+        fwd["Hall"].data_ptr(), fwd["qphi"].data_ptr(), lut_aug.data_ptr(), dc, B, H, L, D, bq,
         J, float(scale), dq.data_ptr(), st), "sla2h_bwd_dq")
     rec(3)
     _lib.check(lib.sla2h_bwd_dkdv(
@@ -471,3 +475,32 @@ def jvp_1d(q, k, v, dq, dk, dv, alpha, lut, bq, scale=None, eps_l=1e-5, return_a
     if return_aux:
         return o, do, dict(comp=comp, **st)
     return o, do
+
+
+def train_fwd_1d(q, k, v, alpha, lut, bq, eps_l=1e-5):
+    """Training forward of the 1-D SLA2 module (16-bit, no INT8) on given routing.
+
+    q, k, v: (B,H,L,64) 16-bit, natural order.  alpha (H, ceil(L/bq)) after the
+    sigmoid; lut (B,H,ceil(L/bq),T) routed 64-row key blocks.  Returns the
+    train_fwd dict (o, o_s, o_l, lse, den, qphi, htot, ztot, Hall, comp, lut_aug).
+    """
+    _need_gpu(q, k, v, lut)
+    q, k, v = (_bhld(t, "qkv") for t in (q, k, v))
+    B, H, L, D = q.shape
+    nb, mq = -(-L // E_TILE), -(-L // bq)
+    lut = lut.to(torch.int32).contiguous()
+    if lut.dim() != 4 or tuple(lut.shape[:3]) != (B, H, mq):
+        raise ValueError(f"lut: expected (B, H, {mq}, T), got {tuple(lut.shape)}")
+    T = lut.shape[-1]
+    st = linear_states_qat(k, v, with_vt=True)
+    o_s, qphi = torch.empty_like(q), torch.empty_like(q)
+    lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
+    _lib.check(_lib.load().sla2h_sparse_fwd_1d(
+        q.data_ptr(), k.data_ptr(), st["vt"].data_ptr(), lut.data_ptr(), _dtype_code(q), B, H, L,
+        D, bq, E_TILE, T, float(D ** -0.5), o_s.data_ptr(), lse.data_ptr(), qphi.data_ptr(),
+        _stream(q.device)), "sla2h_sparse_fwd_1d")
+    comp = complement(st, lut, nb)
+    o, o_l, den = linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha, eps_l, bq=bq)
+    return dict(o=o, o_s=o_s, o_l=o_l, lse=lse, den=den, qphi=qphi,
+                htot=st["Hall"].to(q.dtype).float(), ztot=st["zall"], Hall=st["Hall"], comp=comp,
+                lut_aug=lut)

@@ -225,12 +225,14 @@ int sla2h_sparse_fwd_qat(const void* q, const int8_t* q8, const float* qs, const
  *   Hb (B,H,Nb,D,D), zb (B,H,Nb,D) fp32 per tile; Hall (B,H,D,D), zall (B,H,D)
  *   fp32 sums over the tiles in n order (= htot and ztot before rounding).
  * Feed Hb/zb to sla2h_complement with Np = Nb and the augmented LUT.
+ * vt (B,H,Nb,4,4,64,4) 16-bit or NULL: the primal value operand tiles (as
+ * sla2h_linear_states writes them), needed by sla2h_sparse_fwd_1d.
  * Replaces kphi = softmax(kh).to(dtype) and _precompute_global
  * (models/sla2_cube_qat.py:728-730; models/sla2_vendor/kernel_linear.py:305-313).
  */
 int sla2h_linear_states_qat(const void* k, const void* v, int dtype, int B, int H, int64_t L,
                             int D, int E, float* Hb, float* zb, float* Hall, float* zall,
-                            void* stream);
+                            void* vt, void* stream);
 
 /*
  * Linear branch (state form) and alpha mix of the training forward:
@@ -239,7 +241,9 @@ int sla2h_linear_states_qat(const void* k, const void* v, int dtype, int B, int 
  *   o_l = round16(qphi H_m / den) (B,H,L,D) 16-bit;
  *   o = round16(round16(a o_s) + round16(round16(1 - a) o_l)), a =
  *   round16(alpha[h*alpha_stride + m]) (B,H,L,D) 16-bit.
- * comp = sla2h_complement records over the augmented LUT.  Replaces _lin_fwd2
+ * comp = sla2h_complement records over the augmented LUT.  E = the query block
+ * length (64 for the cube; 64, 128 or 256 for 1-D blocks): records and alpha
+ * are per query block of E rows.  Replaces _lin_fwd2
  * without SCORE_FORM (models/sla2_vendor/kernel_linear.py:206-304) and the mix
  * of _CubeQATFunction.forward (models/sla2_cube_qat.py:733-744).
  */
@@ -247,6 +251,19 @@ int sla2h_linear_mix_qat(const void* qphi, const void* comp, const float* Hall,
                          const void* o_s, const float* alpha, int alpha_stride, int dtype,
                          int B, int H, int64_t L, int D, int E, float eps_l, void* o,
                          void* o_l, float* den, void* stream);
+
+/*
+ * 16-bit sparse branch of the 1-D training forward (no INT8): S = q.k^T on
+ * 16-bit MFMA (fp32 accumulate) * scale * log2(e) over the routed key blocks
+ * of each query block of bq rows (lut (B,H,ceil(L/bq),T)), exact running
+ * maximum, O += round16(P).V; o_s = O / l (16-bit), lse = m + log2 l (fp32),
+ * qphi = softmax_D(q) (16-bit).  vt from sla2h_linear_states_qat.  Replaces
+ * _attn_fwd_qat without USE_INT8 (models/sla2_vendor/kernel_sparse_qat.py:28-117)
+ * as run by _sparse_attention_qat (:265-293) for the SLA2 module.
+ */
+int sla2h_sparse_fwd_1d(const void* q, const void* k, const void* vt, const int32_t* lut,
+                        int dtype, int B, int H, int64_t L, int D, int bq, int bk, int T,
+                        float scale, void* o_s, float* lse, void* qphi, void* stream);
 
 /* ---- training backward (straight-through estimator) --------------------- */
 
@@ -261,7 +278,9 @@ int sla2h_linear_mix_qat(const void* qphi, const void* comp, const float* Hall,
  *   P = qphi^T sat(g) (B,H,Mb,D,D) fp32, Pz = qphi^T s (B,H,Mb,D) fp32;
  *   qtf, ktf, dotf (B,H,Nb,4096) 16-bit: q, k, dos in the transposed fragment
  *     order [ct][p][lane][s] = X[16(2p + (s>>2)) + 4g + (s&3)][16ct + r].
- * sat(x) = clamp(x, -60000, 60000).  Replaces _bwd_split_kernel
+ * sat(x) = clamp(x, -60000, 60000).  E = the query block length (64, or 128 /
+ * 256 for 1-D blocks): alpha and seg have one column per query block of E
+ * rows; every other array is per 64-row block.  Replaces _bwd_split_kernel
  * (models/sla2_cube_qat.py:838-872), _attn_bwd_preprocess
  * (models/sla2_vendor/sla_kernel.py:89-114) and the g, s, dhtot, dztot torch
  * lines of _CubeQATFunction.backward (models/sla2_cube_qat.py:765-797).
@@ -273,7 +292,8 @@ int sla2h_bwd_prep(const void* dout, const void* o_s, const void* o_l, const flo
                    float* Pz, void* qtf, void* ktf, void* dotf, void* stream);
 
 /*
- * Backward complement over the augmented LUT lut_aug (B,H,Mb,J) int32:
+ * Backward complement over the augmented LUT lut_aug (B,H,ceil(Mb*64/bq),J) int32,
+ * one row per query block of bq rows (bq = 64 for the cube), Mb 64-row blocks:
  *   sel (B,H,Mb,ceil(Mb/32)) uint32: bit j of word kc of tile n = 1 where query
  *     block 32kc + j routes tile n;
  *   comp records (B,H,Mb, sla2h_complement_record_bytes(64) bytes), fp32:
@@ -284,7 +304,7 @@ int sla2h_bwd_prep(const void* dout, const void* o_s, const void* o_l, const flo
  * 1045-1095).
  */
 int sla2h_complement_bwd(const float* P, const float* Pz, const int32_t* lut_aug, int B, int H,
-                         int Mb, int J, void* workspace, uint32_t* sel, void* comp,
+                         int Mb, int bq, int J, void* workspace, uint32_t* sel, void* comp,
                          void* stream);
 
 /*
@@ -293,7 +313,8 @@ int sla2h_complement_bwd(const float* P, const float* Pz, const int32_t* lut_aug
  *   p = exp2(min(q.k scale log2e - lse, 4)) on the unquantised 16-bit q, k;
  *   dqphi = g16 H16^T - s z^T, H16 = round16(comp.Hc + (round16(Hall) - Hall)),
  *   z = comp.zc (comp, Hall, lse, qphi from the training forward).
- * J = columns of lut_aug <= 1024.  Replaces _attn_bwd_dq
+ * J = columns of lut_aug <= 1024; E = the query block length (LUT rows and comp
+ * records per query block of E rows).  Replaces _attn_bwd_dq
  * (models/sla2_vendor/sla_kernel.py:117-184), _lin_bwd_dq
  * (models/sla2_vendor/kernel_linear.py:85-138) and the Q-side
  * _phi_chain_add_kernel (models/sla2_cube_qat.py:875-904, 814-818).

@@ -398,7 +398,16 @@ def _round16(x, t16):
     return x.to(t16).float()
 
 
-def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L):
+def _expand_1d(lut, alpha, bq, nb):
+    """Query blocks of bq rows -> 64-row sub-blocks sharing their block's LUT row and alpha."""
+    r = bq // E
+    lut = torch.as_tensor(np.asarray(lut)).repeat_interleave(r, dim=2)[:, :, :nb]
+    alpha = torch.as_tensor(alpha).repeat_interleave(r, dim=-1)[:, :nb]
+    return lut, alpha
+
+
+def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L, int8=True,
+              bq=E):
     """Training-forward semantics (b), blockwise, CPU.
 
     q, k, v: (B,H,L,D) float tensors holding 16-bit values.  alpha: (H, Mb)
@@ -406,18 +415,29 @@ def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L
     blocks are appended (lut_aug).  Returns dict with o (16-bit values, the
     module output), o_s, o_l (16-bit values), lse (fp32, log2 domain), qphi,
     den (the signed-epsilon denominator), htot (16-bit values), ztot.
+    int8=False, bq > 64: the 1-D SLA2 module's forward (_sparse_attention_qat
+    without USE_INT8, models/sla2_vendor/kernel_sparse_qat.py:265-293, and
+    _complement_linear_attention, models/sla2_vendor/kernel_linear.py:340-366):
+    16-bit scores, O += round16(P).V, query blocks of bq rows (LUT rows and
+    alpha per block), Np = Nb key blocks and no prefix tail.
     """
     B, H, L, D = q.shape
     nb = -(-L // E)
     Mb = nb
+    if bq != E:
+        lut, alpha = _expand_1d(lut, alpha, bq, nb)
     n_tail = nb - Np
     lut = torch.as_tensor(np.asarray(lut)).long()
     tails = torch.arange(Np, Np + n_tail).view(1, 1, 1, -1).expand(B, H, Mb, n_tail)
     lut_aug = torch.cat([lut, tails], -1)
     J = lut_aug.shape[-1]
-    q8, qs = quantize_blocks_trunc(q)
-    k8, ks = quantize_blocks_trunc(k)
-    v8, vs = quantize_blocks_trunc(v)
+    if not int8:   # 16-bit operands: the "int8" tensors below hold the 16-bit values, scales 1
+        q8, k8, v8 = (torch.as_tensor(x).float().numpy() for x in (q, k, v))
+        qs = ks = vs = np.ones((B, H, nb), dtype=np.float32)
+    else:
+        q8, qs = quantize_blocks_trunc(q)
+        k8, ks = quantize_blocks_trunc(k)
+        v8, vs = quantize_blocks_trunc(v)
     q8t = _tiles(torch.as_tensor(q8).double(), nb)
     k8t = _tiles(torch.as_tensor(k8).double(), nb)
     v8t = _tiles(torch.as_tensor(v8).double(), nb)
@@ -445,9 +465,12 @@ def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L
         l_ij = p.sum(-1)
         al = torch.exp2(m_i - new_m)
         o_s = o_s * al[..., None]
-        p8 = torch.trunc(p * 127.0 + 0.5)
-        pv = torch.matmul(p8.double(), vt).float()
-        o_s = o_s + pv * (svn / 127.0)[..., None, None]
+        if int8:
+            p8 = torch.trunc(p * 127.0 + 0.5)
+            pv = torch.matmul(p8.double(), vt).float()
+            o_s = o_s + pv * (svn / 127.0)[..., None, None]
+        else:
+            o_s = o_s + torch.matmul(_round16(p, t16).double(), vt).float()
         l_i = l_i * al + l_ij
         m_i = new_m
     o_s = o_s / l_i[..., None]
@@ -482,7 +505,8 @@ def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L
             "htot": htot, "ztot": ztot}
 
 
-def train_bwd(q, k, v, alpha, lut, Np, prefix_len, fwd, do, t16=torch.bfloat16):
+def train_bwd(q, k, v, alpha, lut, Np, prefix_len, fwd, do, t16=torch.bfloat16, bq=E,
+              variant="cube"):
     """Training backward (straight-through estimator), blockwise, CPU.
 
     Restates _CubeQATFunction.backward (models/sla2_cube_qat.py:753-832) and its
@@ -503,7 +527,23 @@ def train_bwd(q, k, v, alpha, lut, Np, prefix_len, fwd, do, t16=torch.bfloat16):
     Returns dict dq, dk, dv (B,H,L,D), d_alpha (H, Mb; the gradient with respect
     to the alpha LOGITS) and the intermediates dq_s, dk_s, dv_s, dqphi, dkphi,
     dv_l, delta.  LUT rows are assumed free of duplicates (top-k rows are).
+
+    bq > 64: query blocks of bq rows (LUT rows and alpha per block).
+    variant="1d": the rounding points of the 1-D SLA2 module's backward, where
+    the mix and the phi maps are torch autograd ops on fp16 tensors
+    (models/sla2_vendor/core.py:168-176) and the linear branch is
+    _complement_linear_attention.backward (kernel_linear.py:368-393):
+    do_s = r16(do a16), do_l = r16(do r16(1 - a16)) with a16 = r16(a); dqphi and
+    dkphi stored in 16 bits; _lin_bwd_dkdv without saturation; the softmax
+    backward rounded to 16 bits and added to the 16-bit sparse gradient.
     """
+    one_d = variant == "1d"
+    B_, H_, L_, D_ = q.shape
+    if bq != E:
+        nb_ = -(-L_ // E)
+        mq = -(-L_ // bq)
+        alpha_q = torch.as_tensor(alpha)
+        lut, alpha = _expand_1d(lut, alpha, bq, nb_)
     exact = t16 is None
     dt = torch.float64 if exact else torch.float32
     r16 = (lambda x: x) if exact else (lambda x: x.to(t16).to(dt))
@@ -523,9 +563,16 @@ def train_bwd(q, k, v, alpha, lut, Np, prefix_len, fwd, do, t16=torch.bfloat16):
     a_blk = cv(alpha)                                          # (H, Mb)
     rows = torch.arange(nb * E)
     a_rows = a_blk[:, (rows[:L] // E)].view(1, H, L, 1)
-    do_s, do_l = r16(do * a_rows), r16(do * (1.0 - a_rows))
+    if one_d:
+        a16 = r16(a_rows)
+        do_s, do_l = r16(do * a16), r16(do * r16(1.0 - a16))
+    else:
+        do_s, do_l = r16(do * a_rows), r16(do * (1.0 - a_rows))
     segr = (do * (o_s - o_l)).sum(-1)                          # (B,H,L)
     seg = _tiles(segr[..., None], nb).sum((-2, -1)).sum(0)     # (H, Mb)
+    if bq != E:   # per query block of bq rows
+        seg = torch.stack([seg[:, i * (bq // E):(i + 1) * (bq // E)].sum(-1) for i in range(mq)], -1)
+        a_blk = cv(alpha_q)
     d_alpha = seg * a_blk * (1.0 - a_blk)
     delta = (o_s * do_s).sum(-1)
     scale = D ** -0.5
@@ -572,6 +619,9 @@ def train_bwd(q, k, v, alpha, lut, Np, prefix_len, fwd, do, t16=torch.bfloat16):
     g16t, st, qpt = _tiles(g16, nb), pad1(s, 0.0), _tiles(qphi, nb)
     dqphi = g16t @ r16(hi).transpose(-1, -2) - st[..., None] * zi[..., None, :]
     dqphi = untile(dqphi)
+    if one_d:
+        dqphi = r16(dqphi)
+        g16t = _tiles(r16(g), nb)
     pm = qpt.transpose(-1, -2) @ g16t                          # (B,H,Mb,D,D)
     pz = (qpt * st[..., None]).sum(-2)                         # (B,H,Mb,D)
     dh = dhtot[:, :, None].expand(B, H, nb, D, D).clone()
@@ -580,19 +630,25 @@ def train_bwd(q, k, v, alpha, lut, Np, prefix_len, fwd, do, t16=torch.bfloat16):
         n = lut_aug[..., j]
         dh.scatter_add_(2, ix(n)[..., :D, :], -pm)
         dz.scatter_add_(2, n.view(B, H, Mb, 1).expand(B, H, Mb, D), pz)
-    dh16 = r16(sat(dh))
+    dh16 = r16(dh) if one_d else r16(sat(dh))
     dkphi = untile(vvt @ dh16.transpose(-1, -2) + dz[..., None, :])
     dv_l = untile(kpt @ dh16)
 
     chain = lambda phi, dphi: phi * (dphi - (phi * dphi).sum(-1, keepdim=True))
-    dq = r16(sat(dq_s + chain(qphi, dqphi)))
-    dk = r16(sat(dk_s + chain(kphi, dkphi)))
-    dv = r16(sat(dv_s + dv_l))
+    if one_d:
+        dkphi, dv_l = r16(dkphi), r16(dv_l)
+        dq = r16(dq_s + r16(chain(qphi, dqphi)))
+        dk = r16(dk_s + r16(chain(kphi, dkphi)))
+        dv = r16(dv_s + dv_l)
+    else:
+        dq = r16(sat(dq_s + chain(qphi, dqphi)))
+        dk = r16(sat(dk_s + chain(kphi, dkphi)))
+        dv = r16(sat(dv_s + dv_l))
     return {"dq": dq, "dk": dk, "dv": dv, "d_alpha": d_alpha, "dq_s": dq_s, "dk_s": dk_s,
             "dv_s": dv_s, "dqphi": dqphi, "dkphi": dkphi, "dv_l": dv_l, "delta": delta}
 
 
-def train_dense_f64(q, k, v, alpha_logit, lut, Np, prefix_len, eps=EPS_L):
+def train_dense_f64(q, k, v, alpha_logit, lut, Np, prefix_len, eps=EPS_L, bq=E):
     """Differentiable float64 restatement of the training op WITHOUT quantisation
     (the straight-through view): masked softmax over the augmented-LUT tiles,
     complement linear attention over the other video tiles, sigmoid mix.
@@ -605,12 +661,14 @@ def train_dense_f64(q, k, v, alpha_logit, lut, Np, prefix_len, eps=EPS_L):
     nb = -(-L // E)
     n_tail = nb - Np
     lut = torch.as_tensor(np.asarray(lut)).long()
-    tails = torch.arange(Np, Np + n_tail).view(1, 1, 1, -1).expand(B, H, nb, n_tail)
+    mq = lut.shape[2]
+    tails = torch.arange(Np, Np + n_tail).view(1, 1, 1, -1).expand(B, H, mq, n_tail)
     lut_aug = torch.cat([lut, tails], -1)
-    sel = torch.zeros(B, H, nb, nb, dtype=torch.bool)
+    sel = torch.zeros(B, H, mq, nb, dtype=torch.bool)
     sel.scatter_(3, lut_aug, True)
     blk = torch.arange(L) // E
-    allowed = sel[:, :, blk][:, :, :, blk]                     # (B,H,L,L)
+    qblk = torch.arange(L) // bq
+    allowed = sel[:, :, qblk][:, :, :, blk]                    # (B,H,L,L)
     s = (q @ k.transpose(-1, -2)) * D ** -0.5
     s = s.masked_fill(~allowed, -math.inf)
     o_s = torch.softmax(s, -1) @ v
@@ -620,7 +678,7 @@ def train_dense_f64(q, k, v, alpha_logit, lut, Np, prefix_len, eps=EPS_L):
     den0 = w.sum(-1)
     den = torch.where(den0 >= 0, den0 + eps, den0 - eps)
     o_l = (w @ v) / den[..., None]
-    a = torch.sigmoid(alpha_logit)[:, blk].view(1, H, L, 1)
+    a = torch.sigmoid(alpha_logit)[:, qblk].view(1, H, L, 1)
     o = a * o_s + (1 - a) * o_l
     fwd = {"o_s": o_s, "o_l": o_l, "lse": lse, "den": den, "qphi": qphi,
            "htot": kphi.transpose(-1, -2) @ v, "ztot": kphi.sum(-2)}

@@ -274,3 +274,82 @@ def test_sla2_mla_jvp_config4_shape():
         print(f"  h{h} o rel {rel_l2(o[:, sl], eo):.2e} do rel {rel_l2(do[:, sl], edo):.2e}", flush=True)
         assert max_abs(o[:, sl], eo) < TOL_MAX and rel_l2(o[:, sl], eo) < TOL_REL
         assert max_abs(do[:, sl], edo) < TOL_MAX and rel_l2(do[:, sl], edo) < TOL_REL
+
+
+# ---------------------------------------------------------------------------
+# 1-D SLA2 module (SLA2AttentionImpl: fp16, no INT8, bq = 128, bk = 64)
+# ---------------------------------------------------------------------------
+def _tm16(t):
+    return t.permute(0, 2, 1, 3).half().float()
+
+
+def test_sla2_attention_impl_forward_and_gradients():
+    say("SLA2AttentionImpl forward + backward (b=2, L=583, H=2)")
+    from imfvideo_amd.sla2_attention import SLA2AttentionImpl
+    torch.manual_seed(2)
+    L, H = 583, 2
+    mod = SLA2AttentionImpl(64, L, H, topk=0.3).cuda()
+    with torch.no_grad():
+        mod.sla2.alpha_logit.add_(torch.linspace(-1, 1, mod.sla2.alpha_logit.numel(),
+                                                 device="cuda").view_as(mod.sla2.alpha_logit))
+    g = torch.Generator().manual_seed(13)
+    x = [torch.randn(2, L, H, 64, generator=g) for _ in range(4)]
+    with torch.no_grad():
+        out0 = mod(*(cuda(t) for t in x[:3])).cpu()
+    xs = [cuda(t).requires_grad_() for t in x[:3]]
+    out = mod(*xs)
+    assert torch.equal(out.detach().cpu(), out0)
+    (out * cuda(x[3])).sum().backward()
+    grads = [t.grad.cpu() for t in xs] + [mod.sla2.alpha_logit.grad.cpu()]
+    qh, kh, vh, doh = (_tm16(t) for t in x)
+    lut, T = O.route_1d(qh, kh, 0.3, 128)
+    nb = -(-L // 64)
+    a = torch.sigmoid(mod.sla2.alpha_logit.detach().cpu())
+    fwd = O.train_fwd(qh, kh, vh, a, lut, nb, 0, t16=torch.float16, int8=False, bq=128)
+    eo = fwd["o"].permute(0, 2, 1, 3)
+    print(f"  o max {max_abs(out0, eo):.2e} rel {rel_l2(out0, eo):.2e}", flush=True)
+    assert max_abs(out0, eo) < TOL_MAX and rel_l2(out0, eo) < TOL_REL
+    ref = O.train_bwd(qh, kh, vh, a, lut, nb, 0, fwd, doh, t16=torch.float16, bq=128,
+                      variant="1d")
+    for got, name in zip(grads[:3], ("dq", "dk", "dv")):
+        want = ref[name].permute(0, 2, 1, 3)
+        print(f"  {name} max {max_abs(got, want):.2e} rel {rel_l2(got, want):.2e}", flush=True)
+        assert rel_l2(got, want) < TOL_REL and max_abs(got, want) < TOL_MAX * max(1, want.abs().max())
+    print(f"  d_alpha rel {rel_l2(grads[3], ref['d_alpha']):.2e}", flush=True)
+    assert rel_l2(grads[3], ref["d_alpha"]) < 1e-2
+
+
+def test_sla2_train_1d_config_shape():
+    say("1-D training forward + backward (1,8,29952,64) bq=128")
+    from imfvideo_amd import ops
+    ins, Np, P = config_inputs(3)
+    x = {n: ins[n].half() for n in ("q", "k", "v")}
+    g = {n: cuda(t) for n, t in x.items()}
+    lut, T = ops.route_1d(g["q"], g["k"], 0.1, 128)
+    alpha = torch.full((8, 234), 0.9)
+    out = ops.train_fwd_1d(g["q"], g["k"], g["v"], cuda(alpha), lut, 128)
+    gen = torch.Generator().manual_seed(17)
+    do = torch.randn(1, 8, 29952, 64, generator=gen).half()
+    dq, dk, dv, da = ops.train_bwd(g["q"], g["k"], g["v"], cuda(alpha), out, cuda(do), bq=128)
+    torch.cuda.synchronize()
+    lut = lut.cpu().numpy()
+    for h in (0, 5):
+        sl = slice(h, h + 1)
+        f = {n: t[:, sl].float() for n, t in x.items()}
+        elut, eT = O.route_1d(f["q"], f["k"], 0.1, 128)
+        assert np.array_equal(lut[:, sl], elut)
+        ref = O.train_fwd(f["q"], f["k"], f["v"], alpha[sl], elut, 468, 0, t16=torch.float16,
+                          int8=False, bq=128)
+        got = {n: out[n][:, sl].cpu().float() for n in ("o", "o_s", "o_l", "qphi")}
+        for n in got:
+            print(f"  h{h} {n} rel {rel_l2(got[n], ref[n]):.2e}", flush=True)
+            assert max_abs(got[n], ref[n]) < TOL_MAX and rel_l2(got[n], ref[n]) < TOL_REL
+        fwd = {n: out[n][:, sl].cpu().float() for n in ("o_s", "o_l", "lse", "den", "qphi",
+                                                        "htot", "ztot")}
+        rb = O.train_bwd(f["q"], f["k"], f["v"], alpha[sl], elut, 468, 0, fwd, do[:, sl].float(),
+                         t16=torch.float16, bq=128, variant="1d")
+        for t_, n in ((dq, "dq"), (dk, "dk"), (dv, "dv")):
+            a_ = t_[:, sl].cpu().float()
+            print(f"  h{h} {n} rel {rel_l2(a_, rb[n]):.2e}", flush=True)
+            assert rel_l2(a_, rb[n]) < TOL_REL and max_abs(a_, rb[n]) < TOL_MAX * max(1, rb[n].abs().max())
+        assert rel_l2(da[sl].cpu(), rb["d_alpha"]) < 1e-2

@@ -56,7 +56,10 @@ def test_invalid_arguments_are_rejected_before_any_launch():
                                     1, 1, 1, None) == bad                   # T > Np
     assert lib.sla2h_sparse_fwd_qat(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 100000, 64, 64, 1, 1,
                                     0.125, 1, 1, 1, None) == bad            # tail > 1024 tiles
-    assert lib.sla2h_linear_states_qat(1, 1, 1, 1, 1, 128, 64, 64, 1, 1, None, 1, None) == bad
+    assert lib.sla2h_linear_states_qat(1, 1, 1, 1, 1, 128, 64, 64, 1, 1, None, 1, None, None) == bad
+    # q, k, vt, lut, dtype, B, H, L, D, bq, bk, T, scale, o_s, lse, qphi: bq 96 unsupported
+    assert lib.sla2h_sparse_fwd_1d(1, 1, 1, 1, 1, 1, 1, 640, 64, 96, 64, 2, 0.125, 1, 1, 1,
+                                   None) == bad
     # qphi, comp, Hall, o_s, alpha, alpha_stride, dtype, B, H, L, D, E, eps, o, o_l, den
     assert lib.sla2h_linear_mix_qat(1, 1, 1, 1, 1, -1, 1, 1, 1, 128, 64, 64, 1e-5, 1, 1, 1,
                                     None) == bad

@@ -437,3 +437,38 @@ def test_route_1d_matches_brute_force_block_scores():
     srt = pc.sort(-1, descending=True).values
     clear = (srt[..., T - 1] - srt[..., T]) > 1e-5
     assert clear.any() and torch.equal(got[clear], want[clear])
+
+
+def test_train_bwd_1d_exact_mode_is_the_autograd_gradient():
+    # 128-row query blocks, every 64-row key block routable, ragged L
+    g = torch.Generator().manual_seed(11)
+    B, H, L, bq = 1, 2, 583, 128
+    nb, mq = -(-L // 64), -(-L // bq)
+    q, k, v, do = (torch.randn(B, H, L, 64, generator=g, dtype=torch.float64) for _ in range(4))
+    logit = torch.randn(H, mq, generator=g, dtype=torch.float64)
+    lut, T = O.route_1d(q.float(), k.float(), 0.3, bq)
+    xs = [t.clone().requires_grad_() for t in (q, k, v, logit)]
+    o, fwd = O.train_dense_f64(*xs[:3], xs[3], lut, nb, 0, bq=bq)
+    want = torch.autograd.grad((o * do).sum(), xs)
+    for variant in ("cube", "1d"):
+        got = O.train_bwd(q, k, v, torch.sigmoid(logit), lut, nb, 0, fwd, do, t16=None, bq=bq,
+                          variant=variant)
+        for name, w in zip(("dq", "dk", "dv", "d_alpha"), want):
+            err = ((got[name] - w).norm() / w.norm()).item()
+            assert err < 1e-10, (variant, name, err)
+
+
+def test_train_fwd_1d_sixteen_bit_matches_dense():
+    # 16-bit scores and P: the sparse branch within fp16 rounding of the dense form
+    g = torch.Generator().manual_seed(12)
+    B, H, L, bq = 1, 2, 583, 128
+    nb, mq = -(-L // 64), -(-L // bq)
+    q, k, v = (torch.randn(B, H, L, 64, generator=g).half().float() for _ in range(3))
+    lut, T = O.route_1d(q, k, 0.3, bq)
+    ones = torch.ones(H, mq)
+    got = O.train_fwd(q, k, v, ones, lut, nb, 0, t16=torch.float16, int8=False, bq=bq)
+    o, fwd = O.train_dense_f64(q.double(), k.double(), v.double(), torch.full((H, mq), 30.0,
+                               dtype=torch.float64), lut, nb, 0, bq=bq)
+    r = ((got["o_s"].double() - fwd["o_s"]).norm() / fwd["o_s"].norm()).item()
+    assert r < 3e-3, r
+    assert (got["lse"].double() - fwd["lse"]).abs().max().item() < 1e-3
