@@ -40,6 +40,14 @@ SIGNATURES = {
     "sla2h_fwd_jvp_1d": (_c_int, [_p, _p, _p, _p, _p, _p, _c_int, _p, _c_int, _c_int, _c_int,
                                   _c_i64, _c_int, _c_int, _c_int, _c_int, _c_f, _c_f, _p, _p,
                                   _p]),
+    "sla2h_rmsnorm_jvp": (_c_int, [_p, _p, _c_int, _p, _c_i64, _c_int, _c_i64, _p, _p, _c_i64,
+                                   _c_int, _c_f, _p]),
+    "sla2h_mla_qkv_prep": (_c_int, [_p, _p, _p, _c_i64, _p, _p, _p, _p, _p, _c_int, _c_int,
+                                    _c_int, _c_int, _c_int, _c_int, _c_int, _c_f, _p, _p, _p, _p,
+                                    _p, _p, _p]),
+    "sla2h_mla_out_gate": (_c_int, [_p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p,
+                                    _p]),
+    "sla2h_situ_jvp": (_c_int, [_p, _c_i64, _c_int, _c_f, _c_int, _p, _p]),
     "sla2h_quant_train": (_c_int, [_p, _p, _p, _c_int, _c_int, _c_int, _c_i64, _c_int, _c_int,
                                    _p, _p, _p, _p, _p, _p, _p]),
     "sla2h_sparse_fwd_qat": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int,

@@ -25,6 +25,7 @@ SOURCES = {
     "attn.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "attn_train.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "attn_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
+    "mla_glue.hip": [],
 }
 
 COMMON_FLAGS = [

@@ -1,0 +1,212 @@
+"""The DiT block around the SLA2 op (reference: models/imf_dit_video.py:121-187,
+266-284, 422-532, 557-602): RMSNorm, SituAndMul / SwiGLUMlp, partial-RoPE MLA
+attention with the output gate, and the vector-gated TransformerBlock.
+
+Eager torch modules with the reference's names, arguments and parameter
+names (state-dict compatible), so a block built here runs the training
+forward (autograd) with any attn_impl of this package, e.g.
+``functools.partial(SLA2CubeQATAttentionImpl, seq_len=L, num_heads=H, grid=...)``;
+the fast forward-mode JVP of the same block is ``mla_jvp_fast.block_jvp``.
+"""
+
+import math
+from functools import partial
+
+import torch
+import torch.nn as nn
+import torch.nn.functional as F
+
+__all__ = ["RMSNorm", "SituAndMul", "SwiGLUMlp", "MLAAttention", "TransformerBlock",
+           "apply_rotary_pos_emb", "precompute_axial_rope_3d", "scaled_variance_linear",
+           "sdpa_math_attention"]
+
+
+def scaled_variance_linear(in_features, out_features, bias=True, init_constant=1.0):
+    """nn.Linear with weights N(0, init_constant / sqrt(in_features))."""
+    linear = nn.Linear(in_features, out_features, bias=bias)
+    nn.init.normal_(linear.weight, std=init_constant / math.sqrt(in_features))
+    if bias:
+        nn.init.zeros_(linear.bias)
+    return linear
+
+
+def sdpa_math_attention(q, k, v):
+    """Dense softmax attention on (b, l, H, hd) tensors (the default attn_impl)."""
+    o = F.scaled_dot_product_attention(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2))
+    return o.transpose(1, 2)
+
+
+class RMSNorm(nn.Module):
+    """Root mean square normalisation with fp32 accumulation."""
+
+    def __init__(self, dim, eps=1e-6):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x):
+        xf = x.float()
+        normed = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
+        return normed.to(x.dtype) * self.weight
+
+
+class SituAndMul(nn.Module):
+    """situ(g) * up with situ(g) = beta tanh(g / beta) sigmoid(g); with
+    linear_beta the up branch is soft-clamped to linear_beta tanh(up / linear_beta)."""
+
+    def __init__(self, beta=1.0, linear_beta=None):
+        super().__init__()
+        self.beta = beta
+        self.linear_beta = linear_beta
+
+    def forward(self, x, up=None):
+        if up is None:
+            d = x.shape[-1] // 2
+            gate, up = x[..., :d], x[..., d:]
+        else:
+            gate = x
+        dtype = gate.dtype
+        g, u = gate.float(), up.float()
+        act = self.beta * torch.tanh(g / self.beta) * torch.sigmoid(g)
+        if self.linear_beta is not None:
+            u = self.linear_beta * torch.tanh(u / self.linear_beta)
+        return (act * u).to(dtype)
+
+
+class SwiGLUMlp(nn.Module):
+    """Gated MLP w2(situ(w1 x) * w3 x)."""
+
+    def __init__(self, in_features, hidden_features, weight_init_constant=1.0, situ_beta=1.0,
+                 situ_linear_beta=None):
+        super().__init__()
+        linear = partial(scaled_variance_linear, bias=False, init_constant=weight_init_constant)
+        self.w1 = linear(in_features, hidden_features)
+        self.w3 = linear(in_features, hidden_features)
+        self.w2 = linear(hidden_features, in_features)
+        self.act = SituAndMul(beta=situ_beta, linear_beta=situ_linear_beta)
+
+    def forward(self, x):
+        return self.w2(self.act(self.w1(x), self.w3(x)))
+
+
+def apply_rotary_pos_emb(x, rope_cos, rope_sin):
+    """Rotate channel pairs (x[..., 2i], x[..., 2i+1]) of x (b, l, H, hd) by the
+    angles of rope_cos / rope_sin (l, hd // 2)."""
+    xf = x.float()
+    re, im = xf[..., 0::2], xf[..., 1::2]
+    c, s = rope_cos[None, :, None, :], rope_sin[None, :, None, :]
+    out = torch.stack([re * c - im * s, re * s + im * c], dim=-1).flatten(-2)
+    return out.to(x.dtype)
+
+
+def precompute_axial_rope_3d(head_dim, grid_size, num_prefix_tokens, axis_dims=None,
+                             theta=10000.0):
+    """3-D axial RoPE angles: head_dim split over (t, h, w) (default ~1/4, 3/8,
+    3/8, each even), standard 1-D RoPE per axis on the t-major patch grid; the
+    prefix tokens come first with the identity rotation.
+    Returns rope_cos, rope_sin: (num_prefix_tokens + T*Gh*Gw, head_dim // 2) fp32."""
+    if axis_dims is None:
+        dim_t = 2 * ((head_dim // 4) // 2)
+        dim_h = 2 * (((head_dim - dim_t) // 2) // 2)
+        axis_dims = (dim_t, dim_h, head_dim - dim_t - dim_h)
+    assert sum(axis_dims) == head_dim and all(d % 2 == 0 for d in axis_dims)
+    gt, gh, gw = grid_size
+    pos = torch.meshgrid(torch.arange(gt, dtype=torch.float32),
+                         torch.arange(gh, dtype=torch.float32),
+                         torch.arange(gw, dtype=torch.float32), indexing="ij")
+    parts = []
+    for p, ad in zip(pos, axis_dims):
+        freqs = 1.0 / (theta ** (torch.arange(0, ad, 2, dtype=torch.float32) / ad))
+        parts.append(torch.outer(p.flatten(), freqs))
+    angles = torch.cat([torch.zeros(num_prefix_tokens, head_dim // 2), torch.cat(parts, -1)], 0)
+    return torch.cos(angles), torch.sin(angles)
+
+
+class MLAAttention(nn.Module):
+    """Multi-head latent attention with decoupled partial RoPE and the output
+    gate.  q: d -> dq (RMSNorm) -> H (dn + dr); k/v: d -> [dc latent (RMSNorm) |
+    dr shared rotary key] -> H (dn + dv); per-head RMSNorm on the nope bands;
+    RoPE on the trailing dr channels (the key's band is shared by the heads);
+    attn_impl(q, k, v) on (b, l, H, hd); output gate sigmoid(g_proj(x))."""
+
+    def __init__(self, hidden_size, num_heads, q_lora_rank, kv_lora_rank, qk_nope_head_dim,
+                 qk_rope_head_dim, v_head_dim, weight_init_constant=1.0, norm_eps=1e-6,
+                 attn_impl=sdpa_math_attention, use_output_gate=True):
+        super().__init__()
+        self.hidden_size, self.num_heads = hidden_size, num_heads
+        self.q_lora_rank, self.kv_lora_rank = q_lora_rank, kv_lora_rank
+        self.qk_nope_head_dim, self.qk_rope_head_dim = qk_nope_head_dim, qk_rope_head_dim
+        self.qk_head_dim = qk_nope_head_dim + qk_rope_head_dim
+        self.v_head_dim = v_head_dim
+        is_factory = isinstance(attn_impl, type) or (
+            isinstance(attn_impl, partial) and isinstance(attn_impl.func, type))
+        if is_factory:
+            assert self.qk_head_dim == v_head_dim, (self.qk_head_dim, v_head_dim)
+            attn_impl = attn_impl(self.qk_head_dim)
+        self.attn_impl = attn_impl
+        linear = partial(scaled_variance_linear, bias=False, init_constant=weight_init_constant)
+        self.q_a_proj = linear(hidden_size, q_lora_rank)
+        self.q_b_proj = linear(q_lora_rank, num_heads * self.qk_head_dim)
+        self.kv_a_proj = linear(hidden_size, kv_lora_rank + qk_rope_head_dim)
+        self.kv_b_proj = linear(kv_lora_rank, num_heads * (qk_nope_head_dim + v_head_dim))
+        self.out_proj = linear(num_heads * v_head_dim, hidden_size)
+        self.use_output_gate = use_output_gate
+        if use_output_gate:
+            self.g_proj = linear(hidden_size, num_heads * v_head_dim)
+        self.q_a_layernorm = RMSNorm(q_lora_rank, eps=norm_eps)
+        self.kv_a_layernorm = RMSNorm(kv_lora_rank, eps=norm_eps)
+        self.q_norm = RMSNorm(qk_nope_head_dim, eps=norm_eps)
+        self.k_norm = RMSNorm(qk_nope_head_dim, eps=norm_eps)
+
+    def forward(self, x, rope_cos, rope_sin):
+        b, l, _ = x.shape
+        H = self.num_heads
+        dn, dr, dv = self.qk_nope_head_dim, self.qk_rope_head_dim, self.v_head_dim
+        q = self.q_b_proj(self.q_a_layernorm(self.q_a_proj(x))).reshape(b, l, H, dn + dr)
+        q_nope, q_rope = q.split([dn, dr], dim=-1)
+        kv_latent, k_rope = self.kv_a_proj(x).split([self.kv_lora_rank, dr], dim=-1)
+        kv = self.kv_b_proj(self.kv_a_layernorm(kv_latent)).reshape(b, l, H, dn + dv)
+        k_nope, v = kv.split([dn, dv], dim=-1)
+        q_nope, k_nope = self.q_norm(q_nope), self.k_norm(k_nope)
+        q_rope = apply_rotary_pos_emb(q_rope, rope_cos, rope_sin)
+        k_rope = apply_rotary_pos_emb(k_rope.unsqueeze(2), rope_cos, rope_sin).expand(b, l, H, dr)
+        q = torch.cat([q_nope, q_rope], dim=-1)
+        k = torch.cat([k_nope, k_rope], dim=-1)
+        attn = self.attn_impl(q, k, v).reshape(b, l, H * dv)
+        if self.use_output_gate:
+            attn = attn * torch.sigmoid(self.g_proj(x))
+        return self.out_proj(attn)
+
+
+class TransformerBlock(nn.Module):
+    """x += attn(norm1(x)) * attn_scale;  x += mlp(norm2(x)) * mlp_scale
+    (vector gates initialised to zero)."""
+
+    def __init__(self, hidden_size, num_heads, q_lora_rank, kv_lora_rank, qk_nope_head_dim,
+                 qk_rope_head_dim, v_head_dim, mlp_ratio=8 / 3, weight_init_constant=1.0,
+                 norm_eps=1e-6, attn_impl=sdpa_math_attention, use_attn_res=False, situ_beta=4.0,
+                 situ_linear_beta=25.0, mla_use_output_gate=True):
+        super().__init__()
+        self.norm1 = RMSNorm(hidden_size, eps=norm_eps)
+        self.attn = MLAAttention(hidden_size, num_heads=num_heads, q_lora_rank=q_lora_rank,
+                                 kv_lora_rank=kv_lora_rank, qk_nope_head_dim=qk_nope_head_dim,
+                                 qk_rope_head_dim=qk_rope_head_dim, v_head_dim=v_head_dim,
+                                 weight_init_constant=weight_init_constant, norm_eps=norm_eps,
+                                 attn_impl=attn_impl, use_output_gate=mla_use_output_gate)
+        self.norm2 = RMSNorm(hidden_size, eps=norm_eps)
+        self.mlp = SwiGLUMlp(hidden_size, int(hidden_size * mlp_ratio),
+                             weight_init_constant=weight_init_constant, situ_beta=situ_beta,
+                             situ_linear_beta=situ_linear_beta)
+        self.attn_scale = nn.Parameter(torch.zeros(hidden_size))
+        self.mlp_scale = nn.Parameter(torch.zeros(hidden_size))
+        if use_attn_res:
+            self.attn_res_norm = RMSNorm(hidden_size, eps=norm_eps)
+            self.mlp_res_norm = RMSNorm(hidden_size, eps=norm_eps)
+            self.attn_res_proj = scaled_variance_linear(hidden_size, 1, bias=False,
+                                                        init_constant=weight_init_constant)
+            self.mlp_res_proj = scaled_variance_linear(hidden_size, 1, bias=False,
+                                                       init_constant=weight_init_constant)
+
+    def forward(self, x, rope_cos, rope_sin):
+        x = x + self.attn(self.norm1(x), rope_cos, rope_sin) * self.attn_scale
+        return x + self.mlp(self.norm2(x)) * self.mlp_scale

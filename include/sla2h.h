@@ -183,6 +183,60 @@ int sla2h_fwd_jvp_1d(const void* q, const void* dq, const void* kt, const void* 
                      int dtype, int B, int H, int64_t L, int D, int bq, int bk, int T,
                      float scale, float eps_l, float* o, float* dout, void* stream);
 
+/* ---- MLA sublayer / MLP sublayer JVP stages (row kernels) --------------- */
+
+/*
+ * RMSNorm JVP over rows of width D (<= 1024): y = w x / r,
+ * dy = w (dx / r - x mean(x dx) / r^3), r = sqrt(mean(x^2) + eps), fp32 math.
+ * x, dx rows at stride sx; y, dy rows at stride sy (elements).  in_dtype /
+ * out_dtype: SLA2H_DTYPE_F16, SLA2H_DTYPE_BF16 or 2 (fp32); fp32 -> 16-bit,
+ * fp32 -> fp32 and 16-bit -> same 16-bit are supported.  Replaces
+ * _rmsnorm_jvp_strided (models/triton_mla_block_jvp.py:237-268).
+ */
+int sla2h_rmsnorm_jvp(const void* x, const void* dx, int in_dtype, const float* w, int64_t rows,
+                      int D, int64_t sx, void* y, void* dy, int64_t sy, int out_dtype, float eps,
+                      void* stream);
+
+/*
+ * MLA head preparation from the stacked [primal; tangent] GEMM outputs
+ * (2*B*S rows): qb (2BS, H*(dn+dr)) = per head [q_nope | q_rope];
+ * kvb (2BS, H*(dn+dv)) = per head [k_nope | v]; kr = the shared k_rope band
+ * (dr values at row stride skr, e.g. a column slice of the fused q_a/kv_a
+ * output).  Per head: RMSNorm JVP of the nope bands (w_qnorm / w_knorm, dn),
+ * RoPE rotation of (2i, 2i+1) pairs by rope_cos/sin (S, dr/2) fp32, v copied.
+ * Outputs q, dq, k, dk, v, dv as (B, H, L=S, 64) 16-bit, token s written at row
+ * pos[s] (pos (S,) int32, e.g. the inverse tile permutation) or s when pos is
+ * NULL.  dn = dr = 32, dv = 64.  Replaces _q_prep_kernel / _kv_prep_kernel and
+ * the (B,S,H,hd) -> (B,H,L,hd) [perm] copies (models/triton_mla_block_jvp.py:
+ * 279-425, models/mla_jvp_fast.py:95-136).
+ */
+int sla2h_mla_qkv_prep(const void* qb, const void* kvb, const void* kr, int64_t skr,
+                       const float* w_qnorm, const float* w_knorm, const float* rope_cos,
+                       const float* rope_sin, const int32_t* pos, int dtype, int B, int S, int H,
+                       int dn, int dr, int dv, float eps, void* q, void* dq, void* k, void* dk,
+                       void* v, void* dv_out, void* stream);
+
+/*
+ * Attention output back to model order, rounded to 16 bits, and the output
+ * gate's JVP: out (2BS, H*dv) stacked, primal row (b,s) = a sigmoid(z), tangent
+ * row = da sigmoid(z) + a sigmoid(z)(1 - sigmoid(z)) dz, with a, da the op's
+ * (B,H,L,dv) fp32 outputs at row pos[s] (or s) and z (2BS, H*dv) 16-bit
+ * stacked gate logits; z NULL = no gate.  Replaces the attention-buffer
+ * scatter and _out_gate_jvp_kernel (models/mla_jvp_fast.py:142-193,
+ * models/triton_mla_block_jvp.py:480-498).
+ */
+int sla2h_mla_out_gate(const float* o, const float* dout, const int32_t* pos, const void* z,
+                       int dtype, int B, int S, int H, int dv, void* out, void* stream);
+
+/*
+ * SituAndMul JVP on stacked rows: gu (2*rows, 2F) = [gate | up] per row,
+ * primal rows first; act (2*rows, F): h = situ(g) u, dh = situ'(g) dg u +
+ * situ(g) du, situ(g) = beta tanh(g / beta) sigmoid(g).  Replaces
+ * _swiglu_row_jvp (models/triton_mla_block_jvp.py:437-471).
+ */
+int sla2h_situ_jvp(const void* gu, int64_t rows, int F, float beta, int dtype, void* act,
+                   void* stream);
+
 /* ---- training forward (the module's autograd forward) ------------------ */
 
 /*

@@ -810,3 +810,129 @@ def dense_1d_f64(q, k, v, lut, alpha, bq, bk=E, eps=EPS_L):
     a = torch.as_tensor(alpha, dtype=torch.float64).repeat_interleave(bq, dim=-1)[:, :L]
     a = a.view(1, H, L, 1)
     return a * o_s + (1.0 - a) * o_l
+
+
+# ---------------------------------------------------------------------------
+# MLA attention sublayer and MLP sublayer JVP (models/mla_jvp_fast.py:53-228,
+# kernels of models/triton_mla_block_jvp.py:237-498) and the eager block they
+# differentiate (models/imf_dit_video.py:121-187, 266-284, 422-532).
+# ---------------------------------------------------------------------------
+def rms_jvp(x, dx, w, eps):
+    """y = w x / r, dy = w (dx / r - x mean(x dx) / r^3), r = sqrt(mean(x^2) + eps)."""
+    inv = 1.0 / torch.sqrt((x * x).mean(-1, keepdim=True) + eps)
+    mxdx = (x * dx).mean(-1, keepdim=True)
+    return w * x * inv, w * (dx * inv - x * (mxdx * inv ** 3))
+
+
+def rope_rotate(x, cos, sin):
+    """Rotate pairs (x[..., 2i], x[..., 2i+1]) of x (B, S, ..., 2*n) by (S, n) angles."""
+    shape = (1, cos.shape[0]) + (1,) * (x.dim() - 3) + (cos.shape[1],)
+    c, s = cos.reshape(shape), sin.reshape(shape)
+    re, im = x[..., 0::2], x[..., 1::2]
+    return torch.stack([re * c - im * s, re * s + im * c], -1).flatten(-2)
+
+
+def mla_attn_jvp(h, dh, p, cos, sin, eps, attn_jvp, t16=torch.float16):
+    """Hand-propagated JVP of a = out_proj(gate(attn(norm1(h)))) * g_attn with the
+    reference fast path's 16-bit rounding points (stacked fp16 buffers, fp16
+    weights, 16-bit GEMM outputs with fp32 accumulation); t16=None: exact.
+    attn_jvp(q, k, v, dq, dk, dv) on (B, H, S, 64) in model order -> (o, do) fp32.
+    Returns (a, da) (B, S, d)."""
+    ex = t16 is None
+    dt = torch.float64 if ex else torch.float32
+    r = (lambda x: x) if ex else (lambda x: x.to(t16).to(dt))
+    f = lambda x: torch.as_tensor(x).to(dt)
+    h, dh = f(h), f(dh)
+    B, S, D = h.shape
+    H, dq, dc, dn, dr, dv = (p[n] for n in ("H", "dq", "dc", "dn", "dr", "dv"))
+    W = lambda n: r(f(p[n]))
+    lin = lambda x, w: r(x @ w.transpose(0, 1))
+    n1, dn1 = (r(t) for t in rms_jvp(h, dh, f(p["w_norm1"]), eps))
+    wa = torch.cat([W("w_qa"), W("w_kva")], 0)
+    a_, da_ = lin(n1, wa), lin(dn1, wa)
+    ql, dql = (r(t) for t in rms_jvp(a_[..., :dq], da_[..., :dq], f(p["w_qa_ln"]), eps))
+    kl, dkl = (r(t) for t in rms_jvp(a_[..., dq:dq + dc], da_[..., dq:dq + dc],
+                                     f(p["w_kva_ln"]), eps))
+    qb = lin(ql, W("w_qb")).view(B, S, H, dn + dr)
+    dqb = lin(dql, W("w_qb")).view(B, S, H, dn + dr)
+    kvb = lin(kl, W("w_kvb")).view(B, S, H, dn + dv)
+    dkvb = lin(dkl, W("w_kvb")).view(B, S, H, dn + dv)
+    qn, dqn = rms_jvp(qb[..., :dn], dqb[..., :dn], f(p["w_qnorm"]), eps)
+    kn, dkn = rms_jvp(kvb[..., :dn], dkvb[..., :dn], f(p["w_knorm"]), eps)
+    c, s = f(cos), f(sin)
+    qr, dqr = rope_rotate(qb[..., dn:], c, s), rope_rotate(dqb[..., dn:], c, s)
+    kr = rope_rotate(a_[..., dq + dc:], c, s)[:, :, None].expand(B, S, H, dr)
+    dkr = rope_rotate(da_[..., dq + dc:], c, s)[:, :, None].expand(B, S, H, dr)
+    hd = lambda x: r(x).permute(0, 2, 1, 3).contiguous()
+    q, dq_ = hd(torch.cat([qn, qr], -1)), hd(torch.cat([dqn, dqr], -1))
+    k, dk = hd(torch.cat([kn, kr], -1)), hd(torch.cat([dkn, dkr], -1))
+    v, dv_ = hd(kvb[..., dn:]), hd(dkvb[..., dn:])
+    o, do = attn_jvp(q, k, v, dq_, dk, dv_)
+    at = r(f(o).permute(0, 2, 1, 3).reshape(B, S, H * dv))
+    dat = r(f(do).permute(0, 2, 1, 3).reshape(B, S, H * dv))
+    if p.get("w_og") is not None:
+        z, dz = lin(n1, W("w_og")), lin(dn1, W("w_og"))
+        sg = torch.sigmoid(z)
+        at, dat = r(at * sg), r(dat * sg + at * sg * (1 - sg) * dz)
+    g = f(p["g_attn"])
+    return lin(at, W("w_out")) * g, lin(dat, W("w_out")) * g
+
+
+def mlp_jvp(h, dh, p, eps, t16=torch.float16):
+    """Hand-propagated JVP of m = down(situ(gate_up(norm2(h)))) * g_mlp (the fast
+    path has no linear_beta clamp of the up branch); t16=None: exact."""
+    ex = t16 is None
+    dt = torch.float64 if ex else torch.float32
+    r = (lambda x: x) if ex else (lambda x: x.to(t16).to(dt))
+    f = lambda x: torch.as_tensor(x).to(dt)
+    h, dh = f(h), f(dh)
+    lin = lambda x, w: r(x @ r(f(w)).transpose(0, 1))
+    n2, dn2 = (r(t) for t in rms_jvp(h, dh, f(p["w_norm2"]), eps))
+    wgu = torch.cat([f(p["w_gate"]), f(p["w_up"])], 0)
+    gu, dgu = lin(n2, wgu), lin(dn2, wgu)
+    F_ = gu.shape[-1] // 2
+    g_, u, dg, du = gu[..., :F_], gu[..., F_:], dgu[..., :F_], dgu[..., F_:]
+    beta = float(p.get("situ_beta", 1.0))
+    sg, th = torch.sigmoid(g_), torch.tanh(g_ / beta)
+    act = beta * th * sg
+    dact = (1 - th * th) * sg + beta * th * sg * (1 - sg)
+    hh, dhh = r(act * u), r(dact * dg * u + act * du)
+    gm = f(p["g_mlp"])
+    return lin(hh, p["w_down"]) * gm, lin(dhh, p["w_down"]) * gm
+
+
+def mla_attn_eager(x, p, cos, sin, eps, attn):
+    """MLAAttention.forward (models/imf_dit_video.py:422-467) applied to norm1(x)
+    and times g_attn, in the dtype of x, with attn(q, k, v) on (B, H, S, 64)."""
+    B, S, D = x.shape
+    H, dq, dc, dn, dr, dv = (p[n] for n in ("H", "dq", "dc", "dn", "dr", "dv"))
+    t = lambda n: torch.as_tensor(p[n]).to(x.dtype)
+    rms = lambda y, w: w * y / torch.sqrt((y * y).mean(-1, keepdim=True) + eps)
+    n1 = rms(x, t("w_norm1"))
+    qb = (rms(n1 @ t("w_qa").T, t("w_qa_ln")) @ t("w_qb").T).view(B, S, H, dn + dr)
+    kva = n1 @ t("w_kva").T
+    kvb = (rms(kva[..., :dc], t("w_kva_ln")) @ t("w_kvb").T).view(B, S, H, dn + dv)
+    c, s = torch.as_tensor(cos).to(x.dtype), torch.as_tensor(sin).to(x.dtype)
+    q = torch.cat([rms(qb[..., :dn], t("w_qnorm")), rope_rotate(qb[..., dn:], c, s)], -1)
+    kr = rope_rotate(kva[..., dc:], c, s)[:, :, None].expand(B, S, H, dr)
+    k = torch.cat([rms(kvb[..., :dn], t("w_knorm")), kr], -1)
+    v = kvb[..., dn:]
+    o = attn(q.permute(0, 2, 1, 3), k.permute(0, 2, 1, 3), v.permute(0, 2, 1, 3))
+    o = o.permute(0, 2, 1, 3).reshape(B, S, H * dv)
+    if p.get("w_og") is not None:
+        o = o * torch.sigmoid(n1 @ t("w_og").T)
+    return (o @ t("w_out").T) * t("g_attn")
+
+
+def mlp_eager(x, p, eps):
+    """SwiGLUMlp(norm2(x)) * g_mlp without the linear_beta clamp."""
+    t = lambda n: torch.as_tensor(p[n]).to(x.dtype)
+    n2 = t("w_norm2") * x / torch.sqrt((x * x).mean(-1, keepdim=True) + eps)
+    g_, u = n2 @ t("w_gate").T, n2 @ t("w_up").T
+    beta = float(p.get("situ_beta", 1.0))
+    return ((beta * torch.tanh(g_ / beta) * torch.sigmoid(g_) * u) @ t("w_down").T) * t("g_mlp")
+
+
+def dense_attn_f64(q, k, v):
+    """Softmax attention on (B, H, S, 64), scale 64^-0.5."""
+    return torch.softmax((q @ k.transpose(-1, -2)) * q.shape[-1] ** -0.5, -1) @ v

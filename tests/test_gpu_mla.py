@@ -1,0 +1,154 @@
+"""GPU parity of the MLA attention-sublayer JVP, the MLP-sublayer JVP and the
+block JVP (models/mla_jvp_fast.py:53-228) against the oracle's hand-propagated
+restatement (O.mla_attn_jvp / O.mlp_jvp, pinned by torch.func.jvp of the eager
+block).  Routing uses every key block (top-k fraction 1) so that 16-bit GEMM
+rounding differences cannot change a LUT entry; the routed attention ops are
+checked on their own elsewhere.  Tolerances: rel-L2 1e-2, max-abs 2e-2 of
+max(1, max|ref|)."""
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import sla2_oracle as O
+from tests.helpers import max_abs, rel_l2
+from tests.test_gpu_parity import TOL_MAX, TOL_REL, cuda, say
+
+pytestmark = pytest.mark.gpu
+
+
+def params(seed, D=256, H=2, dq=128, dc=64, F_=512):
+    g = torch.Generator().manual_seed(seed)
+    rn = lambda *s: torch.randn(*s, generator=g)
+    lin = lambda o, i: rn(o, i) * 0.5 / math.sqrt(i)
+    p = {"H": H, "dq": dq, "dc": dc, "dn": 32, "dr": 32, "dv": 64,
+         "w_norm1": 1 + 0.1 * rn(D), "w_qa": lin(dq, D), "w_kva": lin(dc + 32, D),
+         "w_qa_ln": 1 + 0.1 * rn(dq), "w_kva_ln": 1 + 0.1 * rn(dc), "w_qb": lin(H * 64, dq),
+         "w_kvb": lin(H * 96, dc), "w_qnorm": 1 + 0.1 * rn(32), "w_knorm": 1 + 0.1 * rn(32),
+         "w_out": lin(D, H * 64), "g_attn": 0.1 + 0.01 * rn(D), "w_og": lin(H * 64, D),
+         "w_norm2": 1 + 0.1 * rn(D), "w_gate": lin(F_, D), "w_up": lin(F_, D),
+         "w_down": lin(D, F_), "g_mlp": 0.1 + 0.01 * rn(D), "situ_beta": 4.0}
+    return p, g
+
+
+def gpu_params(p):
+    return {k: (cuda(v) if torch.is_tensor(v) else v) for k, v in p.items()}
+
+
+def rope(S, P):
+    from imfvideo_amd.imf_dit_video import precompute_axial_rope_3d
+    return precompute_axial_rope_3d(32, (4, 8, 8), P, axis_dims=(8, 12, 12))
+
+
+def check(got, want, tag):
+    for a, b, n in zip(got, want, ("out", "tangent")):
+        a = a.cpu().double()
+        b = b.double()
+        bound = TOL_MAX * max(1.0, b.abs().max().item())
+        print(f"  {tag} {n} max {max_abs(a, b):.2e} (bound {bound:.2e}) rel {rel_l2(a, b):.2e}",
+              flush=True)
+        assert max_abs(a, b) < bound and rel_l2(a, b) < TOL_REL
+
+
+@pytest.mark.parametrize("path", ["dense", "sla2", "cube"])
+def test_attn_sublayer_jvp(path):
+    say("attn_sublayer_jvp", path)
+    from imfvideo_amd.mla_jvp_fast import attn_sublayer_jvp, mla_fp16_cache
+    from imfvideo_amd.mla_video_sparse_jvp import tile_permutation
+    p, g = params(3)
+    B, P = 2, 18
+    S = 256 + P
+    h = torch.randn(B, S, 256, generator=g)
+    dh = 0.1 * torch.randn(B, S, 256, generator=g)
+    cos, sin = rope(S, P)
+    H = p["H"]
+    nb = -(-S // 64)
+    if path == "dense":
+        lut = np.broadcast_to(np.arange(nb, dtype=np.int32), (B, H, nb, nb)).copy()
+        ref_attn = lambda q, k, v, dq, dk, dv: O.jvp_1d(q, k, v, dq, dk, dv, torch.ones(H, nb),
+                                                        lut, 64)
+    elif path == "sla2":
+        mq = -(-S // 128)
+        alpha = torch.rand(H, mq, generator=g) * 0.8 + 0.1
+        p["sla2"] = {"alpha": alpha, "proj_q": None, "proj_k": None, "topk": 1.0, "bq": 128,
+                     "bk": 64}
+        lut = np.broadcast_to(np.arange(nb, dtype=np.int32), (B, H, mq, nb)).copy()
+        ref_attn = lambda q, k, v, dq, dk, dv: O.jvp_1d(q, k, v, dq, dk, dv, alpha, lut, 128)
+    else:
+        perm, inv, Np = tile_permutation((4, 8, 8), (4, 4, 4), P, torch.device("cpu"))
+        alpha = torch.rand(H, nb, generator=g) * 0.8 + 0.1
+        p["cube"] = {"alpha": alpha, "proj_q": None, "proj_k": None, "topk": 1.0, "Np": Np,
+                     "E": 64, "P": P, "perm": perm, "inv": inv}
+        lut = np.broadcast_to(np.arange(Np, dtype=np.int32), (B, H, nb, Np)).copy()
+
+        def ref_attn(q, k, v, dq, dk, dv):
+            t = lambda x: x[:, :, perm]
+            o, do = O.cube_jvp(*(t(x) for x in (q, k, v, dq, dk, dv)), alpha, lut, Np, P,
+                               t16=torch.float16)
+            return o[:, :, inv], do[:, :, inv]
+    pg = gpu_params(p)
+    if "cube" in p:
+        pg["cube"] = dict(p["cube"], alpha=cuda(alpha))
+    if "sla2" in p:
+        pg["sla2"] = dict(p["sla2"], alpha=cuda(alpha))
+    a, da = attn_sublayer_jvp(cuda(h), cuda(dh), pg, mla_fp16_cache(pg), cuda(cos), cuda(sin), 1e-6)
+    torch.cuda.synchronize()
+    want = O.mla_attn_jvp(h, dh, p, cos, sin, 1e-6, ref_attn)
+    check((a, da), want, path)
+
+
+def test_mlp_and_block_jvp():
+    say("mlp_sublayer_jvp, block_jvp (cube attention)")
+    from imfvideo_amd.mla_jvp_fast import block_jvp, mla_fp16_cache, mlp_sublayer_jvp
+    from imfvideo_amd.mla_video_sparse_jvp import tile_permutation
+    p, g = params(4)
+    B, P = 1, 18
+    S = 256 + P
+    h = torch.randn(B, S, 256, generator=g)
+    dh = 0.1 * torch.randn(B, S, 256, generator=g)
+    pg = gpu_params(p)
+    w16 = mla_fp16_cache(pg)
+    m, dm = mlp_sublayer_jvp(cuda(h), cuda(dh), pg, w16, 1e-6)
+    check((m, dm), O.mlp_jvp(h, dh, p, 1e-6), "mlp")
+    perm, inv, Np = tile_permutation((4, 8, 8), (4, 4, 4), P, torch.device("cpu"))
+    nb = -(-S // 64)
+    alpha = torch.full((p["H"], nb), 0.7)
+    p["cube"] = {"alpha": alpha, "topk": 1.0, "Np": Np, "E": 64, "P": P, "perm": perm, "inv": inv}
+    pg["cube"] = dict(p["cube"], alpha=cuda(alpha))
+    cos, sin = rope(S, P)
+    x, dx = block_jvp(cuda(h), cuda(dh), pg, w16, cuda(cos), cuda(sin), 1e-6)
+    lut = np.broadcast_to(np.arange(Np, dtype=np.int32), (B, p["H"], nb, Np)).copy()
+
+    def ref_attn(q, k, v, dq, dk, dv):
+        t = lambda y: y[:, :, perm]
+        o, do = O.cube_jvp(*(t(y) for y in (q, k, v, dq, dk, dv)), alpha, lut, Np, P,
+                           t16=torch.float16)
+        return o[:, :, inv], do[:, :, inv]
+    a, da = O.mla_attn_jvp(h, dh, p, cos, sin, 1e-6, ref_attn)
+    h1, dh1 = h + a, dh + da
+    m, dm = O.mlp_jvp(h1, dh1, p, 1e-6)
+    check((x, dx), (h1 + m, dh1 + dm), "block")
+
+
+def test_transformer_block_training_step():
+    say("TransformerBlock with SLA2CubeQATAttentionImpl: forward + backward")
+    from functools import partial
+    from imfvideo_amd.imf_dit_video import TransformerBlock, precompute_axial_rope_3d
+    from imfvideo_amd.sla2_cube_qat import SLA2CubeQATAttentionImpl
+    torch.manual_seed(5)
+    S = 274
+    impl = partial(SLA2CubeQATAttentionImpl, seq_len=S, num_heads=2, grid=(4, 8, 8),
+                   tile=(4, 4, 4), topk=0.5)
+    blk = TransformerBlock(256, 2, 128, 64, 32, 32, 64, mlp_ratio=2, attn_impl=impl).cuda()
+    with torch.no_grad():
+        blk.attn_scale.fill_(0.1)
+        blk.mlp_scale.fill_(0.1)
+    cos, sin = precompute_axial_rope_3d(32, (4, 8, 8), 18, axis_dims=(8, 12, 12))
+    x = torch.randn(2, S, 256, device="cuda", requires_grad=True)
+    out = blk(x, cuda(cos), cuda(sin))
+    (0.5 * out.pow(2).sum()).backward()
+    assert torch.isfinite(out).all() and torch.isfinite(x.grad).all()
+    assert blk.attn.attn_impl.alpha_logit.grad is not None
+    assert torch.isfinite(blk.attn.q_b_proj.weight.grad).all()
+    assert blk.attn.attn_impl.logit_max_log2.shape == (2,)
