@@ -189,13 +189,67 @@ def train_bench(args):
     print(json.dumps(out), flush=True)
 
 
+def mla_bench(args):
+    """Config 4: the MLA attention sublayer (sla2_mla_jvp variant) forward + JVP at
+    N=29,952, d=512, H=8, dq=256, dc=128, dn=dr=32, dv=64, partial axial RoPE
+    (8,12,12) over the 12x48x52 grid, weights N(0, 0.5/sqrt(d_in)), x ~ N(0,1)
+    rounded to bf16, dx = 0.1 N(0,1), top-k 10% of 64-row key blocks with
+    128-row query blocks.  Prints its own JSON line."""
+    import math
+    from imfvideo_amd.imf_dit_video import precompute_axial_rope_3d
+    from imfvideo_amd.mla_jvp_fast import attn_sublayer_jvp, mla_fp16_cache
+
+    B, S, D, H, dq, dc = 1, 29952, 512, 8, 256, 128
+    g = torch.Generator().manual_seed(4)
+    dev = torch.device("cuda:0")
+    lin = lambda o, i: (torch.randn(o, i, generator=g) * 0.5 / math.sqrt(i)).to(dev)
+    ones = lambda n: torch.ones(n, device=dev)
+    p = {"H": H, "dq": dq, "dc": dc, "dn": 32, "dr": 32, "dv": 64, "w_norm1": ones(D),
+         "w_qa": lin(dq, D), "w_kva": lin(dc + 32, D), "w_qa_ln": ones(dq), "w_kva_ln": ones(dc),
+         "w_qb": lin(H * 64, dq), "w_kvb": lin(H * 96, dc), "w_qnorm": ones(32),
+         "w_knorm": ones(32), "w_out": lin(D, H * 64), "g_attn": ones(D), "w_og": lin(H * 64, D),
+         "w_norm2": ones(D), "w_gate": lin(8, D), "w_up": lin(8, D), "w_down": lin(D, 8),
+         "g_mlp": ones(D)}
+    mq = -(-S // 128)
+    p["sla2"] = {"alpha": torch.full((H, mq), 0.9, device=dev), "proj_q": None, "proj_k": None,
+                 "topk": 0.1, "bq": 128, "bk": 64}
+    w16 = mla_fp16_cache(p)
+    x = torch.randn(B, S, D, generator=g).to(torch.bfloat16).float().to(dev)
+    dx = (0.1 * torch.randn(B, S, D, generator=g)).to(dev)
+    cos, sin = (t.to(dev) for t in precompute_axial_rope_3d(32, (12, 48, 52), 0, axis_dims=(8, 12, 12)))
+    for _ in range(args.warmup):
+        attn_sublayer_jvp(x, dx, p, w16, cos, sin, 1e-6)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        evs[i][0].record()
+        attn_sublayer_jvp(x, dx, p, w16, cos, sin, 1e-6, stage_events=evs[i][1:])
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    st = {name: statistics.mean(e[k].elapsed_time(e[k + 1]) for e in evs) * 1e3
+          for k, name in enumerate(["norm_gemms_head_prep", "sla2_mla_jvp", "gate_out_proj"])}
+    print(json.dumps({
+        "metric": "ms per MLA attention sublayer fwd+JVP (sla2_mla_jvp variant) @N=29,952, "
+                  "1 MI355X", "value": round(ms, 4), "unit": "ms", "n_gpus": 1,
+        "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None, "dtype": "fp16",
+        "data": "synthetic (CPU-seeded; weights N(0, 0.5/sqrt(d_in)); x bf16 N(0,1))",
+        "config": {"workload": "MLA attention sublayer JVP (BASELINE Config 4)", "B": B, "N": S,
+                   "d": D, "H": H, "dq": dq, "dc": dc, "bq": 128, "bk": 64, "topk": 0.1},
+        "stages_us": {k_: round(v_, 2) for k_, v_ in st.items()}}), flush=True)
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
-    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 5],
-                    help="5: the attention op's training step at Config 5's shape (own line)")
+    ap.add_argument("--config", type=int, default=3, choices=[1, 2, 3, 4, 5],
+                    help="4: the MLA sublayer JVP (own line); 5: the attention op's training "
+                         "step at Config 5's shape (own line)")
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB fp32 copy kernel (torch.mul by 1) three times: "
@@ -216,6 +270,9 @@ def main():
 
     if args.config == 5:
         train_bench(args)
+        return
+    if args.config == 4:
+        mla_bench(args)
         return
 
     from imfvideo_amd import ops

@@ -79,11 +79,13 @@ def _vec(w, dev):
     return w.detach().to(dev, torch.float32).contiguous()
 
 
-def attn_sublayer_jvp(h, dh, p, w16, cos, sin, eps):
+def attn_sublayer_jvp(h, dh, p, w16, cos, sin, eps, stage_events=None):
     """MLA attention sublayer JVP: a = out_proj(gate(attn(norm1(h)))) * g_attn.
 
-    Returns (a, da): (b, l, d) fp32.
+    Returns (a, da): (b, l, d) fp32.  stage_events: optional three HIP events
+    recorded before the attention op, after it, and at the end.
     """
+    rec = (lambda i: stage_events[i].record()) if stage_events else (lambda i: None)
     ops._need_gpu(h, dh)
     B, S, D = h.shape
     H, dq, dc = p["H"], p["dq"], p["dc"]
@@ -119,6 +121,7 @@ def attn_sublayer_jvp(h, dh, p, w16, cos, sin, eps):
         sin.float().contiguous().data_ptr(), ops._ptr(pos), 0, B, S, H, dn, dr, dv, float(eps),
         *(t.data_ptr() for t in qkv), _stream(dev)), "sla2h_mla_qkv_prep")
     q, dq_, k, dk, v, dv_ = qkv
+    rec(0)
 
     if cube is not None:
         o, do = sla2_cube_qat_jvp_fused(q, k, v, dq_, dk, dv_, cube["alpha"], cube["topk"],
@@ -137,6 +140,7 @@ def attn_sublayer_jvp(h, dh, p, w16, cos, sin, eps):
             B, H, mq, nb).contiguous()
         o, do = ops.jvp_1d(q, k, v, dq_, dk, dv_, torch.ones(H, mq, device=dev), lut, 64)
 
+    rec(1)
     w_og = w16.get("w_og")
     z = F.linear(xs, w_og) if w_og is not None else None             # (M, H*dv)
     gated = torch.empty(M, H * dv, device=dev, dtype=_FP16)
@@ -145,7 +149,9 @@ def attn_sublayer_jvp(h, dh, p, w16, cos, sin, eps):
         gated.data_ptr(), _stream(dev)), "sla2h_mla_out_gate")
     proj = F.linear(gated, w16["w_out"]).float().view(2 * B, S, D)
     g = _vec(p["g_attn"], dev)
-    return proj[:B] * g, proj[B:] * g
+    out = proj[:B] * g, proj[B:] * g
+    rec(2)
+    return out
 
 
 def mlp_sublayer_jvp(h, dh, p, w16, eps):
