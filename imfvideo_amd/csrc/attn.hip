@@ -283,53 +283,61 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
     const float c = tile_c(j);
     const int64_t key0 = (int64_t)n * kTa + 16 * w + 4 * g;
+    // all products of the tile first (scores of both query sub-tiles, then the
+    // tangent scores), one rescale test for the tile, then the exponentials:
+    // one basic block holds the MFMAs and the VALU work they overlap with
+    float sv[kQT][4];  // raw scores (integer-valued for INT8)
+    float mt[kQT];
+    f32x4 dsv[kQT];
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
-      float sv[4];  // raw scores (integer-valued for INT8)
-      float mt;
       if (S16) {
         f32x4 s16 = mfma_16x16x32<T16>(kr.ka[0], qsh[qt][2][l], f32x4{0.f, 0.f, 0.f, 0.f});
         s16 = mfma_16x16x32<T16>(kr.ka[1], qsh[qt][3][l], s16);
-        float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          sv[i] = s16[i];
-          if (!MASK || key0 + i < L) mx = fmaxf(mx, sv[i]);
-        }
-        mt = mx * c;
+        for (int i = 0; i < 4; ++i) sv[qt][i] = s16[i];
       } else {
         const i32x4 si = mfma_i8_16x16x64(kr.k8, q8sh[qt][l], i32x4{0, 0, 0, 0});
-        int mx;
-        if (MASK) {
-          mx = INT_MIN;
 #pragma unroll
-          for (int i = 0; i < 4; ++i)
-            if (key0 + i < L) mx = max(mx, si[i]);
-        } else {
-          mx = max(max(si[0], si[1]), max(si[2], si[3]));
-        }
-#pragma unroll
-        for (int i = 0; i < 4; ++i) sv[i] = (float)si[i];
-        mt = mx == INT_MIN ? -INFINITY : (float)mx * c;
+        for (int i = 0; i < 4; ++i) sv[qt][i] = (float)si[i];
       }
-      if (__builtin_amdgcn_ballot_w64(mt > mthr[qt]) != 0) rescale(qt, mt, pend);
-      float p[4], ds[4], t[4];
-      if (TAN) {
+    }
+    if (TAN) {
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
         f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
         for (int ks = 0; ks < 4; ++ks) d = mfma_16x16x32<T16>(kr.ka[ks], qsh[qt][ks][l], d);
-#pragma unroll
-        for (int i = 0; i < 4; ++i) ds[i] = PRE ? d[i] : d[i] * a.scale;
+        dsv[qt] = d;
       }
+    }
+    bool over = false;
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+      float mx = -INFINITY;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+        if (!MASK || key0 + i < L) mx = fmaxf(mx, sv[qt][i]);
+      mt[qt] = mx * c;
+      over |= mt[qt] > mthr[qt];
+    }
+    if (__builtin_amdgcn_ballot_w64(over) != 0) {
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt)
+        if (__builtin_amdgcn_ballot_w64(mt[qt] > mthr[qt]) != 0) rescale(qt, mt[qt], pend);
+    }
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+      float p[4], t[4];
       const float moff = mrun[qt];
       float ts = 0.f;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float e = fmaf(sv[i], c, -moff);
+        float e = fmaf(sv[qt][i], c, -moff);
         if (MASK && key0 + i >= L) e = -INFINITY;
         p[i] = fast_exp2(e);
         if (TAN) {
-          t[i] = p[i] * ds[i];
+          t[i] = p[i] * (PRE ? dsv[qt][i] : dsv[qt][i] * a.scale);
           ts += t[i];
         }
       }
