@@ -270,10 +270,11 @@ __global__ __launch_bounds__(256) void states_sum_kernel(const float* __restrict
 // ---------------------------------------------------------------------------
 // Complement records.  For each query block m of a head:
 //   Hc[m] = sum over the video tiles n NOT routed for m of Hb[n]   (and dHc, zc, dzc)
-// computed as one GEMM per head, C = Mc . S, with Mc[m][n] = 1 - sel(m, n)
+// computed as a GEMM per head, C = Mc . S, with Mc[m][n] = 1 - sel(m, n)
 // (Mb x Np, 0/1) and S = [Hb | dHb | zb | dzb] (Np x 8320 columns, fp32).  S
 // is split into bf16 hi + lo halves (about 16 significant bits) and the
-// products accumulate in fp32 on MFMA; the mask is exact in bf16.
+// products accumulate in fp32 on MFMA; the mask is exact in bf16.  The H
+// columns run in comp_gemm_kernel, the z columns in comp_mask_kernel.
 //
 // Record of (b,h,m), kRecBytes bytes, fp32:
 //   [0, 16384) Hc[d][v] row-major, [16384, 32768) dHc, [32768, 33024) zc,
@@ -283,11 +284,30 @@ constexpr int kMaskSub = 32;  // 16-row mask sub-tiles per GEMM workgroup (512 r
 constexpr int kCompCols = 64;  // state columns per GEMM workgroup
 constexpr int kCompThreads = 512;  // 8 waves
 
+// 8 mask bits -> the 8 bf16 A-operand slots (1.0 where set)
+__device__ __forceinline__ u32x4 expand_mask8(uint32_t b) {
+  u32x4 o;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const uint32_t v = (b >> (2 * e)) & 3u;
+    o[e] = ((v & 1u) | ((v & 2u) << 15)) * 0x3F80u;
+  }
+  return o;
+}
+
 // Complement bit masks cbits[bh][kc][m] (m < 16 MT): bit j of word (kc, m) is
 // 1 where tile n = 32 kc + j < Np is not routed for query block m < Mb.
+// With zb given, the workgroup also writes the zc (and, with dzb, dzc) parts
+// of its 16 query blocks' records: the same 0/1-mask product as the GEMM
+// below (bf16 hi + lo halves of zb, chunks of 32 tiles in the same order),
+// wave w owning columns 16w..16w+15.  This keeps the 64- and 128-column z
+// parts out of the GEMM's grid.
 __global__ __launch_bounds__(256) void comp_mask_kernel(const int32_t* __restrict__ lut, int Mb,
                                                       int Np, int T, int MT, int NC,
-                                                      uint32_t* __restrict__ cbits) {
+                                                      uint32_t* __restrict__ cbits,
+                                                      const float* __restrict__ zb,
+                                                      const float* __restrict__ dzb,
+                                                      unsigned char* __restrict__ comp) {
   extern __shared__ uint32_t selbits[];  // [16][NC]
   const int mt = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
   for (int i = tid; i < 16 * NC; i += 256) selbits[i] = 0u;
@@ -307,17 +327,65 @@ __global__ __launch_bounds__(256) void comp_mask_kernel(const int32_t* __restric
     const uint32_t valid = nv >= 32 ? 0xffffffffu : ((1u << nv) - 1u);
     cbits[((int64_t)bh * NC + kc) * (MT * 16) + m] = m < Mb ? (~selbits[row * NC + kc] & valid) : 0u;
   }
-}
+  if (zb == nullptr) return;
 
-// 8 mask bits -> the 8 bf16 A-operand slots (1.0 where set)
-__device__ __forceinline__ u32x4 expand_mask8(uint32_t b) {
-  u32x4 o;
+  const int w = tid >> 6, l = tid & 63, r = l & 15, g = l >> 4;
+  const bool tan = dzb != nullptr;
+  const bool rowok = mt * 16 + r < Mb;
+  // tiles n >= Np read as 0 (buffer range check); four chunks of loads in flight
+  const auto rz = make_rsrc(zb + (int64_t)bh * Np * kT, (int64_t)Np * kT * 4);
+  const auto rdz = make_rsrc(tan ? dzb + (int64_t)bh * Np * kT : zb, (int64_t)Np * kT * 4);
+  const int coff = (16 * w + r) * 4;
+  auto split = [](const float* x, u32x4& hi, u32x4& lo) {
 #pragma unroll
-  for (int e = 0; e < 4; ++e) {
-    const uint32_t v = (b >> (2 * e)) & 3u;
-    o[e] = ((v & 1u) | ((v & 2u) << 15)) * 0x3F80u;
+    for (int e = 0; e < 4; ++e) {
+      const uint32_t h = pack_pair<BF16>(x[2 * e], x[2 * e + 1]);
+      hi[e] = h;
+      lo[e] = pack_pair<BF16>(x[2 * e] - __builtin_bit_cast(float, h << 16),
+                              x[2 * e + 1] - __builtin_bit_cast(float, h & 0xffff0000u));
+    }
+  };
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}, dacc = acc;
+  constexpr int kU = 4;
+  for (int kc0 = 0; kc0 < NC; kc0 += kU) {
+    float x[kU][8], dx[kU][8];
+#pragma unroll
+    for (int u = 0; u < kU; ++u)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int off = (32 * (kc0 + u) + 8 * g + j) * (kT * 4) + coff;
+        x[u][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rz, off, 0, 0));
+        dx[u][j] = tan ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rdz, off, 0, 0))
+                       : 0.f;
+      }
+#pragma unroll
+    for (int u = 0; u < kU; ++u) {
+      const int kc = kc0 + u;
+      if (kc >= NC) break;
+      const int nv = Np - 32 * kc;
+      const uint32_t valid = nv >= 32 ? 0xffffffffu : ((1u << nv) - 1u);
+      const uint32_t word = rowok ? (~selbits[r * NC + kc] & valid) : 0u;
+      const u32x4 am = expand_mask8((word >> (8 * g)) & 0xffu);
+      u32x4 hi, lo;
+      split(x[u], hi, lo);
+      acc = mfma_bf16_16x16x32(am, hi, acc);
+      acc = mfma_bf16_16x16x32(am, lo, acc);
+      if (tan) {
+        split(dx[u], hi, lo);
+        dacc = mfma_bf16_16x16x32(am, hi, dacc);
+        dacc = mfma_bf16_16x16x32(am, lo, dacc);
+      }
+    }
   }
-  return o;
+  // lane (g, r) element i = C[query block 16 mt + 4g + i][column 16w + r]
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int m = mt * 16 + 4 * g + i;
+    if (m >= Mb) continue;
+    unsigned char* rec = comp + ((int64_t)bh * Mb + m) * kRecBytes;
+    reinterpret_cast<float*>(rec + 32768)[16 * w + r] = acc[i];
+    if (tan) reinterpret_cast<float*>(rec + 33024)[16 * w + r] = dacc[i];
+  }
 }
 
 // One workgroup of 8 waves: 64 state columns x up to 512 query blocks of one
@@ -609,12 +677,15 @@ extern "C" int sla2h_complement(const float* Hb, const float* dHb, const float* 
   const int MT = (Mb + 15) / 16, NC = (Np + 31) / 32;
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto cbits = static_cast<uint32_t*>(workspace);
-  comp_mask_kernel<<<dim3(MT, B * H), 256, (size_t)16 * NC * 4, st>>>(lut, Mb, Np, T, MT, NC, cbits);
+  auto out = static_cast<unsigned char*>(comp);
+  // mask bits plus the z parts of the records; the GEMM takes the H parts only
+  // (128 or 64 column tiles per head: whole rounds of workgroups)
+  comp_mask_kernel<<<dim3(MT, B * H), 256, (size_t)16 * NC * 4, st>>>(lut, Mb, Np, T, MT, NC,
+                                                                      cbits, zb, dzb, out);
   int err = (int)hipGetLastError();
   if (err) return err;
-  const int ncols = tan ? 8320 : 4160;
+  const int ncols = tan ? 8192 : 4096;
   dim3 grid(ncols / kCompCols, B * H, (MT + kMaskSub - 1) / kMaskSub);
-  auto out = static_cast<unsigned char*>(comp);
   if (tan)
     comp_gemm_kernel<true><<<grid, kCompThreads, 0, st>>>(Hb, dHb, zb, dzb, cbits, Mb, Np, MT, NC, out);
   else

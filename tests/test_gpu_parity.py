@@ -224,6 +224,30 @@ def test_all_tiles_routed_and_zero_tiles():
     assert torch.isfinite(o2).all() and torch.isfinite(do2).all()
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_quantize_half_integer_quotients(dt):
+    """x / s exactly on k + 1/2 (round half away from zero) and random tiles."""
+    from imfvideo_amd import ops
+    say("quantize half-integer quotients", dt)
+    g = torch.Generator().manual_seed(17)
+    halves = (torch.arange(64 * 64, dtype=torch.float32) % 254 - 127 + 0.5).view(64, 64)
+    t0 = halves.clone()
+    t0[0, 0] = 127.0                     # max |x| = 127 -> s = fl(1 + 1e-12) = 1
+    t1 = halves / 8                      # (k + 1/2) / 8 ...
+    t1[5, 7] = 127.0 / 8                 # ... with s = fl(2^-3 + 1e-12) = 2^-3
+    t2 = torch.randn(64, 64, generator=g) * 3.7   # s not a power of two
+    t3 = torch.randn(64, 64, generator=g) * 1e-3
+    x = torch.cat([t0, t1, t2, t3]).view(1, 1, 256, 64).to(dt)
+    q8, qs, k8, ks, _, _ = ops.quant_pool_qk(cuda(x), cuda(x.flip(2).contiguous()), 4)
+    want_q, want_s = O.quantize_blocks(x.float())
+    assert float(want_s[0, 0, 0]) == 1.0 and float(want_s[0, 0, 1]) == 0.125
+    assert np.array_equal(q8.cpu().numpy(), want_q)
+    assert np.array_equal(qs.cpu().numpy(), want_s)
+    want_k, want_ks = O.quantize_blocks(x.flip(2).float())
+    assert np.array_equal(k8.cpu().numpy(), want_k)
+    assert np.array_equal(ks.cpu().numpy(), want_ks)
+
+
 def test_large_inputs_stay_finite():
     say("x20 scaled inputs")
     z, dt, ins = golden("ref_geom_bf16")
