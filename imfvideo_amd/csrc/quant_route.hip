@@ -313,12 +313,17 @@ __global__ __launch_bounds__(256) void route_select_kernel(const float* __restri
                                                            int Mb, int Np, int T, float scale,
                                                            int32_t* __restrict__ lut,
                                                            uint8_t* __restrict__ mask) {
+  // pooled keys of the head, staged in chunks of DC channels (32 KB) that the
+  // four waves share
+  constexpr int DC = 128 / NK;
+  __shared__ float ksh[DC][64 * NK];
   __shared__ uint64_t win[4][64];
-  const int w = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int lane = threadIdx.x & 63;
+  const int tid = threadIdx.x;
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lane = tid & 63;
   const int bh = blockIdx.y;
   const int m0 = __builtin_amdgcn_readfirstlane((blockIdx.x * 4 + w) * R);
-  if (m0 >= Mb) return;  // whole wave; no workgroup barrier below
+  const bool active = m0 < Mb;  // uniform per wave; every wave takes the barriers
 
   const float* kt = kpool_t + (int64_t)bh * kTile * Np;
   float acc[R][NK];
@@ -327,28 +332,40 @@ __global__ __launch_bounds__(256) void route_select_kernel(const float* __restri
 #pragma unroll
     for (int i = 0; i < NK; ++i) acc[rr][i] = 0.f;
   // lane d holds q[row][d] (broadcast with readlane).  Key slots past Np
-  // need no guard: their scores are never selected (ord = 0 below), and the
+  // need no guard: their scores are never selected (ord = 0 below); the
   // buffer range check returns 0 past the end of this head's pooled keys.
   const float* qrow = qpool + ((int64_t)bh * Mb + m0) * kTile;
   float qlane[R];
 #pragma unroll
   for (int rr = 0; rr < R; ++rr) qlane[rr] = (m0 + rr < Mb) ? qrow[rr * kTile + lane] : 0.f;
   const auto rk = make_rsrc(kt, (int64_t)kTile * Np * 4);
-#pragma unroll 4
-  for (int d = 0; d < kTile; ++d) {
-    float kv[NK];
+  for (int d0 = 0; d0 < kTile; d0 += DC) {
+    __syncthreads();  // the previous chunk is consumed
 #pragma unroll
-    for (int i = 0; i < NK; ++i)
-      kv[i] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                            rk, (d * Np + lane + 64 * i) * 4, 0, 0));
+    for (int k = 0; k < DC * 64 * NK / 256; ++k) {
+      const int e = tid + 256 * k;
+      const int dd = e / (64 * NK), n = e % (64 * NK);
+      ksh[dd][n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                 rk, ((d0 + dd) * Np + n) * 4, 0, 0));
+    }
+    __syncthreads();
+    if (active) {
 #pragma unroll
-    for (int rr = 0; rr < R; ++rr) {
-      const float qv = __builtin_bit_cast(
-          float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, qlane[rr]), d));
+      for (int dd = 0; dd < DC; ++dd) {
+        float kv[NK];
 #pragma unroll
-      for (int i = 0; i < NK; ++i) acc[rr][i] = acc[rr][i] + qv * kv[i];
+        for (int i = 0; i < NK; ++i) kv[i] = ksh[dd][lane + 64 * i];
+#pragma unroll
+        for (int rr = 0; rr < R; ++rr) {
+          const float qv = __builtin_bit_cast(
+              float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, qlane[rr]), d0 + dd));
+#pragma unroll
+          for (int i = 0; i < NK; ++i) acc[rr][i] = acc[rr][i] + qv * kv[i];
+        }
+      }
     }
   }
+  if (!active) return;  // whole wave; no workgroup barrier below
 
 #pragma unroll
   for (int rr = 0; rr < R; ++rr) {

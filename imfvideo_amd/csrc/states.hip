@@ -34,8 +34,9 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
     const uint16_t* __restrict__ V, const uint16_t* __restrict__ dV, int64_t L, int Np, int Nb,
     float* __restrict__ Hb, float* __restrict__ dHb, float* __restrict__ zb,
     float* __restrict__ dzb, uint16_t* __restrict__ vt, uint16_t* __restrict__ kt) {
+  // phi^T, then (tangent, second phase) dphi^T: one buffer keeps the LDS
+  // footprint at four workgroups per CU
   __shared__ __align__(16) uint16_t phiT[2][kT][kLds];   // [hi/lo][d][r]
-  __shared__ __align__(16) uint16_t dphiT[2][kT][kLds];
   __shared__ __align__(16) uint16_t vT[kT][kLds];        // [c][r]
   __shared__ __align__(16) uint16_t dvT[kT][kLds];
   __shared__ float zred[2][4][kT];
@@ -95,8 +96,9 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
       *reinterpret_cast<uint4*>(base + ((kw * 4 + ksd + 2) * 64 + lane) * 16) = dkv;
     }
   }
+  float dphi[16];
   if (states) {
-    float x[16], phi[16], dphi[16];
+    float x[16], phi[16];
     float mx = -INFINITY;
 #pragma unroll
     for (int i = 0; i < 16; ++i) {
@@ -137,11 +139,6 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
       const uint16_t hi = T16::from_f32(phi[i]);
       phiT[0][c0 + i][r] = hi;
       phiT[1][c0 + i][r] = T16::from_f32(phi[i] - T16::to_f32(hi));
-      if (TAN) {
-        const uint16_t dhi = T16::from_f32(dphi[i]);
-        dphiT[0][c0 + i][r] = dhi;
-        dphiT[1][c0 + i][r] = T16::from_f32(dphi[i] - T16::to_f32(dhi));
-      }
     }
     // column sums over the 64 rows: 16 rows per wave by shuffles, then LDS
     const int w = tid >> 6;
@@ -198,16 +195,12 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
     acc[vt_] = f32x4{0.f, 0.f, 0.f, 0.f};
     dacc[vt_] = acc[vt_];
   }
+  // phase 1: H = phi^T V and the phi^T dV half of dH
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks) {
     const int k0 = 32 * ks + 8 * g;
     const u32x4 ah = *reinterpret_cast<const u32x4*>(&phiT[0][drow][k0]);
     const u32x4 al = *reinterpret_cast<const u32x4*>(&phiT[1][drow][k0]);
-    u32x4 dah, dal;
-    if (TAN) {
-      dah = *reinterpret_cast<const u32x4*>(&dphiT[0][drow][k0]);
-      dal = *reinterpret_cast<const u32x4*>(&dphiT[1][drow][k0]);
-    }
 #pragma unroll
     for (int vt_ = 0; vt_ < 4; ++vt_) {
       const u32x4 bv = *reinterpret_cast<const u32x4*>(&vT[16 * vt_ + lr][k0]);
@@ -215,10 +208,30 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
       if (!ROUND) acc[vt_] = mfma_16x16x32<T16>(al, bv, acc[vt_]);
       if (TAN) {
         const u32x4 bdv = *reinterpret_cast<const u32x4*>(&dvT[16 * vt_ + lr][k0]);
-        dacc[vt_] = mfma_16x16x32<T16>(dah, bv, dacc[vt_]);
-        dacc[vt_] = mfma_16x16x32<T16>(dal, bv, dacc[vt_]);
         dacc[vt_] = mfma_16x16x32<T16>(ah, bdv, dacc[vt_]);
         dacc[vt_] = mfma_16x16x32<T16>(al, bdv, dacc[vt_]);
+      }
+    }
+  }
+  if (TAN) {  // phase 2: dphi^T replaces phi^T; dH += dphi^T V
+    __syncthreads();
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      const uint16_t dhi = T16::from_f32(dphi[i]);
+      phiT[0][c0 + i][r] = dhi;
+      phiT[1][c0 + i][r] = T16::from_f32(dphi[i] - T16::to_f32(dhi));
+    }
+    __syncthreads();
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int k0 = 32 * ks + 8 * g;
+      const u32x4 dah = *reinterpret_cast<const u32x4*>(&phiT[0][drow][k0]);
+      const u32x4 dal = *reinterpret_cast<const u32x4*>(&phiT[1][drow][k0]);
+#pragma unroll
+      for (int vt_ = 0; vt_ < 4; ++vt_) {
+        const u32x4 bv = *reinterpret_cast<const u32x4*>(&vT[16 * vt_ + lr][k0]);
+        dacc[vt_] = mfma_16x16x32<T16>(dah, bv, dacc[vt_]);
+        dacc[vt_] = mfma_16x16x32<T16>(dal, bv, dacc[vt_]);
       }
     }
   }
