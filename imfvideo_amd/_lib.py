@@ -59,6 +59,14 @@ SIGNATURES = {
                                      _c_int, _c_int, _c_int, _c_f, _p, _p, _p, _p]),
     "sla2h_linear_mix_qat": (_c_int, [_p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int,
                                       _c_i64, _c_int, _c_int, _c_f, _p, _p, _p, _p]),
+    "sla2h_quantize_v8f": (_c_int, [_p, _c_int, _c_i64, _c_i64, _c_int, _c_int, _p, _p, _p]),
+    "sla2h_sparse_fwd_int8": (_c_int, [_p, _p, _p, _c_int, _p, _p, _p, _p, _p, _c_int, _c_int,
+                                       _c_int, _c_i64, _c_int, _c_int, _c_int, _c_f, _p, _p, _p,
+                                       _p]),
+    "sla2h_hblocks_states": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _c_i64, _c_int, _c_int,
+                                      _p, _p, _p, _p, _p, _p]),
+    "sla2h_lin_fwd3": (_c_int, [_p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int,
+                                _c_int, _c_f, _p, _p]),
     "sla2h_bwd_prep": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int,
                                 _c_i64, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
                                 _p]),

@@ -40,7 +40,9 @@ struct TrainArgs {
   uint16_t* qphi;
   int64_t L;
   int Nb, Np, Mb, T, n_tail, nwork, per_xcd;
-  float c2;  // fl32(scale * log2(e))
+  int Mq, qshift;  // LUT rows: query blocks of 64 << qshift rows
+  int Mqs, qsb;    // Q scales: blocks of 1 << qsb rows (per lane)
+  float c2;        // fl32(scale * log2(e))
 };
 
 template <typename T16>
@@ -61,7 +63,7 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
   const bool qok = qrow < L;
 
   const int J = a.T + a.n_tail;
-  const int32_t* lrow = a.lut + ((int64_t)bh * a.Mb + m) * a.T;
+  const int32_t* lrow = a.lut + ((int64_t)bh * a.Mq + (m >> a.qshift)) * a.T;
   for (int j = tid; j < J; j += 256) {
     int n = j < a.T ? lrow[j] : a.Np + (j - a.T);
     n = n < 0 ? 0 : (n >= a.Nb ? a.Nb - 1 : n);
@@ -100,7 +102,7 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
     uint32_t o[8];
 #pragma unroll
     for (int i = 0; i < 8; ++i) o[i] = pack_pair<T16>(x[2 * i] * rd, x[2 * i + 1] * rd);
-    if (qok) {
+    if (qok && a.qphi != nullptr) {
       uint4* dst = reinterpret_cast<uint4*>(a.qphi + (qkbase + qrow) * kT + 16 * g);
       dst[0] = make_uint4(o[0], o[1], o[2], o[3]);
       dst[1] = make_uint4(o[4], o[5], o[6], o[7]);
@@ -111,7 +113,8 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
   // INT8 Q B operand: this lane's query, channels 16g..16g+15
   const i32x4 q8f = qok ? *reinterpret_cast<const i32x4*>(a.q8 + (qkbase + qrow) * kT + 16 * g)
                         : i32x4{0, 0, 0, 0};
-  const float sq = a.qs[(int64_t)bh * a.Nb + m];
+  const int qsi = (int)(qrow >> a.qsb);  // this lane's Q scale block
+  const float sq = a.qs[(int64_t)bh * a.Mqs + (qsi < a.Mqs ? qsi : a.Mqs - 1)];
   const auto rk8 = make_rsrc(a.k8 + qkbase * kT, L * kT);  // key rows past L read as 0
   const auto rv8 = make_rsrc(a.v8f + (int64_t)bh * a.Nb * 4096, (int64_t)a.Nb * 4096);
   const int k8off = r * kT + 16 * g;  // + 16 kb rows + tile base
@@ -400,7 +403,12 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd16_kernel(Fwd16Args a) {
 // lane (g, r) holds query r, output channels 16 ct + 4g + i.
 constexpr int kRecH = 0, kRecZ = 32768, kRecBytes = 33280;
 
-template <typename T16>
+// INFER: the inference law of _lin_fwd3 (models/sla2_vendor/kernel_linear.py:
+// 446-493): H_i = the complement record itself (a sum of 16-bit block
+// states), rounded to the 16-bit type for the product; o_l and the mix stay
+// fp32 (o = a o_s + (1 - a) o_l, one rounding at the store); Hall, o_l and
+// den_out may be null.
+template <typename T16, bool INFER = false>
 __global__ __launch_bounds__(256) void linear_mix_qat_kernel(
     const uint16_t* __restrict__ qphi, const unsigned char* __restrict__ comp,
     const float* __restrict__ Hall, const uint16_t* __restrict__ o_s,
@@ -416,14 +424,19 @@ __global__ __launch_bounds__(256) void linear_mix_qat_kernel(
   {
     const int d = tid >> 2, v0 = (tid & 3) * 16;
     const f32x4* hr = reinterpret_cast<const f32x4*>(rec + kRecH) + (d * kT + v0) / 4;
-    const f32x4* ha = reinterpret_cast<const f32x4*>(Hall + (int64_t)bh * kT * kT + d * kT + v0);
 #pragma unroll
     for (int c = 0; c < 4; ++c) {
-      const f32x4 x = hr[c], t = ha[c];
+      const f32x4 x = hr[c];
+      if (INFER) {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float t16 = T16::to_f32(T16::from_f32(t[i]));
-        hT[v0 + 4 * c + i][d] = T16::from_f32(x[i] + (t16 - t[i]));
+        for (int i = 0; i < 4; ++i) hT[v0 + 4 * c + i][d] = T16::from_f32(x[i]);
+      } else {
+        const f32x4 t = reinterpret_cast<const f32x4*>(Hall + (int64_t)bh * kT * kT + d * kT + v0)[c];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float t16 = T16::to_f32(T16::from_f32(t[i]));
+          hT[v0 + 4 * c + i][d] = T16::from_f32(x[i] + (t16 - t[i]));
+        }
       }
     }
     if (tid < kT) zs[tid] = reinterpret_cast<const float*>(rec + kRecZ)[tid];
@@ -449,8 +462,9 @@ __global__ __launch_bounds__(256) void linear_mix_qat_kernel(
   dn = sum_over_groups(dn);
   dn = dn >= 0.f ? dn + eps_l : dn - eps_l;
   const float rdn = 1.f / dn;
-  const float a16 = T16::to_f32(T16::from_f32(alpha[(int64_t)h * alpha_stride + mq]));
-  const float b16 = T16::to_f32(T16::from_f32(1.f - a16));
+  const float af = alpha[(int64_t)h * alpha_stride + mq];
+  const float a16 = INFER ? af : T16::to_f32(T16::from_f32(af));
+  const float b16 = INFER ? 1.f - af : T16::to_f32(T16::from_f32(1.f - a16));
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) {
     f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -466,19 +480,25 @@ __global__ __launch_bounds__(256) void linear_mix_qat_kernel(
       float ol[4], ov[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        ol[i] = T16::to_f32(T16::from_f32(num[i] * rdn));
         const float os16 = T16::to_f32((uint16_t)(sw[i >> 1] >> (16 * (i & 1))));
-        const float x = T16::to_f32(T16::from_f32(a16 * os16));
-        const float y = T16::to_f32(T16::from_f32(b16 * ol[i]));
-        ov[i] = x + y;
+        if (INFER) {
+          ol[i] = num[i] * rdn;
+          ov[i] = a16 * os16 + b16 * ol[i];
+        } else {
+          ol[i] = T16::to_f32(T16::from_f32(num[i] * rdn));
+          const float x = T16::to_f32(T16::from_f32(a16 * os16));
+          const float y = T16::to_f32(T16::from_f32(b16 * ol[i]));
+          ov[i] = x + y;
+        }
       }
       *reinterpret_cast<uint2*>(o + oo) =
           make_uint2(pack_pair<T16>(ov[0], ov[1]), pack_pair<T16>(ov[2], ov[3]));
-      *reinterpret_cast<uint2*>(o_l + oo) =
-          make_uint2(pack_pair<T16>(ol[0], ol[1]), pack_pair<T16>(ol[2], ol[3]));
+      if (o_l != nullptr)
+        *reinterpret_cast<uint2*>(o_l + oo) =
+            make_uint2(pack_pair<T16>(ol[0], ol[1]), pack_pair<T16>(ol[2], ol[3]));
     }
   }
-  if (qok && g == 0) den_out[(int64_t)bh * L + qrow] = dn;
+  if (qok && g == 0 && den_out != nullptr) den_out[(int64_t)bh * L + qrow] = dn;
 }
 
 }  // namespace
@@ -520,6 +540,71 @@ extern "C" int sla2h_sparse_fwd_qat(const void* q, const int8_t* q8, const float
   a.Mb = Nb;
   a.T = T;
   a.n_tail = Nb - Np;
+  a.Mq = Nb;
+  a.qshift = 0;
+  a.Mqs = Nb;
+  a.qsb = 6;
+  a.nwork = (int)nwork;
+  a.per_xcd = (int)per_xcd;
+  a.c2 = scale * 1.4426950408889634f;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nblocks = (int)(8 * per_xcd);
+  if (dtype == SLA2H_DTYPE_BF16)
+    sparse_fwd_qat_kernel<BF16><<<nblocks, 256, 0, st>>>(a);
+  else
+    sparse_fwd_qat_kernel<F16><<<nblocks, 256, 0, st>>>(a);
+  return (int)hipGetLastError();
+}
+
+static int log2_exact(int x) {
+  int k = 0;
+  while ((1 << k) < x) ++k;
+  return (1 << k) == x ? k : -1;
+}
+
+// Inference INT8 sparse branch of the 1-D SLA2 (_attn_fwd_int8 through
+// sparse_attention_int8, models/sla2_vendor/kernel_sparse_qat.py:154-247; the
+// INT8 branch of _sla2_fwd_fused, kernel_fused.py:81-106): the same
+// recurrence as above over every routable key block (the last one possibly
+// partial), LUT rows per query block of bq rows, Q scales per block of
+// qblock rows (bq for the unfused path, block_m for the fused one).
+extern "C" int sla2h_sparse_fwd_int8(const void* q, const int8_t* q8, const float* qs, int qblock,
+                                     const int8_t* k8, const float* ks, const int8_t* v8f,
+                                     const float* vs, const int32_t* lut, int dtype, int B, int H,
+                                     int64_t L, int D, int bq, int T, float scale, void* o_s,
+                                     float* lse, void* qphi, void* stream) {
+  SLA2H_CHECK_ARG(q && q8 && qs && k8 && ks && v8f && vs && lut && o_s && lse);
+  SLA2H_CHECK_ARG(D == kT && (bq == 64 || bq == 128 || bq == 256));
+  SLA2H_CHECK_ARG(qblock == 32 || qblock == 64 || qblock == 128 || qblock == 256);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && L > 0);
+  const int Nb = (int)((L + kT - 1) / kT);
+  SLA2H_CHECK_ARG(T >= 1 && T <= Nb && T <= kMaxJ);
+  const int64_t nwork = (int64_t)Nb * B * H;
+  const int64_t per_xcd = (nwork + 7) / 8;
+  SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31));
+  TrainArgs a;
+  a.q = static_cast<const uint16_t*>(q);
+  a.q8 = q8;
+  a.k8 = k8;
+  a.v8f = v8f;
+  a.qs = qs;
+  a.ks = ks;
+  a.vs = vs;
+  a.lut = lut;
+  a.os = static_cast<uint16_t*>(o_s);
+  a.lse = lse;
+  a.qphi = static_cast<uint16_t*>(qphi);
+  a.L = L;
+  a.Nb = Nb;
+  a.Np = Nb;
+  a.Mb = Nb;
+  a.T = T;
+  a.n_tail = 0;
+  a.Mq = (int)((L + bq - 1) / bq);
+  a.qshift = log2_exact(bq / kT);
+  a.Mqs = (int)((L + qblock - 1) / qblock);
+  a.qsb = log2_exact(qblock);
   a.nwork = (int)nwork;
   a.per_xcd = (int)per_xcd;
   a.c2 = scale * 1.4426950408889634f;
@@ -554,6 +639,34 @@ extern "C" int sla2h_linear_mix_qat(const void* qphi, const void* comp, const fl
     linear_mix_qat_kernel<BF16><<<grid, 256, 0, st>>>(QP, C, Hall, OS, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, OL, den);
   else
     linear_mix_qat_kernel<F16><<<grid, 256, 0, st>>>(QP, C, Hall, OS, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, OL, den);
+  return (int)hipGetLastError();
+}
+
+// Linear branch and mix of the 1-D SLA2 inference path (_lin_fwd3 through
+// complement_linear_states, models/sla2_vendor/kernel_linear.py:446-513):
+// comp holds the complement records of 16-bit block states
+// (sla2h_hblocks_states + sla2h_complement over the plain LUT), qphi =
+// softmax_D(Q) in the 16-bit type; o = alpha o_s + (1 - alpha) o_l.
+extern "C" int sla2h_lin_fwd3(const void* qphi, const void* comp, const void* o_s,
+                              const float* alpha, int alpha_stride, int dtype, int B, int H,
+                              int64_t L, int D, int bq, float eps_l, void* o, void* stream) {
+  SLA2H_CHECK_ARG(qphi && comp && o_s && alpha && o);
+  SLA2H_CHECK_ARG(D == kT && (bq == 64 || bq == 128 || bq == 256) && alpha_stride >= 0);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && L > 0);
+  const int Mb = (int)((L + kT - 1) / kT);
+  const int Mq = (int)((L + bq - 1) / bq);
+  const int qshift = log2_exact(bq / kT);
+  dim3 grid(Mb, B * H);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto QP = static_cast<const uint16_t*>(qphi);
+  auto C = static_cast<const unsigned char*>(comp);
+  auto OS = static_cast<const uint16_t*>(o_s);
+  auto O = static_cast<uint16_t*>(o);
+  if (dtype == SLA2H_DTYPE_BF16)
+    linear_mix_qat_kernel<BF16, true><<<grid, 256, 0, st>>>(QP, C, nullptr, OS, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, nullptr, nullptr);
+  else
+    linear_mix_qat_kernel<F16, true><<<grid, 256, 0, st>>>(QP, C, nullptr, OS, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, nullptr, nullptr);
   return (int)hipGetLastError();
 }
 

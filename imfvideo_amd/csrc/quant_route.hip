@@ -133,16 +133,19 @@ struct QuantTrainArgs {
   int BH;
   int64_t L;
   int Nb;
+  int t0;                // first tensor of the grid (blockIdx.y / BH counts from it)
 };
 
-template <typename T16>
+// RND: the round-half-away law of quantize_qkv instead (the inference INT8
+// path, sla2h_quantize_v8f).
+template <typename T16, bool RND = false>
 __global__ __launch_bounds__(256) void quant_train_kernel(QuantTrainArgs a) {
   __shared__ float red[4];
   __shared__ __align__(16) int8_t q8t[kTile][kTile + 16];
 
   const int tid = threadIdx.x;
   const int blk = blockIdx.x;
-  const int t = blockIdx.y / a.BH;
+  const int t = a.t0 + blockIdx.y / a.BH;
   const int bh = blockIdx.y % a.BH;
   const int r = tid >> 2;
   const int c0 = (tid & 3) * 16;
@@ -181,8 +184,14 @@ __global__ __launch_bounds__(256) void quant_train_kernel(QuantTrainArgs a) {
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
       const float x = xv[4 * i + b];
-      const float y = x / s + (x >= 0.f ? 0.5f : -0.5f);  // two roundings (no contraction)
-      acc |= ((uint32_t)((int)y & 0xff)) << (8 * b);
+      int qv;
+      if (RND) {
+        qv = (int)roundf(x / s);  // round half away from zero
+      } else {
+        const float y = x / s + (x >= 0.f ? 0.5f : -0.5f);  // two roundings (no contraction)
+        qv = (int)y;
+      }
+      acc |= ((uint32_t)(qv & 0xff)) << (8 * b);
     }
     w[i] = acc;
   }
@@ -206,6 +215,66 @@ __global__ __launch_bounds__(256) void quant_train_kernel(QuantTrainArgs a) {
   }
   *reinterpret_cast<uint4*>(a.xq[2] + ((int64_t)bh * a.Nb + blk) * 4096 + tid * 16) =
       make_uint4(f[0], f[1], f[2], f[3]);
+}
+
+// quantize_qkv / _quant_blocks (models/sla2_vendor/kernel_sparse_qat.py:
+// 120-151) for blocks of E = 32, 128 or 256 rows: one block per workgroup,
+// thread t holds E/4 consecutive elements (a segment of one row), s =
+// max|x| / 127 + 1e-12, q = round half away from zero of x / s.
+template <typename T16, int E>
+__global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restrict__ x, int64_t L,
+                                                         int Nb, int8_t* __restrict__ xq,
+                                                         float* __restrict__ xs) {
+  constexpr int PER = E / 4;
+  __shared__ float red[4];
+  const int tid = threadIdx.x;
+  const int blk = blockIdx.x;
+  const int bh = blockIdx.y;
+  const int e0 = tid * PER;
+  const bool valid = (int64_t)blk * E + e0 / kTile < L;
+  const int64_t off = ((int64_t)bh * L + (int64_t)blk * E) * kTile + e0;
+  float xv[PER];
+#pragma unroll
+  for (int c = 0; c < PER / 8; ++c) {
+    const uint4 u = valid ? reinterpret_cast<const uint4*>(x + off)[c] : make_uint4(0, 0, 0, 0);
+    const uint32_t wd[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      xv[8 * c + 2 * i] = T16::to_f32((uint16_t)(wd[i] & 0xffff));
+      xv[8 * c + 2 * i + 1] = T16::to_f32((uint16_t)(wd[i] >> 16));
+    }
+  }
+  float am = 0.f;
+#pragma unroll
+  for (int i = 0; i < PER; ++i) am = fmaxf(am, fabsf(xv[i]));
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) am = fmaxf(am, __shfl_xor(am, m, 64));
+  if ((tid & 63) == 0) red[tid >> 6] = am;
+  __syncthreads();
+  am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
+  const float s = am / 127.0f + 1e-12f;  // IEEE division, then add
+  uint32_t w[PER / 4];
+#pragma unroll
+  for (int i = 0; i < PER / 4; ++i) {
+    uint32_t acc = 0;
+#pragma unroll
+    for (int b = 0; b < 4; ++b) {
+      const int qv = (int)roundf(xv[4 * i + b] / s);
+      acc |= ((uint32_t)(qv & 0xff)) << (8 * b);
+    }
+    w[i] = acc;
+  }
+  if (valid) {
+    if (PER == 8) {
+      *reinterpret_cast<uint2*>(xq + off) = make_uint2(w[0], w[1]);
+    } else {
+#pragma unroll
+      for (int c = 0; c < PER / 16; ++c)
+        reinterpret_cast<uint4*>(xq + off)[c] =
+            make_uint4(w[4 * c], w[4 * c + 1], w[4 * c + 2], w[4 * c + 3]);
+    }
+  }
+  if (tid == 0) xs[(int64_t)bh * Nb + blk] = s;
 }
 
 // Orderable 64-bit key: high word = monotone map of the fp32 score
@@ -541,6 +610,7 @@ extern "C" int sla2h_quant_train(const void* q, const void* k, const void* v, in
   a.BH = B * H;
   a.L = L;
   a.Nb = (int)((L + E - 1) / E);
+  a.t0 = 0;
   dim3 grid(a.Nb, 3 * a.BH);
   hipStream_t st = static_cast<hipStream_t>(stream);
   if (dtype == SLA2H_DTYPE_BF16)
@@ -550,13 +620,59 @@ extern "C" int sla2h_quant_train(const void* q, const void* k, const void* v, in
   return (int)hipGetLastError();
 }
 
-extern "C" int sla2h_quantize(const void* x, int dtype, int64_t BH, int64_t L, int D, int E,
-                              int8_t* xq, float* xs, void* stream) {
-  SLA2H_CHECK_ARG(x && xq && xs);
+// V of the inference INT8 path: quantize_qkv's law (round half away, one
+// scale per 64-row block) written in the INT8 MFMA fragment order of the
+// sparse kernels (the layout of sla2h_quant_train's v8f).
+extern "C" int sla2h_quantize_v8f(const void* v, int dtype, int64_t BH, int64_t L, int D, int E,
+                                  int8_t* v8f, float* vs, void* stream) {
+  SLA2H_CHECK_ARG(v && v8f && vs);
   SLA2H_CHECK_ARG(D == kTile && E == kTile);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   SLA2H_CHECK_ARG(BH > 0 && BH <= 65535 && L > 0);
+  QuantTrainArgs a = {};
+  a.x[2] = static_cast<const uint16_t*>(v);
+  a.xq[2] = v8f;
+  a.xs[2] = vs;
+  a.BH = (int)BH;
+  a.L = L;
+  a.Nb = (int)((L + E - 1) / E);
+  a.t0 = 2;
+  dim3 grid(a.Nb, (int)BH);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SLA2H_DTYPE_BF16)
+    quant_train_kernel<BF16, true><<<grid, 256, 0, st>>>(a);
+  else
+    quant_train_kernel<F16, true><<<grid, 256, 0, st>>>(a);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_quantize(const void* x, int dtype, int64_t BH, int64_t L, int D, int E,
+                              int8_t* xq, float* xs, void* stream) {
+  SLA2H_CHECK_ARG(x && xq && xs);
+  SLA2H_CHECK_ARG(D == kTile && (E == 32 || E == 64 || E == 128 || E == 256));
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(BH > 0 && BH <= 65535 && L > 0);
   if (BH * L * D == 0) return 0;
+  if (E != kTile) {
+    const int Nb = (int)((L + E - 1) / E);
+    dim3 grid(Nb, (int)BH);
+    hipStream_t st = static_cast<hipStream_t>(stream);
+    auto X = static_cast<const uint16_t*>(x);
+    auto go = [&](auto tag) {
+      using T16 = decltype(tag);
+      if (E == 32)
+        quant_rows_kernel<T16, 32><<<grid, 256, 0, st>>>(X, L, Nb, xq, xs);
+      else if (E == 128)
+        quant_rows_kernel<T16, 128><<<grid, 256, 0, st>>>(X, L, Nb, xq, xs);
+      else
+        quant_rows_kernel<T16, 256><<<grid, 256, 0, st>>>(X, L, Nb, xq, xs);
+    };
+    if (dtype == SLA2H_DTYPE_BF16)
+      go(BF16{});
+    else
+      go(F16{});
+    return (int)hipGetLastError();
+  }
   QuantPoolArgs a = {};
   a.x[0] = static_cast<const uint16_t*>(x);
   a.xq[0] = xq;

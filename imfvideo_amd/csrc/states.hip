@@ -27,8 +27,10 @@ constexpr size_t kRecBytes = 2 * 16384 + 2 * 256;
 // the input's 16-bit type (about 16 significant bits), fp32 accumulate.
 // ROUND (training forward): phi is rounded to the 16-bit type first, as the
 // reference's softmax(K).to(dtype) (models/sla2_cube_qat.py:728), and the lo
-// half vanishes.  The value operand tiles are written when vt is not NULL.
-template <typename T16, bool TAN, bool ROUND = false>
+// half vanishes.  RH (the inference states of _hblocks): H is stored
+// rounded to the 16-bit type, as the reference keeps HALL in V's dtype.  The
+// value operand tiles are written when vt is not NULL.
+template <typename T16, bool TAN, bool ROUND = false, bool RH = false>
 __global__ __launch_bounds__(256) void linear_states_kernel(
     const uint16_t* __restrict__ K, const uint16_t* __restrict__ dK,
     const uint16_t* __restrict__ V, const uint16_t* __restrict__ dV, int64_t L, int Np, int Nb,
@@ -241,7 +243,7 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int64_t o = hbase + (int64_t)(16 * w + 4 * g + i) * kT + 16 * vt_ + lr;
-      Hb[o] = acc[vt_][i];
+      Hb[o] = RH ? T16::to_f32(T16::from_f32(acc[vt_][i])) : acc[vt_][i];
       if (TAN) dHb[o] = dacc[vt_][i];
     }
   }
@@ -604,6 +606,36 @@ extern "C" int sla2h_linear_states_qat(const void* k, const void* v, int dtype, 
     linear_states_kernel<F16, false, true><<<grid, 256, 0, st>>>(K, nullptr, V, nullptr, L, Nb, Nb, Hb, nullptr, zb, nullptr, static_cast<uint16_t*>(vt), nullptr);
   int err = (int)hipGetLastError();
   if (err) return err;
+  dim3 g2((8320 + 255) / 256, B * H);
+  states_sum_kernel<<<g2, 256, 0, st>>>(Hb, nullptr, zb, nullptr, Nb, Hall, nullptr, zall, nullptr);
+  return (int)hipGetLastError();
+}
+
+// Inference states of the 1-D SLA2 (_hblocks through complement_linear_states,
+// models/sla2_vendor/kernel_linear.py:396-427, 496-504): phi(K) rounded to the
+// 16-bit type, HALL_j = phi(K_j)^T V_j rounded to the 16-bit type (held as
+// fp32 values), ZALL_j = colsum phi(K_j) in fp32, for every key block; the
+// sums over the blocks when Hall / zall are given; the primal value operand
+// tiles of the 16-bit sparse kernel when vt is given.
+extern "C" int sla2h_hblocks_states(const void* k, const void* v, int dtype, int B, int H,
+                                    int64_t L, int D, int E, float* Hb, float* zb, float* Hall,
+                                    float* zall, void* vt, void* stream) {
+  SLA2H_CHECK_ARG(k && v && Hb && zb);
+  SLA2H_CHECK_ARG((Hall == nullptr) == (zall == nullptr));
+  SLA2H_CHECK_ARG(D == kT && E == kT);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && L > 0);
+  const int Nb = (int)((L + E - 1) / E);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  dim3 grid(Nb, B * H);
+  auto K = static_cast<const uint16_t*>(k);
+  auto V = static_cast<const uint16_t*>(v);
+  if (dtype == SLA2H_DTYPE_BF16)
+    linear_states_kernel<BF16, false, true, true><<<grid, 256, 0, st>>>(K, nullptr, V, nullptr, L, Nb, Nb, Hb, nullptr, zb, nullptr, static_cast<uint16_t*>(vt), nullptr);
+  else
+    linear_states_kernel<F16, false, true, true><<<grid, 256, 0, st>>>(K, nullptr, V, nullptr, L, Nb, Nb, Hb, nullptr, zb, nullptr, static_cast<uint16_t*>(vt), nullptr);
+  int err = (int)hipGetLastError();
+  if (err || Hall == nullptr) return err;
   dim3 g2((8320 + 255) / 256, B * H);
   states_sum_kernel<<<g2, 256, 0, st>>>(Hb, nullptr, zb, nullptr, Nb, Hall, nullptr, zall, nullptr);
   return (int)hipGetLastError();

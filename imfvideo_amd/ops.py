@@ -504,3 +504,116 @@ def train_fwd_1d(q, k, v, alpha, lut, bq, eps_l=1e-5):
     return dict(o=o, o_s=o_s, o_l=o_l, lse=lse, den=den, qphi=qphi,
                 htot=st["Hall"].to(q.dtype).float(), ztot=st["zall"], Hall=st["Hall"], comp=comp,
                 lut_aug=lut)
+
+
+# ---------------------------------------------------------------------------
+# Inference forward of the 1-D SLA2 module (SLA2.forward without gradients,
+# models/sla2_vendor/core.py:93-128): the INT8 sparse branch of
+# sparse_attention_int8 (or the 16-bit one), the state-subtraction linear
+# branch of complement_linear_states and the alpha mix.
+# ---------------------------------------------------------------------------
+
+def quantize_v8f(v, E=E_TILE):
+    """V (B,H,L,64) 16-bit -> (v8f int8 (B,H,Nb,4096) fragment order, vs fp32 (B,H,Nb))."""
+    _need_gpu(v)
+    v = _bhld(v, "v")
+    B, H, L, D = v.shape
+    nb = -(-L // E)
+    v8f = torch.empty(B, H, nb, 4096, device=v.device, dtype=torch.int8)
+    vs = torch.empty(B, H, nb, device=v.device, dtype=torch.float32)
+    _lib.check(_lib.load().sla2h_quantize_v8f(v.data_ptr(), _dtype_code(v), B * H, L, D, E,
+                                              v8f.data_ptr(), vs.data_ptr(), _stream(v.device)),
+               "sla2h_quantize_v8f")
+    return v8f, vs
+
+
+def sparse_fwd_int8(q, q8, qs, qblock, k8, ks, v8f, vs, lut, bq, scale=None, phi_out=True):
+    """Inference INT8 sparse branch -> (o_s 16-bit, lse fp32, qphi 16-bit | None)."""
+    _need_gpu(q, q8, k8, v8f, lut)
+    B, H, L, D = q.shape
+    lut = lut.to(torch.int32).contiguous()
+    mq = -(-L // bq)
+    if lut.dim() != 4 or tuple(lut.shape[:3]) != (B, H, mq):
+        raise ValueError(f"lut: expected (B, H, {mq}, T), got {tuple(lut.shape)}")
+    scale = D ** -0.5 if scale is None else scale
+    o_s = torch.empty_like(q)
+    lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
+    qphi = torch.empty_like(q) if phi_out else None
+    _lib.check(_lib.load().sla2h_sparse_fwd_int8(
+        q.data_ptr(), q8.data_ptr(), qs.data_ptr(), qblock, k8.data_ptr(), ks.data_ptr(),
+        v8f.data_ptr(), vs.data_ptr(), lut.data_ptr(), _dtype_code(q), B, H, L, D, bq,
+        lut.shape[-1], float(scale), o_s.data_ptr(), lse.data_ptr(), _ptr(qphi),
+        _stream(q.device)), "sla2h_sparse_fwd_int8")
+    return o_s, lse, qphi
+
+
+def hblocks_states(k, v, with_sums=False, with_vt=False):
+    """Inference states of every key block -> dict(Hb, zb [, Hall, zall] [, vt])."""
+    _need_gpu(k, v)
+    k, v = _bhld(k, "k"), _bhld(v, "v")
+    B, H, L, D = k.shape
+    nb = -(-L // E_TILE)
+    f32, dev = torch.float32, k.device
+    st = {"Hb": torch.empty(B, H, nb, D, D, device=dev, dtype=f32),
+          "zb": torch.empty(B, H, nb, D, device=dev, dtype=f32)}
+    if with_sums:
+        st["Hall"] = torch.empty(B, H, D, D, device=dev, dtype=f32)
+        st["zall"] = torch.empty(B, H, D, device=dev, dtype=f32)
+    if with_vt:
+        st["vt"] = torch.empty(B, H, nb, D, E_TILE, device=dev, dtype=v.dtype)
+    _lib.check(_lib.load().sla2h_hblocks_states(
+        k.data_ptr(), v.data_ptr(), _dtype_code(k), B, H, L, D, E_TILE, st["Hb"].data_ptr(),
+        st["zb"].data_ptr(), _ptr(st.get("Hall")), _ptr(st.get("zall")), _ptr(st.get("vt")),
+        _stream(dev)), "sla2h_hblocks_states")
+    return st
+
+
+def lin_fwd3(qphi, comp, o_s, alpha, bq, eps_l=1e-5):
+    """Linear branch + mix of the inference path -> o (16-bit)."""
+    _need_gpu(qphi, comp, o_s)
+    B, H, L, D = qphi.shape
+    a = _alpha_rows(alpha, H, -(-L // bq), qphi.device)
+    o = torch.empty_like(o_s)
+    _lib.check(_lib.load().sla2h_lin_fwd3(
+        qphi.data_ptr(), comp.data_ptr(), o_s.data_ptr(), a.data_ptr(), a.stride(0),
+        _dtype_code(qphi), B, H, L, D, bq, float(eps_l), o.data_ptr(), _stream(qphi.device)),
+        "sla2h_lin_fwd3")
+    return o
+
+
+def sla2_infer(q, k, v, alpha, lut, bq, use_int8=True, qblock=None, eps_l=1e-5,
+               return_parts=False):
+    """SLA2 inference forward on given routing.
+
+    q, k, v: (B,H,L,64) 16-bit, natural order; alpha (H, ceil(L/bq)) after the
+    sigmoid; lut (B,H,ceil(L/bq),T) routed 64-row key blocks.  use_int8: the
+    INT8 sparse branch with Q scales per qblock rows (default bq), else the
+    16-bit one.  Returns o (16-bit) [, dict of the intermediates].
+    """
+    _need_gpu(q, k, v, lut)
+    q, k, v = (_bhld(t, "qkv") for t in (q, k, v))
+    B, H, L, D = q.shape
+    nb = -(-L // E_TILE)
+    lut = lut.to(torch.int32).contiguous()
+    st = hblocks_states(k, v, with_vt=not use_int8)
+    if use_int8:
+        qb = bq if qblock is None else qblock
+        q8, qs = quantize(q, qb)
+        k8, ks = quantize(k)
+        v8f, vs = quantize_v8f(v)
+        o_s, lse, qphi = sparse_fwd_int8(q, q8, qs, qb, k8, ks, v8f, vs, lut, bq)
+    else:
+        mq = -(-L // bq)
+        if lut.dim() != 4 or tuple(lut.shape[:3]) != (B, H, mq):
+            raise ValueError(f"lut: expected (B, H, {mq}, T), got {tuple(lut.shape)}")
+        o_s, qphi = torch.empty_like(q), torch.empty_like(q)
+        lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
+        _lib.check(_lib.load().sla2h_sparse_fwd_1d(
+            q.data_ptr(), k.data_ptr(), st["vt"].data_ptr(), lut.data_ptr(), _dtype_code(q), B,
+            H, L, D, bq, E_TILE, lut.shape[-1], float(D ** -0.5), o_s.data_ptr(),
+            lse.data_ptr(), qphi.data_ptr(), _stream(q.device)), "sla2h_sparse_fwd_1d")
+    comp = complement(st, lut, nb)
+    o = lin_fwd3(qphi, comp, o_s, alpha, bq, eps_l)
+    if return_parts:
+        return o, dict(o_s=o_s, lse=lse, qphi=qphi, comp=comp, **st)
+    return o

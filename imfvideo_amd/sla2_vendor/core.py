@@ -5,11 +5,14 @@
     O_s = softmax(Q K^T / sqrt(d) over the routed key blocks) V
     O_l = phi(Q) [phi(K)^T V over the other key blocks] / (phi(Q) . z + eps)
 
-Query blocks of bq rows (64, 128 or 256), key blocks of bk = 64 rows.  The
-forward runs the training-forward kernels (16-bit sparse branch, 16-bit
-state-form linear branch and mix; with use_int8 and bq = 64, the INT8
-training forward of the cube op); with gradients enabled it goes through an
-autograd Function whose backward is the straight-through HIP backward.
+Query blocks of bq rows (64, 128 or 256), key blocks of bk = 64 rows.  With
+gradients enabled the forward runs the training-forward kernels (16-bit
+sparse branch, 16-bit state-form linear branch and mix; with use_int8 and
+bq = 64, the INT8 training forward of the cube op) inside an autograd
+Function whose backward is the straight-through HIP backward.  Without
+gradients it runs the inference path (ops.sla2_infer): the INT8 sparse
+branch of sparse_attention_int8 (or the 16-bit one), the state-subtraction
+linear branch of complement_linear_states and the alpha mix.
 """
 
 import math
@@ -63,18 +66,21 @@ class SLA2(nn.Module):
         topk            : k%, fraction of key blocks routed to the sparse branch
         bq, bk          : query / key block sizes (bq in {64, 128, 256}, bk = 64)
         use_bf16        : 16-bit compute type bf16 (else fp16)
-        use_int8        : INT8 sparse forward (QAT); built for bq = bk = 64
+        use_int8        : INT8 sparse branch (inference: every bq; training: bq = 64)
         alpha_init      : initial value of alpha (before the logit)
-        block_m, fused, backend : accepted for the reference's signature; the HIP
-                          kernels serve every backend / fused setting
+        block_m, fused  : the fused inference path's query tile (its Q scales run
+                          per block_m rows, default max(32, bq // 2)) and switch
+                          (head-averaged alpha, as kernel_fused takes)
+        backend         : accepted for the reference's signature; the HIP kernels
+                          serve every backend
         """
         super().__init__()
         if bk != ops.E_TILE:
             raise ValueError(f"bk must be {ops.E_TILE}, got {bk}")
         if bq not in (64, 128, 256):
             raise ValueError(f"bq must be 64, 128 or 256, got {bq}")
-        if use_int8 and bq != ops.E_TILE:
-            raise NotImplementedError("the INT8 training forward is built for bq = bk = 64")
+        if block_m is not None and (block_m not in (32, 64, 128, 256) or bq % block_m):
+            raise ValueError(f"block_m must divide bq and be 32..256, got {block_m}")
         self.dtype = torch.bfloat16 if use_bf16 else torch.float16
         self.topk, self.bq, self.bk = topk, bq, bk
         self.use_int8 = use_int8
@@ -100,13 +106,19 @@ class SLA2(nn.Module):
         lut, topk = self.router.route(qh, kh, self.topk)
         alpha_logit = self._get_alpha(H, -(-L // self.bq), q.device)
         if training:
+            if self.use_int8 and self.bq != ops.E_TILE:
+                raise NotImplementedError("the INT8 training forward is built for bq = bk = 64")
             o = _SLA2Function.apply(qh, kh, vh, alpha_logit, lut, self.bq, self.use_int8)
         else:
+            # inference (core.py:98-128): INT8 or 16-bit sparse branch, the
+            # state-subtraction linear branch and the mix
             a = torch.sigmoid(alpha_logit.detach().float())
-            if self.use_int8:
-                o = ops.train_fwd(qh, kh, vh, a, lut, -(-L // ops.E_TILE))["o"]
-            else:
-                o = ops.train_fwd_1d(qh, kh, vh, a, lut, self.bq)["o"]
+            qblock = self.bq
+            if self.fused:  # sla2_forward_fused: head-shared alpha, Q tiles of block_m
+                a = a.mean(0, keepdim=True).expand(H, -1)
+                qblock = self.block_m or max(32, self.bq // 2)
+            o = ops.sla2_infer(qh, kh, vh, a, lut, self.bq, use_int8=self.use_int8,
+                               qblock=qblock)
         if return_sparsity:
             return o.to(out_dtype), 1.0 - topk / -(-L // self.bk)
         return o.to(out_dtype)

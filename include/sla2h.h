@@ -38,7 +38,8 @@ int sla2h_version(void);
 const char* sla2h_error_string(int code);
 
 /*
- * Per-(b,h,64-token block) symmetric INT8 quantisation of one tensor.
+ * Per-(b,h,E-token block) symmetric INT8 quantisation of one tensor,
+ * E = 32, 64, 128 or 256.
  *   x  : (BH, L, D) 16-bit       -> xq (BH, L, D) int8,  xs (BH, ceil(L/E)) fp32
  *   s  = fl32(fl32(max|x|) / 127) + fl32(1e-12);  xq = round_half_away(x / s).
  * Replaces quantize_qkv / _quant_blocks
@@ -394,6 +395,62 @@ int sla2h_bwd_dkdv(const void* q, const void* k, const void* v, const void* dos,
                    const float* delta, const void* qtf, const void* dotf, const uint32_t* sel,
                    const void* comp_bwd, int dtype, int B, int H, int64_t L, int D, int E,
                    float scale, void* dk, void* dv, void* stream);
+
+/* ---------------------------------------------------------------------
+ * Inference path of the 1-D SLA2 module (no-grad forward).
+ * --------------------------------------------------------------------- */
+
+/*
+ * V of the inference INT8 path: sla2h_quantize's law (E = 64) written in the
+ * INT8 MFMA fragment order of sla2h_quant_train's v8f (BH, Nb, 4096).
+ * Replaces quantize_qkv(v, BLOCK_N) as sparse_attention_int8 calls it
+ * (models/sla2_vendor/kernel_sparse_qat.py:238-239).
+ */
+int sla2h_quantize_v8f(const void* v, int dtype, int64_t BH, int64_t L, int D, int E,
+                       int8_t* v8f, float* vs, void* stream);
+
+/*
+ * Inference INT8 sparse branch, every key block routable (the last one may be
+ * partial), query blocks of bq = 64/128/256 rows for the LUT (B,H,ceil(L/bq),T):
+ *   S = int32(Q8 . K8^T) * (sq * sk) * scale * log2(e), keys past L masked,
+ *   exact running maximum, P8 = (int) fl(127 P + 0.5), O += int32(P8 . V8) * sv/127,
+ *   o_s = O / l (16-bit), lse = m + log2(l), qphi = softmax_D(q) (16-bit, optional).
+ * q8/qs from sla2h_quantize with E = qblock (32..256; bq for the unfused path,
+ * block_m for the fused one), k8/ks from sla2h_quantize (E = 64), v8f/vs from
+ * sla2h_quantize_v8f.  Replaces _attn_fwd_int8 / sparse_attention_int8
+ * (models/sla2_vendor/kernel_sparse_qat.py:154-247) and the INT8 sparse half of
+ * _sla2_fwd_fused (models/sla2_vendor/kernel_fused.py:81-106).
+ */
+int sla2h_sparse_fwd_int8(const void* q, const int8_t* q8, const float* qs, int qblock,
+                          const int8_t* k8, const float* ks, const int8_t* v8f, const float* vs,
+                          const int32_t* lut, int dtype, int B, int H, int64_t L, int D, int bq,
+                          int T, float scale, void* o_s, float* lse, void* qphi, void* stream);
+
+/*
+ * Inference linear-branch states of every 64-row key block:
+ *   Hb[j] = round16(round16(phi(K_j))^T V_j) (held as fp32 values, fp32 accumulate),
+ *   zb[j] = colsum round16(phi(K_j)) (fp32), phi = softmax over D;
+ *   Hall / zall = the sums over the blocks when given (both or neither);
+ *   vt (optional): the primal value operand tiles of sla2h_linear_states.
+ * Replaces _hblocks and the totals of complement_linear_states
+ * (models/sla2_vendor/kernel_linear.py:396-427, 496-504).
+ */
+int sla2h_hblocks_states(const void* k, const void* v, int dtype, int B, int H, int64_t L, int D,
+                         int E, float* Hb, float* zb, float* Hall, float* zall, void* vt,
+                         void* stream);
+
+/*
+ * Linear branch and mix of the inference path, per query row of block i
+ * (bq = 64/128/256 rows):
+ *   H_i = round16(comp.Hc), num = qphi . H_i (fp32 accumulate), den = qphi . comp.zc,
+ *   den += eps_l signed, o_l = num / den, o = round16(a o_s + (1 - a) o_l),
+ *   a = alpha[h * alpha_stride + i] (fp32).
+ * comp: sla2h_complement records over the plain LUT of sla2h_hblocks_states.
+ * Replaces _lin_fwd3 (models/sla2_vendor/kernel_linear.py:446-493).
+ */
+int sla2h_lin_fwd3(const void* qphi, const void* comp, const void* o_s, const float* alpha,
+                   int alpha_stride, int dtype, int B, int H, int64_t L, int D, int bq,
+                   float eps_l, void* o, void* stream);
 
 #ifdef __cplusplus
 }

@@ -689,6 +689,103 @@ def train_dense_f64(q, k, v, alpha_logit, lut, Np, prefix_len, eps=EPS_L, bq=E):
 # 1-D SLA2 blocks (query blocks of bq rows, key blocks of bk = 64 rows):
 # route_blocks and sla2_mla_jvp (models/sla2_mla_jvp.py:51-99, 108-385).
 # ---------------------------------------------------------------------------
+def infer_1d(q, k, v, alpha, lut, bq, int8=True, qblock=None, t16=torch.float16, eps=EPS_L):
+    """Inference forward of the 1-D SLA2 module (SLA2.forward without gradients,
+    models/sla2_vendor/core.py:93-128), blockwise, CPU.
+
+    Sparse branch: int8 -- _attn_fwd_int8 (models/sla2_vendor/kernel_sparse_qat.py:
+    154-247): Q quantised per qblock rows (default bq), K and V per 64-row block,
+    all with the round-half-away law of quantize_qkv; S = int(Q8 K8^T) (sq sk)
+    scale log2(e), exact running maximum, P8 = trunc(127 P + 0.5), O += (P8 V8)
+    sv / 127, o_s = O / l rounded to 16 bits.  Otherwise the 16-bit branch
+    (_attn_fwd_qat without USE_INT8: O += round16(P) V).
+    Linear branch: _hblocks and _lin_fwd3 (models/sla2_vendor/kernel_linear.py:
+    396-493): kphi = round16(softmax_D(k)), HALL_j = round16(kphi_j^T V_j),
+    ZALL_j = colsum kphi_j (fp32); H_i = sum_j HALL_j - sum_{j in lut_i} HALL_j,
+    z_i likewise (fp32); num = qphi round16(H_i), den = qphi . z_i +- eps,
+    o = round16(a o_s + (1 - a) o_l) with o_l = num / den, a fp32.
+
+    q, k, v: (B,H,L,D) float tensors holding 16-bit values; alpha (H, ceil(L/bq))
+    after the sigmoid; lut (B,H,ceil(L/bq),T).  Returns dict(o, o_s, lse, qphi,
+    hall, zall).
+    """
+    B, H, L, D = q.shape
+    nb = -(-L // E)
+    lut64, a64 = _expand_1d(lut, alpha, bq, nb)               # per 64-row sub-block
+    lut64 = torch.as_tensor(np.asarray(lut64)).long()
+    T = lut64.shape[-1]
+    if int8:
+        qb = bq if qblock is None else qblock
+        q8, qs_b = quantize_blocks(q, qb)
+        k8, ks = quantize_blocks(k)
+        v8, vs = quantize_blocks(v)
+        qrow_s = torch.as_tensor(qs_b).float().repeat_interleave(qb, dim=-1)[..., :L]
+    else:
+        q8, k8, v8 = (torch.as_tensor(x).float().numpy() for x in (q, k, v))
+        ks = vs = np.ones((B, H, nb), dtype=np.float32)
+        qrow_s = torch.ones(B, H, L)
+    qrow_s = torch.cat([qrow_s, qrow_s.new_ones(B, H, nb * E - L)], -1).view(B, H, nb, E)
+    q8t = _tiles(torch.as_tensor(q8).double(), nb)
+    k8t = _tiles(torch.as_tensor(k8).double(), nb)
+    v8t = _tiles(torch.as_tensor(v8).double(), nb)
+    ks, vs = torch.as_tensor(ks).float(), torch.as_tensor(vs).float()
+    scale = float(np.float32(D ** -0.5))
+    c2 = float(np.float32(scale * LOG2E))
+    rows = torch.arange(nb * E).view(nb, E)
+    m_i = torch.full((B, H, nb, E), -math.inf)
+    l_i = torch.zeros(B, H, nb, E)
+    o_s = torch.zeros(B, H, nb, E, D)
+    for j in range(T):
+        n = lut64[..., j]                                     # (B,H,nb)
+        kt, vt = _gather_tiles(k8t, n), _gather_tiles(v8t, n)
+        skn, svn = torch.gather(ks, 2, n), torch.gather(vs, 2, n)
+        si = torch.matmul(q8t, kt.transpose(-1, -2)).float()  # exact integers (int8)
+        if int8:
+            qk = si * (qrow_s * skn[..., None])[..., None]
+            qk = qk * c2
+        else:
+            qk = si * c2
+        valid = rows[n] < L
+        qk = qk.masked_fill(~valid[..., None, :], -math.inf)
+        new_m = torch.maximum(m_i, qk.amax(-1))
+        p = torch.exp2(qk - new_m[..., None])
+        al = torch.exp2(m_i - new_m)
+        o_s = o_s * al[..., None]
+        if int8:
+            p8 = torch.trunc(p * 127.0 + 0.5)
+            o_s = o_s + torch.matmul(p8.double(), vt).float() * (svn / 127.0)[..., None, None]
+        else:
+            o_s = o_s + torch.matmul(_round16(p, t16).double(), vt).float()
+        l_i = l_i * al + p.sum(-1)
+        m_i = new_m
+    o_s = (o_s / l_i[..., None]).reshape(B, H, nb * E, D)[:, :, :L]
+    lse = (m_i + torch.log2(l_i)).reshape(B, H, nb * E)[:, :, :L]
+    o_s16 = _round16(o_s, t16)
+    qphi = _round16(torch.softmax(q.float(), -1), t16)
+    kphi = _round16(torch.softmax(k.float(), -1), t16)
+    kpt, vvt = _tiles(kphi, nb), _tiles(v.float(), nb)        # padding rows are zero
+    hall = _round16(kpt.transpose(-1, -2) @ vvt, t16)          # (B,H,nb,D,D)
+    zall = kpt.sum(-2)                                         # (B,H,nb,D)
+    htot, ztot = hall.sum(2), zall.sum(2)
+    lutq = torch.as_tensor(np.asarray(lut)).long()             # (B,H,Mq,T)
+    Mq = lutq.shape[2]
+    hsel = torch.stack([torch.stack([hall[b, h][lutq[b, h]].sum(1) for h in range(H)])
+                        for b in range(B)])                    # (B,H,Mq,D,D)
+    zsel = torch.stack([torch.stack([zall[b, h][lutq[b, h]].sum(1) for h in range(H)])
+                        for b in range(B)])
+    hi = htot[:, :, None] - hsel
+    zi = ztot[:, :, None] - zsel
+    qrow = torch.arange(L) // bq                               # query block of each row
+    num = torch.einsum("bhld,bhlde->bhle", qphi, _round16(hi[:, :, qrow], t16))
+    den = (qphi * zi[:, :, qrow]).sum(-1)
+    den = torch.where(den >= 0, den + eps, den - eps)
+    o_l = num / den[..., None]
+    a = torch.as_tensor(alpha).float()[:, qrow][None, :, :, None]
+    o = _round16(a * o_s16 + (1.0 - a) * o_l, t16)
+    return {"o": o, "o_s": o_s16, "lse": lse, "qphi": qphi, "hall": hall, "zall": zall,
+            "o_l": o_l}
+
+
 def route_1d(q, k, topk_frac, bq, bk=E, proj_q=None, proj_k=None):
     """route_blocks with the canonical fp32 order (no smooth-k: the per-(b,h)
     key-mean shift adds a per-row constant to the scores).  Returns (lut, T)."""

@@ -538,3 +538,67 @@ def test_mla_eager_matches_package_module():
 def O_rope(S):
     from imfvideo_amd.imf_dit_video import precompute_axial_rope_3d
     return precompute_axial_rope_3d(32, (1, 10, 10), S - 100, axis_dims=(8, 12, 12))
+
+
+# ---------------------------------------------------------------------------
+# Inference forward of the 1-D SLA2 (infer_1d)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("block", [32, 128, 256])
+def test_quantize_blocks_other_block_sizes_brute_force(block):
+    g = torch.Generator().manual_seed(40 + block)
+    x = (torch.randn(1, 2, 300, 64, generator=g) * 3).half().float()
+    q, s = O.quantize_blocks(x, block)
+    xn = x.numpy().astype(np.float64)
+    for b in range(-(-300 // block)):
+        rows = slice(b * block, min(300, (b + 1) * block))
+        for h in range(2):
+            am = np.float32(np.abs(x.numpy()[0, h, rows]).max())
+            sb = np.float32(np.float32(am / np.float32(127.0)) + np.float32(1e-12))
+            assert s[0, h, b] == sb
+            for val, qv in zip(xn[0, h, rows].ravel()[::97], q[0, h, rows].ravel()[::97]):
+                y = Fraction(float(np.float32(np.float32(val) / sb)))
+                assert qv == _round_half_away_exact(y)
+
+
+def _infer_case(seed, L, bq, dt=torch.float16):
+    g = torch.Generator().manual_seed(seed)
+    q, k, v = (torch.randn(1, 2, L, 64, generator=g).to(dt).float() for _ in range(3))
+    mq = -(-L // bq)
+    lut, _ = O.route_1d(q, k, 0.3, bq)
+    alpha = 0.1 + 0.8 * torch.rand(2, mq, generator=g)
+    return q, k, v, lut, alpha
+
+
+def test_infer_1d_sixteen_bit_matches_dense():
+    q, k, v, lut, alpha = _infer_case(50, 583, 128)
+    got = O.infer_1d(q, k, v, alpha, lut, 128, int8=False)
+    want = O.dense_1d_f64(q.double(), k.double(), v.double(), lut, alpha.double(), 128)
+    assert rel_l2(got["o"], want) < 1e-3
+    assert max_abs(got["o"], want) < 2e-3
+
+
+@pytest.mark.parametrize("bq,qblock", [(128, None), (128, 64), (64, 32)])
+def test_infer_1d_int8_matches_dense_of_the_dequantised_operands(bq, qblock):
+    # sparse branch on the dequantised Q8, K8, V8 (P8 adds <= 1/254 per weight),
+    # linear branch on the raw 16-bit values, alpha mix
+    L = 583
+    q, k, v, lut, alpha = _infer_case(51, L, bq)
+    qb = bq if qblock is None else qblock
+    got = O.infer_1d(q, k, v, alpha, lut, bq, int8=True, qblock=qblock)
+    deq = lambda x, blk: (torch.as_tensor(O.quantize_blocks(x, blk)[0]).double()
+                          * torch.as_tensor(O.quantize_blocks(x, blk)[1]).double()
+                          .repeat_interleave(blk, -1)[..., :L, None])
+    qd, kd, vd = deq(q, qb), deq(k, 64), deq(v, 64)
+    o_s = O.dense_1d_f64(qd, kd, vd, lut, torch.ones_like(alpha).double(), bq)
+    o_l = O.dense_1d_f64(q.double(), k.double(), v.double(), lut,
+                         torch.zeros_like(alpha).double(), bq)
+    a = alpha.double().repeat_interleave(bq, -1)[:, :L].view(1, 2, L, 1)
+    want = a * o_s + (1 - a) * o_l
+    assert rel_l2(got["o_s"], o_s) < 2e-2
+    assert rel_l2(got["o"], want) < 2e-2
+    assert max_abs(got["o"], want) < 5e-2
+    # all key blocks routed: no complement, the output is the sparse branch
+    nb = -(-L // 64)
+    full = torch.arange(nb).view(1, 1, 1, nb).expand(1, 2, -(-L // bq), nb)
+    got1 = O.infer_1d(q, k, v, torch.ones_like(alpha), full, bq, int8=True, qblock=qblock)
+    assert torch.equal(got1["o"], got1["o_s"])
