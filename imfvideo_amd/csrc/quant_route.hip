@@ -218,10 +218,13 @@ __global__ __launch_bounds__(256) void quant_train_kernel(QuantTrainArgs a) {
 }
 
 // quantize_qkv / _quant_blocks (models/sla2_vendor/kernel_sparse_qat.py:
-// 120-151) for blocks of E = 32, 128 or 256 rows: one block per workgroup,
-// thread t holds E/4 consecutive elements (a segment of one row), s =
-// max|x| / 127 + 1e-12, q = round half away from zero of x / s.
-template <typename T16, int E>
+// 120-151) for blocks of E = 32..256 rows: one block per workgroup, thread t
+// holds E/4 consecutive elements (a segment of one row), s = max|x| / 127 +
+// 1e-12, q = round half away from zero of x / s.  TRUNC: the training
+// kernel's law instead, q = (int) fl(fl(x / s) + 0.5 sign(x)) (the in-kernel
+// Q quantisation of _attn_fwd_qat, kernel_sparse_qat.py:56-58, for BLOCK_M =
+// bq rows).
+template <typename T16, int E, bool TRUNC = false>
 __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restrict__ x, int64_t L,
                                                          int Nb, int8_t* __restrict__ xq,
                                                          float* __restrict__ xs) {
@@ -259,7 +262,8 @@ __global__ __launch_bounds__(256) void quant_rows_kernel(const uint16_t* __restr
     uint32_t acc = 0;
 #pragma unroll
     for (int b = 0; b < 4; ++b) {
-      const int qv = (int)roundf(xv[4 * i + b] / s);
+      const float xx = xv[4 * i + b];
+      const int qv = TRUNC ? (int)(xx / s + (xx >= 0.f ? 0.5f : -0.5f)) : (int)roundf(xx / s);
       acc |= ((uint32_t)(qv & 0xff)) << (8 * b);
     }
     w[i] = acc;
@@ -617,6 +621,37 @@ extern "C" int sla2h_quant_train(const void* q, const void* k, const void* v, in
     quant_train_kernel<BF16><<<grid, 256, 0, st>>>(a);
   else
     quant_train_kernel<F16><<<grid, 256, 0, st>>>(a);
+  return (int)hipGetLastError();
+}
+
+// The training kernel's truncating law (sla2h_quant_train) for one tensor in
+// blocks of E = 32..256 rows: Q of the 1-D SLA2 INT8 training forward, whose
+// query tiles are bq rows.
+extern "C" int sla2h_quantize_trunc(const void* x, int dtype, int64_t BH, int64_t L, int D,
+                                    int E, int8_t* xq, float* xs, void* stream) {
+  SLA2H_CHECK_ARG(x && xq && xs);
+  SLA2H_CHECK_ARG(D == kTile && (E == 32 || E == 64 || E == 128 || E == 256));
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(BH > 0 && BH <= 65535 && L > 0);
+  const int Nb = (int)((L + E - 1) / E);
+  dim3 grid(Nb, (int)BH);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto X = static_cast<const uint16_t*>(x);
+  auto go = [&](auto tag) {
+    using T16 = decltype(tag);
+    if (E == 32)
+      quant_rows_kernel<T16, 32, true><<<grid, 256, 0, st>>>(X, L, Nb, xq, xs);
+    else if (E == 64)
+      quant_rows_kernel<T16, 64, true><<<grid, 256, 0, st>>>(X, L, Nb, xq, xs);
+    else if (E == 128)
+      quant_rows_kernel<T16, 128, true><<<grid, 256, 0, st>>>(X, L, Nb, xq, xs);
+    else
+      quant_rows_kernel<T16, 256, true><<<grid, 256, 0, st>>>(X, L, Nb, xq, xs);
+  };
+  if (dtype == SLA2H_DTYPE_BF16)
+    go(BF16{});
+  else
+    go(F16{});
   return (int)hipGetLastError();
 }
 

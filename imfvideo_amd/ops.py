@@ -477,12 +477,14 @@ def jvp_1d(q, k, v, dq, dk, dv, alpha, lut, bq, scale=None, eps_l=1e-5, return_a
     return o, do
 
 
-def train_fwd_1d(q, k, v, alpha, lut, bq, eps_l=1e-5):
-    """Training forward of the 1-D SLA2 module (16-bit, no INT8) on given routing.
+def train_fwd_1d(q, k, v, alpha, lut, bq, eps_l=1e-5, int8=False):
+    """Training forward of the 1-D SLA2 module on given routing.
 
     q, k, v: (B,H,L,64) 16-bit, natural order.  alpha (H, ceil(L/bq)) after the
-    sigmoid; lut (B,H,ceil(L/bq),T) routed 64-row key blocks.  Returns the
-    train_fwd dict (o, o_s, o_l, lse, den, qphi, htot, ztot, Hall, comp, lut_aug).
+    sigmoid; lut (B,H,ceil(L/bq),T) routed 64-row key blocks.  int8: the INT8
+    sparse branch of _attn_fwd_qat (truncating law, Q scales per bq rows, K
+    and V per 64-row block), else the 16-bit one.  Returns the train_fwd dict
+    (o, o_s, o_l, lse, den, qphi, htot, ztot, Hall, comp, lut_aug).
     """
     _need_gpu(q, k, v, lut)
     q, k, v = (_bhld(t, "qkv") for t in (q, k, v))
@@ -492,13 +494,19 @@ def train_fwd_1d(q, k, v, alpha, lut, bq, eps_l=1e-5):
     if lut.dim() != 4 or tuple(lut.shape[:3]) != (B, H, mq):
         raise ValueError(f"lut: expected (B, H, {mq}, T), got {tuple(lut.shape)}")
     T = lut.shape[-1]
-    st = linear_states_qat(k, v, with_vt=True)
-    o_s, qphi = torch.empty_like(q), torch.empty_like(q)
-    lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
-    _lib.check(_lib.load().sla2h_sparse_fwd_1d(
-        q.data_ptr(), k.data_ptr(), st["vt"].data_ptr(), lut.data_ptr(), _dtype_code(q), B, H, L,
-        D, bq, E_TILE, T, float(D ** -0.5), o_s.data_ptr(), lse.data_ptr(), qphi.data_ptr(),
-        _stream(q.device)), "sla2h_sparse_fwd_1d")
+    st = linear_states_qat(k, v, with_vt=not int8)
+    if int8:
+        qz = quant_train(q, k, v)
+        qz["q8"], qz["qs"] = quantize_trunc(q, bq)
+        o_s, lse, qphi = sparse_fwd_int8(q, qz["q8"], qz["qs"], bq, qz["k8"], qz["ks"],
+                                         qz["v8f"], qz["vs"], lut, bq)
+    else:
+        o_s, qphi = torch.empty_like(q), torch.empty_like(q)
+        lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
+        _lib.check(_lib.load().sla2h_sparse_fwd_1d(
+            q.data_ptr(), k.data_ptr(), st["vt"].data_ptr(), lut.data_ptr(), _dtype_code(q), B,
+            H, L, D, bq, E_TILE, T, float(D ** -0.5), o_s.data_ptr(), lse.data_ptr(),
+            qphi.data_ptr(), _stream(q.device)), "sla2h_sparse_fwd_1d")
     comp = complement(st, lut, nb)
     o, o_l, den = linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha, eps_l, bq=bq)
     return dict(o=o, o_s=o_s, o_l=o_l, lse=lse, den=den, qphi=qphi,
@@ -512,6 +520,19 @@ def train_fwd_1d(q, k, v, alpha, lut, bq, eps_l=1e-5):
 # sparse_attention_int8 (or the 16-bit one), the state-subtraction linear
 # branch of complement_linear_states and the alpha mix.
 # ---------------------------------------------------------------------------
+
+def quantize_trunc(x, E=E_TILE):
+    """x (B,H,L,D) 16-bit -> (xq int8, xs fp32 (B,H,ceil(L/E))), the truncating law."""
+    _need_gpu(x)
+    x = _bhld(x, "x")
+    B, H, L, D = x.shape
+    xq = torch.empty_like(x, dtype=torch.int8)
+    xs = torch.empty(B, H, -(-L // E), device=x.device, dtype=torch.float32)
+    _lib.check(_lib.load().sla2h_quantize_trunc(x.data_ptr(), _dtype_code(x), B * H, L, D, E,
+                                                xq.data_ptr(), xs.data_ptr(), _stream(x.device)),
+               "sla2h_quantize_trunc")
+    return xq, xs
+
 
 def quantize_v8f(v, E=E_TILE):
     """V (B,H,L,64) 16-bit -> (v8f int8 (B,H,Nb,4096) fragment order, vs fp32 (B,H,Nb))."""

@@ -7,8 +7,8 @@
 
 Query blocks of bq rows (64, 128 or 256), key blocks of bk = 64 rows.  With
 gradients enabled the forward runs the training-forward kernels (16-bit
-sparse branch, 16-bit state-form linear branch and mix; with use_int8 and
-bq = 64, the INT8 training forward of the cube op) inside an autograd
+sparse branch, or with use_int8 the INT8 one of _attn_fwd_qat; 16-bit
+state-form linear branch and mix) inside an autograd
 Function whose backward is the straight-through HIP backward.  Without
 gradients it runs the inference path (ops.sla2_infer): the INT8 sparse
 branch of sparse_attention_int8 (or the 16-bit one), the state-subtraction
@@ -39,10 +39,7 @@ class _SLA2Function(torch.autograd.Function):
     @staticmethod
     def forward(ctx, qh, kh, vh, alpha_logit, lut, bq, use_int8):
         a = torch.sigmoid(alpha_logit.detach().float())
-        if use_int8:
-            out = ops.train_fwd(qh, kh, vh, a, lut, -(-qh.shape[2] // ops.E_TILE))
-        else:
-            out = ops.train_fwd_1d(qh, kh, vh, a, lut, bq)
+        out = ops.train_fwd_1d(qh, kh, vh, a, lut, bq, int8=use_int8)
         ctx.bq = bq
         ctx.save_for_backward(qh, kh, vh, a, out["o_s"], out["o_l"], out["lse"], out["den"],
                               out["qphi"], out["Hall"], out["comp"], out["lut_aug"])
@@ -66,7 +63,7 @@ class SLA2(nn.Module):
         topk            : k%, fraction of key blocks routed to the sparse branch
         bq, bk          : query / key block sizes (bq in {64, 128, 256}, bk = 64)
         use_bf16        : 16-bit compute type bf16 (else fp16)
-        use_int8        : INT8 sparse branch (inference: every bq; training: bq = 64)
+        use_int8        : INT8 sparse branch
         alpha_init      : initial value of alpha (before the logit)
         block_m, fused  : the fused inference path's query tile (its Q scales run
                           per block_m rows, default max(32, bq // 2)) and switch
@@ -106,8 +103,6 @@ class SLA2(nn.Module):
         lut, topk = self.router.route(qh, kh, self.topk)
         alpha_logit = self._get_alpha(H, -(-L // self.bq), q.device)
         if training:
-            if self.use_int8 and self.bq != ops.E_TILE:
-                raise NotImplementedError("the INT8 training forward is built for bq = bk = 64")
             o = _SLA2Function.apply(qh, kh, vh, alpha_logit, lut, self.bq, self.use_int8)
         else:
             # inference (core.py:98-128): INT8 or 16-bit sparse branch, the

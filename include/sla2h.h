@@ -401,6 +401,17 @@ int sla2h_bwd_dkdv(const void* q, const void* k, const void* v, const void* dos,
  * --------------------------------------------------------------------- */
 
 /*
+ * The training forward's truncating INT8 law (sla2h_quant_train's) for one
+ * tensor in blocks of E = 32, 64, 128 or 256 rows:
+ *   s = fl32(fl32(max|x|) / 127) + fl32(1e-12);  xq = (int) fl(fl(x / s) + 0.5 sign(x)).
+ * Q of the 1-D SLA2 INT8 training forward (query tiles of bq rows); replaces
+ * the in-kernel Q quantisation of _attn_fwd_qat with USE_INT8
+ * (models/sla2_vendor/kernel_sparse_qat.py:56-58).
+ */
+int sla2h_quantize_trunc(const void* x, int dtype, int64_t BH, int64_t L, int D, int E,
+                         int8_t* xq, float* xs, void* stream);
+
+/*
  * V of the inference INT8 path: sla2h_quantize's law (E = 64) written in the
  * INT8 MFMA fragment order of sla2h_quant_train's v8f (BH, Nb, 4096).
  * Replaces quantize_qkv(v, BLOCK_N) as sparse_attention_int8 calls it

@@ -415,11 +415,12 @@ def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L
     blocks are appended (lut_aug).  Returns dict with o (16-bit values, the
     module output), o_s, o_l (16-bit values), lse (fp32, log2 domain), qphi,
     den (the signed-epsilon denominator), htot (16-bit values), ztot.
-    int8=False, bq > 64: the 1-D SLA2 module's forward (_sparse_attention_qat
-    without USE_INT8, models/sla2_vendor/kernel_sparse_qat.py:265-293, and
+    bq > 64: the 1-D SLA2 module's forward (_sparse_attention_qat,
+    models/sla2_vendor/kernel_sparse_qat.py:265-293, and
     _complement_linear_attention, models/sla2_vendor/kernel_linear.py:340-366):
-    16-bit scores, O += round16(P).V, query blocks of bq rows (LUT rows and
-    alpha per block), Np = Nb key blocks and no prefix tail.
+    query blocks of bq rows (LUT rows, alpha and, with int8, the Q scale per
+    block), Np = Nb key blocks and no prefix tail; int8=False: 16-bit scores
+    and O += round16(P).V.
     """
     B, H, L, D = q.shape
     nb = -(-L // E)
@@ -434,8 +435,10 @@ def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L
     if not int8:   # 16-bit operands: the "int8" tensors below hold the 16-bit values, scales 1
         q8, k8, v8 = (torch.as_tensor(x).float().numpy() for x in (q, k, v))
         qs = ks = vs = np.ones((B, H, nb), dtype=np.float32)
-    else:
-        q8, qs = quantize_blocks_trunc(q)
+    else:   # Q per bq rows (the kernel's BLOCK_M), K and V per 64-row block
+        q8, qs = quantize_blocks_trunc(q, bq)
+        if bq != E:
+            qs = np.repeat(qs, bq // E, axis=-1)[..., :nb]
         k8, ks = quantize_blocks_trunc(k)
         v8, vs = quantize_blocks_trunc(v)
     q8t = _tiles(torch.as_tensor(q8).double(), nb)

@@ -154,3 +154,55 @@ def test_sla2_module_no_grad_is_the_inference_path(fused):
                      qblock=64 if fused else 128, t16=torch.float16)
     print(f"  o max {max_abs(o, ref['o']):.2e} rel {rel_l2(o, ref['o']):.2e}", flush=True)
     assert max_abs(o, ref["o"]) < TOL_MAX and rel_l2(o, ref["o"]) < TOL_REL
+
+
+# ---------------------------------------------------------------------------
+# INT8 training forward of the 1-D SLA2 (bq = 128: the reference's default)
+# ---------------------------------------------------------------------------
+@pytest.mark.parametrize("E", [64, 128, 256])
+def test_quantize_trunc_law(E):
+    from imfvideo_amd import ops
+    say("quantize_trunc E", E)
+    x = _inputs(120 + E, 1, 3, 583, torch.bfloat16)[0] * 1.7
+    x8, xs = ops.quantize_trunc(cuda(x), E)
+    want_q, want_s = O.quantize_blocks_trunc(x.float(), E)
+    assert np.array_equal(x8.cpu().numpy(), want_q)
+    assert np.array_equal(xs.cpu().numpy(), want_s)
+
+
+@pytest.mark.parametrize("bq", [128, 256])
+def test_sla2_int8_training_forward_and_backward(bq):
+    """SLA2(use_int8=True, bq) with gradients: the INT8 sparse branch of
+    _attn_fwd_qat (truncating law, Q scales per bq rows) and the STE backward."""
+    from imfvideo_amd.sla2_vendor.core import SLA2
+    say("SLA2 INT8 training bq", bq)
+    torch.manual_seed(4)
+    L, H = 583, 2
+    mq = -(-L // bq)
+    mod = SLA2(64, topk=0.3, bq=bq, use_int8=True).cuda()
+    q, k, v = _inputs(130 + bq, 1, H, L, torch.float16)
+    with torch.no_grad():
+        mod(cuda(q), cuda(k), cuda(v))  # creates alpha
+        mod.alpha_logit.add_(torch.linspace(-1, 1, mod.alpha_logit.numel(), device="cuda")
+                             .view_as(mod.alpha_logit))
+    xs = [cuda(t).requires_grad_() for t in (q, k, v)]
+    out = mod(*xs)
+    g = torch.Generator().manual_seed(9)
+    do = torch.randn(1, H, L, 64, generator=g).half()
+    (out.float() * cuda(do).float()).sum().backward()
+    grads = [t.grad.cpu() for t in xs] + [mod.alpha_logit.grad.cpu()]
+    lut, _ = O.route_1d(q.float(), k.float(), 0.3, bq)
+    nb = -(-L // 64)
+    a = torch.sigmoid(mod.alpha_logit.detach().cpu())
+    fwd = O.train_fwd(q.float(), k.float(), v.float(), a, lut, nb, 0, t16=torch.float16,
+                      int8=True, bq=bq)
+    o = out.detach().cpu().float()
+    print(f"  o max {max_abs(o, fwd['o']):.2e} rel {rel_l2(o, fwd['o']):.2e}", flush=True)
+    assert max_abs(o, fwd["o"]) < TOL_MAX and rel_l2(o, fwd["o"]) < TOL_REL
+    ref = O.train_bwd(q.float(), k.float(), v.float(), a, lut, nb, 0, fwd, do.float(),
+                      t16=torch.float16, bq=bq, variant="1d")
+    for got, name in zip(grads[:3], ("dq", "dk", "dv")):
+        want = ref[name]
+        print(f"  {name} max {max_abs(got, want):.2e} rel {rel_l2(got, want):.2e}", flush=True)
+        assert rel_l2(got, want) < TOL_REL and max_abs(got, want) < TOL_MAX * max(1, want.abs().max())
+    assert rel_l2(grads[3], ref["d_alpha"]) < 1e-2

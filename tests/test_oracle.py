@@ -602,3 +602,25 @@ def test_infer_1d_int8_matches_dense_of_the_dequantised_operands(bq, qblock):
     full = torch.arange(nb).view(1, 1, 1, nb).expand(1, 2, -(-L // bq), nb)
     got1 = O.infer_1d(q, k, v, torch.ones_like(alpha), full, bq, int8=True, qblock=qblock)
     assert torch.equal(got1["o"], got1["o_s"])
+
+
+@pytest.mark.parametrize("bq", [128, 256])
+def test_train_fwd_1d_int8_matches_dense_of_the_dequantised_operands(bq):
+    # INT8 1-D training forward: sparse branch on the truncation-law Q8 (scales
+    # per bq rows), K8, V8; the linear branch on the raw 16-bit values
+    L, H = 583, 2
+    q, k, v, lut, alpha = _infer_case(52, L, bq)
+    nb = -(-L // 64)
+    got = O.train_fwd(q, k, v, alpha, lut, nb, 0, t16=torch.float16, int8=True, bq=bq)
+
+    def deq(x, blk):
+        x8, xs = O.quantize_blocks_trunc(x, blk)
+        return (torch.as_tensor(x8).double()
+                * torch.as_tensor(xs).double().repeat_interleave(blk, -1)[..., :L, None])
+    o_s = O.dense_1d_f64(deq(q, bq), deq(k, 64), deq(v, 64), lut,
+                         torch.ones_like(alpha).double(), bq)
+    assert rel_l2(got["o_s"], o_s) < 2e-2
+    # the Q scale runs per bq rows: with per-64-row scales the integer scores differ
+    q8, _ = O.quantize_blocks_trunc(q, bq)
+    q8_64, _ = O.quantize_blocks_trunc(q, 64)
+    assert not np.array_equal(q8, q8_64)
