@@ -26,7 +26,7 @@ from .sla2_cube_qat import sla2_cube_qat_jvp_fused
 from .sla2_mla_jvp import route_blocks, sla2_mla_jvp
 
 __all__ = ["mla_params_from_block", "mla_fp16_cache", "attn_sublayer_jvp", "mlp_sublayer_jvp",
-           "block_jvp"]
+           "block_jvp", "pack_block", "build_fast_jvp_state"]
 
 _FP16 = torch.float16
 _F32_CODE = 2
@@ -174,6 +174,66 @@ def mlp_sublayer_jvp(h, dh, p, w16, eps):
     dwn = F.linear(act, w16["w_down"]).float().view(2 * B, S, D)
     g = _vec(p["g_mlp"], dev)
     return dwn[:B] * g, dwn[B:] * g
+
+
+def pack_block(block, tile_major=False):
+    """(params, fp16 weight cache) of one TransformerBlock for the fast JVP
+    (the inner pack of models/mla_jvp_fast.py:252-300): the block parameters,
+    the attention-residual heads when the block has them, and a snapshot of the
+    attention's routing / mixing state so that the fast path computes the
+    training forward's attention function --
+      cube (SLA2CubeQATAttentionImpl): alpha = sigmoid(alpha_logit) (H, Mb),
+        proj_q, proj_k, topk, Np, E, P (prefix tokens), perm, inv and
+        pre_permuted = tile_major (the model keeps tokens tile-major);
+      sla2 (SLA2AttentionImpl): alpha (H, Mb), the router projections, topk, bq, bk.
+    Rebuild after every optimizer step (the weights change)."""
+    p = mla_params_from_block(block)
+    for name in ("attn_res_norm", "mlp_res_norm"):
+        if hasattr(block, name):
+            p[name] = getattr(block, name).weight.detach()
+    for name in ("attn_res_proj", "mlp_res_proj"):
+        if hasattr(block, name):
+            p[name] = getattr(block, name).weight.detach()
+    impl = getattr(block.attn, "attn_impl", None)
+    if isinstance(impl, torch.nn.Module) and hasattr(impl, "perm"):
+        p["cube"] = {
+            "pre_permuted": bool(tile_major),
+            "alpha": torch.sigmoid(impl.alpha_logit.detach()).float(),
+            "proj_q": impl.proj_q.detach(), "proj_k": impl.proj_k.detach(),
+            "topk": impl.topk_frac, "Np": impl.Np, "E": impl.E, "P": impl.prefix_len,
+            "perm": impl.perm, "inv": impl.inv,
+        }
+    elif isinstance(impl, torch.nn.Module) and hasattr(impl, "sla2"):
+        sl = impl.sla2
+        if sl.alpha_logit is None:
+            raise ValueError("SLA2 alpha is created by the first forward; run the block once")
+        p["sla2"] = {
+            "alpha": torch.sigmoid(sl.alpha_logit.detach()).float(),
+            "proj_q": sl.router.proj_q.weight.detach(), "proj_k": sl.router.proj_k.weight.detach(),
+            "topk": impl.topk, "bq": impl.bq, "bk": impl.bk,
+        }
+    return p, mla_fp16_cache(p)
+
+
+def build_fast_jvp_state(net):
+    """Per-block (params, fp16 cache) of a DiT's shared trunk and u-heads plus
+    the u-branch output tensors (models/mla_jvp_fast.py:252-316); net needs
+    the reference model's attributes (shared_blocks, u_heads, u_out_res_norm /
+    _proj, u_final_layer, rope_cos / rope_sin, rmsnorm_eps,
+    attn_res_block_size, prefix_tokens, tile_major)."""
+    tm = getattr(net, "tile_major", False)
+    return {
+        "shared": [pack_block(b, tm) for b in net.shared_blocks],
+        "u_heads": [pack_block(b, tm) for b in net.u_heads],
+        "u_out_res": (net.u_out_res_norm.weight.detach(), net.u_out_res_proj.weight.detach()),
+        "u_final": (net.u_final_layer.norm.weight.detach(),
+                    net.u_final_layer.linear.weight.detach(),
+                    net.u_final_layer.linear.bias.detach()),
+        "rope": (net.rope_cos, net.rope_sin),
+        "eps": net.rmsnorm_eps,
+        "bs": net.attn_res_block_size,
+        "prefix_tokens": net.prefix_tokens,
+    }
 
 
 def block_jvp(h, dh, p, w16, cos, sin, eps):

@@ -152,3 +152,49 @@ def test_transformer_block_training_step():
     assert blk.attn.attn_impl.alpha_logit.grad is not None
     assert torch.isfinite(blk.attn.q_b_proj.weight.grad).all()
     assert blk.attn.attn_impl.logit_max_log2.shape == (2,)
+
+
+def test_pack_block_snapshot_drives_the_fast_jvp():
+    """pack_block on a TransformerBlock with the cube attention: the snapshot
+    (sigmoid(alpha_logit), projections, tiling) drives block_jvp, which then
+    matches the oracle restatement fed the block's own weights."""
+    say("pack_block (cube) -> block_jvp")
+    from functools import partial
+    from imfvideo_amd.imf_dit_video import TransformerBlock
+    from imfvideo_amd.mla_jvp_fast import block_jvp, pack_block
+    from imfvideo_amd.sla2_cube_qat import SLA2CubeQATAttentionImpl
+    torch.manual_seed(6)
+    S, P = 274, 18
+    impl = partial(SLA2CubeQATAttentionImpl, seq_len=S, num_heads=2, grid=(4, 8, 8),
+                   tile=(4, 4, 4), topk=1.0)
+    blk = TransformerBlock(256, 2, 128, 64, 32, 32, 64, mlp_ratio=2, attn_impl=impl,
+                           mla_use_output_gate=True).cuda()
+    with torch.no_grad():
+        blk.attn_scale.fill_(0.1)
+        blk.mlp_scale.fill_(0.1)
+        blk.attn.attn_impl.alpha_logit.copy_(torch.linspace(-1, 2, 2 * 5).view(2, 5))
+    p, w16 = pack_block(blk)
+    cube = p["cube"]
+    assert torch.allclose(cube["alpha"], torch.sigmoid(blk.attn.attn_impl.alpha_logit.detach()))
+    assert (cube["Np"], cube["E"], cube["P"], cube["topk"]) == (4, 64, P, 1.0)
+    g = torch.Generator().manual_seed(8)
+    h = torch.randn(1, S, 256, generator=g)
+    dh = 0.1 * torch.randn(1, S, 256, generator=g)
+    cos, sin = rope(S, P)
+    x, dx = block_jvp(cuda(h), cuda(dh), p, w16, cuda(cos), cuda(sin), 1e-6)
+    pc = {k: (v.detach().cpu().float() if torch.is_tensor(v) else v) for k, v in p.items()
+          if k not in ("cube",)}
+    perm, inv, Np = cube["perm"].cpu(), cube["inv"].cpu(), cube["Np"]
+    alpha = cube["alpha"].cpu()
+    nb = -(-S // 64)
+    lut = np.broadcast_to(np.arange(Np, dtype=np.int32), (1, 2, nb, Np)).copy()
+
+    def ref_attn(q, k, v, dq, dk, dv):
+        t = lambda y: y[:, :, perm]
+        o, do = O.cube_jvp(*(t(y) for y in (q, k, v, dq, dk, dv)), alpha, lut, Np, P,
+                           t16=torch.float16)
+        return o[:, :, inv], do[:, :, inv]
+    a, da = O.mla_attn_jvp(h, dh, pc, cos, sin, 1e-6, ref_attn)
+    h1, dh1 = h + a, dh + da
+    m, dm = O.mlp_jvp(h1, dh1, pc, 1e-6)
+    check((x, dx), (h1 + m, dh1 + dm), "packed block")
