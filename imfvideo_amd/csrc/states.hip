@@ -249,7 +249,9 @@ __global__ __launch_bounds__(256) void linear_states_kernel(
   }
 }
 
-// Global sums over the Np tiles, sequential in n (deterministic).
+// Global sums over the Np tiles in a fixed order (deterministic): four
+// contiguous ranges of tiles summed in sequence by four threads of a column,
+// then ((r0 + r1) + (r2 + r3)).  64 columns per workgroup of 256 threads.
 // Column index e spans [Hb 4096 | dHb 4096 | zb 64 | dzb 64].
 __global__ __launch_bounds__(256) void states_sum_kernel(const float* __restrict__ Hb,
                                                         const float* __restrict__ dHb,
@@ -259,7 +261,9 @@ __global__ __launch_bounds__(256) void states_sum_kernel(const float* __restrict
                                                         float* __restrict__ dHall,
                                                         float* __restrict__ zall,
                                                         float* __restrict__ dzall) {
-  const int e = blockIdx.x * 256 + threadIdx.x;
+  __shared__ float part[4][64];
+  const int c = threadIdx.x & 63, part_id = threadIdx.x >> 6;
+  const int e = blockIdx.x * 64 + c;
   const int bh = blockIdx.y;
   const float* src;
   float* dst;
@@ -270,16 +274,20 @@ __global__ __launch_bounds__(256) void states_sum_kernel(const float* __restrict
     src = dHb; dst = dHall; stride = 4096; col = e - 4096;
   } else if (e < 8256) {
     src = zb; dst = zall; stride = 64; col = e - 8192;
-  } else if (e < 8320) {
-    src = dzb; dst = dzall; stride = 64; col = e - 8256;
   } else {
-    return;
+    src = dzb; dst = dzall; stride = 64; col = e - 8256;
   }
-  if (src == nullptr) return;
+  if (src == nullptr) return;  // uniform: a workgroup never spans two parts
+  const int chunk = (Np + 3) / 4;
+  const int n0 = part_id * chunk, n1 = min(Np, n0 + chunk);
   const float* p = src + (int64_t)bh * Np * stride + col;
   float acc = 0.f;
-  for (int nn = 0; nn < Np; ++nn) acc += p[(int64_t)nn * stride];
-  dst[(int64_t)bh * stride + col] = acc;
+#pragma unroll 8
+  for (int nn = n0; nn < n1; ++nn) acc += p[(int64_t)nn * stride];
+  part[part_id][c] = acc;
+  __syncthreads();
+  if (part_id == 0)
+    dst[(int64_t)bh * stride + col] = (part[0][c] + part[1][c]) + (part[2][c] + part[3][c]);
 }
 
 // ---------------------------------------------------------------------------
@@ -582,7 +590,7 @@ extern "C" int sla2h_linear_states(const void* k, const void* dk, const void* v,
   }
   int err = (int)hipGetLastError();
   if (err || Hall == nullptr) return err;
-  dim3 g2((8320 + 255) / 256, B * H);
+  dim3 g2(8320 / 64, B * H);
   states_sum_kernel<<<g2, 256, 0, st>>>(Hb, tan ? dHb : nullptr, zb, tan ? dzb : nullptr, Np, Hall,
                                         dHall, zall, dzall);
   return (int)hipGetLastError();
@@ -606,7 +614,7 @@ extern "C" int sla2h_linear_states_qat(const void* k, const void* v, int dtype, 
     linear_states_kernel<F16, false, true><<<grid, 256, 0, st>>>(K, nullptr, V, nullptr, L, Nb, Nb, Hb, nullptr, zb, nullptr, static_cast<uint16_t*>(vt), nullptr);
   int err = (int)hipGetLastError();
   if (err) return err;
-  dim3 g2((8320 + 255) / 256, B * H);
+  dim3 g2(8320 / 64, B * H);
   states_sum_kernel<<<g2, 256, 0, st>>>(Hb, nullptr, zb, nullptr, Nb, Hall, nullptr, zall, nullptr);
   return (int)hipGetLastError();
 }
@@ -636,7 +644,7 @@ extern "C" int sla2h_hblocks_states(const void* k, const void* v, int dtype, int
     linear_states_kernel<F16, false, true, true><<<grid, 256, 0, st>>>(K, nullptr, V, nullptr, L, Nb, Nb, Hb, nullptr, zb, nullptr, static_cast<uint16_t*>(vt), nullptr);
   int err = (int)hipGetLastError();
   if (err || Hall == nullptr) return err;
-  dim3 g2((8320 + 255) / 256, B * H);
+  dim3 g2(8320 / 64, B * H);
   states_sum_kernel<<<g2, 256, 0, st>>>(Hb, nullptr, zb, nullptr, Nb, Hall, nullptr, zall, nullptr);
   return (int)hipGetLastError();
 }
