@@ -189,6 +189,89 @@ def train_bench(args):
     print(json.dumps(out), flush=True)
 
 
+def block_step_bench(args):
+    """Config 5: 8 stacked DiT blocks (RMSNorm -> MLA attention with the SLA2
+    INT8 cube op -> SwiGLU MLP, ReZero scales 0.1), d=512, H=8, dq=256, dc=128,
+    dn=dr=32, dv=64, MLP ratio 4, weights N(0, 0.5/sqrt(d_in)), B=2 x N=29,952
+    tokens (12x48x52 grid kept tile-major, 4x4x4 tiles, top-k 10%).  One step:
+    the forward with autograd (bf16 autocast), the fast forward + JVP pass
+    (block_jvp from each block's pack_block snapshot, rebuilt every step as the
+    weights change), and the backward of a loss that uses the JVP output only
+    under stop-gradient (as iMF's does).  Prints its own line: ms per block."""
+    from functools import partial
+    from imfvideo_amd.imf_dit_video import TransformerBlock, precompute_axial_rope_3d
+    from imfvideo_amd.mla_jvp_fast import block_jvp, pack_block
+    from imfvideo_amd.mla_video_sparse_jvp import tile_permutation
+    from imfvideo_amd.sla2_cube_qat import SLA2CubeQATAttentionImpl
+
+    B, S, D, H, depth, grid = 2, 29952, 512, 8, 8, (12, 48, 52)
+    dev = torch.device("cuda:0")
+    torch.manual_seed(5)
+    impl = partial(SLA2CubeQATAttentionImpl, seq_len=S, num_heads=H, grid=grid, tile=(4, 4, 4),
+                   topk=0.1, pre_permuted=True)
+    blocks = torch.nn.ModuleList(
+        [TransformerBlock(D, H, 256, 128, 32, 32, 64, mlp_ratio=4, weight_init_constant=0.5,
+                          attn_impl=impl) for _ in range(depth)]).to(dev)
+    with torch.no_grad():
+        for b in blocks:
+            b.attn_scale.fill_(0.1)
+            b.mlp_scale.fill_(0.1)
+    perm, _, _ = tile_permutation(grid, (4, 4, 4), 0, torch.device("cpu"))
+    cos, sin = (t[perm].to(dev) for t in precompute_axial_rope_3d(32, grid, 0,
+                                                                  axis_dims=(8, 12, 12)))
+    g = torch.Generator().manual_seed(5)
+    x = torch.randn(B, S, D, generator=g).to(torch.bfloat16).float().to(dev)
+    dx = (0.1 * torch.randn(B, S, D, generator=g)).to(dev)
+
+    def step(ev=None):
+        rec = (lambda i: ev[i].record()) if ev is not None else (lambda i: None)
+        rec(0)
+        with torch.autocast("cuda", dtype=torch.bfloat16):
+            h = x
+            for b in blocks:
+                h = b(h, cos, sin)
+        rec(1)
+        with torch.no_grad():
+            hj, dhj = x, dx
+            for b in blocks:
+                pk, w16 = pack_block(b, tile_major=True)
+                hj, dhj = block_jvp(hj, dhj, pk, w16, cos, sin, 1e-6)
+        rec(2)
+        loss = (h.float() - dhj).pow(2).mean()
+        loss.backward()
+        rec(3)
+        return loss
+
+    for _ in range(args.warmup):
+        step()
+        blocks.zero_grad(set_to_none=True)
+    torch.cuda.synchronize()
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    start.record()
+    for i in range(args.steps):
+        loss = step(evs[i])
+        blocks.zero_grad(set_to_none=True)
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / args.steps
+    st = {name: statistics.mean(e[k].elapsed_time(e[k + 1]) for e in evs) / depth
+          for k, name in enumerate(["forward", "fast_jvp", "backward"])}
+    print(json.dumps({
+        "metric": "ms per DiT block (fwd + fast JVP + bwd) of an 8-block SLA2-INT8 stack, "
+                  "BASELINE Config 5, 1 MI355X",
+        "value": round(ms / depth, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": False,
+        "scaling": "weak", "vs_baseline": None, "dtype": "bf16 autocast + int8/fp16 attention",
+        "data": "synthetic (CPU-seeded x bf16 N(0,1), dx 0.1 N(0,1); weights N(0, 0.5/sqrt(d_in)))",
+        "config": {"workload": "8 stacked DiT blocks, training step with the du/dt JVP "
+                               "(BASELINE Config 5)", "B": B, "N": S, "d": D, "H": H,
+                   "dq": 256, "dc": 128, "mlp_ratio": 4, "depth": depth, "topk": 0.1,
+                   "tile_major": True},
+        "loss": float(loss.item()),
+        "per_block_ms": {k_: round(v_, 3) for k_, v_ in st.items()}}), flush=True)
+
+
 def mla_bench(args):
     """Config 4: the MLA attention sublayer (sla2_mla_jvp variant) forward + JVP at
     N=29,952, d=512, H=8, dq=256, dc=128, dn=dr=32, dv=64, partial axial RoPE
@@ -251,6 +334,8 @@ def main():
                     help="4: the MLA sublayer JVP (own line); 5: the attention op's training "
                          "step at Config 5's shape (own line)")
     ap.add_argument("--cpu-baseline", type=int, default=1)
+    ap.add_argument("--op-only", action="store_true",
+                    help="Config 5: time the attention op's training step instead of the blocks")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB fp32 copy kernel (torch.mul by 1) three times: "
                          "the reference reading for the FETCH_SIZE / WRITE_SIZE counters")
@@ -269,7 +354,7 @@ def main():
         sys.exit(1)
 
     if args.config == 5:
-        train_bench(args)
+        (train_bench if args.op_only else block_step_bench)(args)
         return
     if args.config == 4:
         mla_bench(args)
