@@ -36,6 +36,15 @@ struct IO<SLA2H_DTYPE_F16> {
     static_cast<uint16_t*>(p)[i] = F16::from_f32(v);
   }
   __device__ static float rt(float v) { return F16::to_f32(F16::from_f32(v)); }
+  // elements i, i + 1 (i even, 4-byte aligned) as one 32-bit access
+  __device__ static float2 ld2(const void* p, int64_t i) {
+    const uint32_t u = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p) + i);
+    return make_float2(F16::to_f32((uint16_t)(u & 0xffff)), F16::to_f32((uint16_t)(u >> 16)));
+  }
+  __device__ static void st2(void* p, int64_t i, float a, float b) {
+    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p) + i) =
+        (uint32_t)F16::from_f32(a) | ((uint32_t)F16::from_f32(b) << 16);
+  }
 };
 template <>
 struct IO<SLA2H_DTYPE_BF16> {
@@ -46,6 +55,15 @@ struct IO<SLA2H_DTYPE_BF16> {
     static_cast<uint16_t*>(p)[i] = BF16::from_f32(v);
   }
   __device__ static float rt(float v) { return BF16::to_f32(BF16::from_f32(v)); }
+  // elements i, i + 1 (i even, 4-byte aligned) as one 32-bit access
+  __device__ static float2 ld2(const void* p, int64_t i) {
+    const uint32_t u = *reinterpret_cast<const uint32_t*>(static_cast<const uint16_t*>(p) + i);
+    return make_float2(BF16::to_f32((uint16_t)(u & 0xffff)), BF16::to_f32((uint16_t)(u >> 16)));
+  }
+  __device__ static void st2(void* p, int64_t i, float a, float b) {
+    *reinterpret_cast<uint32_t*>(static_cast<uint16_t*>(p) + i) =
+        (uint32_t)BF16::from_f32(a) | ((uint32_t)BF16::from_f32(b) << 16);
+  }
 };
 constexpr int kF32 = 2;  // fp32 I/O code used by these kernels only
 template <>
@@ -123,12 +141,14 @@ __global__ __launch_bounds__(256) void qkv_prep_kernel(
     int B, int S, int H, float eps, void* __restrict__ Q, void* __restrict__ DQ,
     void* __restrict__ K, void* __restrict__ DK, void* __restrict__ V, void* __restrict__ DV) {
   constexpr int DN = 32, DR2 = 16, HD = 64, DVW = 64;
-  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);  // (row, head)
+  // (row, head) of this wave, uniform: 32-bit index math pinned to SGPRs
+  const int unit = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
   const int64_t half = (int64_t)B * S;
   if (unit >= half * H) return;
-  const int h = (int)(unit % H);
-  const int64_t row = unit / H;  // primal token row b*S + s
-  const int b = (int)(row / S), s = (int)(row % S);
+  const int h = __builtin_amdgcn_readfirstlane(unit % H);
+  const int row = __builtin_amdgcn_readfirstlane(unit / H);  // primal token row b*S + s
+  const int b = __builtin_amdgcn_readfirstlane(row / S);
+  const int s = row - b * S;
   const int l = threadIdx.x & 63;
   const int i = l & 15;
   const int64_t dst = (((int64_t)b * H + h) * S + (pos ? pos[s] : s)) * HD;  // (B,H,L,64) row
@@ -140,8 +160,8 @@ __global__ __launch_bounds__(256) void qkv_prep_kernel(
     const void* src = sel == 0 ? QB : KVB;
     const int64_t base = sel == 0 ? qrow + h * HD : krow + h * kvw;
     const int64_t base_t = sel == 0 ? qrow_t + h * HD : krow_t + h * kvw;
-    const float x0 = IO<DT>::ld(src, base + 2 * i), x1 = IO<DT>::ld(src, base + 2 * i + 1);
-    const float d0 = IO<DT>::ld(src, base_t + 2 * i), d1 = IO<DT>::ld(src, base_t + 2 * i + 1);
+    const float2 xx = IO<DT>::ld2(src, base + 2 * i), dd = IO<DT>::ld2(src, base_t + 2 * i);
+    const float x0 = xx.x, x1 = xx.y, d0 = dd.x, d1 = dd.y;
     const float ss = sum16(x0 * x0 + x1 * x1);
     const float sxd = sum16(x0 * d0 + x1 * d1);
     const float inv_r = 1.f / sqrtf(ss / (float)DN + eps);
@@ -149,30 +169,28 @@ __global__ __launch_bounds__(256) void qkv_prep_kernel(
     const float* w = sel == 0 ? wqn : wkn;
     void* Y = sel == 0 ? Q : K;
     void* DY = sel == 0 ? DQ : DK;
-    IO<DT>::st(Y, dst + 2 * i, w[2 * i] * x0 * inv_r);
-    IO<DT>::st(Y, dst + 2 * i + 1, w[2 * i + 1] * x1 * inv_r);
-    IO<DT>::st(DY, dst + 2 * i, w[2 * i] * (d0 * inv_r - x0 * k3));
-    IO<DT>::st(DY, dst + 2 * i + 1, w[2 * i + 1] * (d1 * inv_r - x1 * k3));
+    IO<DT>::st2(Y, dst + 2 * i, w[2 * i] * x0 * inv_r, w[2 * i + 1] * x1 * inv_r);
+    IO<DT>::st2(DY, dst + 2 * i, w[2 * i] * (d0 * inv_r - x0 * k3),
+                w[2 * i + 1] * (d1 * inv_r - x1 * k3));
   } else {
     const float c = cosb[(int64_t)s * DR2 + i], sn = sinb[(int64_t)s * DR2 + i];
     float xr, xi, dr_, di;
+    float2 xx, dd;
     if (sel == 2) {
-      xr = IO<DT>::ld(QB, qrow + h * HD + DN + 2 * i);
-      xi = IO<DT>::ld(QB, qrow + h * HD + DN + 2 * i + 1);
-      dr_ = IO<DT>::ld(QB, qrow_t + h * HD + DN + 2 * i);
-      di = IO<DT>::ld(QB, qrow_t + h * HD + DN + 2 * i + 1);
+      xx = IO<DT>::ld2(QB, qrow + h * HD + DN + 2 * i);
+      dd = IO<DT>::ld2(QB, qrow_t + h * HD + DN + 2 * i);
     } else {
-      xr = IO<DT>::ld(KR, row * skr + 2 * i);
-      xi = IO<DT>::ld(KR, row * skr + 2 * i + 1);
-      dr_ = IO<DT>::ld(KR, (row + half) * skr + 2 * i);
-      di = IO<DT>::ld(KR, (row + half) * skr + 2 * i + 1);
+      xx = IO<DT>::ld2(KR, row * skr + 2 * i);
+      dd = IO<DT>::ld2(KR, (row + half) * skr + 2 * i);
     }
+    xr = xx.x;
+    xi = xx.y;
+    dr_ = dd.x;
+    di = dd.y;
     void* Y = sel == 2 ? Q : K;
     void* DY = sel == 2 ? DQ : DK;
-    IO<DT>::st(Y, dst + DN + 2 * i, xr * c - xi * sn);
-    IO<DT>::st(Y, dst + DN + 2 * i + 1, xr * sn + xi * c);
-    IO<DT>::st(DY, dst + DN + 2 * i, dr_ * c - di * sn);
-    IO<DT>::st(DY, dst + DN + 2 * i + 1, dr_ * sn + di * c);
+    IO<DT>::st2(Y, dst + DN + 2 * i, xr * c - xi * sn, xr * sn + xi * c);
+    IO<DT>::st2(DY, dst + DN + 2 * i, dr_ * c - di * sn, dr_ * sn + di * c);
   }
   // v: straight copy of the dv band (lane l = channel l)
   IO<DT>::st(V, dst + l, IO<DT>::ld(KVB, krow + h * kvw + DN + l));
@@ -187,12 +205,13 @@ __global__ __launch_bounds__(256) void out_gate_kernel(const float* __restrict__
                                                       const int32_t* __restrict__ pos,
                                                       const void* __restrict__ Z, int B, int S,
                                                       int H, void* __restrict__ OUT) {
-  const int64_t unit = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  const int unit = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
   const int64_t half = (int64_t)B * S;
   if (unit >= half * H) return;
-  const int h = (int)(unit % H);
-  const int64_t row = unit / H;
-  const int b = (int)(row / S), s = (int)(row % S);
+  const int h = __builtin_amdgcn_readfirstlane(unit % H);
+  const int64_t row = __builtin_amdgcn_readfirstlane(unit / H);
+  const int b = __builtin_amdgcn_readfirstlane((int)row / S);
+  const int s = (int)row - b * S;
   const int l = threadIdx.x & 63;
   const int64_t src = (((int64_t)b * H + h) * S + (pos ? pos[s] : s)) * 64 + l;
   // the op's fp32 output is first stored as 16-bit (the reference's attention buffer)
@@ -277,8 +296,12 @@ extern "C" int sla2h_mla_qkv_prep(const void* qb, const void* kvb, const void* k
   SLA2H_CHECK_ARG(dn == 32 && dr == 32 && dv == 64 && skr >= dr);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   SLA2H_CHECK_ARG(B > 0 && S > 0 && H > 0);
+  // channel pairs move as 32-bit words: even strides, 4-byte aligned rows
+  auto al4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3) == 0; };
+  SLA2H_CHECK_ARG(skr % 2 == 0 && al4(qb) && al4(kvb) && al4(kr) && al4(q) && al4(dq) &&
+                  al4(k) && al4(dk));
   const int64_t units = (int64_t)B * S * H;
-  SLA2H_CHECK_ARG((units + 3) / 4 < (1ll << 31));
+  SLA2H_CHECK_ARG(units + 3 < (1ll << 31));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned grid = (unsigned)((units + 3) / 4);
   if (dtype == SLA2H_DTYPE_F16)
@@ -295,7 +318,7 @@ extern "C" int sla2h_mla_out_gate(const float* o, const float* dout, const int32
   SLA2H_CHECK_ARG(dv == 64 && B > 0 && S > 0 && H > 0);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   const int64_t units = (int64_t)B * S * H;
-  SLA2H_CHECK_ARG((units + 3) / 4 < (1ll << 31));
+  SLA2H_CHECK_ARG(units + 3 < (1ll << 31));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned grid = (unsigned)((units + 3) / 4);
   if (dtype == SLA2H_DTYPE_F16)

@@ -554,7 +554,15 @@ __global__ __launch_bounds__(64) void pool_blocks_kernel(const uint16_t* __restr
   const int cnt = (int)((L - r0) < blk ? (L - r0) : blk);
   const uint16_t* src = x + ((int64_t)bh * L + r0) * kTile + d;
   float acc = 0.f;
-  for (int rr = 0; rr < cnt; ++rr) acc = acc + T16::to_f32(src[(int64_t)rr * kTile]);
+  int rr = 0;
+  for (; rr + 16 <= cnt; rr += 16) {  // 16 loads in flight, then the adds in row order
+    float xv[16];
+#pragma unroll
+    for (int u = 0; u < 16; ++u) xv[u] = T16::to_f32(src[(int64_t)(rr + u) * kTile]);
+#pragma unroll
+    for (int u = 0; u < 16; ++u) acc = acc + xv[u];
+  }
+  for (; rr < cnt; ++rr) acc = acc + T16::to_f32(src[(int64_t)rr * kTile]);
   vec[d] = acc / (float)cnt;
   __syncthreads();
   float outv = vec[d];

@@ -147,9 +147,9 @@ def attn_sublayer_jvp(h, dh, p, w16, cos, sin, eps, stage_events=None):
     _lib.check(_lib.load().sla2h_mla_out_gate(
         o.data_ptr(), do.data_ptr(), ops._ptr(pos), ops._ptr(z), 0, B, S, H, dv,
         gated.data_ptr(), _stream(dev)), "sla2h_mla_out_gate")
-    proj = F.linear(gated, w16["w_out"]).float().view(2 * B, S, D)
-    g = _vec(p["g_attn"], dev)
-    out = proj[:B] * g, proj[B:] * g
+    # fp16 GEMM output times the fp32 gain: one kernel (fp32 by type promotion)
+    proj = F.linear(gated, w16["w_out"]).view(2 * B, S, D) * _vec(p["g_attn"], dev)
+    out = proj[:B], proj[B:]
     rec(2)
     return out
 
@@ -171,9 +171,8 @@ def mlp_sublayer_jvp(h, dh, p, w16, eps):
     act = torch.empty(M, f, device=dev, dtype=_FP16)
     _lib.check(_lib.load().sla2h_situ_jvp(gu.data_ptr(), half, f, float(p.get("situ_beta", 1.0)),
                                           0, act.data_ptr(), _stream(dev)), "sla2h_situ_jvp")
-    dwn = F.linear(act, w16["w_down"]).float().view(2 * B, S, D)
-    g = _vec(p["g_mlp"], dev)
-    return dwn[:B] * g, dwn[B:] * g
+    dwn = F.linear(act, w16["w_down"]).view(2 * B, S, D) * _vec(p["g_mlp"], dev)
+    return dwn[:B], dwn[B:]
 
 
 def pack_block(block, tile_major=False):
