@@ -129,10 +129,44 @@ __global__ __launch_bounds__(256) void rmsnorm_jvp_kernel(const void* __restrict
 }
 
 // ---------------------------------------------------------------------------
-// One wave per (token row, head); dn = dr = 32, dv = 64 (qk head dim 64).
-// Lane l: nope channel pair (l & 15) * 2 .. +1 for the query (lanes 0-15),
-// the key (lanes 16-31); rope pair i = l & 15 for the query (lanes 32-47) and
-// the key (lanes 48-63).  v: every lane copies one channel.
+// 8 16-bit values <-> one 16-byte word (element 2j in the low half of word j)
+template <int DT>
+struct T16Of;
+template <>
+struct T16Of<SLA2H_DTYPE_F16> {
+  using T = F16;
+};
+template <>
+struct T16Of<SLA2H_DTYPE_BF16> {
+  using T = BF16;
+};
+template <int DT>
+__device__ inline void unpack8(const uint4& u, float (&x)[8]) {
+  using T = typename T16Of<DT>::T;
+  const uint32_t w[4] = {u.x, u.y, u.z, u.w};
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    x[2 * j] = T::to_f32((uint16_t)(w[j] & 0xffff));
+    x[2 * j + 1] = T::to_f32((uint16_t)(w[j] >> 16));
+  }
+}
+template <int DT>
+__device__ inline uint4 pack8(const float (&x)[8]) {
+  using T = typename T16Of<DT>::T;
+  uint32_t w[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j)
+    w[j] = (uint32_t)T::from_f32(x[2 * j]) | ((uint32_t)T::from_f32(x[2 * j + 1]) << 16);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
+// One wave per token row (b, s), heads in groups of 8: lane l = 8 hh + c works
+// on 16-byte chunk c (channels 8c..8c+7) of head 8 g + hh for every operand,
+// so each load and store of the wave is one 16-byte access per lane.
+// dn = dr = 32, dv = 64 (qk head dim 64): chunks 0-3 are the nope band
+// (RMSNorm over the head's four nope chunks: xor 1, 2 in the lane group),
+// chunks 4-7 the rope band (q's own, k's shared band from KR, rotated by
+// (cos, sin)[s][4 (c - 4) + j] on pair j); v is a copy of the dv band.
 template <int DT>
 __global__ __launch_bounds__(256) void qkv_prep_kernel(
     const void* __restrict__ QB, const void* __restrict__ KVB, const void* __restrict__ KR,
@@ -140,92 +174,142 @@ __global__ __launch_bounds__(256) void qkv_prep_kernel(
     const float* __restrict__ cosb, const float* __restrict__ sinb, const int32_t* __restrict__ pos,
     int B, int S, int H, float eps, void* __restrict__ Q, void* __restrict__ DQ,
     void* __restrict__ K, void* __restrict__ DK, void* __restrict__ V, void* __restrict__ DV) {
-  constexpr int DN = 32, DR2 = 16, HD = 64, DVW = 64;
-  // (row, head) of this wave, uniform: 32-bit index math pinned to SGPRs
-  const int unit = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+  constexpr int DN = 32, DR2 = 16, HD = 64, KVW = 96;
+  const int row = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
   const int64_t half = (int64_t)B * S;
-  if (unit >= half * H) return;
-  const int h = __builtin_amdgcn_readfirstlane(unit % H);
-  const int row = __builtin_amdgcn_readfirstlane(unit / H);  // primal token row b*S + s
+  if (row >= half) return;
   const int b = __builtin_amdgcn_readfirstlane(row / S);
   const int s = row - b * S;
-  const int l = threadIdx.x & 63;
-  const int i = l & 15;
-  const int64_t dst = (((int64_t)b * H + h) * S + (pos ? pos[s] : s)) * HD;  // (B,H,L,64) row
-  const int64_t qrow = row * (H * HD), qrow_t = (row + half) * (H * HD);
-  const int64_t kvw = DN + DVW;
-  const int64_t krow = row * (H * kvw), krow_t = (row + half) * (H * kvw);
-  const int sel = l >> 4;  // 0 q nope, 1 k nope, 2 q rope, 3 k rope
-  if (sel < 2) {
-    const void* src = sel == 0 ? QB : KVB;
-    const int64_t base = sel == 0 ? qrow + h * HD : krow + h * kvw;
-    const int64_t base_t = sel == 0 ? qrow_t + h * HD : krow_t + h * kvw;
-    const float2 xx = IO<DT>::ld2(src, base + 2 * i), dd = IO<DT>::ld2(src, base_t + 2 * i);
-    const float x0 = xx.x, x1 = xx.y, d0 = dd.x, d1 = dd.y;
-    const float ss = sum16(x0 * x0 + x1 * x1);
-    const float sxd = sum16(x0 * d0 + x1 * d1);
-    const float inv_r = 1.f / sqrtf(ss / (float)DN + eps);
-    const float k3 = (sxd / (float)DN) * inv_r * inv_r * inv_r;
-    const float* w = sel == 0 ? wqn : wkn;
-    void* Y = sel == 0 ? Q : K;
-    void* DY = sel == 0 ? DQ : DK;
-    IO<DT>::st2(Y, dst + 2 * i, w[2 * i] * x0 * inv_r, w[2 * i + 1] * x1 * inv_r);
-    IO<DT>::st2(DY, dst + 2 * i, w[2 * i] * (d0 * inv_r - x0 * k3),
-                w[2 * i + 1] * (d1 * inv_r - x1 * k3));
-  } else {
-    const float c = cosb[(int64_t)s * DR2 + i], sn = sinb[(int64_t)s * DR2 + i];
-    float xr, xi, dr_, di;
-    float2 xx, dd;
-    if (sel == 2) {
-      xx = IO<DT>::ld2(QB, qrow + h * HD + DN + 2 * i);
-      dd = IO<DT>::ld2(QB, qrow_t + h * HD + DN + 2 * i);
-    } else {
-      xx = IO<DT>::ld2(KR, row * skr + 2 * i);
-      dd = IO<DT>::ld2(KR, (row + half) * skr + 2 * i);
+  const int l = threadIdx.x & 63, hh = l >> 3, c = l & 7;
+  const bool nope = c < 4;
+  const int sd = pos ? pos[s] : s;
+  const uint16_t* qb = static_cast<const uint16_t*>(QB);
+  const uint16_t* kvb = static_cast<const uint16_t*>(KVB);
+  const uint16_t* kr = static_cast<const uint16_t*>(KR);
+  auto ld16 = [](const uint16_t* p, int64_t i) { return *reinterpret_cast<const uint4*>(p + i); };
+  auto st16 = [](void* p, int64_t i, const uint4& v) {
+    *reinterpret_cast<uint4*>(static_cast<uint16_t*>(p) + i) = v;
+  };
+  // the rotation factors of this lane's four rope pairs
+  float cs[4], sn[4];
+  if (!nope) {
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      cs[j] = cosb[(int64_t)s * DR2 + 4 * (c - 4) + j];
+      sn[j] = sinb[(int64_t)s * DR2 + 4 * (c - 4) + j];
     }
-    xr = xx.x;
-    xi = xx.y;
-    dr_ = dd.x;
-    di = dd.y;
-    void* Y = sel == 2 ? Q : K;
-    void* DY = sel == 2 ? DQ : DK;
-    IO<DT>::st2(Y, dst + DN + 2 * i, xr * c - xi * sn, xr * sn + xi * c);
-    IO<DT>::st2(DY, dst + DN + 2 * i, dr_ * c - di * sn, dr_ * sn + di * c);
   }
-  // v: straight copy of the dv band (lane l = channel l)
-  IO<DT>::st(V, dst + l, IO<DT>::ld(KVB, krow + h * kvw + DN + l));
-  IO<DT>::st(DV, dst + l, IO<DT>::ld(KVB, krow_t + h * kvw + DN + l));
+  // nope: y = w x / r, dy = w (dx / r - x mean(x dx) / r^3) over the head's 32
+  // channels; rope: rotate (x, dx) pairwise
+  auto head = [&](const uint4& ux, const uint4& ud, const float* w, void* Y, void* DY,
+                  int64_t dst) {
+    float x[8], d[8], y[8], dy[8];
+    unpack8<DT>(ux, x);
+    unpack8<DT>(ud, d);
+    float ss = 0.f, sxd = 0.f;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      ss += x[j] * x[j];
+      sxd += x[j] * d[j];
+    }
+    ss += __shfl_xor(ss, 1, 64);
+    ss += __shfl_xor(ss, 2, 64);
+    sxd += __shfl_xor(sxd, 1, 64);
+    sxd += __shfl_xor(sxd, 2, 64);
+    if (nope) {
+      const float inv_r = 1.f / sqrtf(ss / (float)DN + eps);
+      const float k3 = (sxd / (float)DN) * inv_r * inv_r * inv_r;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float wj = w[8 * c + j];
+        y[j] = wj * x[j] * inv_r;
+        dy[j] = wj * (d[j] * inv_r - x[j] * k3);
+      }
+    } else {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        y[2 * j] = x[2 * j] * cs[j] - x[2 * j + 1] * sn[j];
+        y[2 * j + 1] = x[2 * j] * sn[j] + x[2 * j + 1] * cs[j];
+        dy[2 * j] = d[2 * j] * cs[j] - d[2 * j + 1] * sn[j];
+        dy[2 * j + 1] = d[2 * j] * sn[j] + d[2 * j + 1] * cs[j];
+      }
+    }
+    st16(Y, dst, pack8<DT>(y));
+    st16(DY, dst, pack8<DT>(dy));
+  };
+  for (int g0 = 0; g0 < H; g0 += 8) {
+    const int h = g0 + hh;
+    if (h >= H) continue;
+    const int64_t dst = (((int64_t)b * H + h) * S + sd) * HD + 8 * c;  // (B,H,L,64) chunk
+    const int64_t qo = (int64_t)row * (H * HD) + h * HD + 8 * c;
+    head(ld16(qb, qo), ld16(qb, qo + half * (H * HD)), wqn, Q, DQ, dst);
+    const int64_t ko = (int64_t)row * (H * KVW) + h * KVW;
+    const int64_t kt = half * (H * KVW);
+    // k: the head's nope chunks from KVB, the shared rope band from KR
+    const uint16_t* kx = nope ? kvb + ko + 8 * c : kr + (int64_t)row * skr + 8 * (c - 4);
+    const int64_t kd = nope ? kt : half * skr;
+    head(ld16(kx, 0), ld16(kx, kd), wkn, K, DK, dst);
+    // v: the dv band (64 channels) of this head, chunk c
+    st16(V, dst, ld16(kvb, ko + DN + 8 * c));
+    st16(DV, dst, ld16(kvb, ko + kt + DN + 8 * c));
+  }
 }
 
 // ---------------------------------------------------------------------------
-// One wave per (token row, head): out rows (2BS, H*64) stacked [primal; tangent].
+// One wave per token row, heads in groups of 8 as above: lane 8 hh + c owns
+// channels 8c..8c+7 of head 8 g + hh; out rows (2BS, H*64) stacked
+// [primal; tangent].
 template <int DT>
 __global__ __launch_bounds__(256) void out_gate_kernel(const float* __restrict__ O,
                                                       const float* __restrict__ DO,
                                                       const int32_t* __restrict__ pos,
                                                       const void* __restrict__ Z, int B, int S,
                                                       int H, void* __restrict__ OUT) {
-  const int unit = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
+  const int row = __builtin_amdgcn_readfirstlane((int)blockIdx.x * 4 + (int)(threadIdx.x >> 6));
   const int64_t half = (int64_t)B * S;
-  if (unit >= half * H) return;
-  const int h = __builtin_amdgcn_readfirstlane(unit % H);
-  const int64_t row = __builtin_amdgcn_readfirstlane(unit / H);
-  const int b = __builtin_amdgcn_readfirstlane((int)row / S);
-  const int s = (int)row - b * S;
-  const int l = threadIdx.x & 63;
-  const int64_t src = (((int64_t)b * H + h) * S + (pos ? pos[s] : s)) * 64 + l;
-  // the op's fp32 output is first stored as 16-bit (the reference's attention buffer)
-  const float a = IO<DT>::rt(O[src]), da = IO<DT>::rt(DO[src]);
-  const int64_t op = row * (H * 64) + h * 64 + l, opt = (row + half) * (H * 64) + h * 64 + l;
-  if (Z == nullptr) {
-    IO<DT>::st(OUT, op, a);
-    IO<DT>::st(OUT, opt, da);
-    return;
+  if (row >= half) return;
+  const int b = __builtin_amdgcn_readfirstlane(row / S);
+  const int s = row - b * S;
+  const int l = threadIdx.x & 63, hh = l >> 3, c = l & 7;
+  const int sd = pos ? pos[s] : s;
+  const uint16_t* z16 = static_cast<const uint16_t*>(Z);
+  uint16_t* o16 = static_cast<uint16_t*>(OUT);
+  for (int g0 = 0; g0 < H; g0 += 8) {
+    const int h = g0 + hh;
+    if (h >= H) continue;
+    const int64_t src = (((int64_t)b * H + h) * S + sd) * 64 + 8 * c;
+    const int64_t op = (int64_t)row * (H * 64) + h * 64 + 8 * c;
+    const int64_t opt = op + half * (H * 64);
+    float a[8], da[8];
+#pragma unroll
+    for (int p = 0; p < 2; ++p) {
+      const float4 u = reinterpret_cast<const float4*>(O + src)[p];
+      const float4 du = reinterpret_cast<const float4*>(DO + src)[p];
+      // the op's fp32 output is first stored as 16-bit (the reference's attention buffer)
+      a[4 * p] = IO<DT>::rt(u.x);
+      a[4 * p + 1] = IO<DT>::rt(u.y);
+      a[4 * p + 2] = IO<DT>::rt(u.z);
+      a[4 * p + 3] = IO<DT>::rt(u.w);
+      da[4 * p] = IO<DT>::rt(du.x);
+      da[4 * p + 1] = IO<DT>::rt(du.y);
+      da[4 * p + 2] = IO<DT>::rt(du.z);
+      da[4 * p + 3] = IO<DT>::rt(du.w);
+    }
+    if (Z != nullptr) {
+      float zz[8], dz[8];
+      unpack8<DT>(*reinterpret_cast<const uint4*>(z16 + op), zz);
+      unpack8<DT>(*reinterpret_cast<const uint4*>(z16 + opt), dz);
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const float sg = sigmoidf_(zz[j]);
+        const float ga = a[j] * sg;
+        da[j] = da[j] * sg + a[j] * sg * (1.f - sg) * dz[j];
+        a[j] = ga;
+      }
+    }
+    *reinterpret_cast<uint4*>(o16 + op) = pack8<DT>(a);
+    *reinterpret_cast<uint4*>(o16 + opt) = pack8<DT>(da);
   }
-  const float z = IO<DT>::ld(Z, op), dz = IO<DT>::ld(Z, opt);
-  const float sg = sigmoidf_(z);
-  IO<DT>::st(OUT, op, a * sg);
-  IO<DT>::st(OUT, opt, da * sg + a * sg * (1.f - sg) * dz);
 }
 
 // ---------------------------------------------------------------------------
@@ -296,11 +380,11 @@ extern "C" int sla2h_mla_qkv_prep(const void* qb, const void* kvb, const void* k
   SLA2H_CHECK_ARG(dn == 32 && dr == 32 && dv == 64 && skr >= dr);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   SLA2H_CHECK_ARG(B > 0 && S > 0 && H > 0);
-  // channel pairs move as 32-bit words: even strides, 4-byte aligned rows
-  auto al4 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 3) == 0; };
-  SLA2H_CHECK_ARG(skr % 2 == 0 && al4(qb) && al4(kvb) && al4(kr) && al4(q) && al4(dq) &&
-                  al4(k) && al4(dk));
-  const int64_t units = (int64_t)B * S * H;
+  // 16-byte chunks: row strides a multiple of 8 elements, 16-byte aligned bases
+  auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  SLA2H_CHECK_ARG(skr % 8 == 0 && al16(qb) && al16(kvb) && al16(kr) && al16(q) && al16(dq) &&
+                  al16(k) && al16(dk) && al16(v) && al16(dv_out));
+  const int64_t units = (int64_t)B * S;  // one wave per token row
   SLA2H_CHECK_ARG(units + 3 < (1ll << 31));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned grid = (unsigned)((units + 3) / 4);
@@ -317,7 +401,7 @@ extern "C" int sla2h_mla_out_gate(const float* o, const float* dout, const int32
   SLA2H_CHECK_ARG(o && dout && out);
   SLA2H_CHECK_ARG(dv == 64 && B > 0 && S > 0 && H > 0);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
-  const int64_t units = (int64_t)B * S * H;
+  const int64_t units = (int64_t)B * S;  // one wave per token row
   SLA2H_CHECK_ARG(units + 3 < (1ll << 31));
   hipStream_t st = static_cast<hipStream_t>(stream);
   const unsigned grid = (unsigned)((units + 3) / 4);
