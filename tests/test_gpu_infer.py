@@ -206,3 +206,29 @@ def test_sla2_int8_training_forward_and_backward(bq):
         print(f"  {name} max {max_abs(got, want):.2e} rel {rel_l2(got, want):.2e}", flush=True)
         assert rel_l2(got, want) < TOL_REL and max_abs(got, want) < TOL_MAX * max(1, want.abs().max())
     assert rel_l2(grads[3], ref["d_alpha"]) < 1e-2
+
+
+@pytest.mark.parametrize("L,topk,bq", [(40, 1.0, 64), (256, 0.01, 128), (1024, 1.0, 128),
+                                       (640, 0.5, 256)])
+@pytest.mark.parametrize("int8", [True, False])
+def test_sla2_infer_edge_shapes(L, topk, bq, int8):
+    """One ragged block (L = 40), T = 1, every key block routed (an empty
+    complement: the linear branch is 0 / eps), three batch rows."""
+    from imfvideo_amd import ops
+    say("sla2_infer edge L", L, "topk", topk, "bq", bq, "int8", int8)
+    H = 2
+    q, k, v = _inputs(140 + L, 3, H, L, torch.bfloat16)
+    mq = -(-L // bq)
+    lut, T = O.route_1d(q.float(), k.float(), topk, bq)
+    g = torch.Generator().manual_seed(8)
+    alpha = 0.1 + 0.8 * torch.rand(H, mq, generator=g)
+    o = ops.sla2_infer(cuda(q), cuda(k), cuda(v), cuda(alpha), cuda(torch.as_tensor(lut)), bq,
+                       use_int8=int8)
+    torch.cuda.synchronize()
+    ref = O.infer_1d(q.float(), k.float(), v.float(), alpha, lut, bq, int8=int8,
+                     t16=torch.bfloat16)
+    got = o.cpu().float()
+    print(f"  T {T} o max {max_abs(got, ref['o']):.2e} rel {rel_l2(got, ref['o']):.2e}",
+          flush=True)
+    assert torch.isfinite(got).all()
+    assert max_abs(got, ref["o"]) < TOL_MAX and rel_l2(got, ref["o"]) < TOL_REL
