@@ -18,6 +18,7 @@
 #include "common.h"
 
 #include <climits>
+#include <type_traits>
 
 namespace sla2h {
 
@@ -138,7 +139,10 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
   for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_i = -INFINITY, l_i = 0.f;  // l_i: this lane's 16 keys per tile, reduced at the end
 
-  auto tile = [&](const Frags& f, int j) {
+  // MASK: the tile reaches past L (its keys there are masked); other tiles
+  // skip the per-key test
+  auto tile = [&](const Frags& f, int j, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
     const float sqk = sq * __builtin_bit_cast(float, __builtin_amdgcn_readfirstlane(tiles[j].y));
     const int64_t key0 = (int64_t)n * kT + 4 * g;
@@ -150,7 +154,7 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float x = ((float)si[i] * sqk) * a.c2;
-        if (key0 + 16 * kb + i >= L) x = -INFINITY;
+        if (MASK && key0 + 16 * kb + i >= L) x = -INFINITY;
         s[4 * kb + i] = x;
         lm = fmaxf(lm, x);
       }
@@ -172,6 +176,14 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
       pk[kb] = wd;
     }
     l_i = l_i * alpha + ls;
+    // the exact maximum moves on few tiles: where no lane's does (alpha == 1
+    // everywhere) the rescale acc * alpha is the identity and is skipped
+    if (__builtin_amdgcn_ballot_w64(mn != m_i) != 0) {
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[ct][i] = acc[ct][i] * alpha;
+    }
     m_i = mn;
     const i32x4 p8 = i32x4{(int)pk[0], (int)pk[1], (int)pk[2], (int)pk[3]};
     const float sv = vsc[j];
@@ -179,8 +191,14 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
     for (int ct = 0; ct < 4; ++ct) {
       const i32x4 pv = mfma_i8_16x16x64(f.v[ct], p8, i32x4{0, 0, 0, 0});
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[ct][i] = fmaf((float)pv[i], sv, acc[ct][i] * alpha);
+      for (int i = 0; i < 4; ++i) acc[ct][i] = fmaf((float)pv[i], sv, acc[ct][i]);
     }
+  };
+  auto tile_any = [&](const Frags& f, int j) {
+    if ((int64_t)(__builtin_amdgcn_readfirstlane(tiles[j].x) + 1) * kT > L)
+      tile(f, j, std::true_type{});
+    else
+      tile(f, j, std::false_type{});
   };
 
   Frags fa, fb;
@@ -188,11 +206,11 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
   int j = 0;
   for (; j + 1 < J; j += 2) {
     load(j + 1, fb);
-    tile(fa, j);
+    tile_any(fa, j);
     load(j + 2 < J ? j + 2 : J - 1, fa);
-    tile(fb, j + 1);
+    tile_any(fb, j + 1);
   }
-  if (j < J) tile(fa, j);
+  if (j < J) tile_any(fa, j);
 
   const float lt = sum_over_groups(l_i);
   const float rl = 1.f / lt;
@@ -319,7 +337,9 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd16_kernel(Fwd16Args a) {
   for (int ct = 0; ct < 4; ++ct) acc[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
   float m_i = -INFINITY, l_i = 0.f;
 
-  auto tile = [&](const Frags& f, int j) {
+  // MASK as in sparse_fwd_qat_kernel: only a tile reaching past L tests keys
+  auto tile = [&](const Frags& f, int j, auto mask_tag) {
+    constexpr bool MASK = decltype(mask_tag)::value;
     const int n = __builtin_amdgcn_readfirstlane(tiles[j]);
     const int64_t key0 = (int64_t)n * kT + 4 * g;
     float s[16];
@@ -331,7 +351,7 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd16_kernel(Fwd16Args a) {
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         float x = sc[i] * a.c;
-        if (key0 + 16 * kb + i >= L) x = -INFINITY;
+        if (MASK && key0 + 16 * kb + i >= L) x = -INFINITY;
         s[4 * kb + i] = x;
         lm = fmaxf(lm, x);
       }
@@ -346,9 +366,12 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd16_kernel(Fwd16Args a) {
       ls += s[i];
     }
     l_i = l_i * alpha + ls;
-    m_i = mn;
+    // alpha == 1 on every lane (no maximum moved) leaves acc unchanged
+    if (__builtin_amdgcn_ballot_w64(mn != m_i) != 0) {
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct) acc[ct] *= alpha;
+      for (int ct = 0; ct < 4; ++ct) acc[ct] *= alpha;
+    }
+    m_i = mn;
 #pragma unroll
     for (int pp = 0; pp < 2; ++pp) {
       const u32x4 pb = u32x4{pack_pair<T16>(s[8 * pp], s[8 * pp + 1]),
@@ -363,6 +386,12 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd16_kernel(Fwd16Args a) {
       }
     }
   };
+  auto tile_any = [&](const Frags& f, int j) {
+    if ((int64_t)(__builtin_amdgcn_readfirstlane(tiles[j]) + 1) * kT > L)
+      tile(f, j, std::true_type{});
+    else
+      tile(f, j, std::false_type{});
+  };
 
   const int J = a.T;
   Frags fa, fb;
@@ -370,11 +399,11 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd16_kernel(Fwd16Args a) {
   int j = 0;
   for (; j + 1 < J; j += 2) {
     load(j + 1, fb);
-    tile(fa, j);
+    tile_any(fa, j);
     load(j + 2 < J ? j + 2 : J - 1, fa);
-    tile(fb, j + 1);
+    tile_any(fb, j + 1);
   }
-  if (j < J) tile(fa, j);
+  if (j < J) tile_any(fa, j);
 
   const float lt = sum_over_groups(l_i);
   const float rl = 1.f / lt;
