@@ -248,6 +248,10 @@ template <typename T16>
 __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
   __shared__ int tiles[kMaxJ];
   __shared__ __align__(16) f32x4 mb[2][4][2][4][64];  // [round-robin][src wave][qb sel][ct][lane]
+  // 16-bit complement state H16[d][e] of this query block and its z, staged
+  // while the prologue's other loads are in flight
+  __shared__ __align__(16) uint16_t h16s[kT][kT + 8];
+  __shared__ float zcs[kT];
 
   const int logical = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
   if (logical >= a.nwork) return;
@@ -283,6 +287,30 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
     lse_r[qb] = ok ? a.lse[base + row] : INFINITY;
     del_r[qb] = ok ? a.delta[base + row] : 0.f;
   }
+  const unsigned char* rec = a.comp + ((int64_t)bh * a.Mq + mq) * kRecBytes;
+  {  // H16 = round16(Hc + (round16(Hall) - Hall)); thread: row tid / 4, 16 columns
+    const int d = tid >> 2, c0 = (tid & 3) * 16;
+    const f32x4* hc = reinterpret_cast<const f32x4*>(rec + kRecH) + (d * kT + c0) / 4;
+    const f32x4* ha = reinterpret_cast<const f32x4*>(a.Hall + (int64_t)bh * kT * kT) + (d * kT + c0) / 4;
+    f32x4 hx[4], tx[4];
+#pragma unroll
+    for (int cq = 0; cq < 4; ++cq) {
+      hx[cq] = hc[cq];
+      tx[cq] = ha[cq];
+    }
+    uint32_t wd[8];
+#pragma unroll
+    for (int cq = 0; cq < 4; ++cq) {
+      float hv[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hv[i] = hx[cq][i] + (r16<T16>(tx[cq][i]) - tx[cq][i]);
+      wd[2 * cq] = pack_pair<T16>(hv[0], hv[1]);
+      wd[2 * cq + 1] = pack_pair<T16>(hv[2], hv[3]);
+    }
+    *reinterpret_cast<uint4*>(&h16s[d][c0]) = make_uint4(wd[0], wd[1], wd[2], wd[3]);
+    *reinterpret_cast<uint4*>(&h16s[d][c0 + 8]) = make_uint4(wd[4], wd[5], wd[6], wd[7]);
+    if (tid < kT) zcs[tid] = reinterpret_cast<const float*>(rec + kRecZ)[tid];
+  }
   __syncthreads();
 
   const auto rk = make_rsrc(a.k + base * kT, L * kT * 2);  // key rows past L read as 0
@@ -313,9 +341,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) acc[qb][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
+  // Keys past L need no mask here: their K and V rows read as zero (buffer
+  // range check) and their K^T fragments are zero-filled, so dp = 0, ds stays
+  // finite (p <= 2^4) and K^T ds adds exactly zero to dq.
   auto tile = [&](const Frags& f, int j) {
-    const int n = __builtin_amdgcn_readfirstlane(tiles[j]);
-    const int64_t key0 = (int64_t)n * kT + 16 * w + 4 * g;
 #pragma unroll
     for (int qb = 0; qb < 4; ++qb) {
       f32x4 sc = mfma_16x16x32<T16>(f.k[0], qf[qb][0], f32x4{0.f, 0.f, 0.f, 0.f});
@@ -325,8 +354,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
       float ds[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float p = fast_exp2(fminf(sc[i] * a.c - lse_r[qb], 4.f));
-        if (key0 + i >= L) p = 0.f;
+        const float p = fast_exp2(fminf(sc[i] * a.c - lse_r[qb], 4.f));
         ds[i] = sat(p * (dp[i] - del_r[qb]));
       }
       const u32x2 dsp = pack4<T16>(ds[0], ds[1], ds[2], ds[3]);
@@ -367,10 +395,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
   // epilogue: query row 64m + 16w + r, channels 16ct + 4g + i
   const int64_t row = (int64_t)m * kT + 16 * w + r;
   const bool ok = row < L;
-  const unsigned char* rec = a.comp + ((int64_t)bh * a.Mq + mq) * kRecBytes;
-  const float* Hc = reinterpret_cast<const float*>(rec + kRecH);
-  const float* zc = reinterpret_cast<const float*>(rec + kRecZ);
-  const float* Ha = a.Hall + (int64_t)bh * kT * kT;
   u32x4 gb[2];
 #pragma unroll
   for (int ks = 0; ks < 2; ++ks)
@@ -384,23 +408,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
     f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      // A: H16[d = 16ct + r][e = 32ks + 8g .. +7] = round16(Hc + (round16(Hall) - Hall))
-      const int e0 = (16 * ct + r) * kT + 32 * ks + 8 * g;
-      const f32x4 h0 = *reinterpret_cast<const f32x4*>(Hc + e0);
-      const f32x4 h1 = *reinterpret_cast<const f32x4*>(Hc + e0 + 4);
-      const f32x4 t0 = *reinterpret_cast<const f32x4*>(Ha + e0);
-      const f32x4 t1 = *reinterpret_cast<const f32x4*>(Ha + e0 + 4);
-      float hv[8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        hv[i] = h0[i] + (r16<T16>(t0[i]) - t0[i]);
-        hv[4 + i] = h1[i] + (r16<T16>(t1[i]) - t1[i]);
-      }
-      const u32x4 av = u32x4{pack_pair<T16>(hv[0], hv[1]), pack_pair<T16>(hv[2], hv[3]),
-                             pack_pair<T16>(hv[4], hv[5]), pack_pair<T16>(hv[6], hv[7])};
+      // A: H16[d = 16ct + r][e = 32ks + 8g .. +7]
+      const u32x4 av = *reinterpret_cast<const u32x4*>(&h16s[16 * ct + r][32 * ks + 8 * g]);
       num = mfma_16x16x32<T16>(av, gb[ks], num);
     }
-    const f32x4 z = *reinterpret_cast<const f32x4*>(zc + 16 * ct + 4 * g);
+    const f32x4 z = *reinterpret_cast<const f32x4*>(&zcs[16 * ct + 4 * g]);
     const uint2 qv = ok ? *reinterpret_cast<const uint2*>(a.qphi + (base + row) * kT + 16 * ct + 4 * g)
                         : make_uint2(0, 0);
     const uint32_t qw[2] = {qv.x, qv.y};
@@ -511,7 +523,6 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
 
   const uint32_t* selrow = a.sel + ((int64_t)bh * a.Nb + n) * a.NCq;
   const int tfoff = (((w >> 1) * 64 + l) * 8 + 4 * (w & 1));  // 16-bit elements, + ct * 1024
-  const int64_t keyb = (int64_t)n * kT;
 
   for (int kc = 0; kc < a.NCq; ++kc) {
     uint32_t bits = __builtin_amdgcn_readfirstlane(selrow[kc]);
@@ -555,11 +566,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
           sc = mfma_16x16x32<T16>(qa[ks], kbv, sc);
           dp = mfma_16x16x32<T16>(da[ks], vbv, dp);
         }
-        const bool kok = keyb + 16 * kb + r < L;
+        // a key past L (zero K row, finite p) only feeds its own dk / dv
+        // column, which is never stored: no mask
         float p[4], ds[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          p[i] = kok ? fast_exp2(fminf(sc[i] * a.c - lse4[i], 4.f)) : 0.f;
+          p[i] = fast_exp2(fminf(sc[i] * a.c - lse4[i], 4.f));
           ds[i] = sat(p[i] * (dp[i] - del4[i]));
         }
         const u32x2 pp = pack4<T16>(p[0], p[1], p[2], p[3]);
