@@ -197,19 +197,24 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
     a.Pz[((int64_t)bh * a.Nb + blk) * kT + tid] = z;
   }
 
-  // transposed operand fragments of q, k, do_s
+  // transposed operand fragments of q, k, do_s: 16 x 16 x 16 A operands
+  // [channel 16ct + r][row 16w + 4g + e], 32 contiguous bytes per (w, lane)
+  // holding ct = 0..3, e = 0..3 (element ((w * 64 + lane) * 4 + ct) * 4 + e)
   uint16_t* tfs[3] = {a.qtf, a.ktf, a.dotf};
+  {
+    const int fw = tid >> 6, lane = tid & 63, gg = lane >> 4, rr = lane & 15;
 #pragma unroll
-  for (int x = 0; x < 3; ++x) {
+    for (int x = 0; x < 3; ++x) {
+      uint32_t v[8];
 #pragma unroll
-    for (int half = 0; half < 2; ++half) {
-      const int cc = tid + 256 * half;
-      const int ct = cc >> 7, p = (cc >> 6) & 1, lane = cc & 63, gg = lane >> 4, rr = lane & 15;
-      uint16_t v[8];
+      for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-      for (int s8 = 0; s8 < 8; ++s8) v[s8] = xs[x][16 * (2 * p + (s8 >> 2)) + 4 * gg + (s8 & 3)][16 * ct + rr];
-      *reinterpret_cast<uint4*>(tfs[x] + ((int64_t)bh * a.Nb + blk) * 4096 + cc * 8) =
-          make_uint4(pack2(v[0], v[1]), pack2(v[2], v[3]), pack2(v[4], v[5]), pack2(v[6], v[7]));
+        for (int e = 0; e < 2; ++e)
+          v[2 * ct + e] = pack2(xs[x][16 * fw + 4 * gg + 2 * e][16 * ct + rr],
+                                xs[x][16 * fw + 4 * gg + 2 * e + 1][16 * ct + rr]);
+      uint4* dst = reinterpret_cast<uint4*>(tfs[x] + ((int64_t)bh * a.Nb + blk) * 4096 + tid * 16);
+      dst[0] = make_uint4(v[0], v[1], v[2], v[3]);
+      dst[1] = make_uint4(v[4], v[5], v[6], v[7]);
     }
   }
 }
@@ -316,7 +321,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
   const auto rk = make_rsrc(a.k + base * kT, L * kT * 2);  // key rows past L read as 0
   const auto rv = make_rsrc(a.v + base * kT, L * kT * 2);
   const int rowoff = ((16 * w + r) * kT + 8 * g) * 2;
-  const int tfoff = (((w >> 1) * 64 + l) * 8 + 4 * (w & 1)) * 2;  // + ct * 2048 B
+  const int tfoff = (w * 64 + l) * 32;  // bytes: this lane's four K^T fragments
   const unsigned char* ktf = reinterpret_cast<const unsigned char*>(a.ktf) + (int64_t)bh * a.Nb * 8192;
 
   struct Frags {
@@ -330,9 +335,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
       f.k[ks] = buf_load16(rk, n * kT * kT * 2 + rowoff + 64 * ks, 0);
       f.v[ks] = buf_load16(rv, n * kT * kT * 2 + rowoff + 64 * ks, 0);
     }
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-      f.kt[ct] = *reinterpret_cast<const u32x2*>(ktf + (int64_t)n * 8192 + ct * 2048 + tfoff);
+    const u32x4 k01 = *reinterpret_cast<const u32x4*>(ktf + (int64_t)n * 8192 + tfoff);
+    const u32x4 k23 = *reinterpret_cast<const u32x4*>(ktf + (int64_t)n * 8192 + tfoff + 16);
+    f.kt[0] = u32x2{k01[0], k01[1]};
+    f.kt[1] = u32x2{k01[2], k01[3]};
+    f.kt[2] = u32x2{k23[0], k23[1]};
+    f.kt[3] = u32x2{k23[2], k23[3]};
   };
 
   f32x4 acc[4][4];
@@ -467,12 +475,36 @@ struct DkdvArgs {
   float c, scale;
 };
 
+// Prefetch region of one wave: 8 slots of 64 lanes x 16 B, then lse and delta
+// (64 dwords each).
+constexpr int kPfSlot = 1024;
+constexpr int kPfWave = 8 * kPfSlot + 2 * 256;
+constexpr int kSelLds = 128;  // mask words staged in LDS (query blocks 0 .. 4095)
+// s_waitcnt immediates (gfx9 encoding): vmcnt(0) alone, lgkmcnt(0) alone
+constexpr int kWaitVm0 = 0x0F70;
+constexpr int kWaitLgkm0 = 0xC07F;
+
+// Buffer loads straight into LDS: lane l's bytes land at dst + l * size.
+// dst must be wave-uniform; offsets past the resource's range write zeros.
+__device__ inline void lds_load16(__amdgpu_buffer_rsrc_t rs, void* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 16,
+                                           voff, 0, 0, 0);
+}
+__device__ inline void lds_load4(__amdgpu_buffer_rsrc_t rs, void* dst, int voff) {
+  __builtin_amdgcn_raw_ptr_buffer_load_lds(rs, (__attribute__((address_space(3))) void*)dst, 4,
+                                           voff, 0, 0, 0);
+}
+
 template <typename T16>
 __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
   __shared__ __align__(16) uint16_t kv[2][kT][kT + 8];   // K, V rows of the tile
   __shared__ __align__(16) uint16_t dhs[2][kT][kT + 8];  // dh16 [d][e], dh16^T [e][d]
-  __shared__ __align__(16) f32x4 mb[4][2][4][64];        // [src wave][kb sel][ct][lane]
+  // Per-wave prefetch regions of the query-block loop; after the loop the
+  // same bytes hold the partial-sum exchange mb[src wave][kb sel][ct][lane].
+  __shared__ __align__(16) unsigned char pool[4 * kPfWave];
   __shared__ float dzs[kT];
+  __shared__ uint32_t selsh[kSelLds];  // first words of this tile's query-block mask
+  auto mb = reinterpret_cast<f32x4 (*)[2][4][64]>(pool);
 
   const int logical = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
   if (logical >= a.nwork) return;
@@ -513,6 +545,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
     }
     if (tid < kT) dzs[tid] = -reinterpret_cast<const float*>(rec + kRecZ)[tid];
   }
+  const uint32_t* selrow = a.sel + ((int64_t)bh * a.Nb + n) * a.NCq;
+  for (int j = tid; j < a.NCq && j < kSelLds; j += 256) selsh[j] = selrow[j];
   __syncthreads();
 
   f32x4 dkT[4][4], dvT[4][4];  // [ct][kb]
@@ -521,41 +555,84 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) dkT[ct][kb] = dvT[ct][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-  const uint32_t* selrow = a.sel + ((int64_t)bh * a.Nb + n) * a.NCq;
-  const int tfoff = (((w >> 1) * 64 + l) * 8 + 4 * (w & 1));  // 16-bit elements, + ct * 1024
+  // Query blocks m routed to this tile, ascending.  The operands of block m
+  // (this wave's 16 query rows) are fetched one block ahead straight into the
+  // wave's LDS region (buffer loads to LDS: no registers held in flight):
+  // slots of 64 lanes x 16 B -- Q rows (ks 0, 1), do_s rows (ks 0, 1), the
+  // four Q^T fragments (2 slots), the four do_s^T fragments (2 slots) -- then
+  // 64 dwords of lse and 64 of delta (query 16w + (lane & 15)).  Rows past L
+  // read as zero: such a query then has p = 1 but zero Q, do_s, Q^T and
+  // do_s^T, so it adds exactly zero to dk and dv (as with a masked p).
+  const auto rq = make_rsrc(a.q + base * kT, L * kT * 2);
+  const auto rdo = make_rsrc(a.dos + base * kT, L * kT * 2);
+  const auto rqt = make_rsrc(a.qtf + (int64_t)bh * a.Nb * 4096, (int64_t)a.Nb * 8192);
+  const auto rdt = make_rsrc(a.dotf + (int64_t)bh * a.Nb * 4096, (int64_t)a.Nb * 8192);
+  const auto rls = make_rsrc(a.lse + base, L * 4);
+  const auto rdl = make_rsrc(a.delta + base, L * 4);
+  unsigned char* pf = pool + w * kPfWave;
+  auto prefetch = [&](int m) {
+    const int rowb = (m * kT + 16 * w + r) * (kT * 2) + 16 * g;
+    const int fo = m * 8192 + (w * 64 + l) * 32;
+    const int qo = (m * kT + 16 * w + (l & 15)) * 4;
+    lds_load16(rq, pf + 0 * kPfSlot, rowb);
+    lds_load16(rq, pf + 1 * kPfSlot, rowb + 64);
+    lds_load16(rdo, pf + 2 * kPfSlot, rowb);
+    lds_load16(rdo, pf + 3 * kPfSlot, rowb + 64);
+    lds_load16(rqt, pf + 4 * kPfSlot, fo);
+    lds_load16(rqt, pf + 5 * kPfSlot, fo + 16);
+    lds_load16(rdt, pf + 6 * kPfSlot, fo);
+    lds_load16(rdt, pf + 7 * kPfSlot, fo + 16);
+    lds_load4(rls, pf + 8 * kPfSlot, qo);
+    lds_load4(rdl, pf + 8 * kPfSlot + 256, qo);
+  };
+  int kc = 0;
+  uint32_t bits = 0u;
+  if (a.NCq > 0) bits = __builtin_amdgcn_readfirstlane(selsh[0]);
+  auto next_block = [&]() -> int {
+    while (bits == 0u) {
+      if (++kc >= a.NCq) return -1;
+      bits = __builtin_amdgcn_readfirstlane(kc < kSelLds ? selsh[kc] : selrow[kc]);
+    }
+    const int m = 32 * kc + __builtin_ctz(bits);
+    bits &= bits - 1u;
+    return m;
+  };
 
-  for (int kc = 0; kc < a.NCq; ++kc) {
-    uint32_t bits = __builtin_amdgcn_readfirstlane(selrow[kc]);
-    while (bits) {
-      const int m = 32 * kc + __builtin_ctz(bits);
-      bits &= bits - 1u;
-      const int64_t row = (int64_t)m * kT + 16 * w + r;  // A-operand row of this lane
-      const bool ok = row < L;
-      u32x4 qa[2], da[2];
+  int m = next_block();
+  if (m >= 0) prefetch(m);
+  while (m >= 0) {
+    __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's prefetch of block m has landed
+    u32x4 qa[2], da[2];
+    u32x2 qT[4], dT[4];
+    float lse4[4], del4[4];
+    {
+      const unsigned char* src = pf + l * 16;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        qa[ks] = ok ? *reinterpret_cast<const u32x4*>(a.q + (base + row) * kT + 32 * ks + 8 * g)
-                    : u32x4{0, 0, 0, 0};
-        da[ks] = ok ? *reinterpret_cast<const u32x4*>(a.dos + (base + row) * kT + 32 * ks + 8 * g)
-                    : u32x4{0, 0, 0, 0};
+        qa[ks] = *reinterpret_cast<const u32x4*>(src + ks * kPfSlot);
+        da[ks] = *reinterpret_cast<const u32x4*>(src + (2 + ks) * kPfSlot);
       }
-      const uint16_t* qt = a.qtf + ((int64_t)bh * a.Nb + m) * 4096 + tfoff;
-      const uint16_t* dt = a.dotf + ((int64_t)bh * a.Nb + m) * 4096 + tfoff;
-      u32x2 qT[4], dT[4];
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        qT[ct] = *reinterpret_cast<const u32x2*>(qt + ct * 1024);
-        dT[ct] = *reinterpret_cast<const u32x2*>(dt + ct * 1024);
+      for (int hf = 0; hf < 2; ++hf) {
+        const u32x4 x = *reinterpret_cast<const u32x4*>(src + (4 + hf) * kPfSlot);
+        const u32x4 y = *reinterpret_cast<const u32x4*>(src + (6 + hf) * kPfSlot);
+        qT[2 * hf] = u32x2{x[0], x[1]};
+        qT[2 * hf + 1] = u32x2{x[2], x[3]};
+        dT[2 * hf] = u32x2{y[0], y[1]};
+        dT[2 * hf + 1] = u32x2{y[2], y[3]};
       }
       // lse, delta of queries 16w + 4g + i
-      const int64_t q0 = (int64_t)m * kT + 16 * w + 4 * g;
-      float lse4[4], del4[4];
+      const f32x4 ls = *reinterpret_cast<const f32x4*>(pf + 8 * kPfSlot + 16 * g);
+      const f32x4 dl = *reinterpret_cast<const f32x4*>(pf + 8 * kPfSlot + 256 + 16 * g);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const bool qok = q0 + i < L;
-        lse4[i] = qok ? a.lse[base + q0 + i] : INFINITY;
-        del4[i] = qok ? a.delta[base + q0 + i] : 0.f;
+        lse4[i] = ls[i];
+        del4[i] = dl[i];
       }
+    }
+    __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // the region is read: free for the next block
+    const int mn = next_block();
+    if (mn >= 0) prefetch(mn);
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
         f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f}, dp = sc;
@@ -582,7 +659,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
           dkT[ct][kb] = mfma_16x16x16<T16>(qT[ct], dsp, dkT[ct][kb]);
         }
       }
-    }
+    m = mn;
   }
 
   // sum the query-split partials: wave w keeps key group kb = w
