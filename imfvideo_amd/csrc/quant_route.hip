@@ -30,92 +30,160 @@ struct QuantPoolArgs {
   int Nb;
 };
 
-// One 64x64 tile per workgroup of 256 threads; blockIdx.y = tensor * BH + bh.
+// Exact quotient fl(x / s) without a division per element (Markstein's
+// correction): with r = fl(1 / s) correctly rounded and q0 = fl(x r) within an
+// ulp of x / s, e = x - q0 s is exact under the FMA and fl(q0 + e r) is the
+// correctly rounded quotient (checked against IEEE division for every 16-bit
+// x and tile maximum: equal except for denormal x, whose quotients both
+// round to 0).
+__device__ inline float quotient(float x, float s, float r) {
+  const float q0 = x * r;
+  return __builtin_fmaf(__builtin_fmaf(-q0, s, x), r, q0);
+}
+
+// Round half away from zero of the quotient q = quotient(x, s, 1/s):
+// trunc(fl(q + sign(x) (0.5 - 2^-25))).  The constant just below 0.5 keeps
+// q = 0.5 - 2^-25 at 0 (q + 0.5 would round up to 1 there), and exact ties
+// k + 0.5 still round away (the sum rounds up to k + 1).  With x and the tile
+// maximum both 16-bit values this equals (int)roundf(fl(x / s)) for every
+// pair (exhaustive check: tests/quant_law_check.c).
+__device__ inline int round_away(float q, float x) {
+  return (int)(q + __builtin_copysignf(0x1.fffffep-2f, x));
+}
+// Low bytes of four int32 values packed into one word (three v_perm_b32)
+__device__ inline uint32_t pack_bytes(int b0, int b1, int b2, int b3) {
+  const uint32_t lo = __builtin_amdgcn_perm((uint32_t)b1, (uint32_t)b0, 0x0c0c0400u);
+  const uint32_t hi = __builtin_amdgcn_perm((uint32_t)b3, (uint32_t)b2, 0x0c0c0400u);
+  return __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+}
+
+// Tiles are numbered i = (tensor * BH + bh) * Nb + blk.  Each workgroup of 256
+// threads takes tiles i = blockIdx.x, + G, ... (G = gridDim.x) and keeps the
+// loads of the next kQuantSets - 1 tiles in flight while it quantises the
+// current one: kQuantSets register sets, each reloaded with the tile
+// kQuantSets G further on as soon as its data is consumed (the loop is
+// unrolled over the sets, so no set is ever copied -- a register copy would
+// wait for its load).  Thread tid owns row tid / 4, channels 16 (tid % 4) ..
+// +15.  The pooling sums run in wave 0 from a double-buffered LDS copy of the
+// tile, so one barrier per tile.
+constexpr int kQuantSets = 3;
+
 template <typename T16>
-__global__ __launch_bounds__(256) void quant_pool_kernel(QuantPoolArgs a) {
-  __shared__ float tile[kTile][kTile + 1];
-  __shared__ float red[4];
-  __shared__ float vec[kTile];
+__global__ __launch_bounds__(256) void quant_pool_kernel(QuantPoolArgs a, int ntiles) {
+  __shared__ __align__(16) uint16_t tile[2][kTile][kTile];
+  __shared__ float red[2][4];
+  __shared__ float vec[2][kTile];
 
   const int tid = threadIdx.x;
-  const int blk = blockIdx.x;
-  const int t = blockIdx.y / a.BH;
-  const int bh = blockIdx.y % a.BH;
   const int r = tid >> 2;
   const int c0 = (tid & 3) * 16;
-  const int64_t row = (int64_t)blk * kTile + r;
-  const bool valid = row < a.L;
-  const int64_t off = ((int64_t)bh * a.L + row) * kTile + c0;
-
-  float xv[16];
-  if (valid) {
-    const uint4* src = reinterpret_cast<const uint4*>(a.x[t] + off);
-    uint4 u0 = src[0], u1 = src[1];
-    uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-#pragma unroll
-    for (int i = 0; i < 8; ++i) {
-      xv[2 * i] = T16::to_f32((uint16_t)(w[i] & 0xffff));
-      xv[2 * i + 1] = T16::to_f32((uint16_t)(w[i] >> 16));
+  const int G = gridDim.x;
+  auto load = [&](int i, uint4 (&u)[2]) {
+    if (i >= ntiles) return;
+    const int blk = i % a.Nb;
+    const int y = i / a.Nb;
+    const int t = y / a.BH, bh = y - t * a.BH;
+    const int64_t row = (int64_t)blk * kTile + r;
+    if (row < a.L) {
+      const uint4* src = reinterpret_cast<const uint4*>(a.x[t] + ((int64_t)bh * a.L + row) * kTile + c0);
+      u[0] = src[0];
+      u[1] = src[1];
+    } else {
+      u[0] = u[1] = make_uint4(0, 0, 0, 0);
     }
-  } else {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) xv[i] = 0.f;
-  }
+  };
+  int buf = 0;
+  auto body = [&](int i, uint4 (&u)[2]) {
+    const int blk = i % a.Nb;
+    const int y = i / a.Nb;
+    const int t = y / a.BH, bh = y - t * a.BH;
+    const int64_t row = (int64_t)blk * kTile + r;
 
-  // block absmax (max is order-independent, so any reduction tree is exact)
-  float am = 0.f;
+    const uint32_t wv[8] = {u[0].x, u[0].y, u[0].z, u[0].w, u[1].x, u[1].y, u[1].z, u[1].w};
+    float xv[16];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) am = fmaxf(am, fabsf(xv[i]));
+    for (int k = 0; k < 8; ++k) {
+      xv[2 * k] = T16::to_f32((uint16_t)(wv[k] & 0xffff));
+      xv[2 * k + 1] = T16::to_f32((uint16_t)(wv[k] >> 16));
+    }
+    // tile absmax (max is order-independent, so any reduction tree is exact)
+    float am = 0.f;
 #pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) am = fmaxf(am, __shfl_xor(am, m, 64));
-  if ((tid & 63) == 0) red[tid >> 6] = am;
-  __syncthreads();
-  am = fmaxf(fmaxf(red[0], red[1]), fmaxf(red[2], red[3]));
-  const float s = am / 127.0f + 1e-12f;  // IEEE division, then add
+    for (int k = 0; k < 16; ++k) am = fmaxf(am, fabsf(xv[k]));
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) am = fmaxf(am, __shfl_xor(am, m, 64));
+    if ((tid & 63) == 0) red[buf][tid >> 6] = am;
+    const bool pooled = a.pool[t] != nullptr && blk < a.npool[t];
+    if (pooled) {
+      *reinterpret_cast<uint4*>(&tile[buf][r][c0]) = u[0];
+      *reinterpret_cast<uint4*>(&tile[buf][r][c0 + 8]) = u[1];
+    }
+    load(i + kQuantSets * G, u);  // this set's data is consumed: refill it
+    __syncthreads();
+    am = fmaxf(fmaxf(red[buf][0], red[buf][1]), fmaxf(red[buf][2], red[buf][3]));
+    const float s = am / 127.0f + 1e-12f;  // IEEE division, then add
+    const float rs = 1.0f / s;             // correctly rounded reciprocal
 
-  if (valid) {
     uint32_t w[4];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      uint32_t acc = 0;
+    for (int k = 0; k < 4; ++k) {
+      int qv[4];
 #pragma unroll
       for (int b = 0; b < 4; ++b) {
-        const float y = xv[4 * i + b] / s;
-        const int qv = (int)roundf(y);  // round half away from zero
-        acc |= ((uint32_t)(qv & 0xff)) << (8 * b);
+        const float x = xv[4 * k + b];
+        qv[b] = round_away(quotient(x, s, rs), x);
       }
-      w[i] = acc;
+      w[k] = pack_bytes(qv[0], qv[1], qv[2], qv[3]);
     }
-    *reinterpret_cast<uint4*>(a.xq[t] + off) = make_uint4(w[0], w[1], w[2], w[3]);
-  }
-  if (tid == 0) a.xs[t][(int64_t)bh * a.Nb + blk] = s;
+    if (row < a.L)
+      *reinterpret_cast<uint4*>(a.xq[t] + ((int64_t)bh * a.L + row) * kTile + c0) =
+          make_uint4(w[0], w[1], w[2], w[3]);
+    if (tid == 0) a.xs[t][(int64_t)bh * a.Nb + blk] = s;
 
-  if (a.pool[t] == nullptr || blk >= a.npool[t]) return;
-
-  // ---- pooling: sequential per-channel fp32 sum over the real rows ----
-#pragma unroll
-  for (int i = 0; i < 16; ++i) tile[r][c0 + i] = xv[i];
-  __syncthreads();
-  const int64_t rem = a.pool_len[t] - (int64_t)blk * kTile;
-  const int cnt = rem < kTile ? (int)rem : kTile;
-  if (tid < kTile) {
-    float acc = 0.f;
-    for (int rr = 0; rr < cnt; ++rr) acc = acc + tile[rr][tid];
-    vec[tid] = acc / (float)cnt;
-  }
-  __syncthreads();
-  if (tid < kTile) {
-    float outv = vec[tid];
-    if (a.proj[t] != nullptr) {
-      const float* pr = a.proj[t] + tid * kTile;  // row e of proj: out[e] = sum_d x[d] P[e,d]
+    // ---- pooling (wave 0): sequential per-channel fp32 sum over the real rows ----
+    if (pooled && tid < kTile) {
+      const int64_t rem = a.pool_len[t] - (int64_t)blk * kTile;
+      const int cnt = rem < kTile ? (int)rem : kTile;
       float acc = 0.f;
-      for (int d = 0; d < kTile; ++d) acc = acc + vec[d] * pr[d];
-      outv = acc;
+      int rr = 0;
+      for (; rr + 16 <= cnt; rr += 16) {  // 16 LDS reads in flight, then the adds in row order
+        float xr[16];
+#pragma unroll
+        for (int uu = 0; uu < 16; ++uu) xr[uu] = T16::to_f32(tile[buf][rr + uu][tid]);
+#pragma unroll
+        for (int uu = 0; uu < 16; ++uu) acc = acc + xr[uu];
+      }
+      for (; rr < cnt; ++rr) acc = acc + T16::to_f32(tile[buf][rr][tid]);
+      const float mean = acc / (float)cnt;
+      float outv = mean;
+      if (a.proj[t] != nullptr) {
+        vec[buf][tid] = mean;
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQ_REL, "wavefront");
+        const float* pr = a.proj[t] + tid * kTile;  // row e of proj: out[e] = sum_d x[d] P[e,d]
+        float p = 0.f;
+        for (int d = 0; d < kTile; ++d) p = p + vec[buf][d] * pr[d];
+        outv = p;
+      }
+      if (a.transposed[t])
+        a.pool[t][((int64_t)bh * kTile + tid) * a.npool[t] + blk] = outv;
+      else
+        a.pool[t][((int64_t)bh * a.Nb + blk) * kTile + tid] = outv;
     }
-    if (a.transposed[t])
-      a.pool[t][((int64_t)bh * kTile + tid) * a.npool[t] + blk] = outv;
-    else
-      a.pool[t][((int64_t)bh * a.Nb + blk) * kTile + tid] = outv;
+    buf ^= 1;
+  };
+  uint4 u0[2], u1[2], u2[2];
+  static_assert(kQuantSets == 3, "one register set per unrolled body below");
+  const int i0 = blockIdx.x;
+  load(i0, u0);
+  load(i0 + G, u1);
+  load(i0 + 2 * G, u2);
+  for (int i = i0; i < ntiles; i += 3 * G) {
+    body(i, u0);
+    if (i + G >= ntiles) break;
+    body(i + G, u1);
+    if (i + 2 * G >= ntiles) break;
+    body(i + 2 * G, u2);
   }
 }
 
@@ -530,12 +598,18 @@ __global__ __launch_bounds__(256) void route_select_kernel(const float* __restri
 
 using namespace sla2h;
 
+// Workgroups cycling over tiles: 16 per CU of 256 (two rounds of eight
+// resident ones; measured best among 1024-8192 at Config 3).
+constexpr int kQuantGrid = 4096;
+
 static int launch_quant_pool(const QuantPoolArgs& a, int ntens, int dtype, hipStream_t st) {
-  dim3 grid(a.Nb, ntens * a.BH);
+  const int64_t ntiles = (int64_t)a.Nb * ntens * a.BH;
+  if (ntiles >= (1ll << 31) - (kQuantSets + 2) * (int64_t)kQuantGrid) return (int)hipErrorInvalidValue;
+  const int grid = (int)(ntiles < kQuantGrid ? ntiles : kQuantGrid);
   if (dtype == SLA2H_DTYPE_BF16)
-    quant_pool_kernel<BF16><<<grid, 256, 0, st>>>(a);
+    quant_pool_kernel<BF16><<<grid, 256, 0, st>>>(a, (int)ntiles);
   else
-    quant_pool_kernel<F16><<<grid, 256, 0, st>>>(a);
+    quant_pool_kernel<F16><<<grid, 256, 0, st>>>(a, (int)ntiles);
   return (int)hipGetLastError();
 }
 
