@@ -418,7 +418,7 @@ __global__ __launch_bounds__(256) void comp_mask_kernel(const int32_t* __restric
 // chunks ahead.  Staging: thread (wave w, column c) loads rows 4w..4w+3 of
 // column c, splits them into bf16 hi + lo and writes half a B-operand
 // fragment of each with one 8-byte LDS store.  The A operand (0/1 mask)
-// comes from the row's mask byte through a 256-entry expansion table in LDS.
+// comes from the row's mask byte, one 16-entry nibble table read per half.
 template <bool TAN>
 __global__ __launch_bounds__(kCompThreads, 4) void comp_gemm_kernel(
     const float* __restrict__ Hb, const float* __restrict__ dHb, const float* __restrict__ zb,
@@ -426,7 +426,9 @@ __global__ __launch_bounds__(kCompThreads, 4) void comp_gemm_kernel(
     int NC, unsigned char* __restrict__ comp) {
   __shared__ __align__(16) uint16_t sb[2][2][kCompCols][40];  // [buf][hi/lo][column][n] (+pad)
   __shared__ __align__(16) uint32_t mw[2][16 * kMaskSub];    // [buf][local row] mask words
-  __shared__ __align__(16) u32x4 mexp[256];                  // mask byte -> operand slots
+  // mask nibble -> four bf16 operand slots: 16 entries of 8 bytes occupy 32 distinct LDS
+  // banks, so lanes reading different entries never conflict
+  __shared__ __align__(16) u32x2 mexp[16];
 
   const int tid = threadIdx.x;
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -454,7 +456,10 @@ __global__ __launch_bounds__(kCompThreads, 4) void comp_gemm_kernel(
   const auto rs = make_rsrc(src + (int64_t)bh * Np * stride, (int64_t)Np * stride * 4);
   const auto rb = make_rsrc(cbits + (int64_t)bh * NC * MTp, (int64_t)NC * MTp * 4);
 
-  if (tid < 256) mexp[tid] = expand_mask8(tid);
+  if (tid < 16) {
+    const u32x4 e = expand_mask8(tid);
+    mexp[tid] = u32x2{e[0], e[1]};
+  }
 
   f32x4 acc[4][4];
 #pragma unroll
@@ -500,7 +505,9 @@ __global__ __launch_bounds__(kCompThreads, 4) void comp_gemm_kernel(
     for (int s = 0; s < 4; ++s) {
       const int lt = w + 8 * s;  // local 16-row tile; uniform per wave
       if (mt0 + lt < MT) {
-        const u32x4 am = mexp[mwb[(buf * 16 * kMaskSub + lt * 16 + r) * 4 + g]];
+        const uint32_t mb = mwb[(buf * 16 * kMaskSub + lt * 16 + r) * 4 + g];
+        const u32x2 alo = mexp[mb & 15u], ahi = mexp[mb >> 4];
+        const u32x4 am = u32x4{alo.x, alo.y, ahi.x, ahi.y};
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct) {
           acc[s][ct] = mfma_bf16_16x16x32(am, bhi[ct], acc[s][ct]);
