@@ -248,6 +248,37 @@ def test_quantize_half_integer_quotients(dt):
     assert np.array_equal(ks.cpu().numpy(), want_ks)
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_quant_pool_many_tiles(dt):
+    """More tiles than the quantiser's workgroups hold in their three register
+    sets (2 x 16 x 402 = 12,864 > 3 x 4096): every set and the loop's wrap run.
+    Ragged L, per-row magnitudes over ~4 decades, non-identity projections;
+    INT8, scales and pooled tiles bit-exact."""
+    from imfvideo_amd import ops
+    say("quant_pool many tiles", dt)
+    B, H, Np, E = 2, 8, 401, 64
+    L = Np * E + 17
+    g = torch.Generator().manual_seed(23)
+    mag = torch.exp(2.0 * torch.randn(B, H, L, 1, generator=g))
+    q = (torch.randn(B, H, L, E, generator=g) * mag).to(dt)
+    k = (torch.randn(B, H, L, E, generator=g) * mag.flip(2)).to(dt)
+    pq = torch.randn(E, E, generator=g) / 8
+    pk = torch.eye(E) + torch.randn(E, E, generator=g) / 16
+    q8, qs, k8, ks, qpool, kpool_t = ops.quant_pool_qk(cuda(q), cuda(k), Np, E, cuda(pq), cuda(pk))
+    torch.cuda.synchronize()
+    want_q, want_qs = O.quantize_blocks(q.float())
+    want_k, want_ks = O.quantize_blocks(k.float())
+    assert np.array_equal(q8.cpu().numpy(), want_q)
+    assert np.array_equal(qs.cpu().numpy(), want_qs)
+    assert np.array_equal(k8.cpu().numpy(), want_k)
+    assert np.array_equal(ks.cpu().numpy(), want_ks)
+    Nb = -(-L // E)
+    want_qp = O.project_pool(O.pool_tiles(q.float(), Nb, L), pq)
+    want_kp = O.project_pool(O.pool_tiles(k.float(), Np, Np * E), pk)
+    assert np.array_equal(qpool.cpu().numpy(), want_qp)
+    assert np.array_equal(kpool_t.cpu().numpy(), np.swapaxes(want_kp, -1, -2))
+
+
 def test_large_inputs_stay_finite():
     say("x20 scaled inputs")
     z, dt, ins = golden("ref_geom_bf16")
