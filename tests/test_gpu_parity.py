@@ -224,6 +224,30 @@ def test_all_tiles_routed_and_zero_tiles():
     assert torch.isfinite(o2).all() and torch.isfinite(do2).all()
 
 
+@pytest.mark.parametrize("T", [1, 5])
+@pytest.mark.parametrize("tangent", [True, False])
+def test_odd_routed_count(T, tangent):
+    """An odd number of routed tiles: the last one takes the kernel's unmasked
+    single-tile path (even T and the prefix tails never do).  B = H = 2, no
+    prefix, router-chosen LUT, against the oracle."""
+    say("odd T", T, "tangent", tangent)
+    B, H, Np, P = 2, 2, 12, 0
+    L = Np * 64 + P
+    q, k, v, dq, dk, dv = make_inputs(31 + T, B, H, L)
+    ins = dict(q=q, k=k, v=v, dq=dq, dk=dk, dv=dv)
+    alpha = torch.rand(H, Np, generator=torch.Generator().manual_seed(5)) * 0.8 + 0.1
+    o, do, aux = run_full(ins, alpha, (T + 0.5) / Np, Np, P, tangent=tangent)
+    assert aux["lut"].shape[-1] == T
+    f = {n: t.float() for n, t in ins.items()}
+    eo, edo = O.cube_jvp(*(f[n] for n in ("q", "k", "v", "dq", "dk", "dv")), alpha,
+                         aux["lut"].numpy(), Np, P)
+    assert max_abs(o, eo) < TOL_MAX and rel_l2(o, eo) < TOL_REL
+    if tangent:
+        assert max_abs(do, edo) < TOL_MAX and rel_l2(do, edo) < TOL_REL
+    else:
+        assert do is None
+
+
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
 def test_quantize_half_integer_quotients(dt):
     """x / s exactly on k + 1/2 (round half away from zero) and random tiles."""
