@@ -26,6 +26,7 @@ SOURCES = {
     "attn_train.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "attn_bwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"],
     "mla_glue.hip": [],
+    "block_train.hip": [],
 }
 
 COMMON_FLAGS = [

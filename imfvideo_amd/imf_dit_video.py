@@ -50,9 +50,30 @@ class RMSNorm(nn.Module):
         return normed.to(x.dtype) * self.weight
 
 
+class _SituMulFunction(torch.autograd.Function):
+    """SituAndMul on the GPU: one fused HIP kernel forward, one backward; saves
+    only the inputs (the eager form keeps several fp32 intermediates)."""
+
+    @staticmethod
+    def forward(ctx, gate, up, beta, linear_beta):
+        from . import ops
+        ctx.beta, ctx.linear_beta = beta, linear_beta
+        ctx.save_for_backward(gate, up)
+        return ops.situ_mul_fwd(gate, up, beta, linear_beta)
+
+    @staticmethod
+    def backward(ctx, dh):
+        from . import ops
+        gate, up = ctx.saved_tensors
+        dgate, dup = ops.situ_mul_bwd(dh, gate, up, ctx.beta, ctx.linear_beta)
+        return dgate, dup, None, None
+
+
 class SituAndMul(nn.Module):
     """situ(g) * up with situ(g) = beta tanh(g / beta) sigmoid(g); with
-    linear_beta the up branch is soft-clamped to linear_beta tanh(up / linear_beta)."""
+    linear_beta the up branch is soft-clamped to linear_beta tanh(up / linear_beta).
+    GPU tensors run the fused kernels (sla2h_situ_mul_fwd / _bwd); CPU tensors
+    the eager fp32 expression."""
 
     def __init__(self, beta=1.0, linear_beta=None):
         super().__init__()
@@ -65,6 +86,12 @@ class SituAndMul(nn.Module):
             gate, up = x[..., :d], x[..., d:]
         else:
             gate = x
+        if gate.is_cuda:
+            if up.dtype != gate.dtype:
+                up = up.to(gate.dtype)
+            return _SituMulFunction.apply(gate, up, float(self.beta),
+                                          None if self.linear_beta is None
+                                          else float(self.linear_beta))
         dtype = gate.dtype
         g, u = gate.float(), up.float()
         act = self.beta * torch.tanh(g / self.beta) * torch.sigmoid(g)

@@ -638,3 +638,51 @@ def sla2_infer(q, k, v, alpha, lut, bq, use_int8=True, qblock=None, eps_l=1e-5,
     if return_parts:
         return o, dict(o_s=o_s, lse=lse, qphi=qphi, comp=comp, **st)
     return o
+
+
+# ---------------------------------------------------------------------------
+# DiT block, training forward / backward: fused SituAndMul
+# (models/imf_dit_video.py:136-171)
+# ---------------------------------------------------------------------------
+_SITU_DTYPES = {torch.float16: 0, torch.bfloat16: 1, torch.float32: 2}
+
+
+def _rows_view(t):
+    """(..., F) with a unit last stride -> (rows, F, row stride), without a copy
+    when the leading dimensions collapse to one strided dimension."""
+    F = t.shape[-1]
+    v = t.reshape(-1, F)
+    if v.stride(-1) != 1 or (v.shape[0] > 1 and v.stride(0) < F):
+        v = v.contiguous()
+    return v, F, max(v.stride(0), F)
+
+
+def situ_mul_fwd(gate, up, beta, linear_beta=None):
+    """h = beta tanh(gate / beta) sigmoid(gate) * u' (u' = lb tanh(up / lb) with
+    a soft clamp, else up), fp32 arithmetic, in gate's dtype, shape of gate."""
+    _need_gpu(gate, up)
+    if gate.shape != up.shape or gate.dtype != up.dtype or gate.dtype not in _SITU_DTYPES:
+        raise ValueError("gate and up must share shape and a 16-bit or fp32 dtype")
+    g2, F, sg = _rows_view(gate)
+    u2, _, su = _rows_view(up)
+    out = torch.empty(gate.shape, device=gate.device, dtype=gate.dtype)
+    _lib.check(_lib.load().sla2h_situ_mul_fwd(
+        g2.data_ptr(), u2.data_ptr(), _SITU_DTYPES[gate.dtype], g2.shape[0], F, sg, su,
+        float(beta), float(linear_beta or 0.0), out.data_ptr(), _stream(gate.device)),
+        "sla2h_situ_mul_fwd")
+    return out
+
+
+def situ_mul_bwd(dh, gate, up, beta, linear_beta=None):
+    """Gradients (dgate, dup) of situ_mul_fwd for the output gradient dh."""
+    _need_gpu(dh, gate, up)
+    g2, F, sg = _rows_view(gate)
+    u2, _, su = _rows_view(up)
+    dh = dh.to(gate.dtype).contiguous()
+    dgate = torch.empty(gate.shape, device=gate.device, dtype=gate.dtype)
+    dup = torch.empty_like(dgate)
+    _lib.check(_lib.load().sla2h_situ_mul_bwd(
+        dh.data_ptr(), g2.data_ptr(), u2.data_ptr(), _SITU_DTYPES[gate.dtype], g2.shape[0], F,
+        sg, su, float(beta), float(linear_beta or 0.0), dgate.data_ptr(), dup.data_ptr(),
+        _stream(gate.device)), "sla2h_situ_mul_bwd")
+    return dgate, dup

@@ -238,6 +238,25 @@ int sla2h_mla_out_gate(const float* o, const float* dout, const int32_t* pos, co
 int sla2h_situ_jvp(const void* gu, int64_t rows, int F, float beta, int dtype, void* act,
                    void* stream);
 
+/*
+ * SituAndMul of the DiT block's training forward and its backward (the
+ * autograd path): h = situ(g) u', situ(g) = beta tanh(g / beta) sigmoid(g),
+ * u' = lb tanh(u / lb) for lb > 0 (the linear_beta soft clamp), else u;
+ * dg = dh u' situ'(g), du = dh situ(g) du'/du.  gate / up: (rows, F) with row
+ * strides sg / su elements (views of one [gate | up] tensor allowed); out, dh,
+ * dgate, dup: contiguous (rows, F).  dtype: SLA2H_DTYPE_F16, SLA2H_DTYPE_BF16
+ * or 2 (fp32); fp32 arithmetic.  16-byte accesses when F, the strides and the
+ * pointers allow them (multiples of 8 elements for 16-bit, 4 for fp32), else
+ * one element per thread.
+ * Replaces the eager SituAndMul.forward and its autograd backward
+ * (models/imf_dit_video.py:136-171).
+ */
+int sla2h_situ_mul_fwd(const void* gate, const void* up, int dtype, int64_t rows, int F,
+                       int64_t sg, int64_t su, float beta, float lb, void* out, void* stream);
+int sla2h_situ_mul_bwd(const void* dh, const void* gate, const void* up, int dtype, int64_t rows,
+                       int F, int64_t sg, int64_t su, float beta, float lb, void* dgate,
+                       void* dup, void* stream);
+
 /* ---- training forward (the module's autograd forward) ------------------ */
 
 /*

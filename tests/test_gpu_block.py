@@ -1,0 +1,86 @@
+"""GPU parity of the DiT block's fused training kernels against the eager
+expression of the reference (models/imf_dit_video.py:136-171): SituAndMul
+forward and backward, 16-bit and fp32 I/O, with and without the linear_beta
+soft clamp, on 16-byte (F = 2048, 96) and one-element (F = 1365) paths and on
+[gate | up] views of one tensor.  The eager form is evaluated in float64 on the
+CPU from the same inputs; tolerance: two units in the last place of a 16-bit
+I/O dtype (the kernels round once, from fp32), and 2^-16 relative for fp32 I/O,
+whose evaluation chain (hardware exp and tanh, then products) carries a few tens
+of fp32 ulps (3.7e-6 measured)."""
+import sys
+
+import pytest
+import torch
+
+pytestmark = pytest.mark.gpu
+
+ULP = {torch.bfloat16: 2.0 ** -8, torch.float16: 2.0 ** -11, torch.float32: 2.0 ** -17}
+
+
+def say(*a):
+    print("[case]", *a, flush=True)
+    sys.stdout.flush()
+
+
+def situ_eager(g, u, beta, lb):
+    act = beta * torch.tanh(g / beta) * torch.sigmoid(g)
+    if lb is not None:
+        u = lb * torch.tanh(u / lb)
+    return act * u
+
+
+def close(a, b, dt):
+    """Per element within 2 ulp of the I/O dtype, plus an absolute floor of
+    2 ulp of the tensor's largest magnitude for fp32 I/O: in the saturated clamp
+    1 - tanh^2 cancels in fp32 (as in eager torch's tanh_backward), leaving
+    elements ~1e-7 of the largest one without relative accuracy."""
+    a, b = a.double().cpu(), b.double().cpu()
+    floor = 1.0 if dt == torch.float32 else 1e-3
+    tol = 2 * ULP[dt] * b.abs() + 2 * ULP[dt] * b.abs().max() * floor + 1e-30
+    return bool(((a - b).abs() <= tol).all()), float(((a - b).abs() / (b.abs() + 1e-30)).max())
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16, torch.float32])
+@pytest.mark.parametrize("F", [2048, 1365, 96])
+@pytest.mark.parametrize("lb", [25.0, None])
+@pytest.mark.parametrize("split", [False, True])
+def test_situ_mul_forward_backward(dt, F, lb, split):
+    from imfvideo_amd.imf_dit_video import SituAndMul
+    say("situ_mul", dt, F, lb, split)
+    g = torch.Generator().manual_seed(F + (7 if lb else 0) + (3 if split else 0))
+    rows = 1000
+    beta = 4.0
+    scale = 6.0 if lb is None else 40.0   # reach tanh saturation of both branches
+    x = (torch.randn(2, rows // 2, 2 * F, generator=g) * scale).to(dt)
+    dh = torch.randn(2, rows // 2, F, generator=g).to(dt)
+    m = SituAndMul(beta=beta, linear_beta=lb)
+    xg = x.cuda().requires_grad_(True)
+    if split:
+        h = m(xg)                                   # gate / up as views of x
+    else:
+        gate = xg[..., :F].contiguous()
+        up = xg[..., F:].contiguous()
+        h = m(gate, up)
+    assert h.dtype == dt and h.shape == (2, rows // 2, F)
+    h.backward(dh.cuda())
+    torch.cuda.synchronize()
+    x64 = x.double().requires_grad_(True)
+    want = situ_eager(x64[..., :F], x64[..., F:], beta, lb)
+    want.backward(dh.double())
+    ok, err = close(h.detach(), want.detach(), dt)
+    assert ok, ("forward", err)
+    ok, err = close(xg.grad, x64.grad, dt)
+    assert ok, ("backward", err)
+
+
+def test_situ_mul_matches_eager_module_on_cpu():
+    """The module's CPU branch (the eager fp32 expression) and the fused GPU
+    kernels agree to bf16 rounding on the same bf16 inputs."""
+    from imfvideo_amd.imf_dit_video import SituAndMul
+    say("situ_mul cpu eager vs gpu fused")
+    g = torch.Generator().manual_seed(3)
+    x = (torch.randn(64, 2 * 512, generator=g) * 5).to(torch.bfloat16)
+    m = SituAndMul(beta=4.0, linear_beta=25.0)
+    a = m(x).float()
+    b = m(x.cuda()).float().cpu()
+    assert (a - b).abs().max().item() <= 2 * 2.0 ** -8 * a.abs().max().item()
