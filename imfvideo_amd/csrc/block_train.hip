@@ -216,3 +216,222 @@ extern "C" int sla2h_situ_mul_bwd(const void* dh, const void* gate, const void* 
   if (dtype == SLA2H_DTYPE_F16) return go(std::integral_constant<int, SLA2H_DTYPE_F16>{});
   return go(std::integral_constant<int, kF32>{});
 }
+
+// ---------------------------------------------------------------------------
+// RMSNorm of the training forward and its backward (models/imf_dit_video.py:
+// 121-133): y = round_x(x r) w with r = 1 / sqrt(mean(x^2) + eps) in fp32,
+// round_x the rounding to x's dtype, w fp32, y fp32 (the product promotes).
+// Backward (autograd of that expression): g = round_x(dy w) (the gradient of
+// the cast is taken in x's dtype), dx = round_x(r g - x r^3 mean(g x)),
+// dw = sum over rows of round_x(x r) dy.  One wave per row, each lane a
+// strided set of the row's D <= 1024 channels; dw in two steps: per-block
+// partial sums over kRmsRows rows, then a per-column sum over the blocks in
+// a fixed order (deterministic).
+// ---------------------------------------------------------------------------
+namespace sla2h {
+namespace {
+
+constexpr int kRmsRows = 16;  // rows per workgroup (4 per wave) in the backward's partial dw
+
+template <int DT>
+__device__ inline float ld1(const void* p, int64_t i) {
+  if (DT == kF32) return static_cast<const float*>(p)[i];
+  if (DT == SLA2H_DTYPE_BF16) return BF16::to_f32(static_cast<const uint16_t*>(p)[i]);
+  return F16::to_f32(static_cast<const uint16_t*>(p)[i]);
+}
+template <int DT>
+__device__ inline void st1(void* p, int64_t i, float v) {
+  if (DT == kF32)
+    static_cast<float*>(p)[i] = v;
+  else if (DT == SLA2H_DTYPE_BF16)
+    static_cast<uint16_t*>(p)[i] = BF16::from_f32(v);
+  else
+    static_cast<uint16_t*>(p)[i] = F16::from_f32(v);
+}
+template <int DT>
+__device__ inline float round_to(float v) {
+  if (DT == kF32) return v;
+  if (DT == SLA2H_DTYPE_BF16) return BF16::to_f32(BF16::from_f32(v));
+  return F16::to_f32(F16::from_f32(v));
+}
+__device__ inline float wave_sum64(float v) {
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+template <int DT, int MAXE>
+__global__ __launch_bounds__(256) void rms_fwd_kernel(const void* __restrict__ X, int64_t rows, int D,
+                                                      int64_t sx, const float* __restrict__ W,
+                                                      float eps, float* __restrict__ Y) {
+  const int64_t row = (int64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int l = threadIdx.x & 63;
+  float x[MAXE];
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < MAXE; ++e) {
+    const int c = l + 64 * e;
+    x[e] = c < D ? ld1<DT>(X, row * sx + c) : 0.f;
+    ss += x[e] * x[e];
+  }
+  const float r = 1.f / sqrtf(wave_sum64(ss) / (float)D + eps);
+#pragma unroll
+  for (int e = 0; e < MAXE; ++e) {
+    const int c = l + 64 * e;
+    if (c < D) Y[row * D + c] = round_to<DT>(x[e] * r) * W[c];
+  }
+}
+
+template <int DT, int MAXE>
+__global__ __launch_bounds__(256) void rms_bwd_kernel(const void* __restrict__ X, int64_t rows, int D,
+                                                      int64_t sx, const float* __restrict__ W,
+                                                      const float* __restrict__ DY, float eps,
+                                                      void* __restrict__ DX,
+                                                      float* __restrict__ DWP) {
+  __shared__ float part[4][1024];
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  float dwacc[MAXE];
+#pragma unroll
+  for (int e = 0; e < MAXE; ++e) dwacc[e] = 0.f;
+  // this wave's rows: all loads first (the rows are independent), then the math
+  constexpr int R = kRmsRows / 4;
+  float x[R][MAXE], dy[R][MAXE];
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int64_t row = (int64_t)blockIdx.x * kRmsRows + 4 * k + w;
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) {
+      const int c = l + 64 * e;
+      const bool ok = row < rows && c < D;
+      x[k][e] = ok ? ld1<DT>(X, row * sx + c) : 0.f;
+      dy[k][e] = ok ? DY[row * D + c] : 0.f;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < R; ++k) {
+    const int64_t row = (int64_t)blockIdx.x * kRmsRows + 4 * k + w;
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) ss += x[k][e] * x[k][e];
+    const float r = 1.f / sqrtf(wave_sum64(ss) / (float)D + eps);
+    float g[MAXE];
+    float gx = 0.f;
+#pragma unroll
+    for (int e = 0; e < MAXE; ++e) {
+      const int c = l + 64 * e;
+      g[e] = c < D ? round_to<DT>(dy[k][e] * W[c]) : 0.f;
+      gx += g[e] * x[k][e];
+      dwacc[e] += round_to<DT>(x[k][e] * r) * dy[k][e];  // rows past the end add 0
+    }
+    const float mgx = wave_sum64(gx) / (float)D;
+    const float r3 = r * r * r;
+    if (row < rows) {
+#pragma unroll
+      for (int e = 0; e < MAXE; ++e) {
+        const int c = l + 64 * e;
+        if (c < D) st1<DT>(DX, row * D + c, r * g[e] - x[k][e] * r3 * mgx);
+      }
+    }
+  }
+  // partial dw of this workgroup's rows: the four waves' sums in a fixed order
+#pragma unroll
+  for (int e = 0; e < MAXE; ++e) {
+    const int c = l + 64 * e;
+    if (c < D) part[w][c] = dwacc[e];
+  }
+  __syncthreads();
+  for (int c = threadIdx.x; c < D; c += 256)
+    DWP[(int64_t)blockIdx.x * D + c] = (part[0][c] + part[1][c]) + (part[2][c] + part[3][c]);
+}
+
+// dw[c] = sum over b of partial[b][c]: one workgroup per column, thread t
+// sums b = t, t + 256, ... in order, then a fixed LDS tree (deterministic)
+__global__ __launch_bounds__(256) void col_sum_kernel(const float* __restrict__ P, int64_t nb, int D,
+                                                      float* __restrict__ out) {
+  __shared__ float red[256];
+  const int c = blockIdx.x;
+  float s = 0.f;
+  for (int64_t b = threadIdx.x; b < nb; b += 256) s += P[b * D + c];
+  red[threadIdx.x] = s;
+  __syncthreads();
+#pragma unroll
+  for (int h = 128; h >= 1; h >>= 1) {
+    if ((int)threadIdx.x < h) red[threadIdx.x] += red[threadIdx.x + h];
+    __syncthreads();
+  }
+  if (threadIdx.x == 0) out[c] = red[0];
+}
+
+template <int DT>
+void launch_rms_fwd(const void* x, int64_t rows, int D, int64_t sx, const float* w, float eps,
+                    float* y, hipStream_t st) {
+  const unsigned grid = (unsigned)((rows + 3) / 4);
+  if (D <= 64)
+    rms_fwd_kernel<DT, 1><<<grid, 256, 0, st>>>(x, rows, D, sx, w, eps, y);
+  else if (D <= 256)
+    rms_fwd_kernel<DT, 4><<<grid, 256, 0, st>>>(x, rows, D, sx, w, eps, y);
+  else if (D <= 512)
+    rms_fwd_kernel<DT, 8><<<grid, 256, 0, st>>>(x, rows, D, sx, w, eps, y);
+  else
+    rms_fwd_kernel<DT, 16><<<grid, 256, 0, st>>>(x, rows, D, sx, w, eps, y);
+}
+template <int DT>
+void launch_rms_bwd(const void* x, int64_t rows, int D, int64_t sx, const float* w, const float* dy,
+                    float eps, void* dx, float* dwp, hipStream_t st) {
+  const unsigned grid = (unsigned)((rows + kRmsRows - 1) / kRmsRows);
+  if (D <= 64)
+    rms_bwd_kernel<DT, 1><<<grid, 256, 0, st>>>(x, rows, D, sx, w, dy, eps, dx, dwp);
+  else if (D <= 256)
+    rms_bwd_kernel<DT, 4><<<grid, 256, 0, st>>>(x, rows, D, sx, w, dy, eps, dx, dwp);
+  else if (D <= 512)
+    rms_bwd_kernel<DT, 8><<<grid, 256, 0, st>>>(x, rows, D, sx, w, dy, eps, dx, dwp);
+  else
+    rms_bwd_kernel<DT, 16><<<grid, 256, 0, st>>>(x, rows, D, sx, w, dy, eps, dx, dwp);
+}
+
+}  // namespace
+}  // namespace sla2h
+
+extern "C" size_t sla2h_rmsnorm_bwd_workspace_bytes(int64_t rows, int D) {
+  if (rows <= 0 || D <= 0) return 0;
+  return (size_t)((rows + sla2h::kRmsRows - 1) / sla2h::kRmsRows) * D * sizeof(float);
+}
+
+extern "C" int sla2h_rmsnorm_fwd(const void* x, int dtype, int64_t rows, int D, int64_t sx,
+                                 const float* w, float eps, float* y, void* stream) {
+  SLA2H_CHECK_ARG(x && w && y);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16 || dtype == kF32);
+  SLA2H_CHECK_ARG(rows > 0 && D > 0 && D <= 1024 && sx >= D);
+  SLA2H_CHECK_ARG((rows + 3) / 4 < (1ll << 31));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SLA2H_DTYPE_BF16)
+    launch_rms_fwd<SLA2H_DTYPE_BF16>(x, rows, D, sx, w, eps, y, st);
+  else if (dtype == SLA2H_DTYPE_F16)
+    launch_rms_fwd<SLA2H_DTYPE_F16>(x, rows, D, sx, w, eps, y, st);
+  else
+    launch_rms_fwd<kF32>(x, rows, D, sx, w, eps, y, st);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_rmsnorm_bwd(const void* x, int dtype, int64_t rows, int D, int64_t sx,
+                                 const float* w, const float* dy, float eps, void* dx, float* dw,
+                                 void* workspace, void* stream) {
+  SLA2H_CHECK_ARG(x && w && dy && dx && dw && workspace);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16 || dtype == kF32);
+  SLA2H_CHECK_ARG(rows > 0 && D > 0 && D <= 1024 && sx >= D);
+  const int64_t nb = (rows + kRmsRows - 1) / kRmsRows;
+  SLA2H_CHECK_ARG(nb < (1ll << 31));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* dwp = static_cast<float*>(workspace);
+  if (dtype == SLA2H_DTYPE_BF16)
+    launch_rms_bwd<SLA2H_DTYPE_BF16>(x, rows, D, sx, w, dy, eps, dx, dwp, st);
+  else if (dtype == SLA2H_DTYPE_F16)
+    launch_rms_bwd<SLA2H_DTYPE_F16>(x, rows, D, sx, w, dy, eps, dx, dwp, st);
+  else
+    launch_rms_bwd<kF32>(x, rows, D, sx, w, dy, eps, dx, dwp, st);
+  int err = (int)hipGetLastError();
+  if (err) return err;
+  col_sum_kernel<<<D, 256, 0, st>>>(dwp, nb, D, dw);
+  return (int)hipGetLastError();
+}

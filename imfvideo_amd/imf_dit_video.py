@@ -36,8 +36,29 @@ def sdpa_math_attention(q, k, v):
     return o.transpose(1, 2)
 
 
+class _RMSNormFunction(torch.autograd.Function):
+    """RMSNorm on the GPU: one fused HIP kernel forward, one backward (plus the
+    weight gradient's column sum); saves x only."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps):
+        from . import ops
+        ctx.eps = eps
+        ctx.save_for_backward(x, weight)
+        return ops.rmsnorm_fwd(x, weight, eps)
+
+    @staticmethod
+    def backward(ctx, dy):
+        from . import ops
+        x, weight = ctx.saved_tensors
+        dx, dw = ops.rmsnorm_bwd(dy, x, weight, ctx.eps)
+        return dx, dw.to(weight.dtype), None
+
+
 class RMSNorm(nn.Module):
-    """Root mean square normalisation with fp32 accumulation."""
+    """Root mean square normalisation with fp32 accumulation.  GPU tensors (with
+    an fp32 weight) run the fused kernels (sla2h_rmsnorm_fwd / _bwd); CPU
+    tensors the eager expression."""
 
     def __init__(self, dim, eps=1e-6):
         super().__init__()
@@ -45,6 +66,9 @@ class RMSNorm(nn.Module):
         self.weight = nn.Parameter(torch.ones(dim))
 
     def forward(self, x):
+        if (x.is_cuda and self.weight.dtype == torch.float32 and x.shape[-1] <= 1024
+                and x.dtype in (torch.float32, torch.bfloat16, torch.float16)):
+            return _RMSNormFunction.apply(x, self.weight, float(self.eps))
         xf = x.float()
         normed = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + self.eps)
         return normed.to(x.dtype) * self.weight

@@ -686,3 +686,39 @@ def situ_mul_bwd(dh, gate, up, beta, linear_beta=None):
         sg, su, float(beta), float(linear_beta or 0.0), dgate.data_ptr(), dup.data_ptr(),
         _stream(gate.device)), "sla2h_situ_mul_bwd")
     return dgate, dup
+
+
+# ---------------------------------------------------------------------------
+# DiT block, training forward / backward: fused RMSNorm
+# (models/imf_dit_video.py:121-133)
+# ---------------------------------------------------------------------------
+def rmsnorm_fwd(x, w, eps):
+    """y = (x r).to(x.dtype) * w in fp32, r = rsqrt(mean(x^2) + eps); shape of x."""
+    _need_gpu(x, w)
+    if x.dtype not in _SITU_DTYPES:
+        raise ValueError(f"RMSNorm input dtype {x.dtype} not supported")
+    x2, D, sx = _rows_view(x)
+    w = w.detach().to(torch.float32).contiguous()
+    y = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+    _lib.check(_lib.load().sla2h_rmsnorm_fwd(
+        x2.data_ptr(), _SITU_DTYPES[x.dtype], x2.shape[0], D, sx, w.data_ptr(), float(eps),
+        y.data_ptr(), _stream(x.device)), "sla2h_rmsnorm_fwd")
+    return y
+
+
+def rmsnorm_bwd(dy, x, w, eps):
+    """(dx in x's dtype, dw fp32) of rmsnorm_fwd for the output gradient dy."""
+    _need_gpu(dy, x, w)
+    x2, D, sx = _rows_view(x)
+    w = w.detach().to(torch.float32).contiguous()
+    dy = dy.to(torch.float32).contiguous()
+    dx = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+    dw = torch.empty(D, device=x.device, dtype=torch.float32)
+    lib = _lib.load()
+    ws = torch.empty(lib.sla2h_rmsnorm_bwd_workspace_bytes(x2.shape[0], D) // 4,
+                     device=x.device, dtype=torch.float32)
+    _lib.check(lib.sla2h_rmsnorm_bwd(
+        x2.data_ptr(), _SITU_DTYPES[x.dtype], x2.shape[0], D, sx, w.data_ptr(), dy.data_ptr(),
+        float(eps), dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), _stream(x.device)),
+        "sla2h_rmsnorm_bwd")
+    return dx, dw

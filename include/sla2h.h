@@ -257,6 +257,24 @@ int sla2h_situ_mul_bwd(const void* dh, const void* gate, const void* up, int dty
                        int F, int64_t sg, int64_t su, float beta, float lb, void* dgate,
                        void* dup, void* stream);
 
+/*
+ * RMSNorm of the DiT block's training forward and its backward (the autograd
+ * path): y = round_x(x r) w, r = 1 / sqrt(mean(x^2) + eps) in fp32, round_x the
+ * rounding to x's dtype, w fp32, y fp32 contiguous (rows, D).  Backward:
+ * g = round_x(dy w), dx = round_x(r g - x r^3 mean(g x)) contiguous in x's
+ * dtype, dw = sum over rows of round_x(x r) dy (deterministic two-step sum in
+ * `workspace` of sla2h_rmsnorm_bwd_workspace_bytes).  x: (rows, D <= 1024),
+ * row stride sx elements; dtype SLA2H_DTYPE_F16, SLA2H_DTYPE_BF16 or 2 (fp32).
+ * Replaces RMSNorm.forward and its autograd backward
+ * (models/imf_dit_video.py:121-133).
+ */
+int sla2h_rmsnorm_fwd(const void* x, int dtype, int64_t rows, int D, int64_t sx, const float* w,
+                      float eps, float* y, void* stream);
+size_t sla2h_rmsnorm_bwd_workspace_bytes(int64_t rows, int D);
+int sla2h_rmsnorm_bwd(const void* x, int dtype, int64_t rows, int D, int64_t sx, const float* w,
+                      const float* dy, float eps, void* dx, float* dw, void* workspace,
+                      void* stream);
+
 /* ---- training forward (the module's autograd forward) ------------------ */
 
 /*

@@ -84,3 +84,68 @@ def test_situ_mul_matches_eager_module_on_cpu():
     a = m(x).float()
     b = m(x.cuda()).float().cpu()
     assert (a - b).abs().max().item() <= 2 * 2.0 ** -8 * a.abs().max().item()
+
+
+def _rms_eager(x, w, eps):
+    """The module's eager expression (models/imf_dit_video.py:121-133)."""
+    xf = x.float()
+    normed = xf * torch.rsqrt(xf.pow(2).mean(dim=-1, keepdim=True) + eps)
+    return normed.to(x.dtype) * w
+
+
+@pytest.mark.parametrize("case", ["f32_512", "bf16_256", "f16_1000", "bf16_heads_view"])
+def test_rmsnorm_forward_backward(case):
+    """Fused RMSNorm forward / backward against the module's eager expression
+    on the CPU (fp32 arithmetic, the same rounding points): y and dx within 2
+    ulp of their dtype per element (plus 2 ulp of the largest magnitude: the
+    mean and rsqrt round in another order), dw within 1e-5 (fp32) / 1e-4
+    (16-bit) of its max-norm."""
+    from imfvideo_amd.imf_dit_video import RMSNorm
+    say("rmsnorm", case)
+    g = torch.Generator().manual_seed(len(case))
+    dt = {"f32": torch.float32, "bf16": torch.bfloat16, "f16": torch.float16}[case.split("_")[0]]
+    if case == "bf16_heads_view":
+        base = (torch.randn(2, 300, 8, 64, generator=g) * 3).to(dt)
+        D = 32
+        x = base[..., :D]                                  # strided per-head band
+    else:
+        D = int(case.split("_")[1])
+        base = (torch.randn(2, 300, D, generator=g) * 3).to(dt)
+        x = base
+    m = RMSNorm(D, eps=1e-6)
+    with torch.no_grad():
+        m.weight.copy_(1 + 0.5 * torch.randn(D, generator=g))
+    dy = torch.randn(x.shape, generator=g)
+    # eager on the CPU
+    xc = x.detach().clone().requires_grad_(True)
+    mc = RMSNorm(D, eps=1e-6)
+    with torch.no_grad():
+        mc.weight.copy_(m.weight)
+    yc = _rms_eager(xc, mc.weight, 1e-6)
+    yc.backward(dy)
+    # fused on the GPU (x as a view of a GPU tensor, like the MLA head bands)
+    mg = m.cuda()
+    bg = base.cuda().requires_grad_(True)
+    xg = bg[..., :D] if case == "bf16_heads_view" else bg
+    yg = mg(xg)
+    assert yg.dtype == torch.float32 and yg.shape == x.shape
+    yg.backward(dy.cuda())
+    torch.cuda.synchronize()
+    ulp = ULP[dt] if dt != torch.float32 else 2.0 ** -23
+
+    def within(a, b, u):
+        a, b = a.double().cpu(), b.double().cpu()
+        return bool(((a - b).abs() <= 2 * u * b.abs() + 2 * u * b.abs().max()).all())
+
+    # y carries one rounding to x's dtype and the fp32 product with w
+    assert within(yg.detach(), yc.detach(), max(ulp, 2.0 ** -23))
+    dxg = bg.grad[..., :D] if case == "bf16_heads_view" else bg.grad
+    assert within(dxg, xc.grad, max(ulp, 2.0 ** -20))
+    if case == "bf16_heads_view":
+        assert not bg.grad[..., D:].any()
+    # dw sums round_x(x r) dy over rows: for 16-bit x a rounding of x r that
+    # lands one ulp (2^-8 for bf16) away in a few elements (r is summed in
+    # another order) moves the sum by ~1e-5 of its max-norm
+    dwg, dwc = mg.weight.grad.double().cpu(), mc.weight.grad.double()
+    tol = 1e-5 if dt == torch.float32 else 1e-4
+    assert ((dwg - dwc).abs().max() / dwc.abs().max()).item() < tol
