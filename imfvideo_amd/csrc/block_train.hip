@@ -435,3 +435,59 @@ extern "C" int sla2h_rmsnorm_bwd(const void* x, int dtype, int64_t rows, int D, 
   col_sum_kernel<<<D, 256, 0, st>>>(dwp, nb, D, dw);
   return (int)hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------
+// RoPE of the training forward (models/imf_dit_video.py:266-284): channel pairs
+// (2i, 2i+1) of x (b, l, H, hd) rotated by the angle of token l, in fp32, cast
+// back: (re c - im s, re s + im c).  The backward is the rotation by -angle of
+// the output gradient (inverse = 1): (dre c + dim s, -dre s + dim c).  x may be
+// a strided view (unit channel stride); out is contiguous (b, l, H, hd).
+// One thread per channel pair.
+// ---------------------------------------------------------------------------
+namespace sla2h {
+namespace {
+
+template <int DT>
+__global__ __launch_bounds__(256) void rope_kernel(const void* __restrict__ X, int64_t B, int64_t L,
+                                                   int H, int hd, int64_t sb, int64_t sl,
+                                                   int64_t sh, const float* __restrict__ COS,
+                                                   const float* __restrict__ SIN, float sgn,
+                                                   void* __restrict__ OUT) {
+  const int hp = hd >> 1;
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= B * L * H * hp) return;
+  const int i = (int)(idx % hp);
+  int64_t t = idx / hp;
+  const int h = (int)(t % H);
+  t /= H;
+  const int64_t l = t % L, b = t / L;
+  const int64_t xi = b * sb + l * sl + h * sh + 2 * i;
+  const float re = ld1<DT>(X, xi), im = ld1<DT>(X, xi + 1);
+  const float c = COS[l * hp + i], s = sgn * SIN[l * hp + i];
+  const int64_t oi = 2 * idx;
+  st1<DT>(OUT, oi, re * c - im * s);
+  st1<DT>(OUT, oi + 1, re * s + im * c);
+}
+
+}  // namespace
+}  // namespace sla2h
+
+extern "C" int sla2h_rope(const void* x, int dtype, int64_t B, int64_t L, int H, int hd,
+                          int64_t sb, int64_t sl, int64_t sh, const float* cos_t,
+                          const float* sin_t, int inverse, void* out, void* stream) {
+  SLA2H_CHECK_ARG(x && cos_t && sin_t && out);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16 || dtype == kF32);
+  SLA2H_CHECK_ARG(B > 0 && L > 0 && H > 0 && hd > 0 && hd % 2 == 0);
+  const int64_t n = B * L * H * (hd / 2);
+  const unsigned grid = grid_of(n);
+  SLA2H_CHECK_ARG(grid > 0);
+  const float sgn = inverse ? -1.f : 1.f;
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SLA2H_DTYPE_BF16)
+    rope_kernel<SLA2H_DTYPE_BF16><<<grid, 256, 0, st>>>(x, B, L, H, hd, sb, sl, sh, cos_t, sin_t, sgn, out);
+  else if (dtype == SLA2H_DTYPE_F16)
+    rope_kernel<SLA2H_DTYPE_F16><<<grid, 256, 0, st>>>(x, B, L, H, hd, sb, sl, sh, cos_t, sin_t, sgn, out);
+  else
+    rope_kernel<kF32><<<grid, 256, 0, st>>>(x, B, L, H, hd, sb, sl, sh, cos_t, sin_t, sgn, out);
+  return (int)hipGetLastError();
+}

@@ -140,9 +140,30 @@ class SwiGLUMlp(nn.Module):
         return self.w2(self.act(self.w1(x), self.w3(x)))
 
 
+class _RopeFunction(torch.autograd.Function):
+    """RoPE on the GPU: one HIP kernel forward (sla2h_rope), the inverse rotation
+    of the output gradient backward."""
+
+    @staticmethod
+    def forward(ctx, x, rope_cos, rope_sin):
+        from . import ops
+        ctx.save_for_backward(rope_cos, rope_sin)
+        return ops.rope(x, rope_cos, rope_sin)
+
+    @staticmethod
+    def backward(ctx, dout):
+        from . import ops
+        rope_cos, rope_sin = ctx.saved_tensors
+        return ops.rope(dout.contiguous(), rope_cos, rope_sin, inverse=True), None, None
+
+
 def apply_rotary_pos_emb(x, rope_cos, rope_sin):
     """Rotate channel pairs (x[..., 2i], x[..., 2i+1]) of x (b, l, H, hd) by the
-    angles of rope_cos / rope_sin (l, hd // 2)."""
+    angles of rope_cos / rope_sin (l, hd // 2).  GPU tensors run the HIP kernel
+    (sla2h_rope) forward and backward; CPU tensors the eager expression."""
+    if (x.is_cuda and x.dim() == 4 and x.dtype in (torch.float32, torch.bfloat16, torch.float16)
+            and rope_cos.dtype == torch.float32 and rope_sin.dtype == torch.float32):
+        return _RopeFunction.apply(x, rope_cos, rope_sin)
     xf = x.float()
     re, im = xf[..., 0::2], xf[..., 1::2]
     c, s = rope_cos[None, :, None, :], rope_sin[None, :, None, :]

@@ -722,3 +722,27 @@ def rmsnorm_bwd(dy, x, w, eps):
         float(eps), dx.data_ptr(), dw.data_ptr(), ws.data_ptr(), _stream(x.device)),
         "sla2h_rmsnorm_bwd")
     return dx, dw
+
+
+# ---------------------------------------------------------------------------
+# DiT block, training forward / backward: RoPE (models/imf_dit_video.py:266-284)
+# ---------------------------------------------------------------------------
+def rope(x, cos_t, sin_t, inverse=False):
+    """Pairs (2i, 2i+1) of x (b, l, H, hd) rotated by the angles of each token
+    (by the negated angles with inverse); fp32 arithmetic, contiguous, x's dtype."""
+    _need_gpu(x, cos_t, sin_t)
+    if x.dim() != 4 or x.dtype not in _SITU_DTYPES or x.shape[-1] % 2:
+        raise ValueError(f"rope: expected (b, l, H, even hd) float input, got {tuple(x.shape)}")
+    if x.stride(-1) != 1:
+        x = x.contiguous()
+    B, L, H, hd = x.shape
+    cos_t = cos_t.to(torch.float32).contiguous()
+    sin_t = sin_t.to(torch.float32).contiguous()
+    if tuple(cos_t.shape) != (L, hd // 2) or tuple(sin_t.shape) != (L, hd // 2):
+        raise ValueError("rope: tables must be (l, hd // 2)")
+    out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+    _lib.check(_lib.load().sla2h_rope(
+        x.data_ptr(), _SITU_DTYPES[x.dtype], B, L, H, hd, x.stride(0), x.stride(1), x.stride(2),
+        cos_t.data_ptr(), sin_t.data_ptr(), int(bool(inverse)), out.data_ptr(),
+        _stream(x.device)), "sla2h_rope")
+    return out

@@ -275,6 +275,19 @@ int sla2h_rmsnorm_bwd(const void* x, int dtype, int64_t rows, int D, int64_t sx,
                       const float* dy, float eps, void* dx, float* dw, void* workspace,
                       void* stream);
 
+/*
+ * RoPE of the DiT block's training forward and its backward: channel pairs
+ * (2i, 2i+1) of x (B, L, H, hd), strides sb / sl / sh elements and unit
+ * channel stride, rotated by the angles of token l (cos_t / sin_t (L, hd/2)
+ * fp32) in fp32 and written contiguous (B, L, H, hd) in x's dtype; inverse = 1
+ * rotates by the negated angles (the backward of the output gradient).
+ * Replaces apply_rotary_pos_emb and its autograd backward
+ * (models/imf_dit_video.py:266-284).
+ */
+int sla2h_rope(const void* x, int dtype, int64_t B, int64_t L, int H, int hd, int64_t sb,
+               int64_t sl, int64_t sh, const float* cos_t, const float* sin_t, int inverse,
+               void* out, void* stream);
+
 /* ---- training forward (the module's autograd forward) ------------------ */
 
 /*

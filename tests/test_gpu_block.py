@@ -149,3 +149,48 @@ def test_rmsnorm_forward_backward(case):
     dwg, dwc = mg.weight.grad.double().cpu(), mc.weight.grad.double()
     tol = 1e-5 if dt == torch.float32 else 1e-4
     assert ((dwg - dwc).abs().max() / dwc.abs().max()).item() < tol
+
+
+def _rope_eager(x, c, s):
+    """apply_rotary_pos_emb's eager expression (models/imf_dit_video.py:266-284)."""
+    xf = x.float()
+    re, im = xf[..., 0::2], xf[..., 1::2]
+    c, s = c[None, :, None, :], s[None, :, None, :]
+    return torch.stack([re * c - im * s, re * s + im * c], dim=-1).flatten(-2).to(x.dtype)
+
+
+@pytest.mark.parametrize("case", ["bf16_heads", "bf16_shared_key", "f16_heads", "f32_heads"])
+def test_rope_forward_backward(case):
+    """RoPE forward and backward (the inverse rotation of the gradient) on
+    strided views as the MLA sublayer passes them, against the eager expression
+    on the CPU: within 2 ulp of the dtype per element, plus 2 ulp of the largest
+    magnitude (the cosine / sine products round in another order)."""
+    from imfvideo_amd.imf_dit_video import apply_rotary_pos_emb, precompute_axial_rope_3d
+    say("rope", case)
+    dt = {"bf16": torch.bfloat16, "f16": torch.float16, "f32": torch.float32}[case.split("_")[0]]
+    g = torch.Generator().manual_seed(len(case))
+    cos, sin = precompute_axial_rope_3d(32, (3, 8, 8), 0, axis_dims=(8, 12, 12))
+    L = cos.shape[0]
+    if case == "bf16_shared_key":
+        base = (torch.randn(2, L, 128 + 32, generator=g) * 2).to(dt)
+        view = lambda t: t[..., 128:].unsqueeze(2)            # (b, l, 1, dr)
+    else:
+        base = (torch.randn(2, L, 4, 64, generator=g) * 2).to(dt)
+        view = lambda t: t[..., 32:]                          # (b, l, H, dr) band
+    dout = torch.randn(view(base).shape, generator=g)
+    xc = base.clone().requires_grad_(True)
+    yc = _rope_eager(view(xc), cos, sin)
+    yc.backward(dout.to(dt))
+    xg = base.cuda().requires_grad_(True)
+    yg = apply_rotary_pos_emb(view(xg), cos.cuda(), sin.cuda())
+    assert yg.dtype == dt and yg.shape == yc.shape
+    yg.backward(dout.to(dt).cuda())
+    torch.cuda.synchronize()
+    u = ULP[dt] if dt != torch.float32 else 2.0 ** -22
+
+    def within(a, b):
+        a, b = a.double().cpu(), b.double().cpu()
+        return bool(((a - b).abs() <= 2 * u * b.abs() + 2 * u * b.abs().max()).all())
+
+    assert within(yg.detach(), yc.detach())
+    assert within(xg.grad, xc.grad)
