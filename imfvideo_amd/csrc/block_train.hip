@@ -363,9 +363,150 @@ __global__ __launch_bounds__(256) void col_sum_kernel(const float* __restrict__ 
   if (threadIdx.x == 0) out[c] = red[0];
 }
 
+// Vectorised variant for D = 8 LPR (LPR a power of two <= 64 lanes per row):
+// lane l of a wave owns channels 8 (l % LPR) .. +7 of row slot l / LPR, so a
+// wave covers 64 / LPR rows per pass with 16-byte accesses (two for fp32).
+template <int DT>
+__device__ inline void ld8(const void* p, int64_t i, float (&x)[8]) {
+  if (DT == kF32) {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i + 4);
+    x[0] = a.x, x[1] = a.y, x[2] = a.z, x[3] = a.w, x[4] = b.x, x[5] = b.y, x[6] = b.z, x[7] = b.w;
+  } else {
+    Vec<DT == kF32 ? SLA2H_DTYPE_BF16 : DT>::ld(p, i, x);
+  }
+}
+template <int DT>
+__device__ inline void st8(void* p, int64_t i, const float (&x)[8]) {
+  if (DT == kF32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(p) + i) = make_float4(x[0], x[1], x[2], x[3]);
+    *reinterpret_cast<float4*>(static_cast<float*>(p) + i + 4) = make_float4(x[4], x[5], x[6], x[7]);
+  } else {
+    Vec<DT == kF32 ? SLA2H_DTYPE_BF16 : DT>::st(p, i, x);
+  }
+}
+__device__ inline void ld8f(const float* p, int64_t i, float (&x)[8]) { ld8<kF32>(p, i, x); }
+template <int LPR>
+__device__ inline float group_sum(float v) {  // over the LPR lanes of a row (aligned groups)
+#pragma unroll
+  for (int m = LPR / 2; m >= 1; m >>= 1) v += __shfl_xor(v, m, 64);
+  return v;
+}
+
+template <int DT, int LPR>
+__global__ __launch_bounds__(256) void rms_fwd_vec_kernel(const void* __restrict__ X, int64_t rows,
+                                                          int64_t sx, const float* __restrict__ W,
+                                                          float eps, float* __restrict__ Y) {
+  constexpr int D = 8 * LPR, RPW = 64 / LPR;
+  const int l = threadIdx.x & 63;
+  const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + l / LPR;
+  const int c0 = 8 * (l % LPR);
+  const bool ok = row < rows;
+  float x[8];
+  if (ok)
+    ld8<DT>(X, row * sx + c0, x);
+  else
+    for (int e = 0; e < 8; ++e) x[e] = 0.f;
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+  const float r = 1.f / sqrtf(group_sum<LPR>(ss) / (float)D + eps);
+  float w[8], y[8];
+  ld8f(W, c0, w);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = round_to<DT>(x[e] * r) * w[e];
+  if (ok) st8<kF32>(Y, row * D + c0, y);
+}
+
+// backward: 4 passes of 64 / LPR rows per wave, loads first; dw partials of the
+// workgroup's 16 * 64 / LPR rows
+template <int DT, int LPR>
+__global__ __launch_bounds__(256) void rms_bwd_vec_kernel(const void* __restrict__ X, int64_t rows,
+                                                          int64_t sx, const float* __restrict__ W,
+                                                          const float* __restrict__ DY, float eps,
+                                                          void* __restrict__ DX,
+                                                          float* __restrict__ DWP) {
+  constexpr int D = 8 * LPR, RPW = 64 / LPR, P = 4;
+  __shared__ float part[4][D];
+  const int w = threadIdx.x >> 6, l = threadIdx.x & 63;
+  const int c0 = 8 * (l % LPR);
+  const int64_t row0 = (int64_t)blockIdx.x * (4 * P * RPW);
+  float x[P][8], dy[P][8], wv[8], dwacc[8];
+  ld8f(W, c0, wv);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) dwacc[e] = 0.f;
+#pragma unroll
+  for (int k = 0; k < P; ++k) {
+    const int64_t row = row0 + ((int64_t)(k * 4 + w)) * RPW + l / LPR;
+    if (row < rows) {
+      ld8<DT>(X, row * sx + c0, x[k]);
+      ld8f(DY, row * D + c0, dy[k]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) x[k][e] = dy[k][e] = 0.f;
+    }
+  }
+#pragma unroll
+  for (int k = 0; k < P; ++k) {
+    const int64_t row = row0 + ((int64_t)(k * 4 + w)) * RPW + l / LPR;
+    float ss = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) ss += x[k][e] * x[k][e];
+    const float r = 1.f / sqrtf(group_sum<LPR>(ss) / (float)D + eps);
+    float g[8], gx = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      g[e] = round_to<DT>(dy[k][e] * wv[e]);
+      gx += g[e] * x[k][e];
+      dwacc[e] += round_to<DT>(x[k][e] * r) * dy[k][e];  // rows past the end add 0
+    }
+    const float mgx = group_sum<LPR>(gx) / (float)D;
+    const float r3 = r * r * r;
+    float dx[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) dx[e] = r * g[e] - x[k][e] * r3 * mgx;
+    if (row < rows) st8<DT>(DX, row * D + c0, dx);
+  }
+  // combine the wave's row slots (lanes l, l ^ LPR, ...), fixed order
+#pragma unroll
+  for (int e = 0; e < 8; ++e)
+#pragma unroll
+    for (int m = LPR; m < 64; m <<= 1) dwacc[e] += __shfl_xor(dwacc[e], m, 64);
+  if (l < LPR)
+#pragma unroll
+    for (int e = 0; e < 8; ++e) part[w][c0 + e] = dwacc[e];
+  __syncthreads();
+  for (int c = threadIdx.x; c < D; c += 256)
+    DWP[(int64_t)blockIdx.x * D + c] = (part[0][c] + part[1][c]) + (part[2][c] + part[3][c]);
+}
+
+// lanes per row of the vectorised kernels for this shape, or 0
+template <int DT>
+int rms_vec_lpr(const void* x, int D, int64_t sx) {
+  if (D % 8 || D > 512 || (D & (D - 1)) || reinterpret_cast<uintptr_t>(x) % 16 ||
+      sx % (DT == kF32 ? 4 : 8))
+    return 0;
+  return D / 8;
+}
+
 template <int DT>
 void launch_rms_fwd(const void* x, int64_t rows, int D, int64_t sx, const float* w, float eps,
                     float* y, hipStream_t st) {
+  const int lpr = rms_vec_lpr<DT>(x, D, sx);
+  if (lpr) {
+    const unsigned g = (unsigned)((rows + 4 * (64 / lpr) - 1) / (4 * (64 / lpr)));
+#define SLA2H_RMSF(LPR) rms_fwd_vec_kernel<DT, LPR><<<g, 256, 0, st>>>(x, rows, sx, w, eps, y)
+    switch (lpr) {
+      case 1: SLA2H_RMSF(1); return;
+      case 2: SLA2H_RMSF(2); return;
+      case 4: SLA2H_RMSF(4); return;
+      case 8: SLA2H_RMSF(8); return;
+      case 16: SLA2H_RMSF(16); return;
+      case 32: SLA2H_RMSF(32); return;
+      default: SLA2H_RMSF(64); return;
+    }
+#undef SLA2H_RMSF
+  }
   const unsigned grid = (unsigned)((rows + 3) / 4);
   if (D <= 64)
     rms_fwd_kernel<DT, 1><<<grid, 256, 0, st>>>(x, rows, D, sx, w, eps, y);
@@ -376,9 +517,32 @@ void launch_rms_fwd(const void* x, int64_t rows, int D, int64_t sx, const float*
   else
     rms_fwd_kernel<DT, 16><<<grid, 256, 0, st>>>(x, rows, D, sx, w, eps, y);
 }
+// rows per workgroup of the backward for this shape (partial dw rows)
+template <int DT>
+int64_t rms_bwd_rows_per_block(const void* x, int D, int64_t sx) {
+  const int lpr = rms_vec_lpr<DT>(x, D, sx);
+  return lpr ? 16 * (64 / lpr) : kRmsRows;
+}
+
 template <int DT>
 void launch_rms_bwd(const void* x, int64_t rows, int D, int64_t sx, const float* w, const float* dy,
                     float eps, void* dx, float* dwp, hipStream_t st) {
+  const int lpr = rms_vec_lpr<DT>(x, D, sx);
+  if (lpr) {
+    const int64_t rpb = 16 * (64 / lpr);
+    const unsigned g = (unsigned)((rows + rpb - 1) / rpb);
+#define SLA2H_RMSB(LPR) rms_bwd_vec_kernel<DT, LPR><<<g, 256, 0, st>>>(x, rows, sx, w, dy, eps, dx, dwp)
+    switch (lpr) {
+      case 1: SLA2H_RMSB(1); return;
+      case 2: SLA2H_RMSB(2); return;
+      case 4: SLA2H_RMSB(4); return;
+      case 8: SLA2H_RMSB(8); return;
+      case 16: SLA2H_RMSB(16); return;
+      case 32: SLA2H_RMSB(32); return;
+      default: SLA2H_RMSB(64); return;
+    }
+#undef SLA2H_RMSB
+  }
   const unsigned grid = (unsigned)((rows + kRmsRows - 1) / kRmsRows);
   if (D <= 64)
     rms_bwd_kernel<DT, 1><<<grid, 256, 0, st>>>(x, rows, D, sx, w, dy, eps, dx, dwp);
@@ -420,7 +584,10 @@ extern "C" int sla2h_rmsnorm_bwd(const void* x, int dtype, int64_t rows, int D, 
   SLA2H_CHECK_ARG(x && w && dy && dx && dw && workspace);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16 || dtype == kF32);
   SLA2H_CHECK_ARG(rows > 0 && D > 0 && D <= 1024 && sx >= D);
-  const int64_t nb = (rows + kRmsRows - 1) / kRmsRows;
+  const int64_t rpb = dtype == SLA2H_DTYPE_BF16 ? rms_bwd_rows_per_block<SLA2H_DTYPE_BF16>(x, D, sx)
+                      : dtype == SLA2H_DTYPE_F16 ? rms_bwd_rows_per_block<SLA2H_DTYPE_F16>(x, D, sx)
+                                                 : rms_bwd_rows_per_block<kF32>(x, D, sx);
+  const int64_t nb = (rows + rpb - 1) / rpb;
   SLA2H_CHECK_ARG(nb < (1ll << 31));
   hipStream_t st = static_cast<hipStream_t>(stream);
   float* dwp = static_cast<float*>(workspace);
