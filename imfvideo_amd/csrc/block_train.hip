@@ -658,3 +658,96 @@ extern "C" int sla2h_rope(const void* x, int dtype, int64_t B, int64_t L, int H,
     rope_kernel<kF32><<<grid, 256, 0, st>>>(x, B, L, H, hd, sb, sl, sh, cos_t, sin_t, sgn, out);
   return (int)hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------
+// ReZero residual of the block (models/imf_dit_video.py:529-532):
+// y = x + a s with x fp32 (rows, D), a (rows, D) 16-bit or fp32, s fp32 (D);
+// the product and the sum round separately (no contraction), as in the eager
+// expression.  Backward: da = round_a(dy s), ds = sum over rows of dy a (per
+// 16-row-block partials, then the fixed-order column sum), dx = dy (no kernel).
+// ---------------------------------------------------------------------------
+namespace sla2h {
+namespace {
+
+template <int DT>
+__global__ __launch_bounds__(256) void residual_fwd_kernel(const float* __restrict__ X,
+                                                           const void* __restrict__ A,
+                                                           const float* __restrict__ S,
+                                                           int64_t rows, int D,
+                                                           float* __restrict__ Y) {
+#pragma clang fp contract(off)
+  const int64_t idx = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (idx >= rows * D) return;
+  const int c = (int)(idx % D);
+  const float p = ld1<DT>(A, idx) * S[c];
+  Y[idx] = X[idx] + p;
+}
+
+// one workgroup per 16 rows, thread t owns columns t, t + 256, ...
+template <int DT>
+__global__ __launch_bounds__(256) void residual_bwd_kernel(const float* __restrict__ DY,
+                                                           const void* __restrict__ A,
+                                                           const float* __restrict__ S,
+                                                           int64_t rows, int D,
+                                                           void* __restrict__ DA,
+                                                           float* __restrict__ DSP) {
+#pragma clang fp contract(off)
+  const int64_t r0 = (int64_t)blockIdx.x * kRmsRows;
+  for (int c = threadIdx.x; c < D; c += 256) {
+    const float s = S[c];
+    float acc = 0.f;
+    for (int k = 0; k < kRmsRows; ++k) {
+      const int64_t row = r0 + k;
+      if (row >= rows) break;
+      const int64_t i = row * D + c;
+      const float dy = DY[i];
+      st1<DT>(DA, i, dy * s);
+      acc += dy * ld1<DT>(A, i);
+    }
+    DSP[(int64_t)blockIdx.x * D + c] = acc;
+  }
+}
+
+}  // namespace
+}  // namespace sla2h
+
+extern "C" int sla2h_residual_scale_fwd(const float* x, const void* a, int dtype, const float* s,
+                                        int64_t rows, int D, float* y, void* stream) {
+  SLA2H_CHECK_ARG(x && a && s && y && rows > 0 && D > 0);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16 || dtype == kF32);
+  const unsigned grid = grid_of(rows * D);
+  SLA2H_CHECK_ARG(grid > 0);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SLA2H_DTYPE_BF16)
+    residual_fwd_kernel<SLA2H_DTYPE_BF16><<<grid, 256, 0, st>>>(x, a, s, rows, D, y);
+  else if (dtype == SLA2H_DTYPE_F16)
+    residual_fwd_kernel<SLA2H_DTYPE_F16><<<grid, 256, 0, st>>>(x, a, s, rows, D, y);
+  else
+    residual_fwd_kernel<kF32><<<grid, 256, 0, st>>>(x, a, s, rows, D, y);
+  return (int)hipGetLastError();
+}
+
+extern "C" size_t sla2h_residual_scale_bwd_workspace_bytes(int64_t rows, int D) {
+  return sla2h_rmsnorm_bwd_workspace_bytes(rows, D);
+}
+
+extern "C" int sla2h_residual_scale_bwd(const float* dy, const void* a, int dtype, const float* s,
+                                        int64_t rows, int D, void* da, float* ds, void* workspace,
+                                        void* stream) {
+  SLA2H_CHECK_ARG(dy && a && s && da && ds && workspace && rows > 0 && D > 0);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16 || dtype == kF32);
+  const int64_t nb = (rows + kRmsRows - 1) / kRmsRows;
+  SLA2H_CHECK_ARG(nb < (1ll << 31));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* dsp = static_cast<float*>(workspace);
+  if (dtype == SLA2H_DTYPE_BF16)
+    residual_bwd_kernel<SLA2H_DTYPE_BF16><<<(unsigned)nb, 256, 0, st>>>(dy, a, s, rows, D, da, dsp);
+  else if (dtype == SLA2H_DTYPE_F16)
+    residual_bwd_kernel<SLA2H_DTYPE_F16><<<(unsigned)nb, 256, 0, st>>>(dy, a, s, rows, D, da, dsp);
+  else
+    residual_bwd_kernel<kF32><<<(unsigned)nb, 256, 0, st>>>(dy, a, s, rows, D, da, dsp);
+  int err = (int)hipGetLastError();
+  if (err) return err;
+  col_sum_kernel<<<D, 256, 0, st>>>(dsp, nb, D, ds);
+  return (int)hipGetLastError();
+}

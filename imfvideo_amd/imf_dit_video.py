@@ -250,6 +250,32 @@ class MLAAttention(nn.Module):
         return self.out_proj(attn)
 
 
+class _ResidualScaleFunction(torch.autograd.Function):
+    """x + a * scale on the GPU: one HIP kernel forward, one backward (da and the
+    scale gradient); the gradient of x is the output gradient itself."""
+
+    @staticmethod
+    def forward(ctx, x, a, scale):
+        from . import ops
+        ctx.save_for_backward(a, scale)
+        return ops.residual_scale_fwd(x, a, scale)
+
+    @staticmethod
+    def backward(ctx, dy):
+        from . import ops
+        a, scale = ctx.saved_tensors
+        da, ds = ops.residual_scale_bwd(dy, a, scale)
+        return dy, da, ds.to(scale.dtype)
+
+
+def _residual(x, a, scale):
+    """x + a * scale; GPU tensors (fp32 x and scale) run the fused kernels."""
+    if (x.is_cuda and x.dtype == torch.float32 and scale.dtype == torch.float32
+            and a.shape == x.shape and a.dtype in (torch.float32, torch.bfloat16, torch.float16)):
+        return _ResidualScaleFunction.apply(x, a, scale)
+    return x + a * scale
+
+
 class TransformerBlock(nn.Module):
     """x += attn(norm1(x)) * attn_scale;  x += mlp(norm2(x)) * mlp_scale
     (vector gates initialised to zero)."""
@@ -280,5 +306,5 @@ class TransformerBlock(nn.Module):
                                                        init_constant=weight_init_constant)
 
     def forward(self, x, rope_cos, rope_sin):
-        x = x + self.attn(self.norm1(x), rope_cos, rope_sin) * self.attn_scale
-        return x + self.mlp(self.norm2(x)) * self.mlp_scale
+        x = _residual(x, self.attn(self.norm1(x), rope_cos, rope_sin), self.attn_scale)
+        return _residual(x, self.mlp(self.norm2(x)), self.mlp_scale)

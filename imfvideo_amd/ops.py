@@ -746,3 +746,41 @@ def rope(x, cos_t, sin_t, inverse=False):
         cos_t.data_ptr(), sin_t.data_ptr(), int(bool(inverse)), out.data_ptr(),
         _stream(x.device)), "sla2h_rope")
     return out
+
+
+# ---------------------------------------------------------------------------
+# DiT block, training forward / backward: ReZero residual
+# (models/imf_dit_video.py:529-532)
+# ---------------------------------------------------------------------------
+def residual_scale_fwd(x, a, s):
+    """y = x + a * s (fp32; product and sum rounded separately)."""
+    _need_gpu(x, a, s)
+    x = x.contiguous()
+    a = a.contiguous()
+    D = x.shape[-1]
+    s = s.detach().to(torch.float32).contiguous()
+    y = torch.empty_like(x)
+    _lib.check(_lib.load().sla2h_residual_scale_fwd(
+        x.data_ptr(), a.data_ptr(), _SITU_DTYPES[a.dtype], s.data_ptr(), x.numel() // D, D,
+        y.data_ptr(), _stream(x.device)), "sla2h_residual_scale_fwd")
+    return y
+
+
+def residual_scale_bwd(dy, a, s):
+    """(da in a's dtype, ds fp32) of residual_scale_fwd; dx is dy itself."""
+    _need_gpu(dy, a, s)
+    dy = dy.to(torch.float32).contiguous()
+    a = a.contiguous()
+    D = a.shape[-1]
+    rows = a.numel() // D
+    s = s.detach().to(torch.float32).contiguous()
+    da = torch.empty_like(a)
+    ds = torch.empty(D, device=a.device, dtype=torch.float32)
+    lib = _lib.load()
+    ws = torch.empty(lib.sla2h_residual_scale_bwd_workspace_bytes(rows, D) // 4,
+                     device=a.device, dtype=torch.float32)
+    _lib.check(lib.sla2h_residual_scale_bwd(
+        dy.data_ptr(), a.data_ptr(), _SITU_DTYPES[a.dtype], s.data_ptr(), rows, D,
+        da.data_ptr(), ds.data_ptr(), ws.data_ptr(), _stream(a.device)),
+        "sla2h_residual_scale_bwd")
+    return da, ds

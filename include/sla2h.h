@@ -288,6 +288,22 @@ int sla2h_rope(const void* x, int dtype, int64_t B, int64_t L, int H, int hd, in
                int64_t sl, int64_t sh, const float* cos_t, const float* sin_t, int inverse,
                void* out, void* stream);
 
+/*
+ * ReZero residual of the DiT block's training forward and its backward:
+ * y = x + a s (x, y fp32 (rows, D) contiguous; a (rows, D) contiguous in
+ * dtype SLA2H_DTYPE_F16 / SLA2H_DTYPE_BF16 / 2 (fp32); s fp32 (D)), product and
+ * sum rounded separately.  Backward: da = round_a(dy s), ds = sum over rows of
+ * dy a (deterministic two-step sum in `workspace` of
+ * sla2h_residual_scale_bwd_workspace_bytes).  Replaces `x + sublayer(x) * scale`
+ * and its autograd backward (models/imf_dit_video.py:529-532).
+ */
+int sla2h_residual_scale_fwd(const float* x, const void* a, int dtype, const float* s,
+                             int64_t rows, int D, float* y, void* stream);
+size_t sla2h_residual_scale_bwd_workspace_bytes(int64_t rows, int D);
+int sla2h_residual_scale_bwd(const float* dy, const void* a, int dtype, const float* s,
+                             int64_t rows, int D, void* da, float* ds, void* workspace,
+                             void* stream);
+
 /* ---- training forward (the module's autograd forward) ------------------ */
 
 /*

@@ -194,3 +194,28 @@ def test_rope_forward_backward(case):
 
     assert within(yg.detach(), yc.detach())
     assert within(xg.grad, xc.grad)
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
+def test_residual_scale_forward_backward(dt):
+    """x + a * scale (the block's ReZero residual): forward and da bit-identical
+    to the eager expression on the CPU (product and sum rounded separately);
+    the scale gradient, a sum over rows in another order, within 1e-6."""
+    from imfvideo_amd.imf_dit_video import _residual
+    say("residual scale", dt)
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(2, 333, 512, generator=g)
+    a = torch.randn(2, 333, 512, generator=g).to(dt)
+    s = (0.1 * torch.randn(512, generator=g))
+    dy = torch.randn(2, 333, 512, generator=g)
+    xc, ac, sc = (t.clone().requires_grad_(True) for t in (x, a, s))
+    yc = xc + ac * sc
+    yc.backward(dy)
+    xg, ag, sg = (t.cuda().requires_grad_(True) for t in (x, a, s))
+    yg = _residual(xg, ag, sg)
+    yg.backward(dy.cuda())
+    torch.cuda.synchronize()
+    assert torch.equal(yg.detach().cpu(), yc.detach())
+    assert torch.equal(xg.grad.cpu(), xc.grad)
+    assert torch.equal(ag.grad.cpu(), ac.grad)
+    assert ((sg.grad.cpu() - sc.grad).abs().max() / sc.grad.abs().max()).item() < 1e-6
