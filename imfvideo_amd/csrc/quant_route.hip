@@ -617,16 +617,22 @@ static int launch_quant_pool(const QuantPoolArgs& a, int ntens, int dtype, hipSt
 // one block of one (b, h) per workgroup, one thread per channel, sequential
 // fp32 sum over the block's real rows, then / count, then the optional
 // projection out[e] = sum_d mean[d] proj[e][d] (sequential, no contraction).
-template <typename T16>
-__global__ __launch_bounds__(64) void pool_blocks_kernel(const uint16_t* __restrict__ x, int64_t L,
+// fp32 input "storage tag" for the pooling kernel (16-bit tags: common.h)
+struct F32In {
+  __device__ static inline float to_f32(float f) { return f; }
+};
+
+template <typename TS, typename Raw>
+__global__ __launch_bounds__(64) void pool_blocks_kernel(const Raw* __restrict__ x, int64_t L,
                                                         int blk, int nblk,
                                                         const float* __restrict__ proj,
                                                         int transposed, float* __restrict__ out) {
+  using T16 = TS;
   __shared__ float vec[kTile];
   const int j = blockIdx.x, bh = blockIdx.y, d = threadIdx.x;
   const int64_t r0 = (int64_t)j * blk;
   const int cnt = (int)((L - r0) < blk ? (L - r0) : blk);
-  const uint16_t* src = x + ((int64_t)bh * L + r0) * kTile + d;
+  const Raw* src = x + ((int64_t)bh * L + r0) * kTile + d;
   float acc = 0.f;
   int rr = 0;
   for (; rr + 16 <= cnt; rr += 16) {  // 16 loads in flight, then the adds in row order
@@ -656,17 +662,22 @@ extern "C" int sla2h_pool_blocks(const void* x, int dtype, int64_t BH, int64_t L
                                  const float* proj, int transposed, float* out, void* stream) {
   SLA2H_CHECK_ARG(x && out);
   SLA2H_CHECK_ARG(D == kTile && blk >= 1 && blk <= 4096);
-  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16 || dtype == 2);
   SLA2H_CHECK_ARG(BH > 0 && BH <= 65535 && L > 0);
   const int64_t nblk = (L + blk - 1) / blk;
   SLA2H_CHECK_ARG(nblk < (1ll << 31));
   dim3 grid((unsigned)nblk, (unsigned)BH);
   hipStream_t st = static_cast<hipStream_t>(stream);
   auto X = static_cast<const uint16_t*>(x);
-  if (dtype == SLA2H_DTYPE_BF16)
-    pool_blocks_kernel<BF16><<<grid, kTile, 0, st>>>(X, L, blk, (int)nblk, proj, transposed, out);
+  if (dtype == 2)
+    pool_blocks_kernel<F32In, float><<<grid, kTile, 0, st>>>(static_cast<const float*>(x), L, blk,
+                                                            (int)nblk, proj, transposed, out);
+  else if (dtype == SLA2H_DTYPE_BF16)
+    pool_blocks_kernel<BF16, uint16_t><<<grid, kTile, 0, st>>>(X, L, blk, (int)nblk, proj,
+                                                              transposed, out);
   else
-    pool_blocks_kernel<F16><<<grid, kTile, 0, st>>>(X, L, blk, (int)nblk, proj, transposed, out);
+    pool_blocks_kernel<F16, uint16_t><<<grid, kTile, 0, st>>>(X, L, blk, (int)nblk, proj,
+                                                             transposed, out);
   return (int)hipGetLastError();
 }
 

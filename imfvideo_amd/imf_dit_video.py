@@ -96,8 +96,9 @@ class _SituMulFunction(torch.autograd.Function):
 class SituAndMul(nn.Module):
     """situ(g) * up with situ(g) = beta tanh(g / beta) sigmoid(g); with
     linear_beta the up branch is soft-clamped to linear_beta tanh(up / linear_beta).
-    GPU tensors run the fused kernels (sla2h_situ_mul_fwd / _bwd); CPU tensors
-    the eager fp32 expression."""
+    GPU tensors of one 16-bit or fp32 dtype run the fused kernels
+    (sla2h_situ_mul_fwd / _bwd); anything else (CPU tensors, mixed or other
+    dtypes) the eager fp32 expression, each branch cast to fp32 on its own."""
 
     def __init__(self, beta=1.0, linear_beta=None):
         super().__init__()
@@ -110,9 +111,8 @@ class SituAndMul(nn.Module):
             gate, up = x[..., :d], x[..., d:]
         else:
             gate = x
-        if gate.is_cuda:
-            if up.dtype != gate.dtype:
-                up = up.to(gate.dtype)
+        if (gate.is_cuda and up.is_cuda and up.dtype == gate.dtype
+                and gate.dtype in (torch.float16, torch.bfloat16, torch.float32)):
             return _SituMulFunction.apply(gate, up, float(self.beta),
                                           None if self.linear_beta is None
                                           else float(self.linear_beta))
@@ -269,8 +269,12 @@ class _ResidualScaleFunction(torch.autograd.Function):
 
 
 def _residual(x, a, scale):
-    """x + a * scale; GPU tensors (fp32 x and scale) run the fused kernels."""
-    if (x.is_cuda and x.dtype == torch.float32 and scale.dtype == torch.float32
+    """x + a * scale.  The fused kernels take fp32 x, an a of x's shape on the
+    same device and a (D,) fp32 scale (D = x.shape[-1]): they read scale[c]
+    for every channel c.  Other operands (a broadcast scale, CPU tensors) run
+    the eager expression."""
+    if (x.is_cuda and a.is_cuda and scale.is_cuda and x.dtype == torch.float32
+            and scale.dtype == torch.float32 and tuple(scale.shape) == (x.shape[-1],)
             and a.shape == x.shape and a.dtype in (torch.float32, torch.bfloat16, torch.float16)):
         return _ResidualScaleFunction.apply(x, a, scale)
     return x + a * scale

@@ -1,18 +1,31 @@
-"""Tile geometry and the block router, with the reference's names and signatures.
+"""Tile geometry, the block router and the non-QAT cube JVP, with the
+reference's names and signatures (models/mla_video_sparse_jvp.py).
 
-Mirrors models/mla_video_sparse_jvp.py: ``tile_permutation`` (:61-91),
-``route_tiles`` (:268-295), ``route_tiles_fast`` (:532-566) and
-``_plenty_of_vram`` (:42-55).  Pooling, projections, scores and the top-k
-run in the gfx950 kernels behind ``sla2h_quant_pool_qk`` and
-``sla2h_route_topk`` with one pinned fp32 evaluation order, so the selected
-tile sets are reproducible bit for bit.
+On the gfx950 kernels:
+  ``route_tiles`` (:268-295) and ``route_tiles_fast`` (:532-566): pooling,
+  projections, scores and the top-k behind ``sla2h_quant_pool_qk`` and
+  ``sla2h_route_topk``, one pinned fp32 evaluation order, so the selected
+  tile sets are reproducible bit for bit;
+  ``mla_video_sparse_jvp`` (:403-454): the cube JVP with 16-bit primal
+  scores (``ops.cube_jvp16``).
+Host index math: ``tile_permutation`` (:61-91), ``_plenty_of_vram`` (:42-55).
+
+The reference also exports four torch-level helpers that its tests import:
+``_pool_tiles`` (:241-265), ``_phi_jvp`` (:301-308), ``_linear_jvp``
+(:311-397) and the dense O(L^2) oracle ``mvs_dense_ref`` (:457-498).  They
+are plain torch here as there, run on whatever device their inputs live on,
+and no kernel path of this package calls them.
 """
 
 import torch
+import torch.nn.functional as F
 
 from . import ops
 
-__all__ = ["tile_permutation", "route_tiles", "route_tiles_fast", "_plenty_of_vram"]
+__all__ = ["tile_permutation", "route_tiles", "route_tiles_fast", "_plenty_of_vram",
+           "mla_video_sparse_jvp", "mvs_dense_ref", "_pool_tiles", "_phi_jvp", "_linear_jvp"]
+
+_EPS_L = 1e-5
 
 
 def _plenty_of_vram(device, need_gib=24.0):
@@ -72,3 +85,170 @@ def route_tiles(q, k, topk_frac, Np, E, prefix_len, proj_q=None, proj_k=None):
     shift-free form in the pinned order for both entry points.
     """
     return route_tiles_fast(q, k, topk_frac, Np, E, prefix_len, proj_q, proj_k)
+
+
+# ---------------------------------------------------------------------------
+# The non-QAT cube JVP (16-bit primal scores) on the gfx950 kernels.
+# ---------------------------------------------------------------------------
+def mla_video_sparse_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, Np, E, prefix_len,
+                         proj_q=None, proj_k=None, lut=None, T=None, block_m=64):
+    """Cube-tile SLA2 attention and its forward-mode tangent, 16-bit scores.
+
+    The exact branch attends, for every query block, the routed video tiles
+    plus every prefix tail block; the linear branch takes the video tiles
+    that were not routed (the prefix never enters it); the two are mixed by
+    alpha per query block.  Inputs in tile order: Np tiles of E = 64 tokens
+    and then the prefix_len conditioning tokens (L = Np * E + prefix_len).
+
+    Args:
+        q, k, v, dq, dk, dv: (B, H, L, 64) primal and tangent.  fp16 and bf16
+            keep their type; fp32 is rounded to fp16 (the reference's fp32
+            mode uses IEEE fp32 dots; here it has the fp16 mode's precision).
+        alpha: (H, Mb) mix after the sigmoid, or a scalar.
+        topk_frac: routed fraction of the video tiles (unused with lut).
+        Np, E, prefix_len: tiling geometry; E must be 64.
+        proj_q, proj_k: optional (D, D) router projections.
+        lut, T: precomputed routing (B, H, Mb, T), e.g. from a primal pass.
+        block_m: accepted for the reference's signature (must divide E); the
+            kernel's work unit is fixed.
+
+    Returns:
+        (o, do): (B, H, L, 64) fp32.
+    """
+    if E != ops.E_TILE:
+        raise ValueError(f"mla_video_sparse_jvp: the tile length E must be {ops.E_TILE}, got {E}")
+    if E % block_m:
+        raise ValueError(f"block_m must divide E: {block_m}, {E}")
+    B, H, L, D = q.shape
+    if L != Np * E + prefix_len:
+        raise ValueError(f"L={L} does not match Np={Np}, E={E}, prefix_len={prefix_len}")
+    dt = q.dtype if q.dtype in (torch.float16, torch.bfloat16) else torch.float16
+    qc, kc, vc, dqc, dkc, dvc = (t.to(dt).contiguous() for t in (q, k, v, dq, dk, dv))
+    if lut is None:
+        lut, T = route_tiles(qc, kc, topk_frac, Np, E, prefix_len, proj_q, proj_k)
+    Mb = -(-L // E)
+    if torch.is_tensor(alpha) and alpha.dim() == 2:
+        a = alpha.detach().to(q.device, torch.float32)
+    else:
+        a = torch.full((H, Mb), float(alpha), device=q.device, dtype=torch.float32)
+    return ops.cube_jvp16(qc, kc, vc, dqc, dkc, dvc, a, lut.to(q.device), Np)
+
+
+# ---------------------------------------------------------------------------
+# Torch-level helpers of the reference module (its tests import them).
+# ---------------------------------------------------------------------------
+def _pool_tiles(x, Np, E, prefix_cnt):
+    """Tile means: (B, H, L, D) tile-major -> (B, H, Np + ceil(prefix_cnt / E), D)
+    fp32; every video tile averages its E tokens, every prefix tail block the
+    tokens it really holds (the last one may be short)."""
+    B, H, L, D = x.shape
+    xf = x.float()
+    parts = [xf[:, :, :Np * E].reshape(B, H, Np, E, D).mean(dim=3)]
+    start = Np * E
+    while start < Np * E + prefix_cnt:
+        parts.append(xf[:, :, start:min(start + E, L)].mean(dim=2, keepdim=True))
+        start += E
+    return torch.cat(parts, dim=2)
+
+
+def _phi_jvp(x, dx):
+    """phi(x) = softmax over the channel dim in fp32, and its tangent
+    dphi = phi * (dx - <phi, dx>) -> (phi, dphi), both (B, H, L, D) fp32."""
+    phi = torch.softmax(x.float(), dim=-1)
+    dxf = dx.float()
+    return phi, phi * (dxf - (phi * dxf).sum(dim=-1, keepdim=True))
+
+
+def _linear_jvp(qphi, dqphi, kphi, dkphi, v, dv, lut, Np, E, primal_only=False):
+    """Linear branch over the video tiles each query block did not route.
+
+    For every query block m: H_c = sum over non-routed tiles n of
+    phi(K_n)^T V_n and z_c = sum of phi(K_n) (prefix tokens excluded), then
+    o_l = phi(q) H_c / (phi(q) . z_c + 1e-5), and its tangent by the product
+    and quotient rules from the tangent states.  The routed part is summed
+    one LUT column at a time and subtracted from the totals.
+
+    Args:
+        qphi, dqphi, kphi, dkphi, v, dv: (B, H, L, D) feature maps, values
+            and their tangents (fp32 or 16-bit), tile-major.
+        lut: (B, H, Mb, T) routed video-tile ids.
+        Np, E: number of video tiles and tile length.
+        primal_only: skip the tangent (returns None for it).
+
+    Returns:
+        (o_l, do_l): (B, H, L, D) fp32 (do_l None with primal_only).
+    """
+    B, H, L, D = qphi.shape
+    Dv = v.shape[-1]
+    Mb, T = lut.shape[2], lut.shape[3]
+    tiles = lambda x, w: x.float()[:, :, :Np * E].reshape(B, H, Np, E, w)
+    kt, vt = tiles(kphi, D), tiles(v, Dv)
+    Hb = torch.einsum("bhntd,bhntv->bhndv", kt, vt)
+    zb = kt.sum(dim=3)
+    tan = not primal_only
+    if tan:
+        dkt, dvt = tiles(dkphi, D), tiles(dv, Dv)
+        dHb = torch.einsum("bhntd,bhntv->bhndv", dkt, vt) + torch.einsum(
+            "bhntd,bhntv->bhndv", kt, dvt)
+        dzb = dkt.sum(dim=3)
+
+    def complement(state):
+        total = state.sum(dim=2, keepdim=True)
+        routed = torch.zeros((B, H, Mb) + state.shape[3:], device=state.device,
+                             dtype=state.dtype)
+        idx = lut.long()
+        for j in range(T):
+            ix = idx[..., j].reshape(B, H, Mb, *([1] * (state.dim() - 3)))
+            routed += torch.gather(state, 2, ix.expand((B, H, Mb) + state.shape[3:]))
+        return total - routed
+
+    Hc, zc = complement(Hb), complement(zb)
+    pad = Mb * E - L
+    qg = F.pad(qphi.float(), (0, 0, 0, pad)).reshape(B, H, Mb, E, D)
+    num = torch.einsum("bhmtd,bhmdv->bhmtv", qg, Hc)
+    den = torch.einsum("bhmtd,bhmd->bhmt", qg, zc) + _EPS_L
+    o_l = num / den[..., None]
+    flat = lambda x: x.reshape(B, H, Mb * E, x.shape[-1])[:, :, :L]
+    if not tan:
+        return flat(o_l), None
+    dHc, dzc = complement(dHb), complement(dzb)
+    dqg = F.pad(dqphi.float(), (0, 0, 0, pad)).reshape(B, H, Mb, E, D)
+    dnum = (torch.einsum("bhmtd,bhmdv->bhmtv", dqg, Hc)
+            + torch.einsum("bhmtd,bhmdv->bhmtv", qg, dHc))
+    dden = (torch.einsum("bhmtd,bhmd->bhmt", dqg, zc)
+            + torch.einsum("bhmtd,bhmd->bhmt", qg, dzc))
+    do_l = (dnum - o_l * dden[..., None]) / den[..., None]
+    return flat(o_l), flat(do_l)
+
+
+def mvs_dense_ref(q, k, v, alpha, lut, Np, E, prefix_len):
+    """Dense fp32 form of the cube op for tests (differentiable; O(L^2) memory).
+
+    Token-level mask from the LUT (every routed video tile, plus the prefix
+    columns for every query); exact branch = masked softmax attention with
+    scale D^-1/2; linear branch = phi(q) phi(k)^T restricted to the video
+    columns outside the mask, normalised by its row sum + 1e-5; mixed by
+    alpha (H, Mb), one value per query block.
+
+    Args: q, k, v (B, H, L, D) fp32 tile-major; alpha (H, Mb); lut
+    (B, H, Mb, T); Np, E, prefix_len.  Returns o (B, H, L, D) fp32.
+    """
+    B, H, L, D = q.shape
+    Mb = lut.shape[2]
+    dev = q.device
+    blocks = torch.zeros(B, H, Mb, Np, device=dev)
+    blocks.scatter_(-1, lut.long(), 1.0)
+    rows_of = torch.clamp(torch.arange(L, device=dev) // E, max=Mb - 1)
+    cols_of = torch.clamp(torch.arange(Np * E, device=dev) // E, max=Np - 1)
+    mask = blocks[:, :, rows_of][..., cols_of]                     # (B,H,L,Np*E)
+    if L > Np * E:
+        mask = torch.cat([mask, torch.ones(B, H, L, L - Np * E, device=dev)], dim=-1)
+    scores = (q @ k.transpose(-1, -2)) * D ** -0.5
+    o_s = torch.softmax(scores.masked_fill(mask <= 0, float("-inf")), dim=-1) @ v
+    w = torch.softmax(q, dim=-1) @ torch.softmax(k, dim=-1).transpose(-1, -2)
+    keep = 1.0 - mask
+    keep[..., Np * E:] = 0.0
+    w = w * keep
+    o_l = (w @ v) / (w.sum(dim=-1, keepdim=True) + _EPS_L)
+    a = alpha.to(dev)[:, rows_of].reshape(1, H, L, 1)
+    return a * o_s + (1.0 - a) * o_l

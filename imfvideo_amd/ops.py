@@ -172,6 +172,11 @@ def complement(st, lut, Np):
         g("Hb"), g("dHb"), g("zb"), g("dzb"), lut.contiguous().data_ptr(), B, H, Mb, Np,
         E_TILE, T, ws.data_ptr(), comp.data_ptr(), _stream(lut.device)), "sla2h_complement")
     return comp
+    ws = torch.empty(need, device=lut.device, dtype=torch.uint8)
+    _lib.check(lib.sla2h_complement(
+        g("Hb"), g("dHb"), g("zb"), g("dzb"), lut.contiguous().data_ptr(), B, H, Mb, Np,
+        E_TILE, T, ws.data_ptr(), comp.data_ptr(), _stream(lut.device)), "sla2h_complement")
+    return comp
 
 
 def fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq=None, scale=None, eps_l=1e-5,
@@ -328,24 +333,32 @@ def augment_lut(lut, Np, n_tail):
                      -1).contiguous()
 
 
-def train_fwd(q, k, v, alpha, lut, Np, eps_l=1e-5):
+def train_fwd(q, k, v, alpha, lut, Np, eps_l=1e-5, int8=True):
     """Training forward of the cube-QAT op on given routing.
 
     q, k, v: (B,H,L,64) 16-bit, tile-major.  alpha: (H, Mb) after the sigmoid.
-    lut: (B,H,Mb,T) routed video tiles.  Returns a dict with the module output
-    o and the tensors the reference saves for its backward: o_s, o_l, lse, den,
-    qphi, htot (rounded to 16 bits, held in fp32), ztot, lut_aug, and the
-    quantised operands.
+    lut: (B,H,Mb,T) routed video tiles.  int8: the INT8 sparse branch of
+    _attn_fwd_qat (truncating Q/K/V quantisation, INT8 P.V), else its 16-bit
+    branch (S = q.k^T on 16-bit MFMA, O += round16(P).V), as the reference
+    module's use_int8 flag selects (models/sla2_cube_qat.py:395, 413).
+    Returns a dict with the module output o and the tensors the reference
+    saves for its backward: o_s, o_l, lse, den, qphi, htot (rounded to 16
+    bits, held in fp32), ztot, lut_aug, and (int8) the quantised operands.
     """
     q, k, v = (t.contiguous() for t in (q, k, v))
     B, H, L, D = q.shape
     nb = -(-L // E_TILE)
     n_tail = nb - Np
     lut = lut.to(torch.int32).contiguous()
-    qz = quant_train(q, k, v)
-    o_s, lse, qphi = sparse_fwd_qat(q, qz, lut, Np)
-    st = linear_states_qat(k, v)
     lut_aug = augment_lut(lut, Np, n_tail)
+    qz = {}
+    if int8:
+        qz = quant_train(q, k, v)
+        o_s, lse, qphi = sparse_fwd_qat(q, qz, lut, Np)
+        st = linear_states_qat(k, v)
+    else:
+        st = linear_states_qat(k, v, with_vt=True)
+        o_s, lse, qphi = sparse_fwd_16(q, k, st["vt"], lut_aug, E_TILE)
     comp = complement(st, lut_aug, nb)
     o, o_l, den = linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha, eps_l)
     htot = st["Hall"].to(q.dtype).float()
@@ -422,8 +435,8 @@ def train_bwd(q, k, v, alpha, fwd, do, scale=None, stage_events=None, bq=E_TILE)
 # ---------------------------------------------------------------------------
 
 def pool_blocks(x, blk, proj=None, transposed=False):
-    """Block means of x (B,H,L,64) 16-bit over blk rows (+ projection) -> fp32
-    (B,H,nblk,64), or (B,H,64,nblk) when transposed."""
+    """Block means of x (B,H,L,64) 16-bit or fp32 over blk rows (+ projection)
+    -> fp32 (B,H,nblk,64), or (B,H,64,nblk) when transposed."""
     _need_gpu(x, proj)
     x = _bhld(x, "x")
     B, H, L, D = x.shape
@@ -432,8 +445,9 @@ def pool_blocks(x, blk, proj=None, transposed=False):
     out = torch.empty(shape, device=x.device, dtype=torch.float32)
     if proj is not None:
         proj = proj.detach().to(x.device, torch.float32).contiguous()
+    code = 2 if x.dtype == torch.float32 else _dtype_code(x)
     _lib.check(_lib.load().sla2h_pool_blocks(
-        x.data_ptr(), _dtype_code(x), B * H, L, D, blk, _ptr(proj), 1 if transposed else 0,
+        x.data_ptr(), code, B * H, L, D, blk, _ptr(proj), 1 if transposed else 0,
         out.data_ptr(), _stream(x.device)), "sla2h_pool_blocks")
     return out
 
@@ -477,6 +491,56 @@ def jvp_1d(q, k, v, dq, dk, dv, alpha, lut, bq, scale=None, eps_l=1e-5, return_a
     return o, do
 
 
+def sparse_fwd_16(q, k, vt, lut, bq, scale=None):
+    """16-bit sparse branch of _attn_fwd_qat (no USE_INT8) over the routed
+    64-row key blocks of lut (B,H,ceil(L/bq),J): S = q.k^T on 16-bit MFMA,
+    exact running maximum, O += round16(P).V with V from the primal operand
+    tiles vt of linear_states_qat / hblocks_states.  Any routed block may be
+    the partial last one.  -> (o_s 16-bit, lse fp32 log2 domain, qphi 16-bit)."""
+    _need_gpu(q, k, vt, lut)
+    B, H, L, D = q.shape
+    mq = -(-L // bq)
+    lut = lut.to(torch.int32).contiguous()
+    if lut.dim() != 4 or tuple(lut.shape[:3]) != (B, H, mq):
+        raise ValueError(f"lut: expected (B, H, {mq}, J), got {tuple(lut.shape)}")
+    scale = D ** -0.5 if scale is None else scale
+    o_s, qphi = torch.empty_like(q), torch.empty_like(q)
+    lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
+    _lib.check(_lib.load().sla2h_sparse_fwd_1d(
+        q.data_ptr(), k.data_ptr(), vt.data_ptr(), lut.data_ptr(), _dtype_code(q), B, H, L, D,
+        bq, E_TILE, lut.shape[-1], float(scale), o_s.data_ptr(), lse.data_ptr(),
+        qphi.data_ptr(), _stream(q.device)), "sla2h_sparse_fwd_1d")
+    return o_s, lse, qphi
+
+
+def cube_jvp16(q, k, v, dq, dk, dv, alpha, lut, Np, scale=None, eps_l=1e-5):
+    """Cube-tile SLA2 JVP with 16-bit primal scores (the reference's non-QAT
+    mla_video_sparse_jvp, models/mla_video_sparse_jvp.py:403-454): the sparse
+    branch visits the routed video tiles of lut (B,H,Mb,T) and every prefix
+    tail block, the linear branch the complement over the Np video tiles, then
+    the alpha mix.  q..dv (B,H,L,64) 16-bit tile-major; alpha (H, Mb).
+    -> (o, do) fp32."""
+    _need_gpu(q, k, v, dq, dk, dv, lut)
+    q, k, v, dq, dk, dv = (_bhld(t, "qkv") for t in (q, k, v, dq, dk, dv))
+    B, H, L, D = q.shape
+    nb = -(-L // E_TILE)
+    lut = lut.to(torch.int32).contiguous()
+    _check_lut(lut, B, H, L)
+    alpha = _alpha_rows(alpha, H, nb, q.device)
+    scale = D ** -0.5 if scale is None else scale
+    st = linear_states(k, v, Np, dk, dv, with_sums=False)
+    comp = complement(st, lut, Np)
+    lut_aug = augment_lut(lut, Np, nb - Np)
+    o = torch.empty(B, H, L, D, device=q.device, dtype=torch.float32)
+    do = torch.empty_like(o)
+    _lib.check(_lib.load().sla2h_fwd_jvp_1d(
+        q.data_ptr(), dq.data_ptr(), st["kt"].data_ptr(), st["vt"].data_ptr(), comp.data_ptr(),
+        alpha.data_ptr(), alpha.stride(0), lut_aug.data_ptr(), _dtype_code(q), B, H, L, D,
+        E_TILE, E_TILE, lut_aug.shape[-1], float(scale), float(eps_l), o.data_ptr(),
+        do.data_ptr(), _stream(q.device)), "sla2h_fwd_jvp_1d")
+    return o, do
+
+
 def train_fwd_1d(q, k, v, alpha, lut, bq, eps_l=1e-5, int8=False):
     """Training forward of the 1-D SLA2 module on given routing.
 
@@ -493,7 +557,6 @@ def train_fwd_1d(q, k, v, alpha, lut, bq, eps_l=1e-5, int8=False):
     lut = lut.to(torch.int32).contiguous()
     if lut.dim() != 4 or tuple(lut.shape[:3]) != (B, H, mq):
         raise ValueError(f"lut: expected (B, H, {mq}, T), got {tuple(lut.shape)}")
-    T = lut.shape[-1]
     st = linear_states_qat(k, v, with_vt=not int8)
     if int8:
         qz = quant_train(q, k, v)
@@ -501,12 +564,7 @@ def train_fwd_1d(q, k, v, alpha, lut, bq, eps_l=1e-5, int8=False):
         o_s, lse, qphi = sparse_fwd_int8(q, qz["q8"], qz["qs"], bq, qz["k8"], qz["ks"],
                                          qz["v8f"], qz["vs"], lut, bq)
     else:
-        o_s, qphi = torch.empty_like(q), torch.empty_like(q)
-        lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
-        _lib.check(_lib.load().sla2h_sparse_fwd_1d(
-            q.data_ptr(), k.data_ptr(), st["vt"].data_ptr(), lut.data_ptr(), _dtype_code(q), B,
-            H, L, D, bq, E_TILE, T, float(D ** -0.5), o_s.data_ptr(), lse.data_ptr(),
-            qphi.data_ptr(), _stream(q.device)), "sla2h_sparse_fwd_1d")
+        o_s, lse, qphi = sparse_fwd_16(q, k, st["vt"], lut, bq)
     comp = complement(st, lut, nb)
     o, o_l, den = linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha, eps_l, bq=bq)
     return dict(o=o, o_s=o_s, o_l=o_l, lse=lse, den=den, qphi=qphi,
@@ -624,15 +682,7 @@ def sla2_infer(q, k, v, alpha, lut, bq, use_int8=True, qblock=None, eps_l=1e-5,
         v8f, vs = quantize_v8f(v)
         o_s, lse, qphi = sparse_fwd_int8(q, q8, qs, qb, k8, ks, v8f, vs, lut, bq)
     else:
-        mq = -(-L // bq)
-        if lut.dim() != 4 or tuple(lut.shape[:3]) != (B, H, mq):
-            raise ValueError(f"lut: expected (B, H, {mq}, T), got {tuple(lut.shape)}")
-        o_s, qphi = torch.empty_like(q), torch.empty_like(q)
-        lse = torch.empty(B, H, L, device=q.device, dtype=torch.float32)
-        _lib.check(_lib.load().sla2h_sparse_fwd_1d(
-            q.data_ptr(), k.data_ptr(), st["vt"].data_ptr(), lut.data_ptr(), _dtype_code(q), B,
-            H, L, D, bq, E_TILE, lut.shape[-1], float(D ** -0.5), o_s.data_ptr(),
-            lse.data_ptr(), qphi.data_ptr(), _stream(q.device)), "sla2h_sparse_fwd_1d")
+        o_s, lse, qphi = sparse_fwd_16(q, k, st["vt"], lut, bq)
     comp = complement(st, lut, nb)
     o = lin_fwd3(qphi, comp, o_s, alpha, bq, eps_l)
     if return_parts:

@@ -104,22 +104,22 @@ def _sparse_primal_only(q, k, v, lut, T, Np, E, prefix_len):
 class _CubeQATFunction(torch.autograd.Function):
     """Training op with the straight-through backward (reference :696-832).
 
-    Same argument list as the reference.  ``mask`` and ``a_index`` are
+    Same argument list as the reference.  ``use_int8`` picks the INT8 or the
+    16-bit sparse branch of the forward; the backward is the same 16-bit
+    recompute for both, as in the reference.  ``mask`` and ``a_index`` are
     accepted and unused: the kernels derive the per-tile selection from
     ``lut_aug`` on the device, and the alpha of a row is that of its 64-row
-    block.  ``use_int8`` must be true (the only mode of this build).
+    block.
     """
 
     @staticmethod
     def forward(ctx, qh, kh, vh, alpha_logit, lut, lut_aug, mask, T, E, use_int8, a_index,
                 n_tail=1, stats_out=None):
-        if not use_int8:
-            raise NotImplementedError("_CubeQATFunction: only the INT8 training forward is built")
         assert E == ops.E_TILE, f"E must be {ops.E_TILE}, got {E}"
         B, H, L, D = qh.shape
         Np = -(-L // E) - n_tail
         a = torch.sigmoid(alpha_logit.detach().float())
-        out = ops.train_fwd(qh, kh, vh, a, lut, Np)
+        out = ops.train_fwd(qh, kh, vh, a, lut, Np, int8=bool(use_int8))
         if stats_out is not None:
             stats_out.copy_(out["lse"].amax(dim=(0, 2)))
         ctx.save_for_backward(qh, kh, vh, a, out["o_s"], out["o_l"], out["lse"], out["den"],
@@ -136,27 +136,26 @@ class _CubeQATFunction(torch.autograd.Function):
 
 
 class SLA2CubeQATAttentionImpl(nn.Module):
-    """attn_impl: cube-block sparse-linear attention with INT8 QAT (reference :295-439).
+    """The cube-tile SLA2 attention as a DiT ``attn_impl`` (reference :295-439).
 
-    Args:
-        head_dim: qk head dim D (= v head dim, 64).
-        seq_len: L = prefix + patches.
-        num_heads: H.
-        grid: (T, Hh, Ww) patch grid.
-        tile: (tt, th, tw) 3D tile, prod = E = 64.
-        topk: routed fraction of video tiles.
-        alpha_init: initial sparse/linear mixing ratio in (0, 1).
-        use_int8: INT8 primal scores (the only mode of this build).
-        pre_permuted: tokens are already tile-major.
+    Constructor arguments (the reference's, same names and defaults):
+    ``head_dim`` is the per-head width of q, k and v (64); ``seq_len`` counts
+    the prefix tokens plus the patch tokens of ``grid`` (frames, height,
+    width); ``num_heads`` is H; ``tile`` is the 3-D tile whose volume E must
+    be 64; ``topk`` is the fraction of the video tiles each query block routes
+    to the exact branch; ``alpha_init`` sets every entry of ``alpha_logit``
+    so that its sigmoid starts there; ``use_int8`` selects the INT8 sparse
+    branch of the training forward (False: 16-bit scores and P.V);
+    ``pre_permuted`` says the caller already keeps the tokens in tile order.
 
-    The forward follows the reference module: tokens permuted tile-major and
-    cast to fp16, routed (no gradient reaches proj_q / proj_k), then the
-    training-forward kernels (INT8 sparse branch with truncating quantisation
-    and INT8 P.V, 16-bit state-form linear branch, 16-bit mix;
-    ``ops.train_fwd``), which the reference also runs under no_grad.  With
-    gradients required it goes through ``_CubeQATFunction`` (straight-through
+    forward(q, k, v) takes (b, l, H, hd) tensors, moves them to tile order in
+    fp16 (as the reference does), routes on them without gradient (so
+    proj_q / proj_k never receive one), and runs the training-forward kernels
+    (``ops.train_fwd``: sparse branch, state-form linear branch, alpha mix),
+    also under no_grad as the reference's guidance path does.  With gradients
+    required the call goes through ``_CubeQATFunction`` (straight-through
     backward) and refreshes ``logit_max_log2`` (H,), the per-head maximum of
-    the sparse branch's lse.
+    the sparse branch's lse, for the QK-Clip step.
     """
 
     TILE_MAJOR = True
@@ -210,7 +209,7 @@ class SLA2CubeQATAttentionImpl(nn.Module):
                                        self.logit_max_log2)
         else:
             a = torch.sigmoid(self.alpha_logit.detach().float())
-            o = ops.train_fwd(qh, kh, vh, a, lut, self.Np)["o"]
+            o = ops.train_fwd(qh, kh, vh, a, lut, self.Np, int8=self.use_int8)["o"]
         if self.pre_permuted:
             return o.permute(0, 2, 1, 3).to(q.dtype)
         return o[:, :, self.inv].permute(0, 2, 1, 3).to(q.dtype)

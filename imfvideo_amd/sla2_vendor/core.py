@@ -100,7 +100,8 @@ class SLA2(nn.Module):
         training = torch.is_grad_enabled() and (q.requires_grad or k.requires_grad
                                                 or v.requires_grad)
         qh, kh, vh = (t.to(self.dtype).contiguous() for t in (q, k, v))
-        lut, topk = self.router.route(qh, kh, self.topk)
+        # the router scores the inputs in their own dtype (reference core.py:88)
+        lut, topk = self.router.route(q, k, self.topk)
         alpha_logit = self._get_alpha(H, -(-L // self.bq), q.device)
         if training:
             o = _SLA2Function.apply(qh, kh, vh, alpha_logit, lut, self.bq, self.use_int8)

@@ -53,25 +53,30 @@ class Router(nn.Module):
             for p in self.parameters():
                 p.requires_grad_(False)
 
-    @staticmethod
-    def _c16(x):
-        return (x if x.dtype in (torch.float16, torch.bfloat16) else x.half()).contiguous()
-
     def scores(self, q, k):
         """Differentiable (in proj_q / proj_k) block scores (B, H, Mb, Nb) fp32."""
-        q16, k16 = self._c16(q), self._c16(k)
-        qb = ops.pool_blocks(q16, self.bq)
-        kb = ops.pool_blocks(k16, self.bk) - k16.float().mean(-2, keepdim=True)
+        qi, ki = self._pool_input(q), self._pool_input(k)
+        qb = ops.pool_blocks(qi, self.bq)
+        kb = ops.pool_blocks(ki, self.bk) - ki.float().mean(-2, keepdim=True)
         if self.learnable:
             qb, kb = self.proj_q(qb), self.proj_k(kb)
         return (qb @ kb.transpose(-1, -2)) * (q.shape[-1] ** -0.5)
+
+    @staticmethod
+    def _pool_input(x):
+        # fp32 and 16-bit inputs are pooled as given (the reference pools the
+        # raw q / k); other dtypes go through fp32
+        if x.dtype not in (torch.float32, torch.float16, torch.bfloat16):
+            x = x.float()
+        return x.contiguous()
 
     def route(self, q, k, k_frac):
         """Hard top-k on the HIP kernels -> (lut (B,H,Mb,T) int32, T)."""
         pq = self.proj_q.weight if self.learnable else None
         pk = self.proj_k.weight if self.learnable else None
         with torch.no_grad():
-            return ops.route_1d(self._c16(q), self._c16(k), k_frac, self.bq, self.bk, pq, pk)
+            return ops.route_1d(self._pool_input(q), self._pool_input(k), k_frac, self.bq,
+                                self.bk, pq, pk)
 
     def forward(self, q, k, k_frac, soft=False, need_mask=True):
         """Returns (mask, lut, topk, pc): mask (B,H,Mb,Nb) int8 hard mask (the soft

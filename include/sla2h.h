@@ -163,7 +163,9 @@ int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, const void* vt,
  * models/sla2_vendor/router.py:66-75); the smooth-k shift is a per-row
  * constant of the scores and leaves the top-k selection unchanged.
  * Feed the pooled queries and the transposed pooled keys to sla2h_route_topk
- * with Mb = ceil(L/bq) and Np = ceil(L/64).
+ * with Mb = ceil(L/bq) and Np = ceil(L/64).  dtype: SLA2H_DTYPE_F16,
+ * SLA2H_DTYPE_BF16 or 2 (fp32 input, pooled as given: the reference's router
+ * reads q and k in their own dtype).
  */
 int sla2h_pool_blocks(const void* x, int dtype, int64_t BH, int64_t L, int D, int blk,
                       const float* proj, int transposed, float* out, void* stream);

@@ -131,26 +131,90 @@ def test_mlp_and_block_jvp():
     check((x, dx), (h1 + m, dh1 + dm), "block")
 
 
-def test_transformer_block_training_step():
-    say("TransformerBlock with SLA2CubeQATAttentionImpl: forward + backward")
-    from functools import partial
-    from imfvideo_amd.imf_dit_video import TransformerBlock, precompute_axial_rope_3d
-    from imfvideo_amd.sla2_cube_qat import SLA2CubeQATAttentionImpl
-    torch.manual_seed(5)
-    S = 274
-    impl = partial(SLA2CubeQATAttentionImpl, seq_len=S, num_heads=2, grid=(4, 8, 8),
-                   tile=(4, 4, 4), topk=0.5)
-    blk = TransformerBlock(256, 2, 128, 64, 32, 32, 64, mlp_ratio=2, attn_impl=impl).cuda()
+def _small_block(dev, attn_impl, seed=5):
+    from imfvideo_amd.imf_dit_video import TransformerBlock
+    torch.manual_seed(seed)
+    blk = TransformerBlock(256, 2, 128, 64, 32, 32, 64, mlp_ratio=2, attn_impl=attn_impl)
     with torch.no_grad():
-        blk.attn_scale.fill_(0.1)
-        blk.mlp_scale.fill_(0.1)
+        blk.attn_scale.copy_(0.1 + 0.02 * torch.randn(256))
+        blk.mlp_scale.copy_(0.1 + 0.02 * torch.randn(256))
+        for n, prm in blk.named_parameters():
+            if n.endswith("norm.weight") or n.endswith("layernorm.weight") or "norm1" in n \
+                    or "norm2" in n:
+                prm.add_(0.1 * torch.randn_like(prm))
+    return blk.to(dev)
+
+
+def _block_step(blk, x, w, cos, sin):
+    xg = x.clone().requires_grad_()
+    out = blk(xg, cos, sin)
+    (out * w).sum().backward()
+    return out.detach(), xg.grad
+
+
+def _compare_blocks(gpu_blk, cpu_blk, got, want, rel, mx):
+    from tests.block_ref import grad_report
+    pairs = [("out", got[0], want[0]), ("x.grad", got[1], want[1])]
+    pairs += [(f"grad {n}", a, b) for n, a, b in grad_report(gpu_blk, cpu_blk)]
+    for tag, a, b in pairs:
+        a, b = a.detach().cpu().double(), b.detach().cpu().double()
+        bound = mx * max(1.0, b.abs().max().item())
+        print(f"  {tag}: max {max_abs(a, b):.2e} (bound {bound:.2e}) rel {rel_l2(a, b):.2e}",
+              flush=True)
+        assert torch.isfinite(a).all() and max_abs(a, b) < bound and rel_l2(a, b) < rel, tag
+    return len(pairs)
+
+
+def test_transformer_block_training_step_dense_matches_eager():
+    """The DiT block's training step with the fused GPU layers (RMSNorm,
+    SituAndMul, RoPE on per-head and shared-key views, ReZero residuals)
+    against the same block run eagerly on the CPU, dense attention, fp32:
+    output, input gradient and every parameter gradient."""
+    say("TransformerBlock (sdpa) fused GPU vs eager CPU: forward + backward")
+    from imfvideo_amd.imf_dit_video import precompute_axial_rope_3d, sdpa_math_attention
+    from tests.block_ref import copy_block_to_cpu
+    S = 274
+    blk = _small_block("cuda", sdpa_math_attention)
+    ref = _small_block("cpu", sdpa_math_attention)
+    copy_block_to_cpu(blk, ref)
     cos, sin = precompute_axial_rope_3d(32, (4, 8, 8), 18, axis_dims=(8, 12, 12))
-    x = torch.randn(2, S, 256, device="cuda", requires_grad=True)
-    out = blk(x, cuda(cos), cuda(sin))
-    (0.5 * out.pow(2).sum()).backward()
-    assert torch.isfinite(out).all() and torch.isfinite(x.grad).all()
-    assert blk.attn.attn_impl.alpha_logit.grad is not None
-    assert torch.isfinite(blk.attn.q_b_proj.weight.grad).all()
+    g = torch.Generator().manual_seed(11)
+    x = torch.randn(2, S, 256, generator=g)
+    w = torch.randn(2, S, 256, generator=g)
+    got = _block_step(blk, cuda(x), cuda(w), cuda(cos), cuda(sin))
+    want = _block_step(ref, x, w, cos, sin)
+    n = _compare_blocks(blk, ref, got, want, rel=1e-4, mx=1e-4)
+    assert n == 2 + 17  # every parameter of the block has a gradient
+
+
+def test_transformer_block_training_step_cube_matches_oracle(monkeypatch):
+    """The same block with SLA2CubeQATAttentionImpl (INT8 training forward,
+    straight-through backward) against the eager CPU block whose attention is
+    the oracle's training forward / backward (O.train_fwd / O.train_bwd) on
+    the LUT the GPU block routed."""
+    say("TransformerBlock (cube INT8) GPU vs eager CPU + oracle attention")
+    from functools import partial
+    import imfvideo_amd.sla2_cube_qat as cq
+    from imfvideo_amd.imf_dit_video import precompute_axial_rope_3d
+    from tests.block_ref import LutRecorder, OracleCubeAttention, copy_block_to_cpu
+    S = 274
+    kw = dict(seq_len=S, num_heads=2, grid=(4, 8, 8), tile=(4, 4, 4), topk=0.5)
+    blk = _small_block("cuda", partial(cq.SLA2CubeQATAttentionImpl, **kw))
+    with torch.no_grad():
+        a = blk.attn.attn_impl.alpha_logit
+        a.add_(torch.linspace(-1, 1, a.numel(), device="cuda").view_as(a))
+    rec = LutRecorder(cq.route_tiles_fast)
+    monkeypatch.setattr(cq, "route_tiles_fast", rec)
+    ref = _small_block("cpu", partial(OracleCubeAttention, lut_source=lambda: rec.luts[-1], **kw))
+    copy_block_to_cpu(blk, ref)
+    cos, sin = precompute_axial_rope_3d(32, (4, 8, 8), 18, axis_dims=(8, 12, 12))
+    g = torch.Generator().manual_seed(12)
+    x = torch.randn(2, S, 256, generator=g)
+    w = torch.randn(2, S, 256, generator=g)
+    got = _block_step(blk, cuda(x), cuda(w), cuda(cos), cuda(sin))
+    assert len(rec.luts) == 1
+    want = _block_step(ref, x, w, cos, sin)
+    _compare_blocks(blk, ref, got, want, rel=TOL_REL, mx=TOL_MAX)
     assert blk.attn.attn_impl.logit_max_log2.shape == (2,)
 
 

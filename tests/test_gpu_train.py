@@ -301,7 +301,8 @@ def test_sla2_attention_impl_forward_and_gradients():
     (out * cuda(x[3])).sum().backward()
     grads = [t.grad.cpu() for t in xs] + [mod.sla2.alpha_logit.grad.cpu()]
     qh, kh, vh, doh = (_tm16(t) for t in x)
-    lut, T = O.route_1d(qh, kh, 0.3, 128)
+    # the router pools the fp32 inputs as given (reference core.py:88)
+    lut, T = O.route_1d(x[0].permute(0, 2, 1, 3), x[1].permute(0, 2, 1, 3), 0.3, 128)
     nb = -(-L // 64)
     a = torch.sigmoid(mod.sla2.alpha_logit.detach().cpu())
     fwd = O.train_fwd(qh, kh, vh, a, lut, nb, 0, t16=torch.float16, int8=False, bq=128)
