@@ -32,6 +32,8 @@ SIGNATURES = {
     "sla2h_complement_workspace_bytes": (ctypes.c_size_t, [_c_int, _c_int, _c_int, _c_int]),
     "sla2h_complement": (_c_int, [_p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int,
                                   _c_int, _p, _p, _p]),
+    "sla2h_complement_noalloc": (_c_int, [_p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int,
+                                          _c_int, _c_int, _p, _p]),
     "sla2h_fwd_jvp": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _c_int, _p,
                                _c_int, _c_int, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int,
                                _c_f, _c_f, _c_int, _p, _p, _p]),

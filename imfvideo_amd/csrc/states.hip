@@ -8,6 +8,8 @@
 //   complement     models/sla2_cube_qat.py:510-523, 570-578
 #include "common.h"
 
+#include <mutex>
+
 namespace sla2h {
 
 constexpr int kT = 64;          // E = D = 64
@@ -724,6 +726,40 @@ extern "C" size_t sla2h_complement_workspace_bytes(int B, int H, int Mb, int Np)
   return (size_t)B * H * NC * MT * 16 * 4;
 }
 
+// ---------------------------------------------------------------------------
+// Allocation-free complement: the bit-mask workspace lives in this file-scope
+// device array (one copy per GPU, held until the process ends).  Host code
+// never uses the array's name as an address: the device address of each GPU's
+// copy comes from hipGetSymbolAddress, taken once per device on the first
+// call with that device current, and is kept here.  The mask kernel writes
+// every word the GEMM reads, so nothing needs clearing between calls; calls
+// that overlap on one GPU (several streams or threads) race on the array.
+// ---------------------------------------------------------------------------
+static __device__ __align__(256) unsigned char scratch[SLA2H_COMPLEMENT_SCRATCH_BYTES];
+
+namespace {
+constexpr int kMaxScratchDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kMaxScratchDevices] = {};
+
+int complement_scratch(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return (int)e;
+  if (dev < 0 || dev >= kMaxScratchDevices) return (int)hipErrorInvalidDevice;
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* ptr = nullptr;
+    e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return (int)e;
+    if (ptr == nullptr) return (int)hipErrorInvalidSymbol;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+}  // namespace
+
 extern "C" int sla2h_complement(const float* Hb, const float* dHb, const float* zb,
                                 const float* dzb, const int32_t* lut, int B, int H, int Mb,
                                 int Np, int D, int T, void* workspace, void* comp,
@@ -751,4 +787,17 @@ extern "C" int sla2h_complement(const float* Hb, const float* dHb, const float* 
   else
     comp_gemm_kernel<false><<<grid, kCompThreads, 0, st>>>(Hb, nullptr, zb, nullptr, cbits, Mb, Np, MT, NC, out);
   return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_complement_noalloc(const float* Hb, const float* dHb, const float* zb,
+                                        const float* dzb, const int32_t* lut, int B, int H,
+                                        int Mb, int Np, int D, int T, void* comp, void* stream) {
+  SLA2H_CHECK_ARG(Hb && zb && lut && comp);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && Mb > 0 && Np > 0);
+  SLA2H_CHECK_ARG(sla2h_complement_workspace_bytes(B, H, Mb, Np) <=
+                  (size_t)SLA2H_COMPLEMENT_SCRATCH_BYTES);
+  void* ws = nullptr;
+  const int err = complement_scratch(&ws);
+  if (err) return err;
+  return sla2h_complement(Hb, dHb, zb, dzb, lut, B, H, Mb, Np, D, T, ws, comp, stream);
 }

@@ -160,18 +160,29 @@ def linear_states(k, v, Np, dk=None, dv=None, E=E_TILE, with_sums=True):
     return st
 
 
-def complement(st, lut, Np):
-    """Per-query-block complement records (uint8 (B,H,Mb,REC_BYTES))."""
+COMPLEMENT_SCRATCH_BYTES = 4 << 20  # SLA2H_COMPLEMENT_SCRATCH_BYTES
+
+
+def complement(st, lut, Np, noalloc=False):
+    """Per-query-block complement records (uint8 (B,H,Mb,REC_BYTES)).
+
+    noalloc: run sla2h_complement_noalloc, whose bit-mask workspace is the
+    library's static per-GPU array (at most COMPLEMENT_SCRATCH_BYTES) instead
+    of a torch allocation; concurrent calls on one GPU must not overlap."""
     B, H, Mb, T = lut.shape
     lib = _lib.load()
     comp = torch.empty(B, H, Mb, REC_BYTES, device=lut.device, dtype=torch.uint8)
-    ws = torch.empty(lib.sla2h_complement_workspace_bytes(B, H, Mb, Np), device=lut.device,
-                     dtype=torch.uint8)
     g = lambda n: _ptr(st.get(n))
-    _lib.check(lib.sla2h_complement(
-        g("Hb"), g("dHb"), g("zb"), g("dzb"), lut.contiguous().data_ptr(), B, H, Mb, Np,
-        E_TILE, T, ws.data_ptr(), comp.data_ptr(), _stream(lut.device)), "sla2h_complement")
-    return comp
+    need = lib.sla2h_complement_workspace_bytes(B, H, Mb, Np)
+    if noalloc:
+        if need > COMPLEMENT_SCRATCH_BYTES:
+            raise ValueError(f"complement(noalloc=True): the bit masks need {need} bytes, over "
+                             f"the static {COMPLEMENT_SCRATCH_BYTES}-byte array")
+        with torch.cuda.device(lut.device):
+            _lib.check(lib.sla2h_complement_noalloc(
+                g("Hb"), g("dHb"), g("zb"), g("dzb"), lut.contiguous().data_ptr(), B, H, Mb,
+                Np, E_TILE, T, comp.data_ptr(), _stream(lut.device)), "sla2h_complement_noalloc")
+        return comp
     ws = torch.empty(need, device=lut.device, dtype=torch.uint8)
     _lib.check(lib.sla2h_complement(
         g("Hb"), g("dHb"), g("zb"), g("dzb"), lut.contiguous().data_ptr(), B, H, Mb, Np,

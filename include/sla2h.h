@@ -125,6 +125,27 @@ int sla2h_complement(const float* Hb, const float* dHb, const float* zb, const f
                      const int32_t* lut, int B, int H, int Mb, int Np, int D, int T,
                      void* workspace, void* comp, void* stream);
 
+/* Largest workspace sla2h_complement_noalloc serves (4 MiB: B*H up to 72 at
+ * Mb = Np = 468, the 29,952-token shape). */
+#define SLA2H_COMPLEMENT_SCRATCH_BYTES (4u << 20)
+
+/*
+ * sla2h_complement without the workspace argument: same kernels, same
+ * records, bit for bit.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight
+ * serving loops, harnesses that forbid hipMalloc).  The bit-mask workspace is
+ * a static device array of SLA2H_COMPLEMENT_SCRATCH_BYTES per GPU, held until
+ * the process ends; calls whose sla2h_complement_workspace_bytes(B,H,Mb,Np)
+ * exceeds it return hipErrorInvalidValue.  The call allocates nothing.  Every
+ * call on one GPU shares that GPU's array (the current device's), so calls
+ * that overlap on one GPU (other streams or threads) race.  The device
+ * address of each GPU's array is looked up once, on the first call with that
+ * device current.
+ */
+int sla2h_complement_noalloc(const float* Hb, const float* dHb, const float* zb,
+                             const float* dzb, const int32_t* lut, int B, int H, int Mb,
+                             int Np, int D, int T, void* comp, void* stream);
+
 /*
  * The fused sparse + linear SLA2 op and its forward-mode JVP, tile-major:
  *   sparse branch: for each query block m, keys of tiles lut[m,0..T) and the

@@ -57,6 +57,11 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.sla2h_sparse_fwd_qat(1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 100000, 64, 64, 1, 1,
                                     0.125, 1, 1, 1, None) == bad            # tail > 1024 tiles
     assert lib.sla2h_linear_states_qat(1, 1, 1, 1, 1, 128, 64, 64, 1, 1, None, 1, None, None) == bad
+    # the allocation-free complement: a 6 MiB bit-mask workspace (B=1, H=3, Mb=Np=4096) is
+    # over its 4 MiB static array, rejected before any device call
+    assert lib.sla2h_complement_workspace_bytes(1, 3, 4096, 4096) == 6 << 20
+    assert lib.sla2h_complement_noalloc(1, None, 1, None, 1, 1, 3, 4096, 4096, 64, 1, 1,
+                                        None) == bad
     # q, k, vt, lut, dtype, B, H, L, D, bq, bk, T, scale, o_s, lse, qphi: bq 96 unsupported
     assert lib.sla2h_sparse_fwd_1d(1, 1, 1, 1, 1, 1, 1, 640, 64, 96, 64, 2, 0.125, 1, 1, 1,
                                    None) == bad
