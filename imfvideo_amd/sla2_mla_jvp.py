@@ -32,20 +32,15 @@ def _c16(x):
 
 @torch.no_grad()
 def route_blocks(q, k, topk_frac, bq, bk, proj_q=None, proj_k=None):
-    """SLA2 router: pooled-score hard top-k over key blocks.
+    """Pick, for every bq-row query block, the T = max(1, int(topk_frac * Nb))
+    key blocks (bk = 64 rows) whose pooled means score highest against the
+    query block's pooled mean (after the optional (D, D) projections).
 
-    Args:
-        q, k: (B, H, L, D) primal queries / keys.
-        topk_frac: fraction of key blocks routed to the sparse branch.
-        bq, bk: query / key block lengths (bk = 64).
-        proj_q, proj_k: optional (D, D) router projection weights.
-
-    Returns:
-        lut: (B, H, ceil(L/bq), T) int32 routed key-block ids (descending score).
-        T: topk count (int).
-
-    The reference subtracts the mean pooled key before scoring (smooth-k); that
-    adds a per-row constant to the scores and leaves the selection unchanged.
+    q, k are (B, H, L, D); returns the block ids as a (B, H, ceil(L/bq), T)
+    int32 tensor, best first, and T.  The hard selection is computed in one
+    pinned fp32 order on the GPU (ties go to the lower block id).  The
+    reference centres the pooled keys first (smooth-k); that moves each row of
+    scores by one constant and cannot change which blocks win.
     """
     dt = _c16(q).dtype
     qc, kc = _c16(q).to(dt), _c16(k).to(dt)
@@ -54,20 +49,18 @@ def route_blocks(q, k, topk_frac, bq, bk, proj_q=None, proj_k=None):
 
 @torch.no_grad()
 def sla2_mla_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, bq, bk, lut=None, T=None, block_m=64):
-    """SLA2 attention (primal, tangent) from qkv dual pairs.
+    """The 1-D SLA2 attention of (q, k, v) and its directional derivative along
+    (dq, dk, dv), in one pass.
 
-    Args:
-        q, k, v: (B, H, L, D) primal (D == Dv == 64).
-        dq, dk, dv: (B, H, L, D) tangents.
-        alpha: (H, Mb) mixing ratio in (0,1) (already sigmoided), or scalar.
-        topk_frac: routed fraction of key blocks (ignored when lut given).
-        bq, bk: query / key block lengths.
-        lut, T: optional precomputed routing (from the primal training pass).
-        block_m: accepted for the reference's signature; the kernel's work unit
-            is fixed at 32 query rows.
-
-    Returns:
-        (o, do): (B, H, L, D) fp32 SLA2 output and tangent.
+    Every query block of bq rows attends exactly (softmax with scale D^-1/2)
+    to its routed key blocks of bk = 64 rows and, through the softmax feature
+    map, linearly to all the others; alpha (H, ceil(L/bq)) after the sigmoid,
+    or a scalar, mixes the two per query block.  lut / T skip the router (for
+    example to reuse the routing of the primal pass); without them the router
+    of route_blocks picks topk_frac of the key blocks.  All six tensors are
+    (B, H, L, 64); block_m is accepted for the reference's signature (it must
+    divide bq; the kernel's work unit is fixed).  Returns (o, do), (B, H, L, 64)
+    fp32.
     """
     B, H, L, D = q.shape
     if bq % block_m != 0:
@@ -85,20 +78,22 @@ def sla2_mla_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, bq, bk, lut=None, T=None
 
 
 def sla2_dense_ref(q, k, v, lut, alpha, bq, bk):
-    """Dense fp32 SLA2 reference (mask from LUT), differentiable, for tests.
-
-    The reference's O(L^2) test utility, kept for API parity: plain torch on
-    whatever device the inputs live on.
+    """Dense O(L^2) form of sla2_mla_jvp's primal, for tests (differentiable;
+    torch on the inputs' device).  Token (i, j) takes the exact branch when
+    key block j // bk is in the LUT row of query block i // bq, the linear
+    branch otherwise; alpha (H, ceil(L/bq)) mixes the two per query block.
+    q, k, v (B, H, L, D) fp32, lut (B, H, ceil(L/bq), T) -> (B, H, L, D).
     """
     B, H, L, D = q.shape
-    Nb = (L + bk - 1) // bk
-    mc = torch.zeros(B, H, lut.shape[2], Nb, device=q.device)
-    mc.scatter_(-1, lut.long(), 1.0)
-    m = mc.repeat_interleave(bq, dim=-2).repeat_interleave(bk, dim=-1)[..., :L, :L]
-    s = (q @ k.transpose(-1, -2)) * D ** -0.5
-    p = torch.softmax(s.masked_fill(m <= 0, float("-inf")), dim=-1)
-    o_s = p @ v
-    w = (F.softmax(q, dim=-1) @ F.softmax(k, dim=-1).transpose(-1, -2)) * (1.0 - m)
-    o_l = (w @ v) / (w.sum(-1, keepdim=True) + _EPS_L)
-    a = alpha.repeat_interleave(bq, dim=-1)[:, :L].view(1, H, L, 1)
+    qblk = torch.arange(L, device=q.device) // bq
+    kblk = torch.arange(L, device=q.device) // bk
+    routed = torch.zeros(B, H, lut.shape[2], -(-L // bk), device=q.device)
+    routed.scatter_(-1, lut.long(), 1.0)
+    exact = routed[:, :, qblk][..., kblk] > 0                   # (B, H, L, L)
+    scores = (q @ k.transpose(-1, -2)) * D ** -0.5
+    o_s = torch.softmax(scores.masked_fill(~exact, float("-inf")), dim=-1) @ v
+    kernel = F.softmax(q, dim=-1) @ F.softmax(k, dim=-1).transpose(-1, -2)
+    kernel = kernel.masked_fill(exact, 0.0)
+    o_l = (kernel @ v) / (kernel.sum(-1, keepdim=True) + _EPS_L)
+    a = alpha[:, qblk].reshape(1, H, L, 1)
     return a * o_s + (1.0 - a) * o_l

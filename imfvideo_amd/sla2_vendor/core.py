@@ -26,7 +26,8 @@ from .router import Router
 
 
 def softmax_feature_map(x):
-    """phi(.) of the linear branch: row softmax over head channels. x: (B,H,L,D)."""
+    """The linear branch's feature map: a softmax across the D channels of every
+    token of x (B, H, L, D), evaluated in fp32 and returned in x's dtype."""
     if x.dtype == torch.float32:
         return F.softmax(x, dim=-1)
     return F.softmax(x, dim=-1, dtype=torch.float32).to(x.dtype)
@@ -58,19 +59,17 @@ class SLA2(nn.Module):
     def __init__(self, head_dim, topk=0.03, bq=128, bk=64, tau=0.1, use_bf16=False, use_int8=True,
                  learnable_router=True, alpha_init=0.9, block_m=None, fused=False,
                  backend="cutedsl"):
-        """
-        head_dim        : D, per-head channel count (64)
-        topk            : k%, fraction of key blocks routed to the sparse branch
-        bq, bk          : query / key block sizes (bq in {64, 128, 256}, bk = 64)
-        use_bf16        : 16-bit compute type bf16 (else fp16)
-        use_int8        : INT8 sparse branch
-        alpha_init      : initial value of alpha (before the logit)
-        block_m, fused  : the fused inference path's query tile (its Q scales run
-                          per block_m rows, default max(32, bq // 2)) and switch
-                          (head-averaged alpha, as kernel_fused takes)
-        backend         : accepted for the reference's signature; the HIP kernels
-                          serve every backend
-        """
+        """Arguments keep the reference's names and defaults.  The head width
+        must be 64 and key blocks 64 rows (bk); query blocks (bq) may be 64,
+        128 or 256 rows.  topk is the share of key blocks each query block
+        sends to the exact branch; tau the SoftTop-k temperature of the router;
+        use_bf16 picks bf16 over fp16 as the 16-bit type; use_int8 quantises
+        the exact branch; learnable_router gives the router trainable
+        projections; alpha_init is the mixing weight every (head, query block)
+        starts from.  fused selects the fused inference kernel's conventions
+        (alpha averaged over heads, Q scales per block_m rows, by default
+        max(32, bq // 2)).  backend is accepted and ignored: one set of HIP
+        kernels serves every backend name."""
         super().__init__()
         if bk != ops.E_TILE:
             raise ValueError(f"bk must be {ops.E_TILE}, got {bk}")
@@ -126,7 +125,8 @@ class SLA2(nn.Module):
 # ---------------------------------------------------------------------------
 
 def expand_mask(mc, bq, bk, L):
-    """(B,H,Mb,Nb) block mask -> (B,H,L,L) token mask."""
+    """Spread a (B, H, Mb, Nb) block mask to its (B, H, L, L) token mask: token
+    pair (i, j) takes the value of block pair (i // bq, j // bk)."""
     m = mc.repeat_interleave(bq, dim=-2).repeat_interleave(bk, dim=-1)
     return m[..., :L, :L]
 
@@ -150,7 +150,8 @@ def sla2_dense(q, k, v, mc, alpha, bq, bk):
 
 
 def full_attention(q, k, v):
-    """Full softmax attention in fp32. q,k,v: (B,H,L,D) -> (B,H,L,D)."""
+    """Unmasked softmax attention with scale D^-1/2, computed in fp32:
+    (B, H, L, D) inputs -> (B, H, L, D)."""
     D = q.shape[-1]
     s = (q.float() @ k.float().transpose(-1, -2)) * D ** -0.5
     return torch.softmax(s, dim=-1) @ v.float()

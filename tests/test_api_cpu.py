@@ -189,3 +189,20 @@ def test_fused_paths_fall_back_to_eager_for_unsupported_operands():
     want = (4.0 * torch.tanh(gf / 4.0) * torch.sigmoid(gf) * (25.0 * torch.tanh(uf / 25.0)))
     assert torch.equal(act(gate, up), want.to(torch.float64))
     np.testing.assert_array_equal(act(gate, up).numpy(), want.double().numpy())
+
+
+def test_sla2_dense_ref_matches_the_oracle_dense_form():
+    """models/sla2_mla_jvp.py:388-418's dense test utility against the oracle's
+    fp64 restatement of the same form, ragged L and bq 64 / 128 / 256."""
+    from imfvideo_amd.sla2_mla_jvp import sla2_dense_ref
+    g = torch.Generator().manual_seed(8)
+    for L, bq in ((583, 128), (512, 64), (640, 256)):
+        q, k, v = (torch.randn(1, 2, L, 64, generator=g, dtype=torch.float64) for _ in range(3))
+        mq, nb = -(-L // bq), -(-L // 64)
+        T = max(1, nb // 3)
+        lut = torch.stack([torch.randperm(nb, generator=g)[:T] for _ in range(2 * mq)])
+        lut = lut.view(1, 2, mq, T).to(torch.int32)
+        alpha = torch.rand(2, mq, generator=g, dtype=torch.float64) * 0.8 + 0.1
+        got = sla2_dense_ref(q, k, v, lut, alpha, bq, 64)
+        want = O.dense_1d_f64(q, k, v, lut.numpy(), alpha, bq)
+        assert rel_l2(got, want) < 1e-12, (L, bq)
