@@ -69,12 +69,9 @@ __device__ inline u32x4 scale_bf16x8(u32x4 u, float s) {
   return r;
 }
 
-// A-operand fragment of H^T for numerator MFMAs from a record's fp32 H[d][v]
-// (row-major): 8 consecutive d = 32 ks + 8 g + j at v, split into bf16 hi/lo.
-__device__ inline void load_hfrag(const float* H, int ks, int g, int v, u32x4& hi, u32x4& lo) {
-  float x[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) x[j] = H[(32 * ks + 8 * g + j) * 64 + v];
+// A-operand fragment of H^T for numerator MFMAs: 8 consecutive d = 32 ks + 8 g + j
+// of a record's fp32 H[d][v] at one column v, split into bf16 hi/lo halves.
+__device__ inline void split_hfrag(const float (&x)[8], u32x4& hi, u32x4& lo) {
 #pragma unroll
   for (int e = 0; e < 4; ++e) {
     const uint32_t h = pack_pair<BF16>(x[2 * e], x[2 * e + 1]);
@@ -103,7 +100,9 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   __shared__ __align__(16) u32x4 qsh[kQT][4][64];
   __shared__ __align__(16) i32x4 q8sh[kQT][64];  // INT8 Q B-operand fragments
   // cross-wave merge buffer [wave][column tile of the round x {O, dO}][qt][lane][4]
-  __shared__ __align__(16) float mbuf[4][4][kQT][64][4];
+  // (no dO slots without tangent: the primal instances fit four workgroups per CU)
+  constexpr int kMb = TAN ? 2 : 1;
+  __shared__ __align__(16) float mbuf[4][2 * kMb][kQT][64][4];
   // key tiles of this query block in visiting order: (tile id, key scale)
   __shared__ int2 tiles[kMaxTiles];
   __shared__ int ragged_last;  // the partial key tile was moved to the end of the routed list
@@ -149,7 +148,39 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   for (int j = tid; j < J; j += 256) {
     int n = j < a.T ? lrow[j] : a.Np + (j - a.T);
     n = n < 0 ? 0 : (n >= a.Nb ? a.Nb - 1 : n);  // out-of-range ids are clamped
-    tiles[j] = make_int2(n, S16 ? 0 : __builtin_bit_cast(int, a.ks[(int64_t)bh * a.Nb + n]));
+    tiles[j].x = n;
+  }
+  __syncthreads();
+  // Routed tiles in ascending id order: the workgroups of an XCD (consecutive
+  // query blocks of one head) then sweep the head's key tiles together and
+  // share them in that XCD's L2.  Up to 64 routed tiles: a bitonic sort in the
+  // registers of wave 0; longer lists: rank by counting (ties by position).
+  if (a.T <= 64) {
+    if (w == 0) {
+      int v = l < a.T ? tiles[l].x : INT_MAX;
+#pragma unroll
+      for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+        for (int jj = k >> 1; jj > 0; jj >>= 1) {
+          const int o = __shfl_xor(v, jj);
+          v = (((l & jj) == 0) == ((l & k) == 0)) ? min(v, o) : max(v, o);
+        }
+      }
+      if (l < a.T) tiles[l].x = v;
+    }
+  } else {
+    int* tmp = reinterpret_cast<int*>(&mbuf[0][0][0][0][0]);
+    for (int j = tid; j < a.T; j += 256) {
+      const int nj = tiles[j].x;
+      int c = 0;
+      for (int i = 0; i < a.T; ++i) {
+        const int ni = tiles[i].x;
+        c += (ni < nj) || (ni == nj && i < j);
+      }
+      tmp[c] = nj;
+    }
+    __syncthreads();
+    for (int j = tid; j < a.T; j += 256) tiles[j].x = tmp[j];
   }
   __syncthreads();
   // A partial key tile (1-D blocks over a ragged L) can sit anywhere in a routed
@@ -171,6 +202,12 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     }
     __syncthreads();
     Tu = a.T - ragged_last;
+  }
+  // key scales of the tiles in visiting order; the barrier that publishes
+  // them comes after the first key loads are issued (their latencies overlap)
+  if (!S16) {
+    for (int j = tid; j < J; j += 256)
+      tiles[j].y = __builtin_bit_cast(int, a.ks[(int64_t)bh * a.Nb + tiles[j].x]);
   }
   const float sq = S16 ? 1.f : a.qs[(int64_t)bh * a.Nb + m];
   // log2-domain score factor of key tile j: (sq * sk_j) * scale * log2(e)
@@ -393,6 +430,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   // the prefetch stays in flight.
   KeyRegs ka_, kb_;
   load_keys(0, ka_);
+  __syncthreads();  // key scales in tiles[].y
   int j = 0;
   // routed video tiles in pairs (full, unmasked)
   for (; j + 1 < Tu; j += 2) {
@@ -418,6 +456,31 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
       stage(ka_, vr, j, pb, nullptr, std::true_type{});
     o_single(vr, pb);
     ka_ = kb_;
+  }
+  // this wave's part of the complement record (Hc, dHc fragments of its two
+  // output column tiles, zc, dzc), requested now: the loads stay in flight
+  // through the merge below.  The wave finalises query sub-tile qo and
+  // output column tiles cpair, cpair + 1.
+  const int qo = w >> 1;
+  const int cpair = 2 * (w & 1);
+  float hraw[2][2][2][8];  // [cc][ks][Hc, dHc][j]: H[32 ks + 8 g + j][16 (cpair + cc) + r]
+  f32x4 zraw[2][2][2];     // [ks][zc, dzc][half]: z[32 ks + 8 g + 4 half ..]
+  if (LINEAR) {
+    const float* rec = reinterpret_cast<const float*>(a.comp + ((int64_t)bh * a.Mq + mq) * kRec);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+      for (int mat = 0; mat < (TAN ? 2 : 1); ++mat) {
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj)
+            hraw[cc][ks][mat][jj] = rec[4096 * mat + (32 * ks + 8 * g + jj) * 64 + 16 * (cpair + cc) + r];
+#pragma unroll
+        for (int hf = 0; hf < 2; ++hf)
+          zraw[ks][mat][hf] = *reinterpret_cast<const f32x4*>(rec + 8192 + 64 * mat + 32 * ks + 8 * g + 4 * hf);
+      }
+    }
   }
   float l_i[kQT];
 #pragma unroll
@@ -445,9 +508,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, stat[0][ww][qt][r]);
     fself[qt] = (mrun[qt] == -INFINITY) ? 0.f : fast_exp2(mrun[qt] - M);
   }
-  // this wave finalises query sub-tile qo = w >> 1, output column tiles cpair, cpair+1
-  const int qo = w >> 1;
-  const int cpair = 2 * (w & 1);
+  // this wave finalises query sub-tile qo, output column tiles cpair, cpair+1
   float Mw = -INFINITY;
 #pragma unroll
   for (int ww = 0; ww < 4; ++ww) Mw = fmaxf(Mw, stat[0][ww][qo][r]);
@@ -469,9 +530,9 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     for (int cc = 0; cc < 2; ++cc)
 #pragma unroll
       for (int qt = 0; qt < kQT; ++qt) {
-        *reinterpret_cast<f32x4*>(&mbuf[w][2 * cc][qt][l][0]) = acc_o[2 * rd + cc][qt] * fself[qt];
+        *reinterpret_cast<f32x4*>(&mbuf[w][kMb * cc][qt][l][0]) = acc_o[2 * rd + cc][qt] * fself[qt];
         if (TAN)
-          *reinterpret_cast<f32x4*>(&mbuf[w][2 * cc + 1][qt][l][0]) =
+          *reinterpret_cast<f32x4*>(&mbuf[w][kMb * cc + 1][qt][l][0]) =
               acc_do[2 * rd + cc][qt] * fself[qt];
       }
     __syncthreads();
@@ -481,8 +542,8 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
         f32x4 so = f32x4{0.f, 0.f, 0.f, 0.f}, sd = so;
 #pragma unroll
         for (int ww = 0; ww < 4; ++ww) {
-          so += *reinterpret_cast<const f32x4*>(&mbuf[ww][2 * cc][qo][l][0]);
-          if (TAN) sd += *reinterpret_cast<const f32x4*>(&mbuf[ww][2 * cc + 1][qo][l][0]);
+          so += *reinterpret_cast<const f32x4*>(&mbuf[ww][kMb * cc][qo][l][0]);
+          if (TAN) sd += *reinterpret_cast<const f32x4*>(&mbuf[ww][kMb * cc + 1][qo][l][0]);
         }
         O[cc] = so;
         DO[cc] = sd;
@@ -580,24 +641,14 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
         }
       }
     }
-    const unsigned char* rec = a.comp + ((int64_t)bh * a.Mq + mq) * kRec;
-    const float* zc = reinterpret_cast<const float*>(rec + 32768);
-    const float* dzc = reinterpret_cast<const float*>(rec + 33024);
     float dn = 0.f, ddn = 0.f;
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks) {
-      const f32x4 z0 = *reinterpret_cast<const f32x4*>(zc + 32 * ks + 8 * g);
-      const f32x4 z1 = *reinterpret_cast<const f32x4*>(zc + 32 * ks + 8 * g + 4);
-      f32x4 dz0 = f32x4{0.f, 0.f, 0.f, 0.f}, dz1 = dz0;
-      if (TAN) {
-        dz0 = *reinterpret_cast<const f32x4*>(dzc + 32 * ks + 8 * g);
-        dz1 = *reinterpret_cast<const f32x4*>(dzc + 32 * ks + 8 * g + 4);
-      }
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
-        const float z = e < 4 ? z0[e] : z1[e - 4];
+        const float z = zraw[ks][0][e >> 2][e & 3];
         dn += phi[ks][e] * z;
-        if (TAN) ddn += dphi[ks][e] * z + phi[ks][e] * (e < 4 ? dz0[e] : dz1[e - 4]);
+        if (TAN) ddn += dphi[ks][e] * z + phi[ks][e] * zraw[ks][1][e >> 2][e & 3];
       }
     }
     dn = sum_over_groups(dn);
@@ -607,19 +658,17 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     const float al = a.alpha[(int64_t)h * a.alpha_stride + mq];
 #pragma unroll
     for (int cc = 0; cc < 2; ++cc) {
-      const int vt_ = cpair + cc;
       f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f}, dnum = num;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        const float* Hc = reinterpret_cast<const float*>(rec);
         u32x4 hh, hl;
-        load_hfrag(Hc, ks, g, 16 * vt_ + r, hh, hl);
+        split_hfrag(hraw[cc][ks][0], hh, hl);
         num = mfma_bf16_16x16x32(hh, ph[ks], num);
         num = mfma_bf16_16x16x32(hh, pl[ks], num);
         num = mfma_bf16_16x16x32(hl, ph[ks], num);
         if (TAN) {
           u32x4 dh, dl;
-          load_hfrag(Hc + 4096, ks, g, 16 * vt_ + r, dh, dl);
+          split_hfrag(hraw[cc][ks][1], dh, dl);
           dnum = mfma_bf16_16x16x32(hh, dph[ks], dnum);
           dnum = mfma_bf16_16x16x32(hh, dpl[ks], dnum);
           dnum = mfma_bf16_16x16x32(hl, dph[ks], dnum);

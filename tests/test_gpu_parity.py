@@ -224,6 +224,29 @@ def test_all_tiles_routed_and_zero_tiles():
     assert torch.isfinite(o2).all() and torch.isfinite(do2).all()
 
 
+@pytest.mark.parametrize("T", [40, 64, 70])
+def test_scrambled_routing_lists(T):
+    """Routed lists in arbitrary order (the kernel visits them in ascending
+    tile order): up to 64 tiles are sorted in the registers of one wave,
+    longer lists by counting.  B = 1, H = 2, Np = 80, prefix 10, against the
+    oracle."""
+    say("scrambled LUT T", T)
+    B, H, Np, P = 1, 2, 80, 10
+    L = Np * 64 + P
+    q, k, v, dq, dk, dv = make_inputs(57 + T, B, H, L)
+    ins = dict(q=q, k=k, v=v, dq=dq, dk=dk, dv=dv)
+    Mb = Np + 1
+    rng = np.random.default_rng(T)
+    lut = np.stack([rng.permutation(Np)[:T] for _ in range(B * H * Mb)]).astype(np.int32)
+    lut = lut.reshape(B, H, Mb, T)
+    alpha = torch.rand(H, Mb, generator=torch.Generator().manual_seed(9)) * 0.8 + 0.1
+    o, do, aux = run_full(ins, alpha, T / Np, Np, P, lut=lut)
+    f = {n: t.float() for n, t in ins.items()}
+    eo, edo = O.cube_jvp(*(f[n] for n in ("q", "k", "v", "dq", "dk", "dv")), alpha, lut, Np, P)
+    assert max_abs(o, eo) < TOL_MAX and rel_l2(o, eo) < TOL_REL
+    assert max_abs(do, edo) < TOL_MAX and rel_l2(do, edo) < TOL_REL
+
+
 @pytest.mark.parametrize("T", [1, 5])
 @pytest.mark.parametrize("tangent", [True, False])
 def test_odd_routed_count(T, tangent):
