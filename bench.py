@@ -55,7 +55,11 @@ def measured_traffic(cfg, tangent):
     if cfg != 3 or not tangent or not os.path.exists(path):
         return None
     with open(path) as f:
-        return int(json.load(f)["bytes_per_launch"])
+        rec = json.load(f)
+    # the instance this run launches (bf16, tangent, linear branch, power-of-two scale)
+    if rec.get("kernel") != "void sla2h::fwd_jvp_kernel<sla2h::BF16, true, true, true, false>(sla2h::FwdArgs)":
+        return None
+    return int(rec["bytes_per_launch"])
 
 
 def roofline_work(B, H, Mb, T, n_tail, tangent):
@@ -66,13 +70,74 @@ def roofline_work(B, H, Mb, T, n_tail, tangent):
 
 
 def hbm_bytes(B, H, N, Np, tangent):
+    """Algorithmic HBM bytes of quant_pool and linear_states (each tensor read
+    or written once), plus the operand-tile writes of linear_states (the
+    fragment-ordered kt / vt tiles fwd_jvp streams, a layout choice of this
+    build): (quant, states, states_layout_writes)."""
     t = B * H * N * 64
-    quant = 2 * t * 2 + 2 * t + 2 * B * H * (-(-N // 64)) * 4 + B * H * (-(-N // 64) + Np) * 64 * 4
+    nb = -(-N // 64)
+    quant = 2 * t * 2 + 2 * t + 2 * B * H * nb * 4 + B * H * (nb + Np) * 64 * 4
     n_in = 4 if tangent else 2
-    tiles = B * H * (-(-N // 64)) * 64 * 64 * 2  # one 16-bit (64, 64) operand tile per block
-    states = (n_in * t * 2 + (2 if tangent else 1) * B * H * Np * (64 * 64 + 64) * 4
-              + (4 if tangent else 1) * tiles)  # vt (V|dV) and kt (K|dK) operand tiles
-    return quant, states
+    states = n_in * t * 2 + (2 if tangent else 1) * B * H * Np * (64 * 64 + 64) * 4
+    tile = B * H * nb * 64 * 64 * 2  # one 16-bit (64, 64) operand tile per block
+    layout = (4 if tangent else 1) * tile  # K|dK and V|dV tiles, or V only
+    return quant, states, layout
+
+
+def stream_ceiling(read_bytes, write_bytes):
+    """Fastest time for the same read / write byte counts with a plain
+    streaming kernel (libsla2probe.so: 16 B per lane, nontemporal, grid-stride;
+    best of two grids and five runs), after a 1 GiB write that flushes L2 and
+    the 256 MB MALL ('flushed') and with the inputs just read ('resident')."""
+    import ctypes
+    from imfvideo_amd import build as _b
+    lib = ctypes.CDLL(_b.PROBE_LIB)
+    lib.sla2h_probe_stream.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] + [ctypes.c_int] * 3 + [ctypes.c_void_p]
+    if write_bytes == 0:
+        rd, wr = 1, 0
+    else:
+        ratio = read_bytes / write_bytes
+        rd, wr = min(((2, 1), (1, 1), (1, 2)), key=lambda m: abs(m[0] / m[1] - ratio))
+    n_grp = (read_bytes + write_bytes) // (16 * (rd + wr))
+    dev = torch.device("cuda:0")
+    src = torch.empty(rd * n_grp * 4, dtype=torch.int32, device=dev).fill_(1)
+    dst = torch.empty(wr * n_grp * 4, dtype=torch.int32, device=dev)
+    sink = torch.empty(8192 * 4, dtype=torch.int32, device=dev)
+    junk = torch.empty(256 * 1024 * 1024, dtype=torch.int32, device=dev)
+    stream = torch.cuda.current_stream().cuda_stream
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    best = {"flushed": 1e9, "resident": 1e9}
+    for grid in (1024, 4096):
+        for rep in range(6):
+            for mode in ("flushed", "resident"):
+                if mode == "flushed":
+                    junk.fill_(rep)
+                e0.record()
+                rc = lib.sla2h_probe_stream(src.data_ptr(), dst.data_ptr(), sink.data_ptr(), n_grp,
+                                            rd, wr, grid, stream)
+                e1.record()
+                torch.cuda.synchronize()
+                if rc != 0:
+                    raise RuntimeError(f"sla2h_probe_stream failed ({rc})")
+                if rep:
+                    best[mode] = min(best[mode], e0.elapsed_time(e1) * 1e3)
+    moved = 16 * (rd + wr) * n_grp
+    del src, dst, sink, junk
+    return {"mix": f"read:write {rd}:{wr}", "bytes": moved,
+            "flushed_us": round(best["flushed"], 2), "resident_us": round(best["resident"], 2),
+            "flushed_GB/s": round(moved / best["flushed"] / 1e3, 1),
+            "resident_GB/s": round(moved / best["resident"] / 1e3, 1)}
+
+
+def cpu_model():
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(cfg_d, tangent):
@@ -97,7 +162,7 @@ def cpu_baseline(cfg_d, tangent):
         times.append(time.perf_counter() - t0)
     per_head = statistics.median(times)
     return {"value": per_head * cfg_d["H"] * 1e3, "unit": "ms", "cores": torch.get_num_threads(),
-            "kind": "port",
+            "cpu_model": cpu_model(), "kind": "port",
             "sample": f"oracle (eager torch/numpy fp32, route + quant + states + blockwise op) on "
                       f"1 of {cfg_d['H']} heads of the workload, median of 3 after 1 warm-up, "
                       f"scaled x{cfg_d['H']} (heads are independent)"}
@@ -336,6 +401,9 @@ def main():
     ap.add_argument("--cpu-baseline", type=int, default=1)
     ap.add_argument("--op-only", action="store_true",
                     help="Config 5: time the attention op's training step instead of the blocks")
+    ap.add_argument("--hbm-ceiling", action="store_true",
+                    help="print only the streaming ceilings (libsla2probe.so) for the read:write "
+                         "mixes and byte counts of quant_pool and linear_states, one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB fp32 copy kernel (torch.mul by 1) three times: "
                          "the reference reading for the FETCH_SIZE / WRITE_SIZE counters")
@@ -347,6 +415,15 @@ def main():
             torch.mul(x, 1.0, out=y)
         torch.cuda.synchronize()
         print(json.dumps({"copy_calibration": "256 MiB read + 256 MiB written per dispatch"}))
+        return
+    if args.hbm_ceiling:
+        t_in = 8 * 29952 * 64 * 2  # one (1, 8, 29952, 64) 16-bit tensor
+        cases = {"read only, 247 MB": (247283712, 0),
+                 "read:write 1:1, 247 MB (linear_states, algorithmic)": (4 * t_in, 247283712 - 4 * t_in),
+                 "read:write 2:1, 94 MB (quant_pool)": (2 * t_in, 93959424 - 2 * t_in),
+                 "read:write 1:2, 370 MB (linear_states with operand tiles)": (4 * t_in, 369967104 - 4 * t_in),
+                 "read:write 1:1, 1 GB": (500 << 20, 500 << 20)}
+        print(json.dumps({name: stream_ceiling(r, w) for name, (r, w) in cases.items()}), flush=True)
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
@@ -407,7 +484,24 @@ def main():
     pairs, ops_i8, flops16 = roofline_work(B, H, Mb, T, Mb - Np, tangent)
     t_attn = stage_us["fwd_jvp"] * 1e-6
     achieved = (ops_i8 / 2 + flops16) / t_attn / 1e12
-    qb, sb = hbm_bytes(B, H, N, Np, tangent)
+    qb, sb, sl = hbm_bytes(B, H, N, Np, tangent)
+    # read / write split of each kernel's moved bytes for the matching ceiling
+    t_in = B * H * N * 64 * 2
+    q_read = 2 * t_in
+    s_read = (4 if tangent else 2) * t_in
+    ceil_q = stream_ceiling(q_read, qb - q_read)
+    ceil_s = stream_ceiling(s_read, sb + sl - s_read)
+
+    def hbm_entry(name, alg, moved, ceil):
+        us = stage_us[name]
+        e = {"bytes": alg, "GB/s": round(alg / us / 1e3, 1),
+             "frac": round(alg / us / 1e3 / PEAK_HBM_GBS, 4),
+             "moved_bytes": moved, "moved_GB/s": round(moved / us / 1e3, 1),
+             "ceiling": ceil, "frac_of_ceiling": round(ceil["flushed_us"] / us, 4)}
+        if moved != alg:
+            e["layout_write_bytes"] = moved - alg
+        return e
+
     out = {
         "metric": METRIC,
         "value": round(ms, 4),
@@ -434,10 +528,11 @@ def main():
                                       "at its 2x peak, so frac = t_roofline / t"}},
         "kernels_us": {k_: round(v_, 2) for k_, v_ in stage_us.items()},
         "hbm_kernels": {
-            "quant_pool": {"bytes": qb, "GB/s": round(qb / stage_us["quant_pool"] / 1e3, 1),
-                           "frac": round(qb / stage_us["quant_pool"] / 1e3 / PEAK_HBM_GBS, 4)},
-            "linear_states": {"bytes": sb, "GB/s": round(sb / stage_us["linear_states"] / 1e3, 1),
-                              "frac": round(sb / stage_us["linear_states"] / 1e3 / PEAK_HBM_GBS, 4)},
+            "quant_pool": hbm_entry("quant_pool", qb, qb, ceil_q),
+            "linear_states": hbm_entry("linear_states", sb, sb + sl, ceil_s),
+            "note": "bytes: algorithmic (each tensor once); frac: of 8 TB/s; ceiling: a "
+                    "streaming kernel moving the same bytes at the same read:write mix; "
+                    "frac_of_ceiling = flushed ceiling time / kernel time",
         },
     }
     if args.cpu_baseline:
