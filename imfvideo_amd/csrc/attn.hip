@@ -151,38 +151,10 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     tiles[j].x = n;
   }
   __syncthreads();
-  // Routed tiles in ascending id order: the workgroups of an XCD (consecutive
-  // query blocks of one head) then sweep the head's key tiles together and
-  // share them in that XCD's L2.  Up to 64 routed tiles: a bitonic sort in the
-  // registers of wave 0; longer lists: rank by counting (ties by position).
-  if (a.T <= 64) {
-    if (w == 0) {
-      int v = l < a.T ? tiles[l].x : INT_MAX;
-#pragma unroll
-      for (int k = 2; k <= 64; k <<= 1) {
-#pragma unroll
-        for (int jj = k >> 1; jj > 0; jj >>= 1) {
-          const int o = __shfl_xor(v, jj);
-          v = (((l & jj) == 0) == ((l & k) == 0)) ? min(v, o) : max(v, o);
-        }
-      }
-      if (l < a.T) tiles[l].x = v;
-    }
-  } else {
-    int* tmp = reinterpret_cast<int*>(&mbuf[0][0][0][0][0]);
-    for (int j = tid; j < a.T; j += 256) {
-      const int nj = tiles[j].x;
-      int c = 0;
-      for (int i = 0; i < a.T; ++i) {
-        const int ni = tiles[i].x;
-        c += (ni < nj) || (ni == nj && i < j);
-      }
-      tmp[c] = nj;
-    }
-    __syncthreads();
-    for (int j = tid; j < a.T; j += 256) tiles[j].x = tmp[j];
-  }
-  __syncthreads();
+  // routed tiles in ascending id order (the prefix tails stay at the end)
+  sort_ids_ascending(
+      a.T, tid, [&](int i) { return tiles[i].x; }, [&](int i, int v) { tiles[i].x = v; },
+      reinterpret_cast<int*>(&mbuf[0][0][0][0][0]));
   // A partial key tile (1-D blocks over a ragged L) can sit anywhere in a routed
   // list: move it to the end, where the masked one-tile path handles it.
   int Tu = a.T;

@@ -274,6 +274,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
     const int n = lrow[j];
     tiles[j] = n < 0 ? 0 : (n >= a.Nb ? a.Nb - 1 : n);
   }
+  __syncthreads();
+  // the augmented list in ascending tile order (dq sums over all of it)
+  sort_ids_ascending(
+      a.J, tid, [&](int i) { return tiles[i]; }, [&](int i, int v) { tiles[i] = v; },
+      reinterpret_cast<int*>(&mb[0][0][0][0][0]));
 
   // resident B operands: Q and do_s rows 16qb + r, channels 32ks + 8g .. +7
   u32x4 qf[4][2], df[4][2];
@@ -324,9 +329,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
   const int tfoff = (w * 64 + l) * 32;  // bytes: this lane's four K^T fragments
   const unsigned char* ktf = reinterpret_cast<const unsigned char*>(a.ktf) + (int64_t)bh * a.Nb * 8192;
 
+  // score-side operands (K, V rows) and the K^T fragments of the dq product,
+  // loaded separately: the K^T fragments are used last, by the pair product
   struct Frags {
     u32x4 k[2], v[2];
-    u32x2 kt[4];
   };
   auto load = [&](int j, Frags& f) {
     const int n = __builtin_amdgcn_readfirstlane(tiles[j]);
@@ -335,12 +341,15 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
       f.k[ks] = buf_load16(rk, n * kT * kT * 2 + rowoff + 64 * ks, 0);
       f.v[ks] = buf_load16(rv, n * kT * kT * 2 + rowoff + 64 * ks, 0);
     }
+  };
+  auto load_kt = [&](int j, u32x2 (&kt)[4]) {
+    const int n = __builtin_amdgcn_readfirstlane(tiles[j]);
     const u32x4 k01 = *reinterpret_cast<const u32x4*>(ktf + (int64_t)n * 8192 + tfoff);
     const u32x4 k23 = *reinterpret_cast<const u32x4*>(ktf + (int64_t)n * 8192 + tfoff + 16);
-    f.kt[0] = u32x2{k01[0], k01[1]};
-    f.kt[1] = u32x2{k01[2], k01[3]};
-    f.kt[2] = u32x2{k23[0], k23[1]};
-    f.kt[3] = u32x2{k23[2], k23[3]};
+    kt[0] = u32x2{k01[0], k01[1]};
+    kt[1] = u32x2{k01[2], k01[3]};
+    kt[2] = u32x2{k23[0], k23[1]};
+    kt[3] = u32x2{k23[2], k23[3]};
   };
 
   f32x4 acc[4][4];
@@ -352,7 +361,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
   // Keys past L need no mask here: their K and V rows read as zero (buffer
   // range check) and their K^T fragments are zero-filled, so dp = 0, ds stays
   // finite (p <= 2^4) and K^T ds adds exactly zero to dq.
-  auto tile = [&](const Frags& f, int j) {
+  // ds^T fragments of one tile: lane (g, r) holds keys 16w+4g+i of query 16qb+r
+  auto tile_ds = [&](const Frags& f, u32x2 (&dsp)[4]) {
 #pragma unroll
     for (int qb = 0; qb < 4; ++qb) {
       f32x4 sc = mfma_16x16x32<T16>(f.k[0], qf[qb][0], f32x4{0.f, 0.f, 0.f, 0.f});
@@ -365,23 +375,52 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
         const float p = fast_exp2(fminf(sc[i] * a.c - lse_r[qb], 4.f));
         ds[i] = sat(p * (dp[i] - del_r[qb]));
       }
-      const u32x2 dsp = pack4<T16>(ds[0], ds[1], ds[2], ds[3]);
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) acc[qb][ct] = mfma_16x16x16<T16>(f.kt[ct], dsp, acc[qb][ct]);
+      dsp[qb] = pack4<T16>(ds[0], ds[1], ds[2], ds[3]);
     }
   };
+  // dq^T += K^T ds^T over the wave's 16 keys of one tile (K = 16), or of a pair
+  // of tiles on one K = 32 product (operand slots 4..7 carry the second tile)
+  auto dq_single = [&](const u32x2 (&kt)[4], const u32x2 (&dsp)[4]) {
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) acc[qb][ct] = mfma_16x16x16<T16>(kt[ct], dsp[qb], acc[qb][ct]);
+  };
+  auto dq_pair = [&](const u32x2 (&kta)[4], const u32x2 (&dsa)[4], const u32x2 (&ktb)[4],
+                     const u32x2 (&dsb)[4]) {
+#pragma unroll
+    for (int qb = 0; qb < 4; ++qb)
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+        acc[qb][ct] = mfma_16x16x32<T16>(u32x4{kta[ct].x, kta[ct].y, ktb[ct].x, ktb[ct].y},
+                                         u32x4{dsa[qb].x, dsa[qb].y, dsb[qb].x, dsb[qb].y},
+                                         acc[qb][ct]);
+  };
 
+  // Tiles in pairs: the second tile's operands are requested before the
+  // first tile's scores, the next pair's first tile right after them, the
+  // K^T fragments of the next pair after the pair product that frees theirs.
   const int J = a.J;
   Frags fa, fb;
+  u32x2 kta[4], ktb[4];
   load(0, fa);
+  load_kt(0, kta);
   int j = 0;
   for (; j + 1 < J; j += 2) {
+    u32x2 dsa[4], dsb[4];
     load(j + 1, fb);
-    tile(fa, j);
+    load_kt(j + 1, ktb);
+    tile_ds(fa, dsa);
     load(j + 2 < J ? j + 2 : J - 1, fa);
-    tile(fb, j + 1);
+    tile_ds(fb, dsb);
+    dq_pair(kta, dsa, ktb, dsb);
+    load_kt(j + 2 < J ? j + 2 : J - 1, kta);
   }
-  if (j < J) tile(fa, j);
+  if (j < J) {
+    u32x2 dsa[4];
+    tile_ds(fa, dsa);
+    dq_single(kta, dsa);
+  }
 
   // sum the key-split partials: round t moves query groups 2t, 2t+1
   f32x4 tot[4];

@@ -161,6 +161,44 @@ __device__ inline u32x2 buf_load8(__amdgpu_buffer_rsrc_t rs, int voff, int soff)
 // 2^x on the hardware exp unit (v_exp_f32); inputs here are <= 0 or -inf.
 __device__ inline float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
+// Ascending sort of the n tile ids of a visiting list in LDS (element i read
+// with get(i), written with set(i, id)).  Workgroups that visit their tiles in
+// ascending order sweep the key tiles of a head together and share them in
+// the XCD's L2.  Up to 64 ids: a bitonic sort in the registers of wave 0
+// (threads 0..63); more: rank by counting into tmp (n ints of LDS), ties by
+// position.  Called by every thread of a 256-thread workgroup after the list
+// is complete in LDS (barrier included); ends with a barrier.
+template <typename Get, typename Set>
+__device__ inline void sort_ids_ascending(int n, int tid, Get get, Set set, int* tmp) {
+  if (n <= 64) {
+    if (tid < 64) {
+      int v = tid < n ? get(tid) : 0x7fffffff;
+#pragma unroll
+      for (int k = 2; k <= 64; k <<= 1) {
+#pragma unroll
+        for (int jj = k >> 1; jj > 0; jj >>= 1) {
+          const int o = __shfl_xor(v, jj);
+          v = (((tid & jj) == 0) == ((tid & k) == 0)) ? min(v, o) : max(v, o);
+        }
+      }
+      if (tid < n) set(tid, v);
+    }
+  } else {
+    for (int j = tid; j < n; j += 256) {
+      const int nj = get(j);
+      int c = 0;
+      for (int i = 0; i < n; ++i) {
+        const int ni = get(i);
+        c += (ni < nj) || (ni == nj && i < j);
+      }
+      tmp[c] = nj;
+    }
+    __syncthreads();
+    for (int j = tid; j < n; j += 256) set(j, tmp[j]);
+  }
+  __syncthreads();
+}
+
 }  // namespace sla2h
 
 #define SLA2H_CHECK_ARG(cond) \
