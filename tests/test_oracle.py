@@ -251,6 +251,46 @@ def test_oracle_reproduces_golden(name):
 
 
 # ------------------------------------------------ training forward, semantics (b)
+@pytest.mark.parametrize("path", ["train_fwd", "infer_1d"])
+def test_int8_p_law_recovered_through_identity_values(path):
+    """P enters the INT8 P.V product as trunc(127 p + 0.5) (reference
+    models/sla2_vendor/kernel_sparse_qat.py:103, the truncating cast of a
+    non-negative value), p = exp2(s - m) against the running maximum.  With
+    V = 127 I (its INT8 tile is 127 I and its scale exactly 1), o_s = P8 / l
+    row by row, so round(o_s * l) recovers every P8 exactly (16-bit o_s:
+    relative error <= 2^-9, 127 * 2^-9 < 0.5).  The expected P8 comes from
+    fp64 scores of the INT8 operands (their quantisation is pinned above);
+    entries within 1e-3 of a rounding boundary are left out.  floor(127 p),
+    a plausible slip, differs on about half of the entries."""
+    g = torch.Generator().manual_seed(11)
+    L, D = 64, 64
+    q = torch.randn(1, 1, L, D, generator=g).to(torch.bfloat16).float()
+    k = torch.randn(1, 1, L, D, generator=g).to(torch.bfloat16).float()
+    v = torch.zeros(1, 1, L, D)
+    v[0, 0, torch.arange(D), torch.arange(D)] = 127.0
+    lut = np.zeros((1, 1, 1, 1), dtype=np.int32)
+    if path == "train_fwd":
+        res = O.train_fwd(q, k, v, torch.ones(1, 1), lut, 1, 0)
+    else:
+        res = O.infer_1d(q, k, v, torch.ones(1, 1), lut, 64)
+    q8, qs = O.quantize_blocks_trunc(q)
+    k8, ks = O.quantize_blocks_trunc(k)
+    _, vs = O.quantize_blocks_trunc(v)
+    assert float(vs[0, 0, 0]) == 1.0
+    si = q8[0, 0].astype(np.float64) @ k8[0, 0].astype(np.float64).T
+    c2 = float(np.float32(np.float32(D ** -0.5) * O.LOG2E))
+    qk = si * float(qs[0, 0, 0]) * float(ks[0, 0, 0]) * c2
+    p = np.exp2(qk - qk.max(1, keepdims=True))
+    l = p.sum(1, keepdims=True)
+    got = np.rint(res["o_s"][0, 0].double().numpy() * l)
+    x = 127.0 * p + 0.5
+    want = np.floor(x)
+    keep = np.abs(x - np.rint(x)) > 1e-3
+    assert keep.mean() > 0.95
+    assert np.array_equal(got[keep], want[keep])
+    assert (np.floor(127.0 * p) != want)[keep].mean() > 0.4
+
+
 def test_quantize_trunc_known_answers():
     # amax = 127 -> s = 1 exactly (1e-12 vanishes in fp32): q = trunc(fl(x + 0.5 sign x))
     x = np.zeros((64, 64), np.float32)
