@@ -457,3 +457,54 @@ def test_module_training_step_gradients():
         print(f"  {name} max {max_abs(got, want):.2e} rel {rel_l2(got, want):.2e}", flush=True)
         assert rel_l2(got, want) < TOL_REL and max_abs(got, want) < TOL_MAX * max(1, want.abs().max())
     assert rel_l2(grads[3], ref["d_alpha"]) < 1e-3
+
+
+
+@pytest.mark.parametrize("case", range(12))
+def test_random_shapes_sweep(case):
+    """Seeded random shapes against the oracle: B in 1..2, H in 1..3, Np
+    video tiles in 2..139, a prefix of 0..63 tokens (ragged last block), T in
+    1..Np (above 64 on four cases), bf16 or fp16, primal or tangent,
+    sparse-only on three cases.  The router's LUT and the INT8 quantization
+    bit-exact, o and do within the north-star tolerances."""
+    rng = np.random.default_rng(1000 + case)
+    B, H = int(rng.integers(1, 3)), int(rng.integers(1, 4))
+    Np = int(rng.integers(2, 140))
+    P = int(rng.integers(0, 64))
+    T = int(rng.integers(1, Np + 1))
+    dt = torch.bfloat16 if case % 2 == 0 else torch.float16
+    tangent = case % 3 != 1
+    sparse_only = case % 4 == 3
+    L = Np * 64 + P
+    Mb = -(-L // 64)
+    say("random case", case, dict(B=B, H=H, Np=Np, P=P, T=T, dtype=str(dt), tangent=tangent,
+                                   sparse_only=sparse_only))
+    q, k, v, dq, dk, dv = make_inputs(2000 + case, B, H, L, dtype=dt)
+    ins = dict(q=q, k=k, v=v, dq=dq, dk=dk, dv=dv)
+    alpha = (torch.ones(H, Mb) if sparse_only else
+             torch.rand(H, Mb, generator=torch.Generator().manual_seed(case)) * 0.8 + 0.1)
+    frac = (T + 0.5) / Np
+    o, do, aux = run_full(ins, alpha, frac, Np, P, tangent=tangent)
+    f = {n: t.float() for n, t in ins.items()}
+    ref_lut, refT, _, _ = O.route(f["q"], f["k"], frac, Np, P)
+    assert refT == T and np.array_equal(aux["lut"].numpy(), ref_lut)
+    rq8, rqs = O.quantize_blocks(f["q"])
+    assert np.array_equal(aux["q8"].numpy(), np.asarray(rq8))
+    assert np.array_equal(aux["qs"].numpy(), np.asarray(rqs))
+    tan = [f["dq"], f["dk"], f["dv"]] if tangent else [None, None, None]
+    eo, edo = O.cube_jvp(f["q"], f["k"], f["v"], *tan, alpha, ref_lut, Np, P, t16=dt)
+    print(f"  o max {max_abs(o, eo):.2e} rel {rel_l2(o, eo):.2e}", flush=True)
+    assert max_abs(o, eo) < TOL_MAX and rel_l2(o, eo) < TOL_REL
+    if tangent:
+        print(f"  do max {max_abs(do, edo):.2e} rel {rel_l2(do, edo):.2e}", flush=True)
+        assert max_abs(do, edo) < TOL_MAX and rel_l2(do, edo) < TOL_REL
+    else:
+        assert do is None
+    if sparse_only:
+        from imfvideo_amd.sla2_cube_qat import _sparse_primal_only
+        os_ = _sparse_primal_only(cuda(q), cuda(k), cuda(v), cuda(torch.from_numpy(ref_lut)), T,
+                                  Np, 64, P).cpu()
+        es, _ = O.cube_jvp(f["q"], f["k"], f["v"], None, None, None, alpha, ref_lut, Np, P,
+                           t16=dt, sparse_only=True)
+        print(f"  sparse-only max {max_abs(os_, es):.2e} rel {rel_l2(os_, es):.2e}", flush=True)
+        assert max_abs(os_, es) < TOL_MAX and rel_l2(os_, es) < TOL_REL
