@@ -1,11 +1,12 @@
 // Fused SLA2 sparse + linear attention with forward-mode JVP, gfx950.
 //
-// Work unit: 32 query rows (half of a 64-row query block m) of one (b, h),
-// one workgroup of 4 wave64.  The key tiles of the block (T routed video
-// tiles + n_tail prefix blocks) are split across the waves by key: wave w
-// owns keys 16w..16w+15 of every tile and runs its own softmax over them for
-// the 32 queries; the four partial states are merged once at the end through
-// LDS.  Each wave streams its quarter of every key tile straight from global
+// Work unit: with the tangent, 32 query rows (half of a 64-row query block
+// m) of one (b, h); primal only, all 64 rows of the block (the accumulators
+// of 64 queries fit in the registers without the dO half).  One workgroup of
+// 4 wave64.  The key tiles of the block (T routed video tiles + n_tail prefix
+// blocks) are split across the waves by key: wave w owns keys 16w..16w+15 of
+// every tile and runs its own softmax over them for the unit's queries; the
+// four partial states are merged once at the end through LDS.  Each wave streams its quarter of every key tile straight from global
 // memory into MFMA operand registers (one tile ahead) -- no barriers in the
 // key loop.  One pass over the tiles with a lazy running maximum: it moves
 // only when a tile exceeds it by a margin (one wave ballot per tile), so the
@@ -29,7 +30,6 @@
 namespace sla2h {
 
 constexpr int kTa = 64;
-constexpr int kQT = 2;  // 16-row query sub-tiles per workgroup
 constexpr size_t kRec = 2 * 16384 + 2 * 256;
 constexpr int kMaxTiles = 1024;  // T + n_tail per query block
 
@@ -93,14 +93,16 @@ struct ValRegs {   // value-side operands, loaded at the start of their own tile
 
 // S16: primal scores from the 16-bit K Q^T (the K half of the kt operands and
 // the Q half of the [dQ|Q] operands) instead of INT8 (the 1-D SLA2 JVP).
+// Two workgroups per CU with the tangent (its registers), three primal only.
 template <typename T16, bool TAN, bool LINEAR, bool PRE, bool S16>
-__global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
+__global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
+  constexpr int kQT = TAN ? 2 : 4;  // 16-row query sub-tiles per workgroup
   __shared__ float stat[3][4][kQT][16];  // [m,l,mu][wave][qt][r]
-  // [dQ|Q] B-operand fragments [qt][ks][lane] (16 B each)
-  __shared__ __align__(16) u32x4 qsh[kQT][4][64];
+  // [dQ|Q] B-operand fragments [qt][ks][lane] (16 B each, tangent only)
+  __shared__ __align__(16) u32x4 qsh[TAN ? kQT : 1][4][64];
   __shared__ __align__(16) i32x4 q8sh[kQT][64];  // INT8 Q B-operand fragments
   // cross-wave merge buffer [wave][column tile of the round x {O, dO}][qt][lane][4]
-  // (no dO slots without tangent: the primal instances fit four workgroups per CU)
+  // (no dO slots without tangent)
   constexpr int kMb = TAN ? 2 : 1;
   __shared__ __align__(16) float mbuf[4][2 * kMb][kQT][64][4];
   // key tiles of this query block in visiting order: (tile id, key scale)
@@ -111,13 +113,17 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   if (logical >= a.nwork) return;  // whole workgroup: no barrier skipped
   // integer division runs on the VALU: pin the (uniform) results to SGPRs so
   // that every pointer and buffer descriptor derived from them stays scalar
-  const int half = logical & 1;
-  const int bh = __builtin_amdgcn_readfirstlane((logical >> 1) / a.Mb);
-  const int m = __builtin_amdgcn_readfirstlane((logical >> 1) - bh * a.Mb);
+  const int half = TAN ? (logical & 1) : 0;
+  const int unit = TAN ? (logical >> 1) : logical;  // query block of the work unit
+  const int bh = __builtin_amdgcn_readfirstlane(unit / a.Mb);
+  const int m = __builtin_amdgcn_readfirstlane(unit - bh * a.Mb);
   const int h = __builtin_amdgcn_readfirstlane(bh % a.H);
 
   const int tid = threadIdx.x;
-  const int w = tid >> 6, l = tid & 63, r = l & 15, g = l >> 4;
+  // wave index uniform (SGPR) and lane index from mbcnt: neither holds a
+  // VGPR across the key loop
+  const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int l = __lane_id(), r = l & 15, g = l >> 4;
   const int64_t L = a.L;
   const int64_t qkbase = (int64_t)bh * L;
   const int64_t q0 = (int64_t)m * kTa + 32 * half;  // first query row of the unit
@@ -429,30 +435,44 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     o_single(vr, pb);
     ka_ = kb_;
   }
-  // this wave's part of the complement record (Hc, dHc fragments of its two
+  // this wave's part of the complement record (Hc, dHc fragments of its
   // output column tiles, zc, dzc), requested now: the loads stay in flight
-  // through the merge below.  The wave finalises query sub-tile qo and
-  // output column tiles cpair, cpair + 1.
-  const int qo = w >> 1;
-  const int cpair = 2 * (w & 1);
-  float hraw[2][2][2][8];  // [cc][ks][Hc, dHc][j]: H[32 ks + 8 g + j][16 (cpair + cc) + r]
+  // through the merge below.  The wave finalises query sub-tile qo and the
+  // kNcc output column tiles cpair .. cpair + kNcc - 1: with the tangent two
+  // waves share a sub-tile (column tiles 0-1 and 2-3), primal only each wave
+  // takes one sub-tile whole.
+  constexpr int kNcc = TAN ? 2 : 4;
+  const int qo = TAN ? w >> 1 : w;
+  const int cpair = TAN ? 2 * (w & 1) : 0;
+  // With the tangent all H fragments are requested here; primal only (four
+  // column tiles per wave) each tile's are loaded where the epilogue uses
+  // them, which keeps the workgroup within three per CU.
+  constexpr bool kHEarly = TAN;
+  // [slot][ks][Hc, dHc][j]: H[32 ks + 8 g + j][16 (cpair + cc) + r] of column tile cc
+  float hraw[kHEarly ? kNcc : 1][2][TAN ? 2 : 1][8];
   f32x4 zraw[2][2][2];     // [ks][zc, dzc][half]: z[32 ks + 8 g + 4 half ..]
+  const float* rec = reinterpret_cast<const float*>(a.comp + ((int64_t)bh * a.Mq + mq) * kRec);
+  auto load_h = [&](int slot, int cc) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int mat = 0; mat < (TAN ? 2 : 1); ++mat)
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          hraw[slot][ks][mat][jj] = rec[4096 * mat + (32 * ks + 8 * g + jj) * 64 + 16 * (cpair + cc) + r];
+  };
   if (LINEAR) {
-    const float* rec = reinterpret_cast<const float*>(a.comp + ((int64_t)bh * a.Mq + mq) * kRec);
+    if (kHEarly) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+      for (int cc = 0; cc < kNcc; ++cc) load_h(cc, cc);
+    }
 #pragma unroll
-      for (int mat = 0; mat < (TAN ? 2 : 1); ++mat) {
+    for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj)
-            hraw[cc][ks][mat][jj] = rec[4096 * mat + (32 * ks + 8 * g + jj) * 64 + 16 * (cpair + cc) + r];
+      for (int mat = 0; mat < (TAN ? 2 : 1); ++mat)
 #pragma unroll
         for (int hf = 0; hf < 2; ++hf)
           zraw[ks][mat][hf] = *reinterpret_cast<const f32x4*>(rec + 8192 + 64 * mat + 32 * ks + 8 * g + 4 * hf);
-      }
-    }
   }
   float l_i[kQT];
 #pragma unroll
@@ -493,9 +513,10 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     mutot += stat[2][ww][qo][r] * f;
   }
 
-  // two rounds (column tiles 0-1, then 2-3), O and dO together; round rd
-  // is summed by the waves with (w & 1) == rd
-  f32x4 O[2], DO[2];
+  // two rounds (column tiles 0-1, then 2-3), O and dO together; with the
+  // tangent round rd is summed by the waves with (w & 1) == rd, primal only
+  // every wave sums both rounds for its sub-tile
+  f32x4 O[kNcc], DO[kNcc];
 #pragma unroll
   for (int rd = 0; rd < 2; ++rd) {
 #pragma unroll
@@ -508,7 +529,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
               acc_do[2 * rd + cc][qt] * fself[qt];
       }
     __syncthreads();
-    if ((w & 1) == rd) {
+    if (!TAN || (w & 1) == rd) {
 #pragma unroll
       for (int cc = 0; cc < 2; ++cc) {
         f32x4 so = f32x4{0.f, 0.f, 0.f, 0.f}, sd = so;
@@ -517,8 +538,8 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
           so += *reinterpret_cast<const f32x4*>(&mbuf[ww][kMb * cc][qo][l][0]);
           if (TAN) sd += *reinterpret_cast<const f32x4*>(&mbuf[ww][kMb * cc + 1][qo][l][0]);
         }
-        O[cc] = so;
-        DO[cc] = sd;
+        O[TAN ? cc : 2 * rd + cc] = so;
+        DO[TAN ? cc : 2 * rd + cc] = sd;
       }
     }
     if (rd == 0) __syncthreads();
@@ -528,9 +549,9 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   const int64_t qrow = q0 + 16 * qo + r;
   const float rl = 1.f / ltot;
   const float inv_mu = mutot * rl;
-  f32x4 os[2], dos[2];
+  f32x4 os[kNcc], dos[kNcc];
 #pragma unroll
-  for (int cc = 0; cc < 2; ++cc) {
+  for (int cc = 0; cc < kNcc; ++cc) {
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       os[cc][i] = O[cc][i] * rl;
@@ -629,18 +650,20 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
     if (TAN) ddn = sum_over_groups(ddn);
     const float al = a.alpha[(int64_t)h * a.alpha_stride + mq];
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
+    for (int cc = 0; cc < kNcc; ++cc) {
+      const int hs = kHEarly ? cc : 0;
+      if (!kHEarly) load_h(0, cc);
       f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f}, dnum = num;
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
         u32x4 hh, hl;
-        split_hfrag(hraw[cc][ks][0], hh, hl);
+        split_hfrag(hraw[hs][ks][0], hh, hl);
         num = mfma_bf16_16x16x32(hh, ph[ks], num);
         num = mfma_bf16_16x16x32(hh, pl[ks], num);
         num = mfma_bf16_16x16x32(hl, ph[ks], num);
         if (TAN) {
           u32x4 dh, dl;
-          split_hfrag(hraw[cc][ks][1], dh, dl);
+          split_hfrag(hraw[hs][ks][1], dh, dl);
           dnum = mfma_bf16_16x16x32(hh, dph[ks], dnum);
           dnum = mfma_bf16_16x16x32(hh, dpl[ks], dnum);
           dnum = mfma_bf16_16x16x32(hl, dph[ks], dnum);
@@ -664,7 +687,7 @@ __global__ __launch_bounds__(256, 2) void fwd_jvp_kernel(FwdArgs a) {
   if (qrow < L) {
     const int64_t oo = (qkbase + qrow) * kTa + 4 * g;
 #pragma unroll
-    for (int cc = 0; cc < 2; ++cc) {
+    for (int cc = 0; cc < kNcc; ++cc) {
       *reinterpret_cast<f32x4*>(a.o + oo + 16 * (cpair + cc)) = os[cc];
       if (TAN) *reinterpret_cast<f32x4*>(a.dout + oo + 16 * (cpair + cc)) = dos[cc];
     }
@@ -706,7 +729,8 @@ extern "C" int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, cons
   const bool linear = (flags & SLA2H_FLAG_SPARSE_ONLY) == 0;
   if (linear) SLA2H_CHECK_ARG(comp && alpha && alpha_stride >= 0);
   const int Nb = (int)((L + E - 1) / E);
-  const int64_t nwork = 2ll * Nb * B * H;  // half query blocks
+  // work units: half query blocks with the tangent, whole blocks primal only
+  const int64_t nwork = (tan ? 2ll : 1ll) * Nb * B * H;
   const int64_t per_xcd = (nwork + 7) / 8;
   SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31));
   FwdArgs a;
