@@ -1,24 +1,27 @@
 // Fused SLA2 sparse + linear attention with forward-mode JVP, gfx950.
 //
-// Work unit: with the tangent, 32 query rows (half of a 64-row query block
-// m) of one (b, h); primal only, all 64 rows of the block (the accumulators
-// of 64 queries fit in the registers without the dO half).  One workgroup of
-// 4 wave64.  The key tiles of the block (T routed video tiles + n_tail prefix
-// blocks) are split across the waves by key: wave w owns keys 16w..16w+15 of
-// every tile and runs its own softmax over them for the unit's queries; the
-// four partial states are merged once at the end through LDS.  Each wave streams its quarter of every key tile straight from global
-// memory into MFMA operand registers (one tile ahead) -- no barriers in the
-// key loop.  One pass over the tiles with a lazy running maximum: it moves
-// only when a tile exceeds it by a margin (one wave ballot per tile), so the
-// accumulators are rescaled about once per row.
+// Work unit: one 64-row query block m of one (b, h), one workgroup of 4
+// wave64, over the block's key tiles (T routed video tiles + n_tail prefix
+// blocks).  Primal only, wave w takes all 64 queries (four 16-row sub-tiles)
+// and keys 16w..16w+15 of every tile; the four partial softmax states are
+// merged once at the end through LDS.  With the tangent (twice the
+// accumulators) wave w takes the query half w >> 1 (two sub-tiles) and the
+// key half w & 1 of every tile, whose two 16-key quarters share the K = 32
+// products of O; the two waves of a query half merge their states at the end.
+// Either way each key tile is fetched once per query block, and each wave
+// streams its part of every key tile straight from global memory into MFMA
+// operand registers (one step ahead) -- no barriers in the key loop.  One
+// pass over the tiles with a lazy running maximum: it moves only when a tile
+// exceeds it by a margin (one wave ballot per tile), so the accumulators are
+// rescaled about once per row.
 //
 // Scores are computed transposed (S^T = K Q^T) so that a lane holds one query
 // column: the S^T fragment is directly the B operand of O^T = V^T P^T, and the
 // per-query statistics stay lane-resident.
 //
 // Workgroup ids are remapped so that each XCD (ids = x mod 8) processes a
-// contiguous range of work units: both halves of a query block and all query
-// blocks of one head land on the same XCD and share its L2.
+// contiguous range of work units: the query blocks of one head land on the
+// same XCD and share its L2.
 //
 // Reference semantics: models/sla2_cube_qat.py:448-602 (_cube_fused_jvp_kernel),
 // sparse-only variant :59-169 (_sla2_cube_jvp_qat_kernel).
@@ -96,15 +99,15 @@ struct ValRegs {   // value-side operands, loaded at the start of their own tile
 // Two workgroups per CU with the tangent (its registers), three primal only.
 template <typename T16, bool TAN, bool LINEAR, bool PRE, bool S16>
 __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
-  constexpr int kQT = TAN ? 2 : 4;  // 16-row query sub-tiles per workgroup
+  constexpr int kQT = TAN ? 2 : 4;  // 16-row query sub-tiles per wave
   __shared__ float stat[3][4][kQT][16];  // [m,l,mu][wave][qt][r]
-  // [dQ|Q] B-operand fragments [qt][ks][lane] (16 B each, tangent only)
-  __shared__ __align__(16) u32x4 qsh[TAN ? kQT : 1][4][64];
-  __shared__ __align__(16) i32x4 q8sh[kQT][64];  // INT8 Q B-operand fragments
-  // cross-wave merge buffer [wave][column tile of the round x {O, dO}][qt][lane][4]
-  // (no dO slots without tangent)
-  constexpr int kMb = TAN ? 2 : 1;
-  __shared__ __align__(16) float mbuf[4][2 * kMb][kQT][64][4];
+  // [dQ|Q] B-operand fragments [sub-tile][ks][lane] (16 B each, tangent only)
+  __shared__ __align__(16) u32x4 qsh[TAN ? 4 : 1][4][64];
+  __shared__ __align__(16) i32x4 q8sh[4][64];  // INT8 Q B-operand fragments per sub-tile
+  // cross-wave merge buffer [wave][slot][lane][4], 8 KB per wave: primal the
+  // two column tiles of a round for the four sub-tiles (slot 4 cc + qt); with
+  // the tangent O and dO of the four column tiles of one sub-tile (2 ct + {0,1})
+  __shared__ __align__(16) float mbuf[4][8][64][4];
   // key tiles of this query block in visiting order: (tile id, key scale)
   __shared__ int2 tiles[kMaxTiles];
   __shared__ int ragged_last;  // the partial key tile was moved to the end of the routed list
@@ -113,10 +116,8 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
   if (logical >= a.nwork) return;  // whole workgroup: no barrier skipped
   // integer division runs on the VALU: pin the (uniform) results to SGPRs so
   // that every pointer and buffer descriptor derived from them stays scalar
-  const int half = TAN ? (logical & 1) : 0;
-  const int unit = TAN ? (logical >> 1) : logical;  // query block of the work unit
-  const int bh = __builtin_amdgcn_readfirstlane(unit / a.Mb);
-  const int m = __builtin_amdgcn_readfirstlane(unit - bh * a.Mb);
+  const int bh = __builtin_amdgcn_readfirstlane(logical / a.Mb);
+  const int m = __builtin_amdgcn_readfirstlane(logical - bh * a.Mb);
   const int h = __builtin_amdgcn_readfirstlane(bh % a.H);
 
   const int tid = threadIdx.x;
@@ -124,28 +125,37 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
   // VGPR across the key loop
   const int w = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int l = __lane_id(), r = l & 15, g = l >> 4;
+  const int qs0 = TAN ? 2 * (w >> 1) : 0;  // first query sub-tile of the wave
+  const int kq0 = TAN ? 2 * (w & 1) : w;   // first 16-key quarter of the wave
   const int64_t L = a.L;
   const int64_t qkbase = (int64_t)bh * L;
-  const int64_t q0 = (int64_t)m * kTa + 32 * half;  // first query row of the unit
+  const int64_t q0 = (int64_t)m * kTa;  // first query row of the block
+  // element offset of the block's first row (uniform); per-lane offsets
+  // within the block stay 32-bit, so no 64-bit lane address lives across the
+  // key loop
+  const int64_t blk = (qkbase + q0) * kTa;
 
-  // ---- query side: INT8 B operands in registers; 16-bit [dQ|Q] B operands
-  // staged once in LDS (wave w loads sub-tile w>>1, dQ or Q by w&1).
-  if (!S16 && w < kQT) {
+  // ---- query side: INT8 and 16-bit [dQ|Q] B operands staged once in LDS,
+  // wave w loading sub-tile w.
+  {
     const int64_t row = q0 + 16 * w + r;
-    q8sh[w][l] = row < L ? *reinterpret_cast<const i32x4*>(a.q8 + (qkbase + row) * kTa + 16 * g)
-                         : i32x4{0, 0, 0, 0};
-  }
-  if (TAN) {
-    const int qt = w >> 1;
-    const int64_t row = q0 + 16 * qt + r;
     const bool ok = row < L;
-    const uint16_t* src = (w & 1) ? a.q : a.dq;
-    const int64_t ro = (qkbase + row) * kTa;
+    const int ro = (16 * w + r) * kTa;
+    if (!S16)
+      q8sh[w][l] = ok ? *reinterpret_cast<const i32x4*>(a.q8 + blk + ro + 16 * g)
+                      : i32x4{0, 0, 0, 0};
+    if (TAN) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      u32x4 v = ok ? *reinterpret_cast<const u32x4*>(src + ro + 32 * ks + 8 * g) : u32x4{0, 0, 0, 0};
-      if (PRE) v = scale_bf16x8(v, a.scale);
-      qsh[qt][ks + 2 * (w & 1)][l] = v;
+      for (int part = 0; part < 2; ++part) {  // dQ in ks 0,1, Q in ks 2,3
+        const uint16_t* src = part ? a.q : a.dq;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          u32x4 v = ok ? *reinterpret_cast<const u32x4*>(src + blk + ro + 32 * ks + 8 * g)
+                       : u32x4{0, 0, 0, 0};
+          if (PRE) v = scale_bf16x8(v, a.scale);
+          qsh[w][ks + 2 * part][l] = v;
+        }
+      }
     }
   }
   const int mq = m >> a.qshift;  // LUT row, alpha and record of this query block
@@ -160,7 +170,7 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
   // routed tiles in ascending id order (the prefix tails stay at the end)
   sort_ids_ascending(
       a.T, tid, [&](int i) { return tiles[i].x; }, [&](int i, int v) { tiles[i].x = v; },
-      reinterpret_cast<int*>(&mbuf[0][0][0][0][0]));
+      reinterpret_cast<int*>(&mbuf[0][0][0][0]));
   // A partial key tile (1-D blocks over a ragged L) can sit anywhere in a routed
   // list: move it to the end, where the masked one-tile path handles it.
   int Tu = a.T;
@@ -236,25 +246,28 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
     }
   }
 
-  // per-lane parts of the operand offsets (fragment-ordered tiles: each load
-  // is one contiguous 1 KB per wave); the tile base goes to soffset
-  const int k8off = (16 * w + r) * kTa + 16 * g;
-  const int ktoff = w * 4096 + l * 16;
-  const int vtoff = TAN ? w * 1024 + l * 16 : w * 512 + l * 8;
-  auto load_keys = [&](int j, KeyRegs& kr) {
+  // per-lane parts of the operand offsets of key quarter kq0 (fragment-
+  // ordered tiles: each load is one contiguous 1 KB per wave); the tile base
+  // and the quarter within the wave's half (sub, tangent only) are uniform
+  const int k8off = (16 * kq0 + r) * kTa + 16 * g;
+  const int ktoff = kq0 * 4096 + l * 16;
+  const int vtoff = TAN ? kq0 * 1024 + l * 16 : kq0 * 512 + l * 8;
+  auto load_keys = [&](int j, int sub, KeyRegs& kr) {
     const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
-    if (!S16) kr.k8 = __builtin_bit_cast(i32x4, buf_load16(rk8, k8off + n * kTa * kTa, 0));
+    if (!S16)
+      kr.k8 = __builtin_bit_cast(i32x4, buf_load16(rk8, k8off + n * kTa * kTa, sub * 16 * kTa));
     if (TAN) {
 #pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kr.ka[ks] = buf_load16(rkt, ktoff + ks * 1024, n * 16384);
+      for (int ks = 0; ks < 4; ++ks)
+        kr.ka[ks] = buf_load16(rkt, ktoff + ks * 1024, n * 16384 + sub * 4096);
     }
   };
-  auto load_vals = [&](int j, ValRegs& vr) {
+  auto load_vals = [&](int j, int sub, ValRegs& vr) {
     const int sb = __builtin_amdgcn_readfirstlane(tiles[j].x) * kVtTile;
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       if (TAN) {
-        vr.v[ct] = buf_load16(rvt, vtoff + ct * 4096, sb);
+        vr.v[ct] = buf_load16(rvt, vtoff + ct * 4096, sb + sub * 1024);
       } else {
         const u32x2 x = buf_load8(rvt, vtoff + ct * 2048, sb);
         vr.v[ct] = u32x4{x.x, x.y, 0u, 0u};
@@ -288,16 +301,16 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
     mthr[qt] = mn + kThr;
   };
 
-  // One key tile: scores, the running-maximum check, P (and T = P dS), the
-  // mu sums and the dO^T update; returns the P^T fragments for the O^T update
-  // (pairs of tiles share one K = 32 MFMA).  MASK only for the ragged prefix
-  // tail tiles (j >= T).
-  auto stage = [&](const KeyRegs& kr, const ValRegs& vr, int j, u32x2 (&pb)[kQT], u32x2* pend,
-                   auto mask_tag) {
+  // The wave's 16 keys of one key tile (quarter kq0 + sub): scores, the
+  // running-maximum check, P (and T = P dS), the mu sums and the dO^T
+  // update; returns the P^T fragments for the O^T update (two quarters share
+  // one K = 32 MFMA).  MASK only for the ragged prefix tail tiles (j >= T).
+  auto stage = [&](const KeyRegs& kr, const ValRegs& vr, int j, int sub, u32x2 (&pb)[kQT],
+                   u32x2* pend, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
     const float c = tile_c(j);
-    const int64_t key0 = (int64_t)n * kTa + 16 * w + 4 * g;
+    const int64_t key0 = (int64_t)n * kTa + 16 * (kq0 + sub) + 4 * g;
     // all products of the tile first (scores of both query sub-tiles, then the
     // tangent scores), one rescale test for the tile, then the exponentials:
     // one basic block holds the MFMAs and the VALU work they overlap with
@@ -307,12 +320,12 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
 #pragma unroll
     for (int qt = 0; qt < kQT; ++qt) {
       if (S16) {
-        f32x4 s16 = mfma_16x16x32<T16>(kr.ka[0], qsh[qt][2][l], f32x4{0.f, 0.f, 0.f, 0.f});
-        s16 = mfma_16x16x32<T16>(kr.ka[1], qsh[qt][3][l], s16);
+        f32x4 s16 = mfma_16x16x32<T16>(kr.ka[0], qsh[qs0 + qt][2][l], f32x4{0.f, 0.f, 0.f, 0.f});
+        s16 = mfma_16x16x32<T16>(kr.ka[1], qsh[qs0 + qt][3][l], s16);
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[qt][i] = s16[i];
       } else {
-        const i32x4 si = mfma_i8_16x16x64(kr.k8, q8sh[qt][l], i32x4{0, 0, 0, 0});
+        const i32x4 si = mfma_i8_16x16x64(kr.k8, q8sh[qs0 + qt][l], i32x4{0, 0, 0, 0});
 #pragma unroll
         for (int i = 0; i < 4; ++i) sv[qt][i] = (float)si[i];
       }
@@ -322,7 +335,7 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
       for (int qt = 0; qt < kQT; ++qt) {
         f32x4 d = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) d = mfma_16x16x32<T16>(kr.ka[ks], qsh[qt][ks][l], d);
+        for (int ks = 0; ks < 4; ++ks) d = mfma_16x16x32<T16>(kr.ka[ks], qsh[qs0 + qt][ks][l], d);
         dsv[qt] = d;
       }
     }
@@ -376,8 +389,8 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
       }
     }
   };
-  // O^T += V^T P^T for one tile (K = 16) or a pair (K = 32: the A and B
-  // operand slots 4..7 take the second tile's keys 4g..4g+3)
+  // O^T += V^T P^T for one stage (K = 16) or a pair (K = 32: the A and B
+  // operand slots 4..7 take the second stage's keys 4g..4g+3)
   auto o_single = [&](const ValRegs& vr, const u32x2 (&pb)[kQT]) {
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct)
@@ -403,293 +416,355 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
                                       acc_lm[qt]);
   };
 
-  // Issue order: value loads of a tile, then the score-side prefetch of the
-  // next tile -- the in-order vmcnt lets a tile wait for its own values while
-  // the prefetch stays in flight.
+  // Issue order: value loads of a stage, then the score-side prefetch of the
+  // next stage -- the in-order vmcnt lets a stage wait for its own values
+  // while the prefetch stays in flight.
   KeyRegs ka_, kb_;
-  load_keys(0, ka_);
+  load_keys(0, 0, ka_);
   __syncthreads();  // key scales in tiles[].y
   int j = 0;
-  // routed video tiles in pairs (full, unmasked)
-  for (; j + 1 < Tu; j += 2) {
-    ValRegs va, vb;
-    u32x2 pa[kQT], pbb[kQT];
-    load_vals(j, va);
-    load_keys(j + 1, kb_);
-    stage(ka_, va, j, pa, nullptr, std::false_type{});
-    load_vals(j + 1, vb);
-    load_keys(j + 2 < J ? j + 2 : J - 1, ka_);
-    stage(kb_, vb, j + 1, pbb, pa, std::false_type{});
-    o_pair(va, pa, vb, pbb);
-  }
-  // odd leftover routed tile and the ragged prefix tail tiles, one at a time
-  for (; j < J; ++j) {
-    ValRegs vr;
-    u32x2 pb[kQT];
-    load_vals(j, vr);
-    load_keys(j + 1 < J ? j + 1 : J - 1, kb_);
-    if (j < Tu)
-      stage(ka_, vr, j, pb, nullptr, std::false_type{});
-    else
-      stage(ka_, vr, j, pb, nullptr, std::true_type{});
-    o_single(vr, pb);
-    ka_ = kb_;
-  }
-  // this wave's part of the complement record (Hc, dHc fragments of its
-  // output column tiles, zc, dzc), requested now: the loads stay in flight
-  // through the merge below.  The wave finalises query sub-tile qo and the
-  // kNcc output column tiles cpair .. cpair + kNcc - 1: with the tangent two
-  // waves share a sub-tile (column tiles 0-1 and 2-3), primal only each wave
-  // takes one sub-tile whole.
-  constexpr int kNcc = TAN ? 2 : 4;
-  const int qo = TAN ? w >> 1 : w;
-  const int cpair = TAN ? 2 * (w & 1) : 0;
-  // With the tangent all H fragments are requested here; primal only (four
-  // column tiles per wave) each tile's are loaded where the epilogue uses
-  // them, which keeps the workgroup within three per CU.
-  constexpr bool kHEarly = TAN;
-  // [slot][ks][Hc, dHc][j]: H[32 ks + 8 g + j][16 (cpair + cc) + r] of column tile cc
-  float hraw[kHEarly ? kNcc : 1][2][TAN ? 2 : 1][8];
-  f32x4 zraw[2][2][2];     // [ks][zc, dzc][half]: z[32 ks + 8 g + 4 half ..]
-  const float* rec = reinterpret_cast<const float*>(a.comp + ((int64_t)bh * a.Mq + mq) * kRec);
-  auto load_h = [&](int slot, int cc) {
+  if (TAN) {
+    // both quarters of the wave's key half of every tile, as one pair
+    auto tile_pair = [&](int jt, auto mask_tag) {
+      ValRegs va, vb;
+      u32x2 pa[kQT], pbb[kQT];
+      load_vals(jt, 0, va);
+      load_keys(jt, 1, kb_);
+      stage(ka_, va, jt, 0, pa, nullptr, mask_tag);
+      load_vals(jt, 1, vb);
+      load_keys(jt + 1 < J ? jt + 1 : J - 1, 0, ka_);
+      stage(kb_, vb, jt, 1, pbb, pa, mask_tag);
+      o_pair(va, pa, vb, pbb);
+    };
+    for (; j < Tu; ++j) tile_pair(j, std::false_type{});  // routed video tiles
+    for (; j < J; ++j) tile_pair(j, std::true_type{});    // ragged prefix tails
+  } else {
+    // routed video tiles in pairs (full, unmasked); the two tiles' V
+    // fragments load straight into the slots 0..3 and 4..7 of one K = 32
+    // operand (the primal stage itself reads no values)
+    for (; j + 1 < Tu; j += 2) {
+      u32x4 vp[4];
+      u32x2 pa[kQT], pbb[kQT];
+      auto load_v = [&](int jt, int slot) {
+        const int sb = __builtin_amdgcn_readfirstlane(tiles[jt].x) * kVtTile;
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int mat = 0; mat < (TAN ? 2 : 1); ++mat)
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj)
-          hraw[slot][ks][mat][jj] = rec[4096 * mat + (32 * ks + 8 * g + jj) * 64 + 16 * (cpair + cc) + r];
-  };
-  if (LINEAR) {
-    if (kHEarly) {
-#pragma unroll
-      for (int cc = 0; cc < kNcc; ++cc) load_h(cc, cc);
-    }
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int mat = 0; mat < (TAN ? 2 : 1); ++mat)
-#pragma unroll
-        for (int hf = 0; hf < 2; ++hf)
-          zraw[ks][mat][hf] = *reinterpret_cast<const f32x4*>(rec + 8192 + 64 * mat + 32 * ks + 8 * g + 4 * hf);
-  }
-  float l_i[kQT];
-#pragma unroll
-  for (int qt = 0; qt < kQT; ++qt) {
-    l_i[qt] = acc_lm[qt][0];  // every row of the product holds the column sum
-    if (TAN) mu_i[qt] = sum_over_groups(mu_i[qt]);
-  }
-
-  // ---- merge the four per-wave states (fixed order: deterministic) ----
-  __syncthreads();  // every wave is done with the qsh operands
-  if (g == 0) {
-#pragma unroll
-    for (int qt = 0; qt < kQT; ++qt) {
-      stat[0][w][qt][r] = mrun[qt];
-      stat[1][w][qt][r] = l_i[qt];
-      stat[2][w][qt][r] = mu_i[qt];
-    }
-  }
-  __syncthreads();
-  float fself[kQT];
-#pragma unroll
-  for (int qt = 0; qt < kQT; ++qt) {
-    float M = -INFINITY;
-#pragma unroll
-    for (int ww = 0; ww < 4; ++ww) M = fmaxf(M, stat[0][ww][qt][r]);
-    fself[qt] = (mrun[qt] == -INFINITY) ? 0.f : fast_exp2(mrun[qt] - M);
-  }
-  // this wave finalises query sub-tile qo, output column tiles cpair, cpair+1
-  float Mw = -INFINITY;
-#pragma unroll
-  for (int ww = 0; ww < 4; ++ww) Mw = fmaxf(Mw, stat[0][ww][qo][r]);
-  float ltot = 0.f, mutot = 0.f;
-#pragma unroll
-  for (int ww = 0; ww < 4; ++ww) {
-    const float mw = stat[0][ww][qo][r];
-    const float f = (mw == -INFINITY) ? 0.f : fast_exp2(mw - Mw);
-    ltot += stat[1][ww][qo][r] * f;
-    mutot += stat[2][ww][qo][r] * f;
-  }
-
-  // two rounds (column tiles 0-1, then 2-3), O and dO together; with the
-  // tangent round rd is summed by the waves with (w & 1) == rd, primal only
-  // every wave sums both rounds for its sub-tile
-  f32x4 O[kNcc], DO[kNcc];
-#pragma unroll
-  for (int rd = 0; rd < 2; ++rd) {
-#pragma unroll
-    for (int cc = 0; cc < 2; ++cc)
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
-        *reinterpret_cast<f32x4*>(&mbuf[w][kMb * cc][qt][l][0]) = acc_o[2 * rd + cc][qt] * fself[qt];
-        if (TAN)
-          *reinterpret_cast<f32x4*>(&mbuf[w][kMb * cc + 1][qt][l][0]) =
-              acc_do[2 * rd + cc][qt] * fself[qt];
-      }
-    __syncthreads();
-    if (!TAN || (w & 1) == rd) {
-#pragma unroll
-      for (int cc = 0; cc < 2; ++cc) {
-        f32x4 so = f32x4{0.f, 0.f, 0.f, 0.f}, sd = so;
-#pragma unroll
-        for (int ww = 0; ww < 4; ++ww) {
-          so += *reinterpret_cast<const f32x4*>(&mbuf[ww][kMb * cc][qo][l][0]);
-          if (TAN) sd += *reinterpret_cast<const f32x4*>(&mbuf[ww][kMb * cc + 1][qo][l][0]);
+        for (int ct = 0; ct < 4; ++ct) {
+          const u32x2 x = buf_load8(rvt, vtoff + ct * 2048, sb);
+          vp[ct][2 * slot] = x.x;
+          vp[ct][2 * slot + 1] = x.y;
         }
-        O[TAN ? cc : 2 * rd + cc] = so;
-        DO[TAN ? cc : 2 * rd + cc] = sd;
-      }
+      };
+      load_v(j, 0);
+      load_keys(j + 1, 0, kb_);
+      stage(ka_, ValRegs{}, j, 0, pa, nullptr, std::false_type{});
+      load_v(j + 1, 1);
+      load_keys(j + 2 < J ? j + 2 : J - 1, 0, ka_);
+      stage(kb_, ValRegs{}, j + 1, 0, pbb, pa, std::false_type{});
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt)
+          acc_o[ct][qt] = mfma_16x16x32<T16>(vp[ct], u32x4{pa[qt].x, pa[qt].y, pbb[qt].x, pbb[qt].y},
+                                             acc_o[ct][qt]);
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt)
+        acc_lm[qt] = mfma_16x16x32<T16>(lm_a, u32x4{pa[qt].x, pa[qt].y, pbb[qt].x, pbb[qt].y},
+                                        acc_lm[qt]);
     }
-    if (rd == 0) __syncthreads();
+    // odd leftover routed tile and the ragged prefix tail tiles, one at a time
+    for (; j < J; ++j) {
+      ValRegs vr;
+      u32x2 pb[kQT];
+      load_vals(j, 0, vr);
+      load_keys(j + 1 < J ? j + 1 : J - 1, 0, kb_);
+      if (j < Tu)
+        stage(ka_, vr, j, 0, pb, nullptr, std::false_type{});
+      else
+        stage(ka_, vr, j, 0, pb, nullptr, std::true_type{});
+      o_single(vr, pb);
+      ka_ = kb_;
+    }
   }
+  // Lane indices for the merge and epilogue, re-derived from vtoff (live
+  // through the key loop anyway; the empty asm keeps the compiler from
+  // folding it back): l, r and g themselves then need no register across
+  // the loop.
+  {
+    int lt = vtoff;
+    asm volatile("" : "+v"(lt));
+    const int l = (lt - (TAN ? kq0 * 1024 : kq0 * 512)) >> (TAN ? 4 : 3);
+    const int r = l & 15, g = l >> 4;
 
-  // ---- epilogue: query q0 + 16 qo + r, output columns 16 (cpair + cc) + 4g + i ----
-  const int64_t qrow = q0 + 16 * qo + r;
-  const float rl = 1.f / ltot;
-  const float inv_mu = mutot * rl;
-  f32x4 os[kNcc], dos[kNcc];
-#pragma unroll
-  for (int cc = 0; cc < kNcc; ++cc) {
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      os[cc][i] = O[cc][i] * rl;
-      if (TAN) dos[cc][i] = DO[cc][i] * rl - inv_mu * os[cc][i];
-    }
-  }
-
-  if (LINEAR) {
-    // phi(q), dphi(q) of this lane's query in B-operand layout: d = 32 ks + 8 g + e
-    float qv[2][8], dqv[2][8];
-    const bool qok = qrow < L;
-    const int64_t ro = (qkbase + qrow) * kTa;
-    // tangent: the [dQ|Q] operand fragments in LDS are exactly this lane's
-    // row (zero past L), scaled by the power-of-two softmax scale when PRE
-    const float unscale = PRE ? 1.f / a.scale : 1.f;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      u32x4 u, du = u32x4{0, 0, 0, 0};
-      if (TAN) {
-        u = qsh[qo][2 + ks][l];
-        du = qsh[qo][ks][l];
-      } else {
-        u = qok ? *reinterpret_cast<const u32x4*>(a.q + ro + 32 * ks + 8 * g) : u32x4{0, 0, 0, 0};
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        qv[ks][2 * e] = T16::to_f32((uint16_t)(u[e] & 0xffff)) * unscale;
-        qv[ks][2 * e + 1] = T16::to_f32((uint16_t)(u[e] >> 16)) * unscale;
-        dqv[ks][2 * e] = T16::to_f32((uint16_t)(du[e] & 0xffff)) * unscale;
-        dqv[ks][2 * e + 1] = T16::to_f32((uint16_t)(du[e] >> 16)) * unscale;
-      }
-    }
-    float mx = -INFINITY;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) mx = fmaxf(mx, qv[ks][e]);
-    mx = max_over_groups(mx);
-    float den = 0.f;
-    float phi[2][8], dphi[2][8];
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        phi[ks][e] = __expf(qv[ks][e] - mx);
-        den += phi[ks][e];
-      }
-    den = sum_over_groups(den);
-    const float rden = 1.f / den;
-    float qdot = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        phi[ks][e] = phi[ks][e] * rden;
-        qdot += phi[ks][e] * dqv[ks][e];
-      }
-    if (TAN) {
-      qdot = sum_over_groups(qdot);
+    // The wave finalises block sub-tile qo over all four output column tiles:
+    // primal only its own sub-tile w, with the tangent sub-tile qs0 + (w & 1)
+    // of its query half (the partner wave w ^ 1 takes the other).  The zc, dzc
+    // parts of the complement record are requested now (in flight through the
+    // merge); each column tile's Hc, dHc fragments are loaded where the
+    // epilogue uses them.
+    constexpr int kNcc = 4;
+    const int kh = w & 1;  // tangent: the wave's key half and finalised sub-tile qs0 + kh
+    const int qo = TAN ? qs0 + kh : w;
+    // [ks][Hc, dHc][j]: H[32 ks + 8 g + j][16 cc + r] of the column tile cc in use
+    float hraw[2][TAN ? 2 : 1][8];
+    f32x4 zraw[2][2][2];     // [ks][zc, dzc][half]: z[32 ks + 8 g + 4 half ..]
+    const float* rec = reinterpret_cast<const float*>(a.comp + ((int64_t)bh * a.Mq + mq) * kRec);
+    auto load_h = [&](int cc) {
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) dphi[ks][e] = phi[ks][e] * (dqv[ks][e] - qdot);
+        for (int mat = 0; mat < (TAN ? 2 : 1); ++mat)
+#pragma unroll
+          for (int jj = 0; jj < 8; ++jj)
+            hraw[ks][mat][jj] = rec[4096 * mat + (32 * ks + 8 * g + jj) * 64 + 16 * cc + r];
+    };
+    if (LINEAR) {
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int mat = 0; mat < (TAN ? 2 : 1); ++mat)
+#pragma unroll
+          for (int hf = 0; hf < 2; ++hf)
+            zraw[ks][mat][hf] = *reinterpret_cast<const f32x4*>(rec + 8192 + 64 * mat + 32 * ks + 8 * g + 4 * hf);
     }
-    // bf16 hi/lo operand halves
-    u32x4 ph[2], pl[2], dph[2], dpl[2];
+    float l_i[kQT];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
+    for (int qt = 0; qt < kQT; ++qt) {
+      l_i[qt] = acc_lm[qt][0];  // every row of the product holds the column sum
+      if (TAN) mu_i[qt] = sum_over_groups(mu_i[qt]);
+    }
+
+    // ---- merge the per-wave states (fixed order: deterministic) ----
+    __syncthreads();  // every wave is done with the sort's use of mbuf
+    if (g == 0) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float a0 = phi[ks][2 * e], a1 = phi[ks][2 * e + 1];
-        ph[ks][e] = pack_pair<BF16>(a0, a1);
-        pl[ks][e] = pack_pair<BF16>(a0 - bf16_val((uint16_t)(ph[ks][e] & 0xffff)),
-                                    a1 - bf16_val((uint16_t)(ph[ks][e] >> 16)));
-        if (TAN) {
-          const float b0 = dphi[ks][2 * e], b1 = dphi[ks][2 * e + 1];
-          dph[ks][e] = pack_pair<BF16>(b0, b1);
-          dpl[ks][e] = pack_pair<BF16>(b0 - bf16_val((uint16_t)(dph[ks][e] & 0xffff)),
-                                       b1 - bf16_val((uint16_t)(dph[ks][e] >> 16)));
+      for (int qt = 0; qt < kQT; ++qt) {
+        stat[0][w][qt][r] = mrun[qt];
+        stat[1][w][qt][r] = l_i[qt];
+        stat[2][w][qt][r] = mu_i[qt];
+      }
+    }
+    __syncthreads();
+    // waves holding parts of the same queries: the pair w0, w0 + 1 of the
+    // query half with the tangent, all four primal only
+    constexpr int kNw = TAN ? 2 : 4;
+    const int w0 = TAN ? (w & ~1) : 0;
+    const int qsel = TAN ? kh : qo;  // the finalised sub-tile among the wave's own
+    float fself[kQT];
+#pragma unroll
+    for (int qt = 0; qt < kQT; ++qt) {
+      float M = -INFINITY;
+#pragma unroll
+      for (int ww = 0; ww < kNw; ++ww) M = fmaxf(M, stat[0][w0 + ww][qt][r]);
+      fself[qt] = (mrun[qt] == -INFINITY) ? 0.f : fast_exp2(mrun[qt] - M);
+    }
+    float Mw = -INFINITY;
+#pragma unroll
+    for (int ww = 0; ww < kNw; ++ww) Mw = fmaxf(Mw, stat[0][w0 + ww][qsel][r]);
+    float ltot = 0.f, mutot = 0.f;
+#pragma unroll
+    for (int ww = 0; ww < kNw; ++ww) {
+      const float mw = stat[0][w0 + ww][qsel][r];
+      const float f = (mw == -INFINITY) ? 0.f : fast_exp2(mw - Mw);
+      ltot += stat[1][w0 + ww][qsel][r] * f;
+      mutot += stat[2][w0 + ww][qsel][r] * f;
+    }
+
+    f32x4 O[kNcc], DO[kNcc];
+    if (TAN) {
+      // hand the partner its sub-tile (the wave's other one, 1 - kh), scaled to
+      // the pair's maximum; add the partner's part of sub-tile kh to our own.
+      // Values are picked, never addressed, by kh: register arrays indexed by
+      // a runtime value would move to scratch memory.
+      auto pick = [](bool c, auto x, auto y) { return c ? x : y; };
+      const bool k1 = kh != 0;
+      const float fo = pick(k1, fself[0], fself[1]);
+      const float fm = pick(k1, fself[1], fself[0]);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        *reinterpret_cast<f32x4*>(&mbuf[w][2 * ct][l][0]) = pick(k1, acc_o[ct][0], acc_o[ct][1]) * fo;
+        *reinterpret_cast<f32x4*>(&mbuf[w][2 * ct + 1][l][0]) =
+            pick(k1, acc_do[ct][0], acc_do[ct][1]) * fo;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        O[ct] = pick(k1, acc_o[ct][1], acc_o[ct][0]) * fm +
+                *reinterpret_cast<const f32x4*>(&mbuf[w ^ 1][2 * ct][l][0]);
+        DO[ct] = pick(k1, acc_do[ct][1], acc_do[ct][0]) * fm +
+                 *reinterpret_cast<const f32x4*>(&mbuf[w ^ 1][2 * ct + 1][l][0]);
+      }
+    } else {
+      // two rounds (column tiles 0-1, then 2-3); every wave sums its sub-tile
+#pragma unroll
+      for (int rd = 0; rd < 2; ++rd) {
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc)
+#pragma unroll
+          for (int qt = 0; qt < kQT; ++qt)
+            *reinterpret_cast<f32x4*>(&mbuf[w][4 * cc + qt][l][0]) = acc_o[2 * rd + cc][qt] * fself[qt];
+        __syncthreads();
+#pragma unroll
+        for (int cc = 0; cc < 2; ++cc) {
+          f32x4 so = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+          for (int ww = 0; ww < 4; ++ww) so += *reinterpret_cast<const f32x4*>(&mbuf[ww][4 * cc + qo][l][0]);
+          O[2 * rd + cc] = so;
         }
+        if (rd == 0) __syncthreads();
       }
     }
-    float dn = 0.f, ddn = 0.f;
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const float z = zraw[ks][0][e >> 2][e & 3];
-        dn += phi[ks][e] * z;
-        if (TAN) ddn += dphi[ks][e] * z + phi[ks][e] * zraw[ks][1][e >> 2][e & 3];
-      }
-    }
-    dn = sum_over_groups(dn);
-    dn = dn >= 0.f ? dn + a.eps_l : dn - a.eps_l;
-    const float rdn = 1.f / dn;
-    if (TAN) ddn = sum_over_groups(ddn);
-    const float al = a.alpha[(int64_t)h * a.alpha_stride + mq];
+
+    // ---- epilogue: query q0 + 16 qo + r, output columns 16 cc + 4g + i ----
+    // the lane's row within the block; the block's rows inside L are reached
+    // through buffer resources (SGPR base, 32-bit offsets, rows past L read as
+    // zeros and are not written), so no 64-bit lane address is formed here
+    const int erow = 16 * qo + r;
+    const int brows = (int)(L - q0 < kTa ? L - q0 : kTa);
+    const float rl = 1.f / ltot;
+    const float inv_mu = mutot * rl;
+    f32x4 os[kNcc], dos[kNcc];
 #pragma unroll
     for (int cc = 0; cc < kNcc; ++cc) {
-      const int hs = kHEarly ? cc : 0;
-      if (!kHEarly) load_h(0, cc);
-      f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f}, dnum = num;
-#pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        u32x4 hh, hl;
-        split_hfrag(hraw[hs][ks][0], hh, hl);
-        num = mfma_bf16_16x16x32(hh, ph[ks], num);
-        num = mfma_bf16_16x16x32(hh, pl[ks], num);
-        num = mfma_bf16_16x16x32(hl, ph[ks], num);
-        if (TAN) {
-          u32x4 dh, dl;
-          split_hfrag(hraw[hs][ks][1], dh, dl);
-          dnum = mfma_bf16_16x16x32(hh, dph[ks], dnum);
-          dnum = mfma_bf16_16x16x32(hh, dpl[ks], dnum);
-          dnum = mfma_bf16_16x16x32(hl, dph[ks], dnum);
-          dnum = mfma_bf16_16x16x32(dh, ph[ks], dnum);
-          dnum = mfma_bf16_16x16x32(dh, pl[ks], dnum);
-          dnum = mfma_bf16_16x16x32(dl, ph[ks], dnum);
-        }
-      }
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        const float ol = num[i] * rdn;
-        os[cc][i] = al * os[cc][i] + (1.f - al) * ol;
+        os[cc][i] = O[cc][i] * rl;
+        if (TAN) dos[cc][i] = DO[cc][i] * rl - inv_mu * os[cc][i];
+      }
+    }
+
+    if (LINEAR) {
+      // phi(q), dphi(q) of this lane's query in B-operand layout: d = 32 ks + 8 g + e
+      float qv[2][8], dqv[2][8];
+      const auto rq = make_rsrc(a.q + blk, (int64_t)brows * kTa * 2);
+      // tangent: the [dQ|Q] operand fragments in LDS are exactly this lane's
+      // row (zero past L), scaled by the power-of-two softmax scale when PRE
+      const float unscale = PRE ? 1.f / a.scale : 1.f;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        u32x4 u, du = u32x4{0, 0, 0, 0};
         if (TAN) {
-          const float dol = (dnum[i] - ol * ddn) * rdn;
-          dos[cc][i] = al * dos[cc][i] + (1.f - al) * dol;
+          u = qsh[qo][2 + ks][l];
+          du = qsh[qo][ks][l];
+        } else {
+          u = buf_load16(rq, (erow * kTa + 32 * ks + 8 * g) * 2, 0);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          qv[ks][2 * e] = T16::to_f32((uint16_t)(u[e] & 0xffff)) * unscale;
+          qv[ks][2 * e + 1] = T16::to_f32((uint16_t)(u[e] >> 16)) * unscale;
+          dqv[ks][2 * e] = T16::to_f32((uint16_t)(du[e] & 0xffff)) * unscale;
+          dqv[ks][2 * e + 1] = T16::to_f32((uint16_t)(du[e] >> 16)) * unscale;
+        }
+      }
+      float mx = -INFINITY;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, qv[ks][e]);
+      mx = max_over_groups(mx);
+      float den = 0.f;
+      float phi[2][8], dphi[2][8];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          phi[ks][e] = __expf(qv[ks][e] - mx);
+          den += phi[ks][e];
+        }
+      den = sum_over_groups(den);
+      const float rden = 1.f / den;
+      float qdot = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          phi[ks][e] = phi[ks][e] * rden;
+          qdot += phi[ks][e] * dqv[ks][e];
+        }
+      if (TAN) {
+        qdot = sum_over_groups(qdot);
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dphi[ks][e] = phi[ks][e] * (dqv[ks][e] - qdot);
+      }
+      // bf16 hi/lo operand halves
+      u32x4 ph[2], pl[2], dph[2], dpl[2];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const float a0 = phi[ks][2 * e], a1 = phi[ks][2 * e + 1];
+          ph[ks][e] = pack_pair<BF16>(a0, a1);
+          pl[ks][e] = pack_pair<BF16>(a0 - bf16_val((uint16_t)(ph[ks][e] & 0xffff)),
+                                      a1 - bf16_val((uint16_t)(ph[ks][e] >> 16)));
+          if (TAN) {
+            const float b0 = dphi[ks][2 * e], b1 = dphi[ks][2 * e + 1];
+            dph[ks][e] = pack_pair<BF16>(b0, b1);
+            dpl[ks][e] = pack_pair<BF16>(b0 - bf16_val((uint16_t)(dph[ks][e] & 0xffff)),
+                                         b1 - bf16_val((uint16_t)(dph[ks][e] >> 16)));
+          }
+        }
+      }
+      float dn = 0.f, ddn = 0.f;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float z = zraw[ks][0][e >> 2][e & 3];
+          dn += phi[ks][e] * z;
+          if (TAN) ddn += dphi[ks][e] * z + phi[ks][e] * zraw[ks][1][e >> 2][e & 3];
+        }
+      }
+      dn = sum_over_groups(dn);
+      dn = dn >= 0.f ? dn + a.eps_l : dn - a.eps_l;
+      const float rdn = 1.f / dn;
+      if (TAN) ddn = sum_over_groups(ddn);
+      const float al = a.alpha[(int64_t)h * a.alpha_stride + mq];
+#pragma unroll
+      for (int cc = 0; cc < kNcc; ++cc) {
+        load_h(cc);
+        f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f}, dnum = num;
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          u32x4 hh, hl;
+          split_hfrag(hraw[ks][0], hh, hl);
+          num = mfma_bf16_16x16x32(hh, ph[ks], num);
+          num = mfma_bf16_16x16x32(hh, pl[ks], num);
+          num = mfma_bf16_16x16x32(hl, ph[ks], num);
+          if (TAN) {
+            u32x4 dh, dl;
+            split_hfrag(hraw[ks][1], dh, dl);
+            dnum = mfma_bf16_16x16x32(hh, dph[ks], dnum);
+            dnum = mfma_bf16_16x16x32(hh, dpl[ks], dnum);
+            dnum = mfma_bf16_16x16x32(hl, dph[ks], dnum);
+            dnum = mfma_bf16_16x16x32(dh, ph[ks], dnum);
+            dnum = mfma_bf16_16x16x32(dh, pl[ks], dnum);
+            dnum = mfma_bf16_16x16x32(dl, ph[ks], dnum);
+          }
+        }
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float ol = num[i] * rdn;
+          os[cc][i] = al * os[cc][i] + (1.f - al) * ol;
+          if (TAN) {
+            const float dol = (dnum[i] - ol * ddn) * rdn;
+            dos[cc][i] = al * dos[cc][i] + (1.f - al) * dol;
+          }
         }
       }
     }
-  }
 
-  if (qrow < L) {
-    const int64_t oo = (qkbase + qrow) * kTa + 4 * g;
+    {
+      const auto ro_ = make_rsrc(a.o + blk, (int64_t)brows * kTa * 4);
+      const auto rdo = make_rsrc(TAN ? a.dout + blk : a.o + blk, (int64_t)brows * kTa * 4);
+      const int oo = (erow * kTa + 4 * g) * 4;
 #pragma unroll
-    for (int cc = 0; cc < kNcc; ++cc) {
-      *reinterpret_cast<f32x4*>(a.o + oo + 16 * (cpair + cc)) = os[cc];
-      if (TAN) *reinterpret_cast<f32x4*>(a.dout + oo + 16 * (cpair + cc)) = dos[cc];
+      for (int cc = 0; cc < kNcc; ++cc) {
+        __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, os[cc]), ro_, oo + 64 * cc, 0, 0);
+        if (TAN)
+          __builtin_amdgcn_raw_buffer_store_b128(__builtin_bit_cast(u32x4, dos[cc]), rdo, oo + 64 * cc, 0, 0);
+      }
     }
   }
 }
@@ -729,8 +804,7 @@ extern "C" int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, cons
   const bool linear = (flags & SLA2H_FLAG_SPARSE_ONLY) == 0;
   if (linear) SLA2H_CHECK_ARG(comp && alpha && alpha_stride >= 0);
   const int Nb = (int)((L + E - 1) / E);
-  // work units: half query blocks with the tangent, whole blocks primal only
-  const int64_t nwork = (tan ? 2ll : 1ll) * Nb * B * H;
+  const int64_t nwork = (int64_t)Nb * B * H;  // query blocks
   const int64_t per_xcd = (nwork + 7) / 8;
   SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31));
   FwdArgs a;
@@ -794,7 +868,7 @@ extern "C" int sla2h_fwd_jvp_1d(const void* q, const void* dq, const void* kt, c
   SLA2H_CHECK_ARG(B > 0 && H > 0 && L > 0 && scale > 0.f);
   const int Nb = (int)((L + bk - 1) / bk);
   SLA2H_CHECK_ARG(T >= 1 && T <= Nb && T <= kMaxTiles);
-  const int64_t nwork = 2ll * Nb * B * H;
+  const int64_t nwork = (int64_t)Nb * B * H;  // 64-row query blocks
   const int64_t per_xcd = (nwork + 7) / 8;
   SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31));
   FwdArgs a = {};

@@ -176,6 +176,12 @@ def test_config3_full_size():
 
 
 def test_primal_matches_tangent_run_and_is_deterministic():
+    """Repeated runs are bit-identical; the primal-only instance's o agrees with
+    the tangent instance's.  The two split a tile's keys differently across
+    their waves (a 16-key quarter per wave primal only, a 32-key half with the
+    tangent), so their lazy running maxima, and with them the 16-bit rounding
+    of P, differ: the bound is a few 16-bit ulps of o, well inside the
+    tolerance both meet against the oracle."""
     say("primal vs tangent kernels, determinism")
     z, dt, ins = golden("ref_geom_bf16")
     Np, P = int(z["Np"]), int(z["P"])
@@ -184,7 +190,10 @@ def test_primal_matches_tangent_run_and_is_deterministic():
     o2, do2, _ = run_full(ins, alpha, 0.5, Np, P)
     assert torch.equal(o1, o2) and torch.equal(do1, do2)
     o3, _, _ = run_full(ins, alpha, 0.5, Np, P, tangent=False)
-    assert max_abs(o3, o1) < 1e-5
+    o4, _, _ = run_full(ins, alpha, 0.5, Np, P, tangent=False)
+    assert torch.equal(o3, o4)
+    print(f"  primal vs tangent o max {max_abs(o3, o1):.2e}", flush=True)
+    assert max_abs(o3, o1) < 3e-3
 
 
 def test_sparse_only_and_alpha_one():
