@@ -11,6 +11,7 @@ launch stream between the stages inside the timed region.  Prints one JSON line.
 """
 
 import argparse
+import hashlib
 import json
 import os
 import statistics
@@ -50,7 +51,9 @@ def make_config(cfg):
 def measured_traffic(cfg, tangent):
     """HBM bytes per fwd_jvp launch from the committed rocprofv3 FETCH_SIZE /
     WRITE_SIZE passes (scaled by the same counters on a plain copy kernel),
-    for the Config 3 tangent workload only; None otherwise."""
+    for the Config 3 tangent workload only; None otherwise, and None when the
+    record was measured on another kernel instance or another version of the
+    kernel source (its sha256 is stored with the figures)."""
     path = os.path.join(ROOT, "profiles", "fwd_jvp_config3_traffic.json")
     if cfg != 3 or not tangent or not os.path.exists(path):
         return None
@@ -59,6 +62,10 @@ def measured_traffic(cfg, tangent):
     # the instance this run launches (bf16, tangent, linear branch, power-of-two scale)
     if rec.get("kernel") != "void sla2h::fwd_jvp_kernel<sla2h::BF16, true, true, true, false>(sla2h::FwdArgs)":
         return None
+    src = os.path.join(ROOT, rec.get("source", "imfvideo_amd/csrc/attn.hip"))
+    with open(src, "rb") as f:
+        if hashlib.sha256(f.read()).hexdigest() != rec.get("source_sha256"):
+            return None
     return int(rec["bytes_per_launch"])
 
 
@@ -427,7 +434,7 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); "
-              "the op shards by head with no exchange, see DESIGN.md", file=sys.stderr)
+              "the op shards by (batch, head) with no exchange between GPUs", file=sys.stderr)
         sys.exit(1)
 
     if args.config == 5:
