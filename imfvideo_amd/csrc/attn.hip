@@ -497,14 +497,14 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
 
     // The wave finalises block sub-tile qo over all four output column tiles:
     // primal only its own sub-tile w, with the tangent sub-tile qs0 + (w & 1)
-    // of its query half (the partner wave w ^ 1 takes the other).  The zc, dzc
-    // parts of the complement record are requested now (in flight through the
-    // merge); each column tile's Hc, dHc fragments are loaded where the
-    // epilogue uses them.
+    // of its query half (the partner wave w ^ 1 takes the other).  The
+    // complement record is requested now (in flight through the merge): the
+    // zc, dzc parts by every wave, the Hc, dHc fragments of column tile w by
+    // wave w, which splits them once for the workgroup after the merge.
     constexpr int kNcc = 4;
     const int kh = w & 1;  // tangent: the wave's key half and finalised sub-tile qs0 + kh
     const int qo = TAN ? qs0 + kh : w;
-    // [ks][Hc, dHc][j]: H[32 ks + 8 g + j][16 cc + r] of the column tile cc in use
+    // [ks][Hc, dHc][j]: H[32 ks + 8 g + j][16 w + r]
     float hraw[2][TAN ? 2 : 1][8];
     f32x4 zraw[2][2][2];     // [ks][zc, dzc][half]: z[32 ks + 8 g + 4 half ..]
     const float* rec = reinterpret_cast<const float*>(a.comp + ((int64_t)bh * a.Mq + mq) * kRec);
@@ -518,6 +518,7 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
             hraw[ks][mat][jj] = rec[4096 * mat + (32 * ks + 8 * g + jj) * 64 + 16 * cc + r];
     };
     if (LINEAR) {
+      load_h(w);
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
@@ -612,6 +613,27 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
         }
         if (rd == 0) __syncthreads();
       }
+    }
+
+    // ---- Hc (dHc) as bf16 hi/lo A-operand fragments in LDS, in the
+    // merge buffer (free again): wave w splits column tile w once for the
+    // workgroup; entry [mat][ct][ks][hi, lo][lane] is the u32x4 lane l uses ----
+    u32x4* hfrag = reinterpret_cast<u32x4*>(&mbuf[0][0][0][0]);
+    auto hidx = [&](int mat, int ct, int ks, int part) {
+      return (((mat * 4 + ct) * 2 + ks) * 2 + part) * 64 + l;
+    };
+    if (LINEAR) {
+      __syncthreads();  // every wave has read its merge inputs
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+        for (int mat = 0; mat < (TAN ? 2 : 1); ++mat) {
+          u32x4 hi, lo;
+          split_hfrag(hraw[ks][mat], hi, lo);
+          hfrag[hidx(mat, w, ks, 0)] = hi;
+          hfrag[hidx(mat, w, ks, 1)] = lo;
+        }
+      __syncthreads();
     }
 
     // ---- epilogue: query q0 + 16 qo + r, output columns 16 cc + 4g + i ----
@@ -723,18 +745,15 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
       const float al = a.alpha[(int64_t)h * a.alpha_stride + mq];
 #pragma unroll
       for (int cc = 0; cc < kNcc; ++cc) {
-        load_h(cc);
         f32x4 num = f32x4{0.f, 0.f, 0.f, 0.f}, dnum = num;
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          u32x4 hh, hl;
-          split_hfrag(hraw[ks][0], hh, hl);
+          const u32x4 hh = hfrag[hidx(0, cc, ks, 0)], hl = hfrag[hidx(0, cc, ks, 1)];
           num = mfma_bf16_16x16x32(hh, ph[ks], num);
           num = mfma_bf16_16x16x32(hh, pl[ks], num);
           num = mfma_bf16_16x16x32(hl, ph[ks], num);
           if (TAN) {
-            u32x4 dh, dl;
-            split_hfrag(hraw[ks][1], dh, dl);
+            const u32x4 dh = hfrag[hidx(1, cc, ks, 0)], dl = hfrag[hidx(1, cc, ks, 1)];
             dnum = mfma_bf16_16x16x32(hh, dph[ks], dnum);
             dnum = mfma_bf16_16x16x32(hh, dpl[ks], dnum);
             dnum = mfma_bf16_16x16x32(hl, dph[ks], dnum);
