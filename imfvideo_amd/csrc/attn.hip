@@ -226,12 +226,16 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
     // ---- one pass: P = exp2(s - m), O^T += V^T P^T, dO^T += [V|dV]^T [T;P]^T ----
     // Lazy running maximum: m only moves when a tile's row maximum exceeds it
     // by more than kThr (log2 units), so P <= 2^kThr and a rescale of the
-    // accumulators is rare (every row's first tile, then hardly ever).  fp16
-    // operands keep kThr = 0 (P <= 1 and the +-60000 clamp of T act as in the
-    // reference's per-block online softmax).  The check is one ballot per
-    // sub-tile and tile: c > 0 and rounding is monotonic, so the maximum of
-    // fl(s * c) over a tile is fl(max(s) * c) from the integer maximum.
-    constexpr float kThr = T16::kDtype == SLA2H_DTYPE_F16 ? 0.f : 8.f;
+    // accumulators is rare (every row's first tile, then hardly ever).  The
+    // check is one ballot per sub-tile and tile: c > 0 and rounding is
+    // monotonic, so the maximum of fl(s * c) over a tile is fl(max(s) * c)
+    // from the integer maximum.  With fp16 operands and the tangent, T is
+    // clamped to +-60000 before its fp16 conversion as in the reference: a
+    // tile whose T would reach the clamp under the lazy maximum is recomputed
+    // at the exact running maximum of the wave's keys (mref), so the clamp
+    // acts exactly as with an exact online maximum and T always fits fp16.
+    constexpr float kThr = 8.f;
+    constexpr bool kClampT = TAN && T16::kDtype == SLA2H_DTYPE_F16;
     // Row sum l = sum_k p on the matrix core: acc_lm accumulates an all-ones A
     // operand times the same P^T fragments as the O^T update (one MFMA per
     // pair of tiles instead of eight VALU adds per sub-tile and tile).  The
@@ -241,6 +245,7 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
     float mu_i[kQT];
     f32x4 acc_o[4][kQT], acc_do[4][kQT];  // [ct][qt]
     float mrun[kQT], mthr[kQT];  // running maximum (uniform per query column), + kThr
+    float mref[kQT];  // fp16 tangent: exact running maximum of the lane's keys
     constexpr uint32_t kOne2 = T16::kDtype == SLA2H_DTYPE_F16 ? 0x3C003C00u : 0x3F803F80u;
     const u32x4 lm_a = u32x4{kOne2, kOne2, kOne2, kOne2};
 #pragma unroll
@@ -249,6 +254,7 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
       mu_i[qt] = 0.f;
       mrun[qt] = -INFINITY;
       mthr[qt] = -INFINITY;
+      mref[qt] = -INFINITY;
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
         acc_o[ct][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -358,39 +364,65 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
           if (!MASK || key0 + i < L) mx = fmaxf(mx, sv[qt][i]);
         mt[qt] = mx * c;
         over |= mt[qt] > mthr[qt];
+        if (kClampT) mref[qt] = fmaxf(mref[qt], mt[qt]);
       }
       if (__builtin_amdgcn_ballot_w64(over) != 0) {
 #pragma unroll
         for (int qt = 0; qt < kQT; ++qt)
           if (__builtin_amdgcn_ballot_w64(mt[qt] > mthr[qt]) != 0) rescale(qt, mt[qt], pend);
       }
-#pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
-        float p[4], t[4];
+      float p[kQT][4], t[kQT][4];
+      auto expo = [&](int qt) {
         const float moff = mrun[qt];
-        float ts = 0.f;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float e = fmaf(sv[qt][i], c, -moff);
           if (MASK && key0 + i >= L) e = -INFINITY;
-          p[i] = fast_exp2(e);
-          if (TAN) {
-            t[i] = p[i] * (PRE ? dsv[qt][i] : dsv[qt][i] * a.scale);
-            ts += t[i];
-          }
+          p[qt][i] = fast_exp2(e);
+          if (TAN) t[qt][i] = p[qt][i] * (PRE ? dsv[qt][i] : dsv[qt][i] * a.scale);
         }
-        if (TAN) mu_i[qt] += ts;
-
-        pb[qt].x = pack_pair<T16>(p[0], p[1]);
-        pb[qt].y = pack_pair<T16>(p[2], p[3]);
-        if (TAN) {
-          if (T16::kDtype == SLA2H_DTYPE_F16) {
+      };
+      if (kClampT) {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) t[i] = fminf(fmaxf(t[i], -60000.f), 60000.f);
-          }
+        for (int qt = 0; qt < kQT; ++qt) expo(qt);
+        // a T at or past the clamp under the lazy maximum: redo the sub-tile
+        // at the exact running maximum (rare)
+        bool big[kQT], any = false;
+#pragma unroll
+        for (int qt = 0; qt < kQT; ++qt) {
+          const float tm = fmaxf(fmaxf(fabsf(t[qt][0]), fabsf(t[qt][1])),
+                                 fmaxf(fabsf(t[qt][2]), fabsf(t[qt][3])));
+          big[qt] = tm >= 60000.f;
+          any |= big[qt];
+        }
+        if (__builtin_amdgcn_ballot_w64(any) != 0) {
+#pragma unroll
+          for (int qt = 0; qt < kQT; ++qt)
+            if (__builtin_amdgcn_ballot_w64(big[qt]) != 0) {
+              rescale(qt, mref[qt], pend);
+              expo(qt);
+            }
+        }
+      }
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
+        if (!kClampT) expo(qt);
+        if (TAN) {
+          float ts = 0.f;
+#pragma unroll
+          for (int i = 0; i < 4; ++i) ts += t[qt][i];
+          mu_i[qt] += ts;
+        }
+        pb[qt].x = pack_pair<T16>(p[qt][0], p[qt][1]);
+        pb[qt].y = pack_pair<T16>(p[qt][2], p[qt][3]);
+        if (TAN) {
+          float tc[4];
+#pragma unroll
+          for (int i = 0; i < 4; ++i)
+            tc[i] = kClampT ? fminf(fmaxf(t[qt][i], -60000.f), 60000.f) : t[qt][i];
           u32x4 bt;
-          bt.x = pack_pair<T16>(t[0], t[1]);
-          bt.y = pack_pair<T16>(t[2], t[3]);
+          bt.x = pack_pair<T16>(tc[0], tc[1]);
+          bt.y = pack_pair<T16>(tc[2], tc[3]);
           bt.z = pb[qt].x;
           bt.w = pb[qt].y;
 #pragma unroll

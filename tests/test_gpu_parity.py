@@ -517,3 +517,70 @@ def test_random_shapes_sweep(case):
                            t16=dt, sparse_only=True)
         print(f"  sparse-only max {max_abs(os_, es):.2e} rel {rel_l2(os_, es):.2e}", flush=True)
         assert max_abs(os_, es) < TOL_MAX and rel_l2(os_, es) < TOL_REL
+
+
+@pytest.mark.parametrize("scale_t", [2000.0, 3000.0])
+def test_fp16_tangent_at_the_clamp(scale_t):
+    """fp16 operands with tangents so large that T = P dS passes the +-60000
+    clamp the reference applies before the fp16 conversion: q = k (each
+    query's own key dominates its softmax) and dq = scale_t * k, so the
+    diagonal dS reaches 1.1e5-1.7e5.  The kernel's lazy running maximum must
+    fall back to the exact one for such tiles, so that the clamp acts as in
+    the oracle's exact online softmax.  B = 1, H = 2, Np = 12, every tile
+    routed."""
+    say("fp16 clamp, dq scale", scale_t)
+    B, H, Np, P = 1, 2, 12, 0
+    L = Np * 64
+    g = torch.Generator().manual_seed(3)
+    k = torch.randn(B, H, L, 64, generator=g) * 2.0
+    v = torch.randn(B, H, L, 64, generator=g)
+    dq = (k * scale_t + torch.randn(B, H, L, 64, generator=g)).clamp(-30000, 30000)
+    dk = torch.randn(B, H, L, 64, generator=g) * 0.1
+    dv = torch.randn(B, H, L, 64, generator=g) * 0.1
+    ins = dict(zip(("q", "k", "v", "dq", "dk", "dv"), (t.half() for t in (k, k, v, dq, dk, dv))))
+    f = {n: t.float() for n, t in ins.items()}
+    ds_diag = (f["dq"] * f["k"]).sum(-1) * 0.125
+    assert ds_diag.abs().max() > 1e5  # the clamp is active on the diagonal
+    alpha = torch.full((H, Np), 0.7)
+    lut = torch.stack([torch.randperm(Np, generator=g) for _ in range(B * H * Np)])
+    lut = lut.view(B, H, Np, Np).int().numpy()
+    o, do, _ = run_full(ins, alpha, 1.0, Np, P, lut=lut)
+    eo, edo = O.cube_jvp(*(f[n] for n in ("q", "k", "v", "dq", "dk", "dv")), alpha, lut, Np, P,
+                         t16=torch.float16)
+    big = edo.abs().max().item()
+    bound = TOL_MAX * max(1.0, eo.abs().max().item())  # o up to ~2 on this sharp softmax
+    print(f"  o max {max_abs(o, eo):.2e} (bound {bound:.2e})  do max {max_abs(do, edo):.2e} "
+          f"of {big:.2e} rel {rel_l2(do, edo):.2e}", flush=True)
+    assert max_abs(o, eo) < bound and rel_l2(o, eo) < TOL_REL
+    assert rel_l2(do, edo) < 2e-3 and max_abs(do, edo) < 1e-3 * big
+
+
+def test_fp16_clamp_follows_the_exact_maximum():
+    """A T below the +-60000 clamp at the exact running maximum but above it
+    under a lazy one: query 0 sees key 0 (score 1.44 in log2 units), then key
+    64 of the next tile 4 units higher (within the lazy margin), with dS =
+    40,000 on that key, so the exact T is 40,000 (no clamp) while 2^4 * T
+    would be clamped.  The kernel must evaluate the clamp at the exact
+    maximum, as the oracle's online softmax does (a lazy-scale clamp is off
+    by 10x on that entry).  fp16, B = H = 1, two tiles, both routed."""
+    say("fp16 clamp at the exact maximum")
+    B, H, Np, P = 1, 1, 2, 0
+    L = 128
+    z = lambda: torch.zeros(B, H, L, 64)
+    q, k, dq, dk, dv = z(), z(), z(), z(), z()
+    v = torch.randn(B, H, L, 64, generator=torch.Generator().manual_seed(1))
+    a, b0, b1 = 4.0, 2.0, 7.55  # log2-domain scores 1.44 and 5.44
+    q[0, 0, 0, 0], k[0, 0, 0, 0], k[0, 0, 64, 0] = a, b0, b1
+    dq[0, 0, 0, 0] = 320000.0 / b1  # dS of key 64 for query 0: 40,000
+    ins = dict(zip(("q", "k", "v", "dq", "dk", "dv"), (t.half() for t in (q, k, v, dq, dk, dv))))
+    f = {n: t.float() for n, t in ins.items()}
+    alpha = torch.ones(H, Np)
+    lut = np.array([[[[0, 1], [0, 1]]]], dtype=np.int32)
+    o, do, _ = run_full(ins, alpha, 1.0, Np, P, lut=lut)
+    eo, edo = O.cube_jvp(*(f[n] for n in ("q", "k", "v", "dq", "dk", "dv")), alpha, lut, Np, P,
+                         t16=torch.float16)
+    assert edo[0, 0, 0].abs().max() > 1e4  # the large tangent row
+    print(f"  o max {max_abs(o, eo):.2e}  do max {max_abs(do, edo):.2e} rel {rel_l2(do, edo):.2e}",
+          flush=True)
+    assert max_abs(o, eo) < TOL_MAX and rel_l2(o, eo) < TOL_REL
+    assert rel_l2(do, edo) < 1e-3
