@@ -85,6 +85,18 @@ def attn_sublayer_jvp(h, dh, p, w16, cos, sin, eps, stage_events=None):
     Returns (a, da): (b, l, d) fp32.  stage_events: optional three HIP events
     recorded before the attention op, after it, and at the end.
     """
+    proj = _attn_sublayer_proj(h, dh, p, w16, cos, sin, eps, stage_events)
+    # fp16 GEMM output times the fp32 gain: one kernel (fp32 by type promotion)
+    out = proj * _vec(p["g_attn"], h.device)
+    if stage_events:
+        stage_events[2].record()
+    B = h.shape[0]
+    return out[:B], out[B:]
+
+
+def _attn_sublayer_proj(h, dh, p, w16, cos, sin, eps, stage_events=None):
+    """The attention sublayer JVP up to its output projection: the fp16 GEMM
+    output (2b, l, d), rows [primal; tangent], before the gain g_attn."""
     rec = (lambda i: stage_events[i].record()) if stage_events else (lambda i: None)
     ops._need_gpu(h, dh)
     B, S, D = h.shape
@@ -147,17 +159,21 @@ def attn_sublayer_jvp(h, dh, p, w16, cos, sin, eps, stage_events=None):
     _lib.check(_lib.load().sla2h_mla_out_gate(
         o.data_ptr(), do.data_ptr(), ops._ptr(pos), ops._ptr(z), 0, B, S, H, dv,
         gated.data_ptr(), _stream(dev)), "sla2h_mla_out_gate")
-    # fp16 GEMM output times the fp32 gain: one kernel (fp32 by type promotion)
-    proj = F.linear(gated, w16["w_out"]).view(2 * B, S, D) * _vec(p["g_attn"], dev)
-    out = proj[:B], proj[B:]
-    rec(2)
-    return out
+    return F.linear(gated, w16["w_out"]).view(2 * B, S, D)
 
 
 def mlp_sublayer_jvp(h, dh, p, w16, eps):
     """MLP sublayer JVP: m = down(situ(gate_up(norm2(h)))) * g_mlp -> (m, dm) fp32.
     As in the reference's fast JVP, the up branch is not soft-clamped (the
     eager SwiGLUMlp's linear_beta is ignored here)."""
+    dwn = _mlp_sublayer_proj(h, dh, p, w16, eps) * _vec(p["g_mlp"], h.device)
+    B = h.shape[0]
+    return dwn[:B], dwn[B:]
+
+
+def _mlp_sublayer_proj(h, dh, p, w16, eps):
+    """The MLP sublayer JVP up to its down projection: the fp16 GEMM output
+    (2b, l, d), rows [primal; tangent], before the gain g_mlp."""
     ops._need_gpu(h, dh)
     B, S, D = h.shape
     dev = h.device
@@ -171,8 +187,7 @@ def mlp_sublayer_jvp(h, dh, p, w16, eps):
     act = torch.empty(M, f, device=dev, dtype=_FP16)
     _lib.check(_lib.load().sla2h_situ_jvp(gu.data_ptr(), half, f, float(p.get("situ_beta", 1.0)),
                                           0, act.data_ptr(), _stream(dev)), "sla2h_situ_jvp")
-    dwn = F.linear(act, w16["w_down"]).view(2 * B, S, D) * _vec(p["g_mlp"], dev)
-    return dwn[:B], dwn[B:]
+    return F.linear(act, w16["w_down"]).view(2 * B, S, D)
 
 
 def pack_block(block, tile_major=False):
@@ -236,11 +251,19 @@ def build_fast_jvp_state(net):
 
 
 def block_jvp(h, dh, p, w16, cos, sin, eps):
-    """TransformerBlock JVP: x += attn sublayer; x += MLP sublayer -> (x, dx) fp32."""
-    a, da = attn_sublayer_jvp(h, dh, p, w16, cos, sin, eps)
-    h, dh = h + a, dh + da
-    m, dm = mlp_sublayer_jvp(h, dh, p, w16, eps)
-    return h + m, dh + dm
+    """TransformerBlock JVP: x += attn sublayer; x += MLP sublayer -> (x, dx) fp32.
+    Each residual update x + proj * g is one HIP kernel per half (the gain's
+    product and the sum rounded separately, as the two torch operations
+    would), reading the sublayer's fp16 GEMM output directly."""
+    h, dh = h.float().contiguous(), dh.float().contiguous()
+    B = h.shape[0]
+    dev = h.device
+    a = _attn_sublayer_proj(h, dh, p, w16, cos, sin, eps)
+    g = _vec(p["g_attn"], dev)
+    h, dh = ops.residual_scale_fwd(h, a[:B], g), ops.residual_scale_fwd(dh, a[B:], g)
+    m = _mlp_sublayer_proj(h, dh, p, w16, eps)
+    g = _vec(p["g_mlp"], dev)
+    return ops.residual_scale_fwd(h, m[:B], g), ops.residual_scale_fwd(dh, m[B:], g)
 
 
 # reference-private names (models/mla_jvp_fast.py:53, 198)
