@@ -83,15 +83,14 @@ SIGNATURES = {
                                       _p, _p, _p, _p, _p, _p]),
     "sla2h_lin_fwd3": (_c_int, [_p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_i64, _c_int,
                                 _c_int, _c_f, _p, _p]),
-    "sla2h_bwd_prep": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int,
-                                _c_i64, _c_int, _c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p,
-                                _p]),
+    "sla2h_bwd_prep": (_c_int, [_p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_i64,
+                                _c_int, _c_int, _p, _p, _p, _p, _p, _p, _p, _p]),
     "sla2h_complement_bwd": (_c_int, [_p, _p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _p,
                                       _p, _p, _p]),
-    "sla2h_bwd_dq": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _c_int, _c_int,
+    "sla2h_bwd_dq": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _c_int, _c_int,
                               _c_int, _c_i64, _c_int, _c_int, _c_int, _c_f, _p, _p]),
-    "sla2h_bwd_dkdv": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int,
-                                _c_i64, _c_int, _c_int, _c_f, _p, _p, _p]),
+    "sla2h_bwd_dkdv": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_i64,
+                                _c_int, _c_int, _c_f, _p, _p, _p]),
 }
 
 _LIB = None

@@ -16,18 +16,15 @@
 //                  (models/sla2_cube_qat.py:875-904).
 //
 // Kernels: bwd_prep (per 64-row block: gradient split, delta, g, s, the alpha
-// segment sums, the per-block partial states P = qphi^T g and Pz = qphi^T s,
-// and the transposed operand fragments of q, k and do_s), then the dq kernel
-// (per query block, key-split waves) and the dk/dv kernel (per key tile,
-// query-split waves).  The complement GEMM of the partial states lives with
-// the forward's complement (states.hip).
+// segment sums and the per-block partial states P = qphi^T g and Pz =
+// qphi^T s), then the dq kernel (per query block, key-split waves) and the
+// dk/dv kernel (per key tile, query-split waves).  The complement GEMM of the
+// partial states lives with the forward's complement (states.hip).
 //
-// Transposed operand fragments (16-bit, per 64-row block, 8 KB):
-//   tf[ct][p][lane][s] = X[16 (2p + (s>>2)) + 4g + (s&3)][16 ct + r],
-//   lane = 16 g + r; rows past L are zero.  A wave that owns rows
-//   16w..16w+15 reads the 8-byte half s = 4 (w&1) .. 4 (w&1) + 3 of chunk
-//   (ct, p = w>>1): the A operand of a 16x16x16 MFMA that contracts over those
-//   16 rows.
+// The products that contract over 16 rows of a wave (dq over keys, dk and dv
+// over queries) take those rows transposed as their A operand: the wave holds
+// the rows row-major in LDS and reads the operand with the gfx950 transposing
+// LDS read, so no transposed copy of q, k or do_s goes through memory.
 #include "common.h"
 
 #include <climits>
@@ -66,8 +63,6 @@ struct PrepArgs {
   const uint16_t* o_l;
   const float* den;
   const uint16_t* qphi;
-  const uint16_t* q;
-  const uint16_t* k;
   const float* alpha;
   uint16_t* dos;
   float* delta;
@@ -76,9 +71,6 @@ struct PrepArgs {
   float* seg;
   float* P;
   float* Pz;
-  uint16_t* qtf;
-  uint16_t* ktf;
-  uint16_t* dotf;
   int64_t L;
   int Nb, H, alpha_stride;
   int Mq, qshift;  // alpha rows / seg: query blocks of 64 << qshift rows
@@ -89,7 +81,6 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
   __shared__ float qps[kT][kT + 1];  // qphi [row][d]
   __shared__ float gs[kT][kT + 1];   // saturated g [row][e]
   __shared__ float ss[kT];
-  __shared__ __align__(16) uint16_t xs[3][kT][kT + 8];  // q, k, do_s rows
   __shared__ float red[4];
 
   const int blk = blockIdx.x, bh = blockIdx.y, h = bh % a.H;
@@ -122,7 +113,7 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
     p[1] = make_uint4(w[4], w[5], w[6], w[7]);
   };
 
-  uint16_t dob[16], osb[16], olb[16], qpb[16], xb[16], g16b[16], dsb[16];
+  uint16_t dob[16], osb[16], olb[16], qpb[16], g16b[16], dsb[16];
   ld(a.dout, dob);
   ld(a.o_s, osb);
   ld(a.o_l, olb);
@@ -134,6 +125,8 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
   for (int i = 0; i < 16; ++i) {
     const float d = T16::to_f32(dob[i]);
     const float os = T16::to_f32(osb[i]), ol = T16::to_f32(olb[i]);
+    // (do * a).to(16-bit), (do * (1 - a)).to(16-bit) of the reference's split
+    // kernel: the fp32 products round before the 16-bit conversion
     dsb[i] = T16::from_f32(d * al);
     const float dl = r16<T16>(d * (1.f - al));
     dsum += os * T16::to_f32(dsb[i]);
@@ -143,7 +136,6 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
     gs[r][c0 + i] = g;
     g16b[i] = T16::from_f32(g);
     qps[r][c0 + i] = T16::to_f32(qpb[i]);
-    xs[2][r][c0 + i] = dsb[i];
   }
   dsum += __shfl_xor(dsum, 1, 64);
   dsum += __shfl_xor(dsum, 2, 64);
@@ -159,12 +151,6 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
       a.s[(int64_t)bh * a.L + row] = srow;
     }
   }
-  ld(a.q, xb);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) xs[0][r][c0 + i] = xb[i];
-  ld(a.k, xb);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) xs[1][r][c0 + i] = xb[i];
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) segp += __shfl_xor(segp, m, 64);
   if ((tid & 63) == 0) red[tid >> 6] = segp;
@@ -196,27 +182,15 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
     for (int rw = 0; rw < kT; ++rw) z += qps[rw][tid] * ss[rw];
     a.Pz[((int64_t)bh * a.Nb + blk) * kT + tid] = z;
   }
+}
 
-  // transposed operand fragments of q, k, do_s: 16 x 16 x 16 A operands
-  // [channel 16ct + r][row 16w + 4g + e], 32 contiguous bytes per (w, lane)
-  // holding ct = 0..3, e = 0..3 (element ((w * 64 + lane) * 4 + ct) * 4 + e)
-  uint16_t* tfs[3] = {a.qtf, a.ktf, a.dotf};
-  {
-    const int fw = tid >> 6, lane = tid & 63, gg = lane >> 4, rr = lane & 15;
-#pragma unroll
-    for (int x = 0; x < 3; ++x) {
-      uint32_t v[8];
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-        for (int e = 0; e < 2; ++e)
-          v[2 * ct + e] = pack2(xs[x][16 * fw + 4 * gg + 2 * e][16 * ct + rr],
-                                xs[x][16 * fw + 4 * gg + 2 * e + 1][16 * ct + rr]);
-      uint4* dst = reinterpret_cast<uint4*>(tfs[x] + ((int64_t)bh * a.Nb + blk) * 4096 + tid * 16);
-      dst[0] = make_uint4(v[0], v[1], v[2], v[3]);
-      dst[1] = make_uint4(v[4], v[5], v[6], v[7]);
-    }
-  }
+// gfx950 transposing LDS read (ds_read_b64_tr_b16): within each group of 16
+// lanes, lane j receives element j % 4 of the 8 bytes addressed by lanes
+// j / 4, 4 + j / 4, 8 + j / 4 and 12 + j / 4 of its group, in that order.
+__device__ inline u32x2 lds_read_tr16(const void* p) {
+  typedef short v4s __attribute__((ext_vector_type(4)));
+  const v4s v = __builtin_amdgcn_ds_read_tr16_b64_v4i16((__attribute__((address_space(3))) v4s*)p);
+  return __builtin_bit_cast(u32x2, v);
 }
 
 // ---------------------------------------------------------------------------
@@ -233,7 +207,6 @@ struct DqArgs {
   const uint16_t* k;
   const uint16_t* v;
   const uint16_t* dos;
-  const uint16_t* ktf;
   const uint16_t* g16;
   const uint16_t* qphi;
   const float* lse;
@@ -326,8 +299,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
   const auto rk = make_rsrc(a.k + base * kT, L * kT * 2);  // key rows past L read as 0
   const auto rv = make_rsrc(a.v + base * kT, L * kT * 2);
   const int rowoff = ((16 * w + r) * kT + 8 * g) * 2;
-  const int tfoff = (w * 64 + l) * 32;  // bytes: this lane's four K^T fragments
-  const unsigned char* ktf = reinterpret_cast<const unsigned char*>(a.ktf) + (int64_t)bh * a.Nb * 8192;
+  // The wave's K rows of two tiles, staged in its own 8 KB of the merge
+  // buffer (free during the key loop: the sort is done, the partial sums come
+  // after it) for the transposed reads of the K^T operands; rows padded to
+  // 144 bytes against bank conflicts.
+  constexpr int kKs = 144;
+  unsigned char* kst = reinterpret_cast<unsigned char*>(&mb[0][w][0][0][0]);
 
   // score-side operands (K, V rows) and the K^T fragments of the dq product,
   // loaded separately: the K^T fragments are used last, by the pair product
@@ -342,14 +319,17 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
       f.v[ks] = buf_load16(rv, n * kT * kT * 2 + rowoff + 64 * ks, 0);
     }
   };
-  auto load_kt = [&](int j, u32x2 (&kt)[4]) {
-    const int n = __builtin_amdgcn_readfirstlane(tiles[j]);
-    const u32x4 k01 = *reinterpret_cast<const u32x4*>(ktf + (int64_t)n * 8192 + tfoff);
-    const u32x4 k23 = *reinterpret_cast<const u32x4*>(ktf + (int64_t)n * 8192 + tfoff + 16);
-    kt[0] = u32x2{k01[0], k01[1]};
-    kt[1] = u32x2{k01[2], k01[3]};
-    kt[2] = u32x2{k23[0], k23[1]};
-    kt[3] = u32x2{k23[2], k23[3]};
+  auto stage_k = [&](const Frags& f, int slot) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      *reinterpret_cast<u32x4*>(kst + slot * 16 * kKs + r * kKs + 64 * ks + 16 * g) = f.k[ks];
+  };
+  // K^T operand [channel 16 ct + r][key 16 w + 4 g + e]: this lane addresses
+  // key row 4 g + r / 4, channels 16 ct + 4 (r % 4) .. + 3
+  auto read_kt = [&](int slot, u32x2 (&kt)[4]) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct)
+      kt[ct] = lds_read_tr16(kst + slot * 16 * kKs + (4 * g + (r >> 2)) * kKs + 2 * (16 * ct + 4 * (r & 3)));
   };
 
   f32x4 acc[4][4];
@@ -359,7 +339,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
     for (int ct = 0; ct < 4; ++ct) acc[qb][ct] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   // Keys past L need no mask here: their K and V rows read as zero (buffer
-  // range check) and their K^T fragments are zero-filled, so dp = 0, ds stays
+  // range check), so are their K^T operands, so dp = 0, ds stays
   // finite (p <= 2^4) and K^T ds adds exactly zero to dq.
   // ds^T fragments of one tile: lane (g, r) holds keys 16w+4g+i of query 16qb+r
   auto tile_ds = [&](const Frags& f, u32x2 (&dsp)[4]) {
@@ -398,27 +378,31 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
   };
 
   // Tiles in pairs: the second tile's operands are requested before the
-  // first tile's scores, the next pair's first tile right after them, the
-  // K^T fragments of the next pair after the pair product that frees theirs.
+  // first tile's scores, the next pair's first tile right after them.  Each
+  // tile's K rows go to the wave's staging slot once they arrive; the K^T
+  // operands of the pair product are read back transposed.
   const int J = a.J;
   Frags fa, fb;
   u32x2 kta[4], ktb[4];
   load(0, fa);
-  load_kt(0, kta);
   int j = 0;
   for (; j + 1 < J; j += 2) {
     u32x2 dsa[4], dsb[4];
     load(j + 1, fb);
-    load_kt(j + 1, ktb);
+    stage_k(fa, 0);
     tile_ds(fa, dsa);
     load(j + 2 < J ? j + 2 : J - 1, fa);
+    stage_k(fb, 1);
     tile_ds(fb, dsb);
+    read_kt(0, kta);
+    read_kt(1, ktb);
     dq_pair(kta, dsa, ktb, dsb);
-    load_kt(j + 2 < J ? j + 2 : J - 1, kta);
   }
   if (j < J) {
     u32x2 dsa[4];
+    stage_k(fa, 0);
     tile_ds(fa, dsa);
+    read_kt(0, kta);
     dq_single(kta, dsa);
   }
 
@@ -501,8 +485,6 @@ struct DkdvArgs {
   const uint16_t* k;
   const uint16_t* v;
   const uint16_t* dos;
-  const uint16_t* qtf;
-  const uint16_t* dotf;
   const float* lse;
   const float* delta;
   const uint32_t* sel;
@@ -514,10 +496,12 @@ struct DkdvArgs {
   float c, scale;
 };
 
-// Prefetch region of one wave: 8 slots of 64 lanes x 16 B, then lse and delta
-// (64 dwords each).
+// Prefetch region of one wave: 4 slots of 64 lanes x 16 B, then lse and delta
+// (64 dwords each).  The four regions also hold the partial-sum exchange
+// after the loop (32 KB).
 constexpr int kPfSlot = 1024;
-constexpr int kPfWave = 8 * kPfSlot + 2 * 256;
+constexpr int kPfWave = 4 * kPfSlot + 2 * 256;
+constexpr int kPoolBytes = 4 * kPfWave > 32768 ? 4 * kPfWave : 32768;
 constexpr int kSelLds = 128;  // mask words staged in LDS (query blocks 0 .. 4095)
 // s_waitcnt immediates (gfx9 encoding): vmcnt(0) alone, lgkmcnt(0) alone
 constexpr int kWaitVm0 = 0x0F70;
@@ -540,7 +524,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
   __shared__ __align__(16) uint16_t dhs[2][kT][kT + 8];  // dh16 [d][e], dh16^T [e][d]
   // Per-wave prefetch regions of the query-block loop; after the loop the
   // same bytes hold the partial-sum exchange mb[src wave][kb sel][ct][lane].
-  __shared__ __align__(16) unsigned char pool[4 * kPfWave];
+  __shared__ __align__(16) unsigned char pool[kPoolBytes];
   __shared__ float dzs[kT];
   __shared__ uint32_t selsh[kSelLds];  // first words of this tile's query-block mask
   auto mb = reinterpret_cast<f32x4 (*)[2][4][64]>(pool);
@@ -597,32 +581,26 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
   // Query blocks m routed to this tile, ascending.  The operands of block m
   // (this wave's 16 query rows) are fetched one block ahead straight into the
   // wave's LDS region (buffer loads to LDS: no registers held in flight):
-  // slots of 64 lanes x 16 B -- Q rows (ks 0, 1), do_s rows (ks 0, 1), the
-  // four Q^T fragments (2 slots), the four do_s^T fragments (2 slots) -- then
-  // 64 dwords of lse and 64 of delta (query 16w + (lane & 15)).  Rows past L
-  // read as zero: such a query then has p = 1 but zero Q, do_s, Q^T and
-  // do_s^T, so it adds exactly zero to dk and dv (as with a masked p).
+  // slots of 64 lanes x 16 B -- Q rows (ks 0, 1), do_s rows (ks 0, 1), lane
+  // (g, r) holding row 16w + r, channels 32 ks + 8 g .. + 7 -- then 64 dwords
+  // of lse and 64 of delta (query 16w + (lane & 15)).  The Q^T and do_s^T
+  // operands of dk and dv are read transposed from the same rows.  Rows past
+  // L read as zero: such a query then has p = 1 but zero Q and do_s rows, so
+  // it adds exactly zero to dk and dv (as with a masked p).
   const auto rq = make_rsrc(a.q + base * kT, L * kT * 2);
   const auto rdo = make_rsrc(a.dos + base * kT, L * kT * 2);
-  const auto rqt = make_rsrc(a.qtf + (int64_t)bh * a.Nb * 4096, (int64_t)a.Nb * 8192);
-  const auto rdt = make_rsrc(a.dotf + (int64_t)bh * a.Nb * 4096, (int64_t)a.Nb * 8192);
   const auto rls = make_rsrc(a.lse + base, L * 4);
   const auto rdl = make_rsrc(a.delta + base, L * 4);
   unsigned char* pf = pool + w * kPfWave;
   auto prefetch = [&](int m) {
     const int rowb = (m * kT + 16 * w + r) * (kT * 2) + 16 * g;
-    const int fo = m * 8192 + (w * 64 + l) * 32;
     const int qo = (m * kT + 16 * w + (l & 15)) * 4;
     lds_load16(rq, pf + 0 * kPfSlot, rowb);
     lds_load16(rq, pf + 1 * kPfSlot, rowb + 64);
     lds_load16(rdo, pf + 2 * kPfSlot, rowb);
     lds_load16(rdo, pf + 3 * kPfSlot, rowb + 64);
-    lds_load16(rqt, pf + 4 * kPfSlot, fo);
-    lds_load16(rqt, pf + 5 * kPfSlot, fo + 16);
-    lds_load16(rdt, pf + 6 * kPfSlot, fo);
-    lds_load16(rdt, pf + 7 * kPfSlot, fo + 16);
-    lds_load4(rls, pf + 8 * kPfSlot, qo);
-    lds_load4(rdl, pf + 8 * kPfSlot + 256, qo);
+    lds_load4(rls, pf + 4 * kPfSlot, qo);
+    lds_load4(rdl, pf + 4 * kPfSlot + 256, qo);
   };
   int kc = 0;
   uint32_t bits = 0u;
@@ -651,18 +629,20 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
         qa[ks] = *reinterpret_cast<const u32x4*>(src + ks * kPfSlot);
         da[ks] = *reinterpret_cast<const u32x4*>(src + (2 + ks) * kPfSlot);
       }
+      // Q^T, do_s^T operands [channel 16 ct + r][query 16 w + 4 g + e], read
+      // transposed from the rows: this lane addresses row 4 g + r / 4,
+      // channels 16 ct + 4 (r % 4) .. + 3, held in slot ct / 2 by the prefetch
+      // lane 16 (2 (ct % 2) + (r % 4) / 2) + row, at byte 8 (r % 2) of its 16
 #pragma unroll
-      for (int hf = 0; hf < 2; ++hf) {
-        const u32x4 x = *reinterpret_cast<const u32x4*>(src + (4 + hf) * kPfSlot);
-        const u32x4 y = *reinterpret_cast<const u32x4*>(src + (6 + hf) * kPfSlot);
-        qT[2 * hf] = u32x2{x[0], x[1]};
-        qT[2 * hf + 1] = u32x2{x[2], x[3]};
-        dT[2 * hf] = u32x2{y[0], y[1]};
-        dT[2 * hf + 1] = u32x2{y[2], y[3]};
+      for (int ct = 0; ct < 4; ++ct) {
+        const int off = (ct >> 1) * kPfSlot +
+                        (16 * (2 * (ct & 1) + ((r & 3) >> 1)) + 4 * g + (r >> 2)) * 16 + 8 * (r & 1);
+        qT[ct] = lds_read_tr16(pf + off);
+        dT[ct] = lds_read_tr16(pf + 2 * kPfSlot + off);
       }
       // lse, delta of queries 16w + 4g + i
-      const f32x4 ls = *reinterpret_cast<const f32x4*>(pf + 8 * kPfSlot + 16 * g);
-      const f32x4 dl = *reinterpret_cast<const f32x4*>(pf + 8 * kPfSlot + 256 + 16 * g);
+      const f32x4 ls = *reinterpret_cast<const f32x4*>(pf + 4 * kPfSlot + 16 * g);
+      const f32x4 dl = *reinterpret_cast<const f32x4*>(pf + 4 * kPfSlot + 256 + 16 * g);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         lse4[i] = ls[i];
@@ -810,12 +790,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
 using namespace sla2h;
 
 extern "C" int sla2h_bwd_prep(const void* dout, const void* o_s, const void* o_l, const float* den,
-                              const void* qphi, const void* q, const void* k, const float* alpha,
-                              int alpha_stride, int dtype, int B, int H, int64_t L, int D, int E,
-                              void* dos, float* delta, void* g16, float* s, float* seg, float* P,
-                              float* Pz, void* qtf, void* ktf, void* dotf, void* stream) {
-  SLA2H_CHECK_ARG(dout && o_s && o_l && den && qphi && q && k && alpha && dos && delta && g16 &&
-                  s && seg && P && Pz && qtf && ktf && dotf);
+                              const void* qphi, const float* alpha, int alpha_stride, int dtype,
+                              int B, int H, int64_t L, int D, int E, void* dos, float* delta,
+                              void* g16, float* s, float* seg, float* P, float* Pz, void* stream) {
+  SLA2H_CHECK_ARG(dout && o_s && o_l && den && qphi && alpha && dos && delta && g16 && s && seg &&
+                  P && Pz);
   SLA2H_CHECK_ARG(D == kT && (E == 64 || E == 128 || E == 256) && alpha_stride >= 0);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && L > 0);
@@ -827,8 +806,6 @@ extern "C" int sla2h_bwd_prep(const void* dout, const void* o_s, const void* o_l
   a.o_l = static_cast<const uint16_t*>(o_l);
   a.den = den;
   a.qphi = static_cast<const uint16_t*>(qphi);
-  a.q = static_cast<const uint16_t*>(q);
-  a.k = static_cast<const uint16_t*>(k);
   a.alpha = alpha;
   a.dos = static_cast<uint16_t*>(dos);
   a.delta = delta;
@@ -837,9 +814,6 @@ extern "C" int sla2h_bwd_prep(const void* dout, const void* o_s, const void* o_l
   a.seg = seg;
   a.P = P;
   a.Pz = Pz;
-  a.qtf = static_cast<uint16_t*>(qtf);
-  a.ktf = static_cast<uint16_t*>(ktf);
-  a.dotf = static_cast<uint16_t*>(dotf);
   a.L = L;
   a.Nb = (int)((L + kT - 1) / kT);
   a.H = H;
@@ -854,11 +828,11 @@ extern "C" int sla2h_bwd_prep(const void* dout, const void* o_s, const void* o_l
 }
 
 extern "C" int sla2h_bwd_dq(const void* q, const void* k, const void* v, const void* dos,
-                            const float* lse, const float* delta, const void* ktf,
-                            const void* g16, const float* s, const void* comp, const float* Hall,
-                            const void* qphi, const int32_t* lut_aug, int dtype, int B, int H,
-                            int64_t L, int D, int E, int J, float scale, void* dq, void* stream) {
-  SLA2H_CHECK_ARG(q && k && v && dos && lse && delta && ktf && g16 && s && comp && Hall && qphi &&
+                            const float* lse, const float* delta, const void* g16, const float* s,
+                            const void* comp, const float* Hall, const void* qphi,
+                            const int32_t* lut_aug, int dtype, int B, int H, int64_t L, int D,
+                            int E, int J, float scale, void* dq, void* stream) {
+  SLA2H_CHECK_ARG(q && k && v && dos && lse && delta && g16 && s && comp && Hall && qphi &&
                   lut_aug && dq);
   SLA2H_CHECK_ARG(D == kT && (E == 64 || E == 128 || E == 256) && scale > 0.f);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
@@ -872,7 +846,6 @@ extern "C" int sla2h_bwd_dq(const void* q, const void* k, const void* v, const v
   a.k = static_cast<const uint16_t*>(k);
   a.v = static_cast<const uint16_t*>(v);
   a.dos = static_cast<const uint16_t*>(dos);
-  a.ktf = static_cast<const uint16_t*>(ktf);
   a.g16 = static_cast<const uint16_t*>(g16);
   a.qphi = static_cast<const uint16_t*>(qphi);
   a.lse = lse;
@@ -901,11 +874,10 @@ extern "C" int sla2h_bwd_dq(const void* q, const void* k, const void* v, const v
 }
 
 extern "C" int sla2h_bwd_dkdv(const void* q, const void* k, const void* v, const void* dos,
-                              const float* lse, const float* delta, const void* qtf,
-                              const void* dotf, const uint32_t* sel, const void* comp_bwd,
-                              int dtype, int B, int H, int64_t L, int D, int E, float scale,
-                              void* dk, void* dv, void* stream) {
-  SLA2H_CHECK_ARG(q && k && v && dos && lse && delta && qtf && dotf && sel && comp_bwd && dk && dv);
+                              const float* lse, const float* delta, const uint32_t* sel,
+                              const void* comp_bwd, int dtype, int B, int H, int64_t L, int D,
+                              int E, float scale, void* dk, void* dv, void* stream) {
+  SLA2H_CHECK_ARG(q && k && v && dos && lse && delta && sel && comp_bwd && dk && dv);
   SLA2H_CHECK_ARG(D == kT && E == kT && scale > 0.f);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
   SLA2H_CHECK_ARG(B > 0 && H > 0 && L > 0);
@@ -918,8 +890,6 @@ extern "C" int sla2h_bwd_dkdv(const void* q, const void* k, const void* v, const
   a.k = static_cast<const uint16_t*>(k);
   a.v = static_cast<const uint16_t*>(v);
   a.dos = static_cast<const uint16_t*>(dos);
-  a.qtf = static_cast<const uint16_t*>(qtf);
-  a.dotf = static_cast<const uint16_t*>(dotf);
   a.lse = lse;
   a.delta = delta;
   a.sel = sel;

@@ -19,6 +19,17 @@ typedef __attribute__((ext_vector_type(4))) short s16x4;
 typedef __attribute__((ext_vector_type(4))) uint32_t u32x4;
 typedef __attribute__((ext_vector_type(2))) uint32_t u32x2;
 
+// An fp32 result held as such before a 16-bit conversion.  (x * y).to(f16)
+// rounds the fp32 product and then the 16-bit value; left alone, the compiler
+// fuses a multiply (or fma) and the conversion into one rounding
+// (v_fma_mix*_f16), which differs where the fp32 result lands on a 16-bit
+// rounding midpoint.  Every fp16 conversion here goes through it (bf16 has no
+// fused form).
+__device__ inline float keep_f32(float x) {
+  asm("" : "+v"(x));
+  return x;
+}
+
 // 16-bit storage tags.  Values travel as raw uint16 bits; `to_f32` widens
 // exactly, `from_f32` rounds to nearest even (hardware cvt on gfx950).
 struct F16 {
@@ -27,7 +38,7 @@ struct F16 {
     return (float)__builtin_bit_cast(_Float16, b);
   }
   __device__ static inline uint16_t from_f32(float f) {
-    return __builtin_bit_cast(uint16_t, (_Float16)f);
+    return __builtin_bit_cast(uint16_t, (_Float16)keep_f32(f));
   }
 };
 struct BF16 {
@@ -106,7 +117,8 @@ __device__ inline uint32_t pack_pair<BF16>(float lo, float hi) {
 }
 template <>
 __device__ inline uint32_t pack_pair<F16>(float lo, float hi) {
-  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{lo, hi}), f16x2));
+  return __builtin_bit_cast(uint32_t,
+                            __builtin_convertvector((f32x2{keep_f32(lo), keep_f32(hi)}), f16x2));
 }
 
 // Reductions over the four 16-lane rows of a wave64 (lanes l, l^16, l^32,

@@ -402,18 +402,15 @@ def train_bwd(q, k, v, alpha, fwd, do, scale=None, stage_events=None, bq=E_TILE)
     seg = torch.zeros(H, mq, device=dev)
     P = torch.empty(B, H, nb, D, D, device=dev)
     Pz = torch.empty(B, H, nb, D, device=dev)
-    tf = lambda: torch.empty(B, H, nb, 4096, device=dev, dtype=q.dtype)
-    qtf, ktf, dotf = tf(), tf(), tf()
     dc = _dtype_code(q)
     st = _stream(dev)
     rec = (lambda i: stage_events[i].record()) if stage_events else (lambda i: None)
     rec(0)
     _lib.check(lib.sla2h_bwd_prep(
         do.data_ptr(), fwd["o_s"].data_ptr(), fwd["o_l"].data_ptr(), fwd["den"].data_ptr(),
-        fwd["qphi"].data_ptr(), q.data_ptr(), k.data_ptr(), alpha.data_ptr(), alpha.stride(0), dc,
-        B, H, L, D, bq, dos.data_ptr(), delta.data_ptr(), g16.data_ptr(), srow.data_ptr(),
-        seg.data_ptr(), P.data_ptr(), Pz.data_ptr(), qtf.data_ptr(), ktf.data_ptr(),
-        dotf.data_ptr(), st), "sla2h_bwd_prep")
+        fwd["qphi"].data_ptr(), alpha.data_ptr(), alpha.stride(0), dc, B, H, L, D, bq,
+        dos.data_ptr(), delta.data_ptr(), g16.data_ptr(), srow.data_ptr(), seg.data_ptr(),
+        P.data_ptr(), Pz.data_ptr(), st), "sla2h_bwd_prep")
     lut_aug = fwd["lut_aug"]
     J = lut_aug.shape[-1]
     ncq = -(-nb // 32)
@@ -429,13 +426,13 @@ def train_bwd(q, k, v, alpha, fwd, do, scale=None, stage_events=None, bq=E_TILE)
     rec(2)
     _lib.check(lib.sla2h_bwd_dq(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), dos.data_ptr(), fwd["lse"].data_ptr(),
-        delta.data_ptr(), ktf.data_ptr(), g16.data_ptr(), srow.data_ptr(), fwd["comp"].data_ptr(),
+        delta.data_ptr(), g16.data_ptr(), srow.data_ptr(), fwd["comp"].data_ptr(),
         fwd["Hall"].data_ptr(), fwd["qphi"].data_ptr(), lut_aug.data_ptr(), dc, B, H, L, D, bq,
         J, float(scale), dq.data_ptr(), st), "sla2h_bwd_dq")
     rec(3)
     _lib.check(lib.sla2h_bwd_dkdv(
         q.data_ptr(), k.data_ptr(), v.data_ptr(), dos.data_ptr(), fwd["lse"].data_ptr(),
-        delta.data_ptr(), qtf.data_ptr(), dotf.data_ptr(), sel.data_ptr(), compb.data_ptr(), dc,
+        delta.data_ptr(), sel.data_ptr(), compb.data_ptr(), dc,
         B, H, L, D, E_TILE, float(scale), dk.data_ptr(), dv.data_ptr(), st), "sla2h_bwd_dkdv")
     d_alpha = seg * alpha * (1.0 - alpha)
     return dq, dk, dv, d_alpha

@@ -413,15 +413,14 @@ int sla2h_sparse_fwd_1d(const void* q, const void* k, const void* vt, const int3
 
 /*
  * Per 64-row block: the gradient split and the row statistics of the
- * backward, plus the operands the dq and dk/dv kernels share.
- *   dos = round16(dout * a), do_l = round16(dout * (1 - a)), a = alpha[h,m] fp32;
+ * backward.
+ *   dos = round16(fl32(dout * a)), do_l = round16(fl32(dout * (1 - a))),
+ *     a = alpha[h,m] fp32 (the fp32 product rounds first, as in the reference);
  *   delta = sum_d o_s * dos (B,H,L) fp32;
  *   g16 = round16(sat(do_l / den)) (B,H,L,D) 16-bit, s = sum_d do_l o_l / den (B,H,L);
  *   seg (H,Mb) fp32 += sum over the block of dout * (o_s - o_l) (atomic over b;
  *     zero it first), so d(alpha logit) = seg * a * (1 - a);
- *   P = qphi^T sat(g) (B,H,Mb,D,D) fp32, Pz = qphi^T s (B,H,Mb,D) fp32;
- *   qtf, ktf, dotf (B,H,Nb,4096) 16-bit: q, k, dos in the transposed fragment
- *     order [ct][p][lane][s] = X[16(2p + (s>>2)) + 4g + (s&3)][16ct + r].
+ *   P = qphi^T sat(g) (B,H,Mb,D,D) fp32, Pz = qphi^T s (B,H,Mb,D) fp32.
  * sat(x) = clamp(x, -60000, 60000).  E = the query block length (64, or 128 /
  * 256 for 1-D blocks): alpha and seg have one column per query block of E
  * rows; every other array is per 64-row block.  Replaces _bwd_split_kernel
@@ -430,10 +429,9 @@ int sla2h_sparse_fwd_1d(const void* q, const void* k, const void* vt, const int3
  * lines of _CubeQATFunction.backward (models/sla2_cube_qat.py:765-797).
  */
 int sla2h_bwd_prep(const void* dout, const void* o_s, const void* o_l, const float* den,
-                   const void* qphi, const void* q, const void* k, const float* alpha,
-                   int alpha_stride, int dtype, int B, int H, int64_t L, int D, int E,
-                   void* dos, float* delta, void* g16, float* s, float* seg, float* P,
-                   float* Pz, void* qtf, void* ktf, void* dotf, void* stream);
+                   const void* qphi, const float* alpha, int alpha_stride, int dtype, int B,
+                   int H, int64_t L, int D, int E, void* dos, float* delta, void* g16, float* s,
+                   float* seg, float* P, float* Pz, void* stream);
 
 /*
  * Backward complement over the augmented LUT lut_aug (B,H,ceil(Mb*64/bq),J) int32,
@@ -464,10 +462,9 @@ int sla2h_complement_bwd(const float* P, const float* Pz, const int32_t* lut_aug
  * _phi_chain_add_kernel (models/sla2_cube_qat.py:875-904, 814-818).
  */
 int sla2h_bwd_dq(const void* q, const void* k, const void* v, const void* dos, const float* lse,
-                 const float* delta, const void* ktf, const void* g16, const float* s,
-                 const void* comp, const float* Hall, const void* qphi, const int32_t* lut_aug,
-                 int dtype, int B, int H, int64_t L, int D, int E, int J, float scale, void* dq,
-                 void* stream);
+                 const float* delta, const void* g16, const float* s, const void* comp,
+                 const float* Hall, const void* qphi, const int32_t* lut_aug, int dtype, int B,
+                 int H, int64_t L, int D, int E, int J, float scale, void* dq, void* stream);
 
 /*
  * dk = round16(sat(dk_s + kphi (dkphi - <kphi, dkphi>))), dv = round16(sat(dv_s + dv_l))
@@ -481,9 +478,9 @@ int sla2h_bwd_dq(const void* q, const void* k, const void* v, const void* dos, c
  * sum (:819-830).
  */
 int sla2h_bwd_dkdv(const void* q, const void* k, const void* v, const void* dos, const float* lse,
-                   const float* delta, const void* qtf, const void* dotf, const uint32_t* sel,
-                   const void* comp_bwd, int dtype, int B, int H, int64_t L, int D, int E,
-                   float scale, void* dk, void* dv, void* stream);
+                   const float* delta, const uint32_t* sel, const void* comp_bwd, int dtype,
+                   int B, int H, int64_t L, int D, int E, float scale, void* dk, void* dv,
+                   void* stream);
 
 /* ---------------------------------------------------------------------
  * Inference path of the 1-D SLA2 module (no-grad forward).
