@@ -231,6 +231,51 @@ def test_train_bwd_config3_full_size():
         compare_bwd(got, ref, f"h{h} ", sl)
 
 
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_bwd_prep_gradient_split_rounds_as_the_reference(dt):
+    """do_s = (do * a).to(16-bit) as the reference's split kernel rounds it: the
+    fp32 product first, then the 16-bit value.  A fused multiply-convert rounds
+    once and differs wherever the fp32 product lands on a 16-bit rounding
+    midpoint, which 16-bit do values times one fixed a hit for a few percent of
+    the entries (fp16 with a = 0.9: about 4 %).  Bit for bit against the CPU's
+    fp32 product, through the C ABI on bwd_prep's own output."""
+    from imfvideo_amd import _lib, ops
+    say("bwd_prep gradient split rounding", dt)
+    B, H, L, D = 1, 2, 256, 64
+    nb = L // 64
+    g = torch.Generator().manual_seed(11)
+    do = torch.randn(B, H, L, D, generator=g).to(dt)
+    alpha = torch.tensor([[0.9, 0.3, 0.7, 0.55], [0.123, 0.999, 0.5, 0.8]], dtype=torch.float32)
+    o_s = torch.randn(B, H, L, D, generator=g).to(dt)
+    o_l = torch.randn(B, H, L, D, generator=g).to(dt)
+    qphi = torch.softmax(torch.randn(B, H, L, D, generator=g), -1).to(dt)
+    den = torch.rand(B, H, L, generator=g) + 1.0
+    dv = lambda t: cuda(t).contiguous()
+    gdo, gos, gol, gqp, gden, gal = (dv(t) for t in (do, o_s, o_l, qphi, den, alpha))
+    dos, g16 = torch.empty_like(gdo), torch.empty_like(gdo)
+    delta = torch.empty(B, H, L, device=gdo.device)
+    srow = torch.empty_like(delta)
+    seg = torch.zeros(H, nb, device=gdo.device)
+    P = torch.empty(B, H, nb, D, D, device=gdo.device)
+    Pz = torch.empty(B, H, nb, D, device=gdo.device)
+    lib = _lib.load()
+    _lib.check(lib.sla2h_bwd_prep(
+        gdo.data_ptr(), gos.data_ptr(), gol.data_ptr(), gden.data_ptr(), gqp.data_ptr(),
+        gal.data_ptr(), gal.stride(0), ops._dtype_code(gdo), B, H, L, D, 64, dos.data_ptr(),
+        delta.data_ptr(), g16.data_ptr(), srow.data_ptr(), seg.data_ptr(), P.data_ptr(),
+        Pz.data_ptr(), ops._stream(gdo.device)), "sla2h_bwd_prep")
+    torch.cuda.synchronize()
+    a_rows = alpha[:, torch.arange(L) // 64].view(1, H, L, 1)
+    ref = (do.float() * a_rows).to(dt)  # fp32 product, then 16-bit (RNE)
+    got = dos.cpu()
+    assert torch.equal(got.view(torch.int16), ref.view(torch.int16))
+    if dt == torch.float16:
+        # the data reaches the midpoint cases the check is about: one rounding of
+        # the exact product (numpy's float64 -> float16) differs from ref there
+        exact = torch.from_numpy((do.double() * a_rows.double()).numpy().astype(np.float16))
+        assert (exact.view(torch.int16) != ref.view(torch.int16)).float().mean() > 0.005
+
+
 # ---------------------------------------------------------------------------
 # 1-D SLA2 JVP (sla2_mla_jvp): bit-exact routing, outputs against O.jvp_1d
 # ---------------------------------------------------------------------------
