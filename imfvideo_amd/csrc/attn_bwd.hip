@@ -306,8 +306,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
   constexpr int kKs = 144;
   unsigned char* kst = reinterpret_cast<unsigned char*>(&mb[0][w][0][0][0]);
 
-  // score-side operands (K, V rows) and the K^T fragments of the dq product,
-  // loaded separately: the K^T fragments are used last, by the pair product
+  // score-side operands: the K and V rows of the wave's 16 keys (the K rows
+  // also give the K^T operands of the dq product through the staging slots)
   struct Frags {
     u32x4 k[2], v[2];
   };
