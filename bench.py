@@ -458,7 +458,7 @@ def main():
     def step(ev=None):
         rec = (lambda i: ev[i].record()) if ev is not None else (lambda i: None)
         rec(0)
-        q8, qs, k8, ks, qpool, kpool_t = ops.quant_pool_qk(q, k, Np)
+        q8, qs, k8, ks, qpool, kpool_t, kb = ops.quant_pool_qk(q, k, Np, with_kb=True)
         rec(1)
         lut = ops.route_topk(qpool, kpool_t, T, 0.125)
         rec(2)
@@ -466,7 +466,7 @@ def main():
         rec(3)
         comp = ops.complement(st, lut, Np)
         rec(4)
-        o, do = ops.fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq)
+        o, do = ops.fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq, kb=kb)
         rec(5)
         return o, do
 

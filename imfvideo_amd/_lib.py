@@ -22,7 +22,7 @@ SIGNATURES = {
     "sla2h_error_string": (ctypes.c_char_p, [_c_int]),
     "sla2h_quantize": (_c_int, [_p, _c_int, _c_i64, _c_i64, _c_int, _c_int, _p, _p, _p]),
     "sla2h_quant_pool_qk": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _c_i64, _c_int, _c_int,
-                                     _c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
+                                     _c_int, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p]),
     "sla2h_route_topk": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _c_int, _c_int, _c_int,
                                   _c_f, _p, _p, _p]),
     "sla2h_linear_states": (_c_int, [_p, _p, _p, _p, _c_int, _c_int, _c_int, _c_i64, _c_int,
@@ -34,7 +34,7 @@ SIGNATURES = {
                                   _c_int, _p, _p, _p]),
     "sla2h_complement_noalloc": (_c_int, [_p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int,
                                           _c_int, _c_int, _p, _p]),
-    "sla2h_fwd_jvp": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _c_int, _p,
+    "sla2h_fwd_jvp": (_c_int, [_p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _p, _c_int, _p,
                                _c_int, _c_int, _c_int, _c_i64, _c_int, _c_int, _c_int, _c_int,
                                _c_f, _c_f, _c_int, _p, _p, _p]),
     "sla2h_pool_blocks": (_c_int, [_p, _c_int, _c_i64, _c_i64, _c_int, _c_int, _p, _c_int, _p,

@@ -49,6 +49,7 @@ struct FwdArgs {
   const unsigned char* comp;
   const float* alpha;
   const int32_t* lut;
+  const float* kb;     // per key tile: bound on ||k8_j|| ks over its rows (quant_pool), or null
   float* o;
   float* dout;
   int64_t L;
@@ -112,6 +113,8 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
   // key tiles of this query block in visiting order: (tile id, key scale)
   __shared__ int2 tiles[kMaxTiles];
   __shared__ int ragged_last;  // the partial key tile was moved to the end of the routed list
+  __shared__ float wmax[2][4];  // per wave: max kb, max ks over the block's key tiles
+  __shared__ int redo;          // a row of the static-shift pass came out below its range
 
   // With the tangent the workgroups are persistent: slot s of XCD x takes the
   // XCD's units s, s + slots, ... in turn (the dispatch order of the one-shot
@@ -204,8 +207,24 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
     // key scales of the tiles in visiting order; the barrier that publishes
     // them comes after the first key loads are issued (their latencies overlap)
     if (!S16) {
-      for (int j = tid; j < J; j += 256)
-        tiles[j].y = __builtin_bit_cast(int, a.ks[(int64_t)bh * a.Nb + tiles[j].x]);
+      float kbm = 0.f, ksm = 0.f;
+      for (int j = tid; j < J; j += 256) {
+        const int64_t ti = (int64_t)bh * a.Nb + tiles[j].x;
+        const float ksj = a.ks[ti];
+        tiles[j].y = __builtin_bit_cast(int, ksj);
+        ksm = fmaxf(ksm, ksj);
+        if (a.kb != nullptr) kbm = fmaxf(kbm, a.kb[ti]);
+      }
+#pragma unroll
+      for (int o = 32; o >= 1; o >>= 1) {
+        kbm = fmaxf(kbm, __shfl_xor(kbm, o, 64));
+        ksm = fmaxf(ksm, __shfl_xor(ksm, o, 64));
+      }
+      if (l == 0) {
+        wmax[0][w] = kbm;
+        wmax[1][w] = ksm;
+      }
+      if (tid == 0) redo = 0;
     }
     const float sq = S16 ? 1.f : a.qs[(int64_t)bh * a.Nb + m];
     // log2-domain score factor of key tile j: (sq * sk_j) * scale * log2(e)
@@ -241,26 +260,48 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
     // pair of tiles instead of eight VALU adds per sub-tile and tile).  The
     // JVP's mu = sum_k p dS stays an fp32 VALU sum: dO subtracts (mu / l) O
     // from a nearly equal term, so mu keeps the reference's unrounded t.
+    //
+    // Static shift (INT8 scores, no fp16 clamp): a per-row shift M_i at or
+    // above every score of the row, fixed before the loop, replaces the
+    // running maximum.  By Cauchy-Schwarz s_ij c_j <= ||q8_i|| qs ||k8_j|| ks_j
+    // scale log2(e) <= ||q8_i|| qs scale log2(e) max_j kb_j (kb from
+    // quant_pool).  P = 2^(s c - M_i) <= 1 then needs no maximum, no ballot and
+    // no rescale, the waves of a query block share M_i (the merge adds), and
+    // the softmax is unchanged by the choice of M_i.  The integer score needs
+    // no conversion either: the INT8 MFMA accumulates onto C = 0x4B400000, so
+    // the result read as fp32 is 1.5 * 2^23 + s exactly, and s c - M_i =
+    // fl(f c - M') with M' = fl(1.5 * 2^23 c + M_i) per tile and row, whose
+    // rounding moves a whole tile's exponent by at most ulp(M') / 2 < c.
+    // The block falls back to the exact running maximum when a score factor
+    // c exceeds 2^-9 (that shift would then reach 2^-10 log2 units), and
+    // after the pass when a row's sum l fell below 2^-64 (the bound was more
+    // than ~64 log2 units above the row's largest score).
+    constexpr bool kStatOK = !S16 && !kClampT;
+    constexpr float kMagicF = 12582912.0f;  // 1.5 * 2^23, bits 0x4B400000
+    const i32x4 kMagic4 = i32x4{0x4B400000, 0x4B400000, 0x4B400000, 0x4B400000};
     f32x4 acc_lm[kQT];
     float mu_i[kQT];
     f32x4 acc_o[4][kQT], acc_do[4][kQT];  // [ct][qt]
     float mrun[kQT], mthr[kQT];  // running maximum (uniform per query column), + kThr
     float mref[kQT];  // fp16 tangent: exact running maximum of the lane's keys
+    float mstat[kQT];  // static-shift pass: M_i of the lane's query column
     constexpr uint32_t kOne2 = T16::kDtype == SLA2H_DTYPE_F16 ? 0x3C003C00u : 0x3F803F80u;
     const u32x4 lm_a = u32x4{kOne2, kOne2, kOne2, kOne2};
+    auto init_acc = [&](bool stat) {
 #pragma unroll
-    for (int qt = 0; qt < kQT; ++qt) {
-      acc_lm[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-      mu_i[qt] = 0.f;
-      mrun[qt] = -INFINITY;
-      mthr[qt] = -INFINITY;
-      mref[qt] = -INFINITY;
+      for (int qt = 0; qt < kQT; ++qt) {
+        acc_lm[qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+        mu_i[qt] = 0.f;
+        mrun[qt] = stat ? mstat[qt] : -INFINITY;
+        mthr[qt] = -INFINITY;
+        mref[qt] = -INFINITY;
 #pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        acc_o[ct][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
-        acc_do[ct][qt] = acc_o[ct][qt];
+        for (int ct = 0; ct < 4; ++ct) {
+          acc_o[ct][qt] = f32x4{0.f, 0.f, 0.f, 0.f};
+          acc_do[ct][qt] = acc_o[ct][qt];
+        }
       }
-    }
+    };
 
     // per-lane parts of the operand offsets of key quarter kq0 (fragment-
     // ordered tiles: each load is one contiguous 1 KB per wave); the tile base
@@ -322,8 +363,9 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
     // update; returns the P^T fragments for the O^T update (two quarters share
     // one K = 32 MFMA).  MASK only for the ragged prefix tail tiles (j >= T).
     auto stage = [&](const KeyRegs& kr, const ValRegs& vr, int j, int sub, u32x2 (&pb)[kQT],
-                     u32x2* pend, auto mask_tag) {
+                     u32x2* pend, auto mask_tag, auto stat_tag) {
       constexpr bool MASK = decltype(mask_tag)::value;
+      constexpr bool STAT = decltype(stat_tag)::value && kStatOK;
       const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
       const float c = tile_c(j);
       const int64_t key0 = (int64_t)n * kTa + 16 * (kq0 + sub) + 4 * g;
@@ -340,6 +382,15 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
           s16 = mfma_16x16x32<T16>(kr.ka[1], qsh[qs0 + qt][3][l], s16);
 #pragma unroll
           for (int i = 0; i < 4; ++i) sv[qt][i] = s16[i];
+        } else if (STAT) {
+          const i32x4 si = mfma_i8_16x16x64(kr.k8, q8sh[qs0 + qt][l], kMagic4);
+          // element by element through a scalar: clang's __builtin_bit_cast of
+          // an ext-vector element expression reads element 0 whatever the index
+#pragma unroll
+          for (int i = 0; i < 4; ++i) {
+            const int bits = si[i];
+            sv[qt][i] = __builtin_bit_cast(float, bits);
+          }
         } else {
           const i32x4 si = mfma_i8_16x16x64(kr.k8, q8sh[qs0 + qt][l], i32x4{0, 0, 0, 0});
 #pragma unroll
@@ -355,25 +406,27 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
           dsv[qt] = d;
         }
       }
-      bool over = false;
+      if constexpr (!STAT) {
+        bool over = false;
 #pragma unroll
-      for (int qt = 0; qt < kQT; ++qt) {
-        float mx = -INFINITY;
+        for (int qt = 0; qt < kQT; ++qt) {
+          float mx = -INFINITY;
 #pragma unroll
-        for (int i = 0; i < 4; ++i)
-          if (!MASK || key0 + i < L) mx = fmaxf(mx, sv[qt][i]);
-        mt[qt] = mx * c;
-        over |= mt[qt] > mthr[qt];
-        if (kClampT) mref[qt] = fmaxf(mref[qt], mt[qt]);
-      }
-      if (__builtin_amdgcn_ballot_w64(over) != 0) {
+          for (int i = 0; i < 4; ++i)
+            if (!MASK || key0 + i < L) mx = fmaxf(mx, sv[qt][i]);
+          mt[qt] = mx * c;
+          over |= mt[qt] > mthr[qt];
+          if (kClampT) mref[qt] = fmaxf(mref[qt], mt[qt]);
+        }
+        if (__builtin_amdgcn_ballot_w64(over) != 0) {
 #pragma unroll
-        for (int qt = 0; qt < kQT; ++qt)
-          if (__builtin_amdgcn_ballot_w64(mt[qt] > mthr[qt]) != 0) rescale(qt, mt[qt], pend);
+          for (int qt = 0; qt < kQT; ++qt)
+            if (__builtin_amdgcn_ballot_w64(mt[qt] > mthr[qt]) != 0) rescale(qt, mt[qt], pend);
+        }
       }
       float p[kQT][4], t[kQT][4];
       auto expo = [&](int qt) {
-        const float moff = mrun[qt];
+        const float moff = STAT ? fmaf(kMagicF, c, mstat[qt]) : mrun[qt];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           float e = fmaf(sv[qt][i], c, -moff);
@@ -463,8 +516,30 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
     // while the prefetch stays in flight.
     KeyRegs ka_, kb_;
     load_keys(0, 0, ka_);
-    __syncthreads();  // key scales in tiles[].y
+    __syncthreads();  // key scales in tiles[].y, block maxima in wmax
+    // Per-block choice of the static shift (uniform): kb given, every score
+    // factor c_j <= 2^-9; M_i = ||q8_i|| qs scale log2(e) max_j kb_j.
+    bool exact = true;
+    if (kStatOK && a.kb != nullptr) {
+      const float kbm = fmaxf(fmaxf(wmax[0][0], wmax[0][1]), fmaxf(wmax[0][2], wmax[0][3]));
+      const float ksm = fmaxf(fmaxf(wmax[1][0], wmax[1][1]), fmaxf(wmax[1][2], wmax[1][3]));
+      const float cq = sq * a.c_log2;
+      exact = !(cq * ksm <= 0x1p-9f);
+#pragma unroll
+      for (int qt = 0; qt < kQT; ++qt) {
+        // ||q8_i||^2 of query column r of sub-tile qs0 + qt: 16 bytes per lane
+        // group, summed over the four groups (integers below 2^21: exact)
+        const i32x4 v = q8sh[qs0 + qt][l];
+        int n2 = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) n2 = __builtin_amdgcn_sdot4(v[e], v[e], n2, false);
+        mstat[qt] = __builtin_sqrtf(sum_over_groups((float)n2)) * cq * kbm;
+      }
+    }
+    for (;;) {  // passes: static shift, or (first or after an underflow) exact maximum
+    init_acc(!exact);
     int j = 0;
+    auto run_tiles = [&](auto stat_tag) {
     if (TAN) {
       // both quarters of the wave's key half of every tile, as one pair
       auto tile_pair = [&](int jt, auto mask_tag) {
@@ -472,10 +547,10 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
         u32x2 pa[kQT], pbb[kQT];
         load_vals(jt, 0, va);
         load_keys(jt, 1, kb_);
-        stage(ka_, va, jt, 0, pa, nullptr, mask_tag);
+        stage(ka_, va, jt, 0, pa, nullptr, mask_tag, stat_tag);
         load_vals(jt, 1, vb);
         load_keys(jt + 1 < J ? jt + 1 : J - 1, 0, ka_);
-        stage(kb_, vb, jt, 1, pbb, pa, mask_tag);
+        stage(kb_, vb, jt, 1, pbb, pa, mask_tag, stat_tag);
         o_pair(va, pa, vb, pbb);
       };
       for (; j < Tu; ++j) tile_pair(j, std::false_type{});  // routed video tiles
@@ -498,10 +573,10 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
         };
         load_v(j, 0);
         load_keys(j + 1, 0, kb_);
-        stage(ka_, ValRegs{}, j, 0, pa, nullptr, std::false_type{});
+        stage(ka_, ValRegs{}, j, 0, pa, nullptr, std::false_type{}, stat_tag);
         load_v(j + 1, 1);
         load_keys(j + 2 < J ? j + 2 : J - 1, 0, ka_);
-        stage(kb_, ValRegs{}, j + 1, 0, pbb, pa, std::false_type{});
+        stage(kb_, ValRegs{}, j + 1, 0, pbb, pa, std::false_type{}, stat_tag);
 #pragma unroll
         for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
@@ -520,13 +595,18 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
         load_vals(j, 0, vr);
         load_keys(j + 1 < J ? j + 1 : J - 1, 0, kb_);
         if (j < Tu)
-          stage(ka_, vr, j, 0, pb, nullptr, std::false_type{});
+          stage(ka_, vr, j, 0, pb, nullptr, std::false_type{}, stat_tag);
         else
-          stage(ka_, vr, j, 0, pb, nullptr, std::true_type{});
+          stage(ka_, vr, j, 0, pb, nullptr, std::true_type{}, stat_tag);
         o_single(vr, pb);
         ka_ = kb_;
       }
     }
+    };
+    if (!kStatOK || exact)
+      run_tiles(std::false_type{});
+    else
+      run_tiles(std::true_type{});
     // Lane indices for the merge and epilogue, re-derived from vtoff (live
     // through the key loop anyway; the empty asm keeps the compiler from
     // folding it back): l, r and g themselves then need no register across
@@ -611,6 +691,9 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
         ltot += stat[1][w0 + ww][qsel][r] * f;
         mutot += stat[2][w0 + ww][qsel][r] * f;
       }
+      // static shift: a row sum below 2^-64 sends the block to the exact pass
+      // (read after the merge's barriers below)
+      if (!exact && !(ltot >= 0x1p-64f)) redo = 1;
 
       f32x4 O[kNcc], DO[kNcc];
       if (TAN) {
@@ -655,6 +738,12 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
           }
           if (rd == 0) __syncthreads();
         }
+      }
+
+      if (!exact && redo != 0) {  // uniform: written before the merge's barriers
+        exact = true;
+        load_keys(0, 0, ka_);
+        continue;
       }
 
       // ---- Hc (dHc) as bf16 hi/lo A-operand fragments in LDS, in the
@@ -828,6 +917,8 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
         }
       }
     }
+    break;
+    }  // pass loop
     if (!TAN) break;
   }  // unit loop
 }
@@ -875,7 +966,7 @@ using namespace sla2h;
 
 extern "C" int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, const void* vt,
                              const int8_t* q8, const int8_t* k8,
-                             const float* qs, const float* ks, const void* comp,
+                             const float* qs, const float* ks, const float* kb, const void* comp,
                              const float* alpha, int alpha_stride, const int32_t* lut, int dtype,
                              int B, int H, int64_t L, int D, int E, int Np, int T, float scale,
                              float eps_l, int flags, float* o, float* dout, void* stream) {
@@ -904,6 +995,7 @@ extern "C" int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, cons
   a.k8 = k8;
   a.qs = qs;
   a.ks = ks;
+  a.kb = kb;
   a.comp = static_cast<const unsigned char*>(comp);
   a.alpha = alpha;
   a.lut = lut;

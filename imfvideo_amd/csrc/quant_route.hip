@@ -25,6 +25,7 @@ struct QuantPoolArgs {
   int npool[2];           // number of leading blocks to pool
   int64_t pool_len[2];    // rows that count for pooling (L for q, Np*E for k)
   int transposed[2];
+  float* kb[2];           // (BH, Nb) or null: bound on the tile's dequantised row norms
   int BH;
   int64_t L;
   int Nb;
@@ -72,6 +73,7 @@ template <typename T16>
 __global__ __launch_bounds__(256) void quant_pool_kernel(QuantPoolArgs a, int ntiles) {
   __shared__ __align__(16) uint16_t tile[2][kTile][kTile];
   __shared__ float red[2][4];
+  __shared__ float rnorm[2][4];
   __shared__ float vec[2][kTile];
 
   const int tid = threadIdx.x;
@@ -113,6 +115,16 @@ __global__ __launch_bounds__(256) void quant_pool_kernel(QuantPoolArgs a, int nt
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) am = fmaxf(am, __shfl_xor(am, m, 64));
     if ((tid & 63) == 0) red[buf][tid >> 6] = am;
+    // largest squared row norm of the tile (the bound below needs no exact
+    // sum: rounding only moves a softmax shift)
+    float ss = 0.f;
+#pragma unroll
+    for (int k = 0; k < 16; ++k) ss = __builtin_fmaf(xv[k], xv[k], ss);
+    ss = ss + __shfl_xor(ss, 1, 64);
+    ss = ss + __shfl_xor(ss, 2, 64);
+#pragma unroll
+    for (int m = 4; m <= 32; m <<= 1) ss = fmaxf(ss, __shfl_xor(ss, m, 64));
+    if ((tid & 63) == 0) rnorm[buf][tid >> 6] = ss;
     const bool pooled = a.pool[t] != nullptr && blk < a.npool[t];
     if (pooled) {
       *reinterpret_cast<uint4*>(&tile[buf][r][c0]) = u[0];
@@ -139,6 +151,12 @@ __global__ __launch_bounds__(256) void quant_pool_kernel(QuantPoolArgs a, int nt
       *reinterpret_cast<uint4*>(a.xq[t] + ((int64_t)bh * a.L + row) * kTile + c0) =
           make_uint4(w[0], w[1], w[2], w[3]);
     if (tid == 0) a.xs[t][(int64_t)bh * a.Nb + blk] = s;
+    // kb >= max_j ||x8_j|| s over the tile's rows: each element of x8 s is
+    // within s / 2 of x, so ||x8_j s - x_j|| <= 4 s over 64 channels
+    if (tid == 0 && a.kb[t] != nullptr) {
+      const float mx = fmaxf(fmaxf(rnorm[buf][0], rnorm[buf][1]), fmaxf(rnorm[buf][2], rnorm[buf][3]));
+      a.kb[t][(int64_t)bh * a.Nb + blk] = __builtin_sqrtf(mx) * 1.000001f + 4.f * s;
+    }
 
     // ---- pooling (wave 0): sequential per-channel fp32 sum over the real rows ----
     if (pooled && tid < kTile) {
@@ -814,7 +832,8 @@ extern "C" int sla2h_quantize(const void* x, int dtype, int64_t BH, int64_t L, i
 extern "C" int sla2h_quant_pool_qk(const void* q, const void* k, int dtype, int B, int H,
                                    int64_t L, int D, int E, int Np, const float* proj_q,
                                    const float* proj_k, int8_t* q8, float* qs, int8_t* k8,
-                                   float* ks, float* qpool, float* kpool_t, void* stream) {
+                                   float* ks, float* qpool, float* kpool_t, float* kbound,
+                                   void* stream) {
   SLA2H_CHECK_ARG(q && k && q8 && qs && k8 && ks && qpool && kpool_t);
   SLA2H_CHECK_ARG(D == kTile && E == kTile);
   SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
@@ -840,6 +859,7 @@ extern "C" int sla2h_quant_pool_qk(const void* q, const void* k, int dtype, int 
   a.pool_len[1] = (int64_t)Np * E;
   a.transposed[0] = 0;
   a.transposed[1] = 1;
+  a.kb[1] = kbound;
   return launch_quant_pool(a, 2, dtype, static_cast<hipStream_t>(stream));
 }
 

@@ -77,10 +77,12 @@ def quantize(x, E=E_TILE):
     return xq, xs
 
 
-def quant_pool_qk(q, k, Np, E=E_TILE, proj_q=None, proj_k=None):
+def quant_pool_qk(q, k, Np, E=E_TILE, proj_q=None, proj_k=None, with_kb=False):
     """INT8 Q/K with per-block scales plus the router's pooled (projected) tiles.
 
-    Returns q8, qs, k8, ks, qpool (B,H,Nb,D) fp32, kpool_t (B,H,D,Np) fp32.
+    Returns q8, qs, k8, ks, qpool (B,H,Nb,D) fp32, kpool_t (B,H,D,Np) fp32,
+    and with with_kb also kb (B,H,Nb) fp32: per key block a bound on
+    max ||k8_j|| * ks over its rows (the static softmax shift of fwd_jvp).
     """
     _need_gpu(q, k)
     q, k = _bhld(q, "q"), _bhld(k, "k")
@@ -97,10 +99,13 @@ def quant_pool_qk(q, k, Np, E=E_TILE, proj_q=None, proj_k=None):
     ks = torch.empty_like(qs)
     qpool = torch.empty(B, H, nb, D, device=dev, dtype=torch.float32)
     kpool_t = torch.empty(B, H, D, Np, device=dev, dtype=torch.float32)
+    kb = torch.empty(B, H, nb, device=dev, dtype=torch.float32) if with_kb else None
     _lib.check(_lib.load().sla2h_quant_pool_qk(
         q.data_ptr(), k.data_ptr(), _dtype_code(q), B, H, L, D, E, Np,
         _ptr(pq), _ptr(pk), q8.data_ptr(), qs.data_ptr(), k8.data_ptr(), ks.data_ptr(),
-        qpool.data_ptr(), kpool_t.data_ptr(), _stream(dev)), "sla2h_quant_pool_qk")
+        qpool.data_ptr(), kpool_t.data_ptr(), _ptr(kb), _stream(dev)), "sla2h_quant_pool_qk")
+    if with_kb:
+        return q8, qs, k8, ks, qpool, kpool_t, kb
     return q8, qs, k8, ks, qpool, kpool_t
 
 
@@ -191,11 +196,13 @@ def complement(st, lut, Np, noalloc=False):
 
 
 def fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq=None, scale=None, eps_l=1e-5,
-            sparse_only=False):
+            sparse_only=False, kb=None):
     """The fused sparse+linear op (and JVP when dq is given) -> (o, do|None) fp32.
 
     The key side comes from k8/ks and the operand tiles of `st`
-    (linear_states with tangents when dq is given).
+    (linear_states with tangents when dq is given).  kb (quant_pool_qk's
+    with_kb output) enables the static softmax shift; None keeps the running
+    maximum everywhere.
     """
     _need_gpu(q, dq, alpha, lut)
     B, H, L, D = q.shape
@@ -212,7 +219,7 @@ def fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq=None, scale=None, ep
     _lib.check(_lib.load().sla2h_fwd_jvp(
         q.data_ptr(), _ptr(dq), _ptr(st.get("kt")) if tan else None, st["vt"].data_ptr(),
         q8.data_ptr(), k8.data_ptr(), qs.data_ptr(),
-        ks.data_ptr(), _ptr(comp), _ptr(alpha), 0 if alpha is None else alpha.stride(0),
+        ks.data_ptr(), _ptr(kb), _ptr(comp), _ptr(alpha), 0 if alpha is None else alpha.stride(0),
         lut.contiguous().data_ptr(), _dtype_code(q), B, H, L, D, E_TILE, Np, T, float(scale),
         float(eps_l), 1 if sparse_only else 0, o.data_ptr(), _ptr(do), _stream(q.device)),
         "sla2h_fwd_jvp")
@@ -235,7 +242,7 @@ def cube_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, Np, prefix_len=0, proj_q=Non
     tan = dq is not None
     if tan:
         dq, dk, dv = (t.to(q.dtype).contiguous() for t in (dq, dk, dv))
-    q8, qs, k8, ks, qpool, kpool_t = quant_pool_qk(q, k, Np, E, proj_q, proj_k)
+    q8, qs, k8, ks, qpool, kpool_t, kb = quant_pool_qk(q, k, Np, E, proj_q, proj_k, with_kb=True)
     if lut is None:
         T = topk_count(topk_frac, Np)
         lut = route_topk(qpool, kpool_t, T, D ** -0.5)
@@ -244,9 +251,9 @@ def cube_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, Np, prefix_len=0, proj_q=Non
         T = lut.shape[-1]
     st = linear_states(k, v, Np, dk if tan else None, dv if tan else None, E, with_sums=False)
     comp = complement(st, lut, Np)
-    o, do = fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq if tan else None)
+    o, do = fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq if tan else None, kb=kb)
     if return_aux:
-        aux = dict(q8=q8, qs=qs, k8=k8, ks=ks, qpool=qpool, kpool_t=kpool_t, lut=lut, T=T,
+        aux = dict(q8=q8, qs=qs, k8=k8, ks=ks, kb=kb, qpool=qpool, kpool_t=kpool_t, lut=lut, T=T,
                    comp=comp, **st)
         return o, do, aux
     return o, do

@@ -95,9 +95,9 @@ def _sparse_primal_only(q, k, v, lut, T, Np, E, prefix_len):
     dt = _c16(q).dtype
     qc, kc, vc = (_c16(t, dt) for t in (q, k, v))
     lut = lut.to(torch.int32).contiguous()
-    q8, qs, k8, ks, _, _ = ops.quant_pool_qk(qc, kc, Np, E)
+    q8, qs, k8, ks, _, _, kb = ops.quant_pool_qk(qc, kc, Np, E, with_kb=True)
     st = ops.linear_states(kc, vc, Np)
-    o, _ = ops.fwd_jvp(qc, q8, k8, qs, ks, st, None, None, lut, Np, sparse_only=True)
+    o, _ = ops.fwd_jvp(qc, q8, k8, qs, ks, st, None, None, lut, Np, sparse_only=True, kb=kb)
     return o
 
 

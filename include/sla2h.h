@@ -57,6 +57,10 @@ int sla2h_quantize(const void* x, int dtype, int64_t BH, int64_t L, int D, int E
  *   kpool_t (B,H,D,Np) fp32: the same for the Np video tiles of k, stored
  *     transposed (channel-major) for the router's coalesced score loop.
  *   proj_q / proj_k: (D,D) fp32 or NULL (identity).
+ *   kbound (B,H,Nb) fp32 or NULL: per key block an upper bound on
+ *     max_j ||k8_j|| * ks over its rows (sqrt of the largest fp32 row sum of
+ *     squares of k, plus 4 ks for the int8 rounding), the input of the
+ *     static softmax shift of sla2h_fwd_jvp.
  * Replaces the quantize_qkv(Q), quantize_qkv(K) calls of
  * sla2_cube_qat_jvp_fused (models/sla2_cube_qat.py:629-631) and the
  * _route_pool_kernel launches + projections of route_tiles_fast
@@ -66,7 +70,7 @@ int sla2h_quant_pool_qk(const void* q, const void* k, int dtype, int B, int H,
                         int64_t L, int D, int E, int Np,
                         const float* proj_q, const float* proj_k,
                         int8_t* q8, float* qs, int8_t* k8, float* ks,
-                        float* qpool, float* kpool_t, void* stream);
+                        float* qpool, float* kpool_t, float* kbound, void* stream);
 
 /*
  * Block router: scores pc[m,n] = (sum_d qpool[m,d]*kpool[n,d]) * scale
@@ -159,13 +163,19 @@ int sla2h_complement_noalloc(const float* Hb, const float* dHb, const float* zb,
  *   vt, kt = the operand tiles of sla2h_linear_states (tangent layouts and kt
  *   required when dq is given).
  *   comp = sla2h_complement records (unused with SLA2H_FLAG_SPARSE_ONLY).
+ *   kb = the kbound output of sla2h_quant_pool_qk, or NULL.  Given kb, a query
+ *     block whose score factors qs*ks*scale*log2(e) stay <= 2^-9 runs with a
+ *     fixed per-row softmax shift (a Cauchy-Schwarz bound on the row's
+ *     scores) instead of a running maximum, and falls back to the running
+ *     maximum when a row's sum lands below 2^-64; the softmax is the same up
+ *     to fp32 and 16-bit rounding.
  * Replaces _cube_fused_jvp_kernel (models/sla2_cube_qat.py:448-602) and,
  * with SLA2H_FLAG_SPARSE_ONLY, _sla2_cube_jvp_qat_kernel's sparse branch
  * (models/sla2_cube_qat.py:59-169, 172-207).
  */
 int sla2h_fwd_jvp(const void* q, const void* dq, const void* kt, const void* vt,
                   const int8_t* q8, const int8_t* k8,
-                  const float* qs, const float* ks, const void* comp,
+                  const float* qs, const float* ks, const float* kb, const void* comp,
                   const float* alpha, int alpha_stride, const int32_t* lut,
                   int dtype, int B, int H, int64_t L, int D, int E, int Np, int T,
                   float scale, float eps_l, int flags,

@@ -39,9 +39,9 @@ def test_invalid_arguments_are_rejected_before_any_launch():
     assert lib.sla2h_quantize(1, 7, 1, 64, 64, 64, 1, 1, None) == bad       # dtype
     assert lib.sla2h_route_topk(1, 1, 1, 1, 4, 5000, 64, 3, 0.125, 1, None, None) == bad  # Np
     assert lib.sla2h_route_topk(1, 1, 1, 1, 4, 8, 64, 9, 0.125, 1, None, None) == bad     # T > Np
-    # q, dq, kt(NULL), vt, q8, k8, qs, ks, comp, alpha, alpha_stride, lut, dtype, B, H, L,
+    # q, dq, kt(NULL), vt, q8, k8, qs, ks, kb, comp, alpha, alpha_stride, lut, dtype, B, H, L,
     # D, E, Np, T, scale, eps_l, flags, o, dout, stream: dq without the key operand tiles
-    assert lib.sla2h_fwd_jvp(1, 1, None, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 1, 128, 64,
+    assert lib.sla2h_fwd_jvp(1, 1, None, 1, 1, 1, 1, 1, None, 1, 1, 1, 1, 1, 1, 1, 128, 64,
                              64, 2, 1, 0.125, 1e-5, 0, 1, 1, None) == bad
     assert lib.sla2h_linear_states(1, None, 1, None, 1, 1, 1, 100, 64, 64, 3, 1, None, 1, None,
                                    1, None, 1, None, 1, None, None) == bad  # Np > ceil(L/E)
