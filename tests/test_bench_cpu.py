@@ -1,6 +1,7 @@
 """CPU checks of bench.py's reporting helpers (no GPU): the algorithmic work
 behind roofline.achieved, the staleness guard of the committed HBM-traffic
 record, and the one-GPU contract."""
+import hashlib
 import json
 import os
 import shutil
@@ -29,7 +30,10 @@ def test_measured_traffic_only_for_the_measured_source(tmp_path, monkeypatch):
     rec_path = os.path.join(ROOT, "profiles", "fwd_jvp_config3_traffic.json")
     with open(rec_path) as f:
         rec = json.load(f)
-    assert bench.measured_traffic(3, True) == rec["bytes_per_launch"]
+    with open(os.path.join(ROOT, rec["source"]), "rb") as f:
+        current = hashlib.sha256(f.read()).hexdigest() == rec["source_sha256"]
+    # the figure is reported exactly while the record matches the kernel source
+    assert bench.measured_traffic(3, True) == (rec["bytes_per_launch"] if current else None)
     assert bench.measured_traffic(2, False) is None
     assert bench.measured_traffic(3, False) is None
     # the same record next to an edited kernel source is stale: no figure
