@@ -91,14 +91,33 @@ def hbm_bytes(B, H, N, Np, tangent):
     return quant, states, layout
 
 
+PROBE_SRC = os.path.join(ROOT, "bench_stream_probe.hip")
+PROBE_LIB = os.path.join(ROOT, "bench_stream_probe.so")
+
+
+def build_probe():
+    """Compile the streaming-ceiling kernel (measurement only, not part of the
+    product library) into bench_stream_probe.so for gfx950."""
+    import subprocess
+    from imfvideo_amd import build as _b
+    tmp = PROBE_LIB + ".tmp"
+    res = subprocess.run([_b.hipcc(), *_b.COMMON_FLAGS, "-shared", PROBE_SRC, "-o", tmp],
+                         stdout=subprocess.PIPE, stderr=subprocess.STDOUT, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"building {PROBE_SRC} failed:\n{res.stdout}")
+    os.replace(tmp, PROBE_LIB)
+    return PROBE_LIB
+
+
 def stream_ceiling(read_bytes, write_bytes):
     """Fastest time for the same read / write byte counts with a plain
-    streaming kernel (libsla2probe.so: 16 B per lane, nontemporal, grid-stride;
+    streaming kernel (bench_stream_probe.so: 16 B per lane, nontemporal, grid-stride;
     best of two grids and five runs), after a 1 GiB write that flushes L2 and
     the 256 MB MALL ('flushed') and with the inputs just read ('resident')."""
     import ctypes
-    from imfvideo_amd import build as _b
-    lib = ctypes.CDLL(_b.PROBE_LIB)
+    if not os.path.exists(PROBE_LIB):
+        build_probe()
+    lib = ctypes.CDLL(PROBE_LIB)
     lib.sla2h_probe_stream.argtypes = [ctypes.c_void_p] * 3 + [ctypes.c_int64] + [ctypes.c_int] * 3 + [ctypes.c_void_p]
     if write_bytes == 0:
         rd, wr = 1, 0
@@ -408,7 +427,7 @@ def main():
     ap.add_argument("--op-only", action="store_true",
                     help="Config 5: time the attention op's training step instead of the blocks")
     ap.add_argument("--hbm-ceiling", action="store_true",
-                    help="print only the streaming ceilings (libsla2probe.so) for the read:write "
+                    help="print only the streaming ceilings (bench_stream_probe.so) for the read:write "
                          "mixes and byte counts of quant_pool and linear_states, one JSON line")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 256 MiB fp32 copy kernel (torch.mul by 1) three times: "
@@ -464,9 +483,10 @@ def main():
         rec(2)
         st = ops.linear_states(k, v, Np, dk, dv, with_sums=False)
         rec(3)
-        comp = ops.complement(st, lut, Np)
+        comp = ops.complement(st, lut, Np, check_ids=False)
         rec(4)
-        o, do = ops.fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq, kb=kb)
+        o, do = ops.fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq, kb=kb,
+                            check_ids=False)
         rec(5)
         return o, do
 

@@ -4,7 +4,8 @@
 // loads and stores), i.e. the fastest data movement of a given read/write
 // mix and byte count on this device.  bench.py times it at the byte counts
 // and read/write mixes of quant_pool and linear_states.  Measurement only:
-// built into its own library, not part of the path.
+// bench.py builds it into its own library (bench_stream_probe.so), apart
+// from the product library.
 #include <hip/hip_runtime.h>
 
 #include <cstdint>

@@ -16,9 +16,6 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 CSRC = os.path.join(HERE, "csrc")
 BUILD = os.path.join(HERE, "_build")
 LIB = os.path.join(HERE, "libsla2hip.so")
-# measurement-only streaming kernel timed by bench.py (not part of the path)
-PROBE_SRC = os.path.join(CSRC, "probe", "stream_ceiling.hip")
-PROBE_LIB = os.path.join(HERE, "libsla2probe.so")
 ARCH = os.environ.get("SLA2H_ARCH", "gfx950")
 
 SOURCES = {
@@ -65,8 +62,7 @@ def _run(cmd):
 
 
 def build(verbose=False):
-    """Compile every HIP source for gfx950 and link libsla2hip.so (and the
-    measurement library libsla2probe.so); returns the path of libsla2hip.so."""
+    """Compile every HIP source for gfx950 and link libsla2hip.so; returns its path."""
     cc = hipcc()
     os.makedirs(BUILD, exist_ok=True)
     objs = []
@@ -80,9 +76,6 @@ def build(verbose=False):
     tmp = LIB + ".tmp"
     _run([cc, f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp])
     os.replace(tmp, LIB)
-    tmp = PROBE_LIB + ".tmp"
-    _run([cc, *COMMON_FLAGS, "-shared", PROBE_SRC, "-o", tmp])
-    os.replace(tmp, PROBE_LIB)
     return LIB
 
 

@@ -64,13 +64,20 @@ def _to16(x):
 def route_tiles_fast(q, k, topk_frac, Np, E, prefix_len, proj_q=None, proj_k=None):
     """Hard top-k router on pooled tiles (reference :532-566).
 
-    q, k: (B, H, L, D) 16-bit tile-major.  Returns (lut (B,H,Mb,T) int32, T).
-    Rows of the LUT are ordered by descending score (the reference returns
-    them unordered, ``torch.topk(sorted=False)``).
+    q, k: (B, H, L, D) tile-major, 16-bit or fp32 (fp32 is pooled as given,
+    unrounded).  Returns (lut (B,H,Mb,T) int32, T).  Rows of the LUT are
+    ordered by descending score (the reference returns them unordered,
+    ``torch.topk(sorted=False)``).
     """
     B, H, L, D = q.shape
-    q, k = _to16(q), _to16(k)
-    _, _, _, _, qpool, kpool_t = ops.quant_pool_qk(q, k.to(q.dtype), Np, E, proj_q, proj_k)
+    if q.dtype == torch.float32 and k.dtype == torch.float32:
+        # the same pooling law (sequential fp32 row sums, / count, projection
+        # as a sequential dot) on the unrounded inputs
+        qpool = ops.pool_blocks(q, E, proj_q)
+        kpool_t = ops.pool_blocks(k[:, :, :Np * E].contiguous(), E, proj_k, transposed=True)
+    else:
+        q, k = _to16(q), _to16(k)
+        _, _, _, _, qpool, kpool_t = ops.quant_pool_qk(q, k.to(q.dtype), Np, E, proj_q, proj_k)
     T = ops.topk_count(topk_frac, Np)
     lut = ops.route_topk(qpool, kpool_t, T, D ** -0.5)
     return lut, T
@@ -90,6 +97,22 @@ def route_tiles(q, k, topk_frac, Np, E, prefix_len, proj_q=None, proj_k=None):
 # ---------------------------------------------------------------------------
 # The non-QAT cube JVP (16-bit primal scores) on the gfx950 kernels.
 # ---------------------------------------------------------------------------
+def alpha_blocks(alpha, H, Np, Mb, device, dtype=torch.float32, detach=True):
+    """Per-query-block mix ratios (H, Mb) fp32 from either form the callers use:
+    (H, Mb) as given, or the reference's (H, Np + 1) -- one column per video
+    tile and one shared by the whole prefix (its repeat_interleave of
+    [E] * Np + [P], models/mla_video_sparse_jvp.py) -- whose last column covers
+    every prefix block when the prefix spans more than one."""
+    a = (alpha.detach() if detach else alpha).to(device, dtype)
+    if a.dim() != 2 or a.shape[0] != H:
+        raise ValueError(f"alpha: expected (H, Mb) or (H, Np + 1), got {tuple(a.shape)}")
+    if a.shape[1] == Mb:
+        return a
+    if a.shape[1] == Np + 1 and Mb > Np:
+        return torch.cat([a[:, :Np], a[:, Np:].expand(H, Mb - Np)], dim=1)
+    raise ValueError(f"alpha: expected (H, {Mb}) or (H, {Np + 1}), got {tuple(a.shape)}")
+
+
 def mla_video_sparse_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, Np, E, prefix_len,
                          proj_q=None, proj_k=None, lut=None, T=None, block_m=64):
     """Cube-tile SLA2 attention and its forward-mode tangent, 16-bit scores.
@@ -102,8 +125,10 @@ def mla_video_sparse_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, Np, E, prefix_le
 
     Args:
         q, k, v, dq, dk, dv: (B, H, L, 64) primal and tangent.  fp16 and bf16
-            keep their type; fp32 is rounded to fp16 (the reference's fp32
-            mode uses IEEE fp32 dots; here it has the fp16 mode's precision).
+            keep their type; fp32 inputs are routed as given but computed in
+            fp16 (the reference's fp32 mode uses IEEE fp32 dots and meets
+            o 2e-4 / do 2e-3 against the dense fp32 JVP; here fp32 inputs get
+            the fp16 mode's precision, o ~1e-2).
         alpha: (H, Mb) mix after the sigmoid, or a scalar.
         topk_frac: routed fraction of the video tiles (unused with lut).
         Np, E, prefix_len: tiling geometry; E must be 64.
@@ -125,10 +150,15 @@ def mla_video_sparse_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, Np, E, prefix_le
     dt = q.dtype if q.dtype in (torch.float16, torch.bfloat16) else torch.float16
     qc, kc, vc, dqc, dkc, dvc = (t.to(dt).contiguous() for t in (q, k, v, dq, dk, dv))
     if lut is None:
-        lut, T = route_tiles(qc, kc, topk_frac, Np, E, prefix_len, proj_q, proj_k)
+        # routed on the inputs as given (fp32 unrounded), as the reference does
+        lut, T = route_tiles(q.contiguous(), k.to(q.dtype).contiguous(), topk_frac, Np, E,
+                             prefix_len, proj_q, proj_k)
+    else:
+        lut = lut.to(device=q.device, dtype=torch.int32).contiguous()
+        ops.check_lut_ids(lut, Np)
     Mb = -(-L // E)
     if torch.is_tensor(alpha) and alpha.dim() == 2:
-        a = alpha.detach().to(q.device, torch.float32)
+        a = alpha_blocks(alpha, H, Np, Mb, q.device)
     else:
         a = torch.full((H, Mb), float(alpha), device=q.device, dtype=torch.float32)
     return ops.cube_jvp16(qc, kc, vc, dqc, dkc, dvc, a, lut.to(q.device), Np)
@@ -230,7 +260,8 @@ def mvs_dense_ref(q, k, v, alpha, lut, Np, E, prefix_len):
     columns outside the mask, normalised by its row sum + 1e-5; mixed by
     alpha (H, Mb), one value per query block.
 
-    Args: q, k, v (B, H, L, D) fp32 tile-major; alpha (H, Mb); lut
+    Args: q, k, v (B, H, L, D) fp32 tile-major; alpha (H, Mb) or the
+    reference's (H, Np + 1) (see alpha_blocks); lut
     (B, H, Mb, T); Np, E, prefix_len.  Returns o (B, H, L, D) fp32.
     """
     B, H, L, D = q.shape
@@ -250,5 +281,6 @@ def mvs_dense_ref(q, k, v, alpha, lut, Np, E, prefix_len):
     keep[..., Np * E:] = 0.0
     w = w * keep
     o_l = (w @ v) / (w.sum(dim=-1, keepdim=True) + _EPS_L)
-    a = alpha.to(dev)[:, rows_of].reshape(1, H, L, 1)
+    a = alpha_blocks(alpha, H, Np, Mb, dev, dtype=q.dtype, detach=False)[:, rows_of].reshape(
+        1, H, L, 1)
     return a * o_s + (1.0 - a) * o_l

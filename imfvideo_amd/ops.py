@@ -53,6 +53,20 @@ def _check_lut(lut, B, H, L):
         raise ValueError(f"lut: expected (B, H, Mb, T) = ({B}, {H}, {Mb}, T), got {tuple(lut.shape)}")
 
 
+def check_lut_ids(lut, Np):
+    """Raise ValueError unless every routed tile id of `lut` lies in [0, Np).
+
+    The kernels take the ids as given (the fused kernel clamps them into range,
+    the complement skips them), so a caller-supplied LUT holding -1 padding or
+    a prefix-tail id would otherwise return wrong numbers.  One reduction and
+    a device-to-host read: used on LUTs from outside, not on route_topk's."""
+    if lut.numel() == 0:
+        return
+    lo, hi = int(lut.min().item()), int(lut.max().item())
+    if lo < 0 or hi >= Np:
+        raise ValueError(f"lut: tile ids must lie in [0, {Np}), got min {lo} max {hi}")
+
+
 def _alpha_rows(alpha, H, Mb, device):
     """(H, Mb) fp32 with unit column stride (the kernels read alpha[h * stride + m])."""
     alpha = alpha.detach().to(device, torch.float32)
@@ -168,13 +182,17 @@ def linear_states(k, v, Np, dk=None, dv=None, E=E_TILE, with_sums=True):
 COMPLEMENT_SCRATCH_BYTES = 4 << 20  # SLA2H_COMPLEMENT_SCRATCH_BYTES
 
 
-def complement(st, lut, Np, noalloc=False):
+def complement(st, lut, Np, noalloc=False, check_ids=True):
     """Per-query-block complement records (uint8 (B,H,Mb,REC_BYTES)).
 
     noalloc: run sla2h_complement_noalloc, whose bit-mask workspace is the
     library's static per-GPU array (at most COMPLEMENT_SCRATCH_BYTES) instead
-    of a torch allocation; concurrent calls on one GPU must not overlap."""
+    of a torch allocation; concurrent calls on one GPU must not overlap.
+    check_ids: validate the LUT's tile ids (check_lut_ids); False for a LUT
+    straight from route_topk."""
     B, H, Mb, T = lut.shape
+    if check_ids:
+        check_lut_ids(lut, Np)
     lib = _lib.load()
     comp = torch.empty(B, H, Mb, REC_BYTES, device=lut.device, dtype=torch.uint8)
     g = lambda n: _ptr(st.get(n))
@@ -196,15 +214,18 @@ def complement(st, lut, Np, noalloc=False):
 
 
 def fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq=None, scale=None, eps_l=1e-5,
-            sparse_only=False, kb=None):
+            sparse_only=False, kb=None, check_ids=True):
     """The fused sparse+linear op (and JVP when dq is given) -> (o, do|None) fp32.
 
     The key side comes from k8/ks and the operand tiles of `st`
     (linear_states with tangents when dq is given).  kb (quant_pool_qk's
     with_kb output) enables the static softmax shift; None keeps the running
-    maximum everywhere.
+    maximum everywhere.  check_ids validates the LUT's tile ids
+    (check_lut_ids); False for a LUT straight from route_topk.
     """
     _need_gpu(q, dq, alpha, lut)
+    if check_ids:
+        check_lut_ids(lut, Np)
     B, H, L, D = q.shape
     T = lut.shape[-1]
     tan = dq is not None
@@ -249,9 +270,11 @@ def cube_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, Np, prefix_len=0, proj_q=Non
     else:
         lut = lut.to(torch.int32).contiguous()
         T = lut.shape[-1]
+        check_lut_ids(lut, Np)
     st = linear_states(k, v, Np, dk if tan else None, dv if tan else None, E, with_sums=False)
-    comp = complement(st, lut, Np)
-    o, do = fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq if tan else None, kb=kb)
+    comp = complement(st, lut, Np, check_ids=False)
+    o, do = fwd_jvp(q, q8, k8, qs, ks, st, comp, alpha, lut, Np, dq if tan else None, kb=kb,
+                    check_ids=False)
     if return_aux:
         aux = dict(q8=q8, qs=qs, k8=k8, ks=ks, kb=kb, qpool=qpool, kpool_t=kpool_t, lut=lut, T=T,
                    comp=comp, **st)
@@ -377,7 +400,7 @@ def train_fwd(q, k, v, alpha, lut, Np, eps_l=1e-5, int8=True):
     else:
         st = linear_states_qat(k, v, with_vt=True)
         o_s, lse, qphi = sparse_fwd_16(q, k, st["vt"], lut_aug, E_TILE)
-    comp = complement(st, lut_aug, nb)
+    comp = complement(st, lut_aug, nb, check_ids=False)
     o, o_l, den = linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha, eps_l)
     htot = st["Hall"].to(q.dtype).float()
     return dict(o=o, o_s=o_s, o_l=o_l, lse=lse, den=den, qphi=qphi, htot=htot,
@@ -493,7 +516,7 @@ def jvp_1d(q, k, v, dq, dk, dv, alpha, lut, bq, scale=None, eps_l=1e-5, return_a
     alpha = _alpha_rows(alpha, H, mq, q.device)
     scale = D ** -0.5 if scale is None else scale
     st = linear_states(k, v, nb, dk, dv, with_sums=False)
-    comp = complement(st, lut, nb)
+    comp = complement(st, lut, nb, check_ids=False)
     o = torch.empty(B, H, L, D, device=q.device, dtype=torch.float32)
     do = torch.empty_like(o)
     _lib.check(_lib.load().sla2h_fwd_jvp_1d(
@@ -544,7 +567,7 @@ def cube_jvp16(q, k, v, dq, dk, dv, alpha, lut, Np, scale=None, eps_l=1e-5):
     alpha = _alpha_rows(alpha, H, nb, q.device)
     scale = D ** -0.5 if scale is None else scale
     st = linear_states(k, v, Np, dk, dv, with_sums=False)
-    comp = complement(st, lut, Np)
+    comp = complement(st, lut, Np, check_ids=False)
     lut_aug = augment_lut(lut, Np, nb - Np)
     o = torch.empty(B, H, L, D, device=q.device, dtype=torch.float32)
     do = torch.empty_like(o)
@@ -580,7 +603,7 @@ def train_fwd_1d(q, k, v, alpha, lut, bq, eps_l=1e-5, int8=False):
                                          qz["v8f"], qz["vs"], lut, bq)
     else:
         o_s, lse, qphi = sparse_fwd_16(q, k, st["vt"], lut, bq)
-    comp = complement(st, lut, nb)
+    comp = complement(st, lut, nb, check_ids=False)
     o, o_l, den = linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha, eps_l, bq=bq)
     return dict(o=o, o_s=o_s, o_l=o_l, lse=lse, den=den, qphi=qphi,
                 htot=st["Hall"].to(q.dtype).float(), ztot=st["zall"], Hall=st["Hall"], comp=comp,
@@ -698,7 +721,7 @@ def sla2_infer(q, k, v, alpha, lut, bq, use_int8=True, qblock=None, eps_l=1e-5,
         o_s, lse, qphi = sparse_fwd_int8(q, q8, qs, qb, k8, ks, v8f, vs, lut, bq)
     else:
         o_s, lse, qphi = sparse_fwd_16(q, k, st["vt"], lut, bq)
-    comp = complement(st, lut, nb)
+    comp = complement(st, lut, nb, check_ids=False)
     o = lin_fwd3(qphi, comp, o_s, alpha, bq, eps_l)
     if return_parts:
         return o, dict(o_s=o_s, lse=lse, qphi=qphi, comp=comp, **st)

@@ -69,6 +69,9 @@ def sla2_mla_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, bq, bk, lut=None, T=None
     qc, kc, vc, dqc, dkc, dvc = (t.to(dt).contiguous() for t in (q, k, v, dq, dk, dv))
     if lut is None:
         lut, T = ops.route_1d(qc, kc, topk_frac, bq, bk)
+    else:
+        lut = lut.to(device=q.device, dtype=torch.int32).contiguous()
+        ops.check_lut_ids(lut, -(-L // bk))
     mq = -(-L // bq)
     if torch.is_tensor(alpha) and alpha.dim() == 2:
         a = alpha.detach().to(q.device, torch.float32)

@@ -129,7 +129,7 @@ int sla2h_complement(const float* Hb, const float* dHb, const float* zb, const f
                      const int32_t* lut, int B, int H, int Mb, int Np, int D, int T,
                      void* workspace, void* comp, void* stream);
 
-/* Largest workspace sla2h_complement_noalloc serves (4 MiB: B*H up to 72 at
+/* Largest workspace sla2h_complement_noalloc serves (4 MiB: B*H up to 145 at
  * Mb = Np = 468, the 29,952-token shape). */
 #define SLA2H_COMPLEMENT_SCRATCH_BYTES (4u << 20)
 

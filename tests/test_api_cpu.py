@@ -6,6 +6,7 @@ form or by the oracle's dense fp64 form."""
 from functools import partial
 
 import numpy as np
+import pytest
 import torch
 
 from oracle import sla2_oracle as O
@@ -206,3 +207,44 @@ def test_sla2_dense_ref_matches_the_oracle_dense_form():
         got = sla2_dense_ref(q, k, v, lut, alpha, bq, 64)
         want = O.dense_1d_f64(q, k, v, lut.numpy(), alpha, bq)
         assert rel_l2(got, want) < 1e-12, (L, bq)
+
+
+def test_alpha_reference_shape_with_a_long_prefix():
+    """The reference's mix ratio alpha (H, Np + 1) has one column per video tile
+    and one for the whole prefix, spread per token by repeat_interleave of
+    [E] * Np + [P].  With a prefix of 150 tokens (three 64-row query blocks)
+    alpha_blocks must give every prefix block that last column, and
+    mvs_dense_ref must accept either form with the same result."""
+    from imfvideo_amd.mla_video_sparse_jvp import alpha_blocks, mvs_dense_ref
+    H, Np, P, E = 2, 3, 150, 64
+    L = Np * E + P
+    Mb = -(-L // E)
+    g = torch.Generator().manual_seed(7)
+    alpha_ref = torch.rand(H, Np + 1, generator=g)
+    per_token = alpha_ref.repeat_interleave(torch.tensor([E] * Np + [P]), dim=1)  # (H, L)
+    rows_of = torch.clamp(torch.arange(L) // E, max=Mb - 1)
+    got = alpha_blocks(alpha_ref, H, Np, Mb, "cpu")
+    assert got.shape == (H, Mb)
+    assert torch.equal(got[:, rows_of], per_token)
+    full = torch.rand(H, Mb, generator=g)
+    assert torch.equal(alpha_blocks(full, H, Np, Mb, "cpu"), full)
+    with pytest.raises(ValueError):
+        alpha_blocks(torch.rand(H, Np), H, Np, Mb, "cpu")
+    q, k, v = (torch.randn(1, H, L, 64, generator=g) for _ in range(3))
+    lut = torch.stack([torch.randperm(Np, generator=g)[:2] for _ in range(H * Mb)]).view(1, H, Mb, 2)
+    a = mvs_dense_ref(q, k, v, alpha_ref, lut, Np, E, P)
+    b = mvs_dense_ref(q, k, v, got, lut, Np, E, P)
+    assert torch.equal(a, b)
+
+
+def test_caller_lut_ids_are_checked():
+    """LUT ids outside [0, Np) (-1 padding, a prefix-tail id) are rejected before
+    any kernel: the fused kernel would clamp them and the complement skip them."""
+    from imfvideo_amd import ops
+    lut = torch.tensor([[[[0, 3], [1, 2]]]], dtype=torch.int32)
+    ops.check_lut_ids(lut, 4)
+    for bad in (-1, 4):
+        x = lut.clone()
+        x[0, 0, 1, 0] = bad
+        with pytest.raises(ValueError):
+            ops.check_lut_ids(x, 4)

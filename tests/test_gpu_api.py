@@ -149,7 +149,8 @@ def test_reference_recipe_mla_video_sparse_jvp(dt):
     proj_q = torch.eye(64) + 0.05 * torch.randn(64, 64, generator=g)
     proj_k = torch.eye(64) + 0.05 * torch.randn(64, 64, generator=g)
     ct = torch.float16 if dt == torch.float32 else dt   # the compute type
-    lut, T = route_tiles(*(cuda(t.to(ct)) for t in x[:2]), 0.25, Np, 64, P,
+    # routed on the inputs as given (fp32 unrounded), as lut=None does below
+    lut, T = route_tiles(*(cuda(t.to(dt)) for t in x[:2]), 0.25, Np, 64, P,
                          proj_q=cuda(proj_q), proj_k=cuda(proj_k))
     assert T == 2
     o_ref, do_ref = dense_jvp(x, alpha, lut, Np, P)
@@ -167,6 +168,29 @@ def test_reference_recipe_mla_video_sparse_jvp(dt):
     o2, do2 = mla_video_sparse_jvp(*gx, cuda(alpha), 0.25, Np, 64, P, proj_q=cuda(proj_q),
                                    proj_k=cuda(proj_k))
     assert torch.equal(o2, o) and torch.equal(do2, do)
+
+
+@pytest.mark.xfail(strict=True, reason="fp32 inputs are computed in fp16 on the 16-bit MFMA path "
+                   "(documented deviation): o ~1e-2 against the reference's fp32 bound 2e-4")
+def test_reference_fp32_bound_of_the_non_qat_cube_jvp():
+    """The reference's fp32 tolerance (tests/test_mla_video_sparse_jvp.py:54: o 2e-4,
+    do 2e-3 against the dense fp32 JVP).  Its fp32 mode runs IEEE fp32 dots; this
+    build's kernels take 16-bit operands, so fp32 inputs get the fp16 bound
+    (checked above) and this bound is not met: strict xfail, so a future fp32
+    path that meets it turns the test into a failure to remove the marker."""
+    from imfvideo_amd.mla_video_sparse_jvp import mla_video_sparse_jvp, route_tiles
+    x, alpha, Np, P, g = ref_geometry(3, Np=8)
+    proj_q = torch.eye(64) + 0.05 * torch.randn(64, 64, generator=g)
+    proj_k = torch.eye(64) + 0.05 * torch.randn(64, 64, generator=g)
+    lut, T = route_tiles(*(cuda(t) for t in x[:2]), 0.25, Np, 64, P,
+                         proj_q=cuda(proj_q), proj_k=cuda(proj_k))
+    o_ref, do_ref = dense_jvp(x, alpha, lut, Np, P)
+    o, do = mla_video_sparse_jvp(*(cuda(t) for t in x), cuda(alpha), 0.25, Np, 64, P, lut=lut,
+                                 T=T, block_m=32)
+    torch.cuda.synchronize()
+    r_o, r_do = rel_fro(o, o_ref), rel_fro(do, do_ref)
+    print(f"  fp32 inputs: o {r_o:.2e} (reference bound 2e-4) do {r_do:.2e} (2e-3)", flush=True)
+    assert r_o < 2e-4 and r_do < 2e-3
 
 
 def test_module_pre_permuted_matches_model_order():

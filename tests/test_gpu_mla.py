@@ -262,3 +262,52 @@ def test_pack_block_snapshot_drives_the_fast_jvp():
     h1, dh1 = h + a, dh + da
     m, dm = O.mlp_jvp(h1, dh1, pc, 1e-6)
     check((x, dx), (h1 + m, dh1 + dm), "packed block")
+
+
+def test_build_fast_jvp_state_packs_every_block_of_a_net():
+    """build_fast_jvp_state on a stand-in net with the reference model's
+    attributes (two shared blocks, one u-head, the u-branch output layers,
+    RoPE tables, eps, attention-residual block size, prefix tokens,
+    tile_major): one pack_block per block in order, the u-branch tensors
+    detached, the scalars passed through, and each packed block drives
+    block_jvp to the same result as packing that block directly."""
+    say("build_fast_jvp_state on a stand-in net")
+    from functools import partial
+    from types import SimpleNamespace
+    from imfvideo_amd.imf_dit_video import TransformerBlock
+    from imfvideo_amd.mla_jvp_fast import block_jvp, build_fast_jvp_state, pack_block
+    from imfvideo_amd.sla2_cube_qat import SLA2CubeQATAttentionImpl
+    torch.manual_seed(9)
+    S, P, D = 274, 18, 256
+    impl = partial(SLA2CubeQATAttentionImpl, seq_len=S, num_heads=2, grid=(4, 8, 8),
+                   tile=(4, 4, 4), topk=0.5)
+    mk = lambda: TransformerBlock(D, 2, 128, 64, 32, 32, 64, mlp_ratio=2, attn_impl=impl,
+                                  mla_use_output_gate=True).cuda()
+    blocks = [mk(), mk(), mk()]
+    lin = torch.nn.Linear(D, 16).cuda()
+    cos, sin = rope(S, P)
+    net = SimpleNamespace(
+        shared_blocks=blocks[:2], u_heads=blocks[2:], tile_major=False,
+        u_out_res_norm=SimpleNamespace(weight=torch.nn.Parameter(torch.ones(D, device="cuda"))),
+        u_out_res_proj=torch.nn.Linear(D, D, bias=False).cuda(),
+        u_final_layer=SimpleNamespace(norm=SimpleNamespace(weight=torch.nn.Parameter(
+            torch.ones(D, device="cuda"))), linear=lin),
+        rope_cos=cuda(cos), rope_sin=cuda(sin), rmsnorm_eps=1e-6, attn_res_block_size=4,
+        prefix_tokens=P)
+    st = build_fast_jvp_state(net)
+    assert len(st["shared"]) == 2 and len(st["u_heads"]) == 1
+    assert st["eps"] == 1e-6 and st["bs"] == 4 and st["prefix_tokens"] == P
+    assert st["rope"][0] is net.rope_cos and st["rope"][1] is net.rope_sin
+    for t_ in (*st["u_out_res"], *st["u_final"]):
+        assert not t_.requires_grad
+    assert torch.equal(st["u_final"][1], lin.weight.detach())
+    assert torch.equal(st["u_final"][2], lin.bias.detach())
+    g = torch.Generator().manual_seed(10)
+    h = cuda(torch.randn(1, S, D, generator=g))
+    dh = cuda(0.1 * torch.randn(1, S, D, generator=g))
+    for packed, blk in zip(st["shared"] + st["u_heads"], blocks):
+        p1, w1 = packed
+        p2, w2 = pack_block(blk, False)
+        x1, dx1 = block_jvp(h, dh, p1, w1, cuda(cos), cuda(sin), 1e-6)
+        x2, dx2 = block_jvp(h, dh, p2, w2, cuda(cos), cuda(sin), 1e-6)
+        assert torch.equal(x1, x2) and torch.equal(dx1, dx2)

@@ -135,7 +135,7 @@ def test_train_fwd_config3_full_size():
     out = run_train(ins, alpha, lut, Np)
     assert torch.isfinite(out["o"].float()).all() and torch.isfinite(out["lse"]).all()
     check_quant(out, f, 29952)
-    for h in (0, 5):
+    for h in range(8):  # every head
         sl = slice(h, h + 1)
         ref = O.train_fwd(f["q"][:, sl], f["k"][:, sl], f["v"][:, sl], alpha[sl], lut[:, sl],
                           Np, P)
@@ -223,7 +223,7 @@ def test_train_bwd_config3_full_size():
     got = dict(dq=dq.cpu().float(), dk=dk.cpu().float(), dv=dv.cpu().float(), d_alpha=da.cpu())
     for n in ("dq", "dk", "dv"):
         assert torch.isfinite(got[n]).all(), n
-    for h in (0, 5):
+    for h in range(8):  # every head
         sl = slice(h, h + 1)
         fwd = {n: out[n][:, sl].cpu().float() for n in ("o_s", "o_l", "lse", "den", "qphi", "htot", "ztot")}
         ref = O.train_bwd(f["q"][:, sl], f["k"][:, sl], f["v"][:, sl], alpha[sl], lut[:, sl], Np, P,
@@ -311,7 +311,7 @@ def test_sla2_mla_jvp_config4_shape():
     o, do = sla2_mla_jvp(*(cuda(t) for t in x), 0.9, 0.1, 128, 64)
     o, do = o.cpu(), do.cpu()
     assert torch.isfinite(o).all() and torch.isfinite(do).all()
-    for h in (0, 5):
+    for h in range(8):  # every head
         sl = slice(h, h + 1)
         xs = [t[:, sl].float() for t in x]
         lut, T = O.route_1d(xs[0], xs[1], 0.1, 128)
@@ -382,7 +382,7 @@ def test_sla2_train_1d_config_shape():
     dq, dk, dv, da = ops.train_bwd(g["q"], g["k"], g["v"], cuda(alpha), out, cuda(do), bq=128)
     torch.cuda.synchronize()
     lut = lut.cpu().numpy()
-    for h in (0, 5):
+    for h in range(8):  # every head
         sl = slice(h, h + 1)
         f = {n: t[:, sl].float() for n, t in x.items()}
         elut, eT = O.route_1d(f["q"], f["k"], 0.1, 128)

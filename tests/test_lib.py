@@ -84,3 +84,13 @@ def test_missing_library_raises(monkeypatch, tmp_path):
     monkeypatch.setattr(_lib, "_LIB", None)
     with pytest.raises(RuntimeError, match="build it"):
         _lib.load()
+
+
+def test_no_alloc_capacity_at_the_29952_token_shape():
+    """The static 4 MiB bit-mask array of sla2h_complement_noalloc covers B*H up to
+    145 heads at Mb = Np = 468 (28,800 B each), the figure the header states."""
+    lib = _lib.load()
+    cap = 4 << 20
+    assert lib.sla2h_complement_workspace_bytes(1, 1, 468, 468) == 28_800
+    assert lib.sla2h_complement_workspace_bytes(1, 145, 468, 468) <= cap
+    assert lib.sla2h_complement_workspace_bytes(1, 146, 468, 468) > cap
