@@ -74,6 +74,9 @@ SIGNATURES = {
                                      _c_int, _c_int, _c_int, _c_f, _p, _p, _p, _p]),
     "sla2h_linear_mix_qat": (_c_int, [_p, _p, _p, _p, _p, _c_int, _c_int, _c_int, _c_int,
                                       _c_i64, _c_int, _c_int, _c_f, _p, _p, _p, _p]),
+    "sla2h_linear_mix_score": (_c_int, [_p, _p, _p, _p, _p, _p, _c_int, _p, _p, _c_int, _c_int,
+                                        _c_int, _c_int, _c_i64, _c_int, _c_int, _c_f, _p, _p, _p,
+                                        _p]),
     "sla2h_quantize_v8f": (_c_int, [_p, _c_int, _c_i64, _c_i64, _c_int, _c_int, _p, _p, _p]),
     "sla2h_quantize_trunc": (_c_int, [_p, _c_int, _c_i64, _c_i64, _c_int, _c_int, _p, _p, _p]),
     "sla2h_sparse_fwd_int8": (_c_int, [_p, _p, _p, _c_int, _p, _p, _p, _p, _p, _c_int, _c_int,

@@ -530,6 +530,174 @@ __global__ __launch_bounds__(256) void linear_mix_qat_kernel(
   if (qok && g == 0 && den_out != nullptr) den_out[(int64_t)bh * L + qrow] = dn;
 }
 
+// Score form of the same linear branch (_lin_fwd2 with SCORE_FORM,
+// models/sla2_vendor/kernel_linear.py:260-272), which the reference selects
+// while the augmented LUT has at most 4 columns: the routed tiles are
+// subtracted in the score domain instead of from the state,
+//   num = qphi round16(Hall) - sum_j round16(W_j) V_j,  W_j = qphi kphi_j^T (fp32),
+//   den = qphi . zall - sum_j rowsum(W_j), then +-eps_l (signed),
+// kphi_j = round16(softmax_D(K rows of tile j)), zero past L.  The mix is
+// linear_mix_qat_kernel's.  Wave w owns queries 16w..16w+15 and computes
+// W^T = kphi_j qphi^T, so lane (g, r) holds keys 16 kt + 4g + i of query r.
+// Those 8 keys of key tiles 2ks, 2ks+1 are directly the B operand of
+// num^T -= V_j^T round16(W^T) for contraction chunk ks, with the K slot
+// 8g + e standing for key 16 (2ks + e/4) + 4g + e%4; the A operand V_j^T is
+// read from LDS in that key order.  Tile ids outside [0, Nb) are clamped.
+template <typename T16>
+__global__ __launch_bounds__(256) void linear_mix_score_kernel(
+    const uint16_t* __restrict__ qphi, const uint16_t* __restrict__ K,
+    const uint16_t* __restrict__ V, const float* __restrict__ Hall,
+    const float* __restrict__ zall, const int32_t* __restrict__ lut, int J, int Nb,
+    const uint16_t* __restrict__ o_s, const float* __restrict__ alpha, int alpha_stride,
+    int64_t L, int Mq, int qshift, int H, float eps_l, uint16_t* __restrict__ o,
+    uint16_t* __restrict__ o_l, float* __restrict__ den_out) {
+  __shared__ __align__(16) uint16_t hT[kT][kT + 8];  // round16(Hall)^T [value ch][key ch]
+  __shared__ __align__(16) uint16_t kp[kT][kT + 8];  // kphi_j [key][ch]
+  __shared__ __align__(16) uint16_t vT[kT][kT + 8];  // V_j^T [value ch][key]
+  __shared__ float zs[kT];
+
+  const int m = blockIdx.x, bh = blockIdx.y, h = bh % H;
+  const int mq = m >> qshift;
+  const int tid = threadIdx.x;
+  {
+    const int d = tid >> 2, v0 = (tid & 3) * 16;
+    const f32x4* hr = reinterpret_cast<const f32x4*>(Hall + (int64_t)bh * kT * kT + d * kT + v0);
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      const f32x4 x = hr[c];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) hT[v0 + 4 * c + i][d] = T16::from_f32(x[i]);
+    }
+    if (tid < kT) zs[tid] = zall[(int64_t)bh * kT + tid];
+  }
+  __syncthreads();
+
+  const int w = tid >> 6, l = tid & 63, r = l & 15, g = l >> 4;
+  const int64_t qrow = (int64_t)m * kT + 16 * w + r;
+  const bool qok = qrow < L;
+  const int64_t rowoff = ((int64_t)bh * L + qrow) * kT;
+  u32x4 qb[2];
+  float dn = 0.f;
+#pragma unroll
+  for (int ks = 0; ks < 2; ++ks) {
+    qb[ks] = qok ? *reinterpret_cast<const u32x4*>(qphi + rowoff + 32 * ks + 8 * g)
+                 : u32x4{0, 0, 0, 0};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      dn += T16::to_f32((uint16_t)(qb[ks][e] & 0xffff)) * zs[32 * ks + 8 * g + 2 * e];
+      dn += T16::to_f32((uint16_t)(qb[ks][e] >> 16)) * zs[32 * ks + 8 * g + 2 * e + 1];
+    }
+  }
+  dn = sum_over_groups(dn);
+  f32x4 num[4];
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) {
+    num[ct] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const u32x4 av = *reinterpret_cast<const u32x4*>(&hT[16 * ct + r][32 * ks + 8 * g]);
+      num[ct] = mfma_16x16x32<T16>(av, qb[ks], num[ct]);
+    }
+  }
+
+  // staging: thread (row sr, 16 channels from c0) of each selected tile
+  const int sr = tid >> 2, c0 = (tid & 3) * 16;
+  const int32_t* lrow = lut + ((int64_t)bh * Mq + mq) * J;
+  float wsum = 0.f;  // this lane's keys of every tile, summed
+  for (int j = 0; j < J; ++j) {
+    const int n = min(max(lrow[j], 0), Nb - 1);
+    const int64_t krow = (int64_t)n * kT + sr;
+    const bool kok = krow < L;
+    const int64_t koff = ((int64_t)bh * L + krow) * kT + c0;
+    uint32_t kw[8], vw[8];
+#pragma unroll
+    for (int i = 0; i < 2; ++i) {
+      const uint4 ku = kok ? reinterpret_cast<const uint4*>(K + koff)[i] : make_uint4(0, 0, 0, 0);
+      const uint4 vu = kok ? reinterpret_cast<const uint4*>(V + koff)[i] : make_uint4(0, 0, 0, 0);
+      kw[4 * i + 0] = ku.x; kw[4 * i + 1] = ku.y; kw[4 * i + 2] = ku.z; kw[4 * i + 3] = ku.w;
+      vw[4 * i + 0] = vu.x; vw[4 * i + 1] = vu.y; vw[4 * i + 2] = vu.z; vw[4 * i + 3] = vu.w;
+    }
+    float x[16];
+    float mx = -INFINITY;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x[i] = T16::to_f32((uint16_t)(kw[i >> 1] >> (16 * (i & 1))));
+      mx = fmaxf(mx, x[i]);
+    }
+    mx = fmaxf(mx, __shfl_xor(mx, 1, 64));
+    mx = fmaxf(mx, __shfl_xor(mx, 2, 64));
+    float sum = 0.f;
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      x[i] = __expf(x[i] - mx);
+      sum += x[i];
+    }
+    sum += __shfl_xor(sum, 1, 64);
+    sum += __shfl_xor(sum, 2, 64);
+    __syncthreads();  // the previous tile's kp / vT reads are done
+#pragma unroll
+    for (int i = 0; i < 8; ++i) {
+      const uint32_t p = kok ? pack_pair<T16>(x[2 * i] / sum, x[2 * i + 1] / sum) : 0u;
+      *reinterpret_cast<uint32_t*>(&kp[sr][c0 + 2 * i]) = p;
+      vT[c0 + 2 * i][sr] = (uint16_t)(vw[i] & 0xffff);
+      vT[c0 + 2 * i + 1][sr] = (uint16_t)(vw[i] >> 16);
+    }
+    __syncthreads();
+
+    f32x4 wt[4];
+#pragma unroll
+    for (int kt = 0; kt < 4; ++kt) {
+      wt[kt] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        const u32x4 av = *reinterpret_cast<const u32x4*>(&kp[16 * kt + r][32 * ks + 8 * g]);
+        wt[kt] = mfma_16x16x32<T16>(av, qb[ks], wt[kt]);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) wsum += wt[kt][i];
+    }
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const f32x4 a0 = wt[2 * ks], a1 = wt[2 * ks + 1];
+      const u32x4 bw = u32x4{pack_pair<T16>(-a0[0], -a0[1]), pack_pair<T16>(-a0[2], -a0[3]),
+                             pack_pair<T16>(-a1[0], -a1[1]), pack_pair<T16>(-a1[2], -a1[3])};
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const u32x2 v0 = *reinterpret_cast<const u32x2*>(&vT[16 * ct + r][32 * ks + 4 * g]);
+        const u32x2 v1 = *reinterpret_cast<const u32x2*>(&vT[16 * ct + r][32 * ks + 16 + 4 * g]);
+        num[ct] = mfma_16x16x32<T16>(u32x4{v0.x, v0.y, v1.x, v1.y}, bw, num[ct]);
+      }
+    }
+  }
+  dn -= sum_over_groups(wsum);
+  dn = dn >= 0.f ? dn + eps_l : dn - eps_l;
+  const float rdn = 1.f / dn;
+  const float a16 = T16::to_f32(T16::from_f32(alpha[(int64_t)h * alpha_stride + mq]));
+  const float b16 = T16::to_f32(T16::from_f32(1.f - a16));
+  if (qok) {
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const int64_t oo = rowoff + 16 * ct + 4 * g;
+      const uint2 sv = *reinterpret_cast<const uint2*>(o_s + oo);
+      const uint32_t sw[2] = {sv.x, sv.y};
+      float ol[4], ov[4];
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        const float os16 = T16::to_f32((uint16_t)(sw[i >> 1] >> (16 * (i & 1))));
+        ol[i] = T16::to_f32(T16::from_f32(num[ct][i] * rdn));
+        const float x = T16::to_f32(T16::from_f32(a16 * os16));
+        const float y = T16::to_f32(T16::from_f32(b16 * ol[i]));
+        ov[i] = x + y;
+      }
+      *reinterpret_cast<uint2*>(o + oo) =
+          make_uint2(pack_pair<T16>(ov[0], ov[1]), pack_pair<T16>(ov[2], ov[3]));
+      *reinterpret_cast<uint2*>(o_l + oo) =
+          make_uint2(pack_pair<T16>(ol[0], ol[1]), pack_pair<T16>(ol[2], ol[3]));
+    }
+    if (g == 0) den_out[(int64_t)bh * L + qrow] = dn;
+  }
+}
+
 }  // namespace
 
 }  // namespace sla2h
@@ -668,6 +836,34 @@ extern "C" int sla2h_linear_mix_qat(const void* qphi, const void* comp, const fl
     linear_mix_qat_kernel<BF16><<<grid, 256, 0, st>>>(QP, C, Hall, OS, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, OL, den);
   else
     linear_mix_qat_kernel<F16><<<grid, 256, 0, st>>>(QP, C, Hall, OS, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, OL, den);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_linear_mix_score(const void* qphi, const void* k, const void* v,
+                                      const float* Hall, const float* zall, const int32_t* lut,
+                                      int J, const void* o_s, const float* alpha,
+                                      int alpha_stride, int dtype, int B, int H, int64_t L, int D,
+                                      int E, float eps_l, void* o, void* o_l, float* den,
+                                      void* stream) {
+  SLA2H_CHECK_ARG(qphi && k && v && Hall && zall && lut && o_s && alpha && o && o_l && den);
+  SLA2H_CHECK_ARG(D == kT && (E == 64 || E == 128 || E == 256) && alpha_stride >= 0);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && L > 0 && J >= 1 && J <= kMaxJ);
+  const int Nb = (int)((L + kT - 1) / kT);
+  const int Mq = (int)((L + E - 1) / E);
+  const int qshift = E == 64 ? 0 : (E == 128 ? 1 : 2);
+  dim3 grid(Nb, B * H);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  auto QP = static_cast<const uint16_t*>(qphi);
+  auto Kp = static_cast<const uint16_t*>(k);
+  auto Vp = static_cast<const uint16_t*>(v);
+  auto OS = static_cast<const uint16_t*>(o_s);
+  auto O = static_cast<uint16_t*>(o);
+  auto OL = static_cast<uint16_t*>(o_l);
+  if (dtype == SLA2H_DTYPE_BF16)
+    linear_mix_score_kernel<BF16><<<grid, 256, 0, st>>>(QP, Kp, Vp, Hall, zall, lut, J, Nb, OS, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, OL, den);
+  else
+    linear_mix_score_kernel<F16><<<grid, 256, 0, st>>>(QP, Kp, Vp, Hall, zall, lut, J, Nb, OS, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, OL, den);
   return (int)hipGetLastError();
 }
 

@@ -366,6 +366,37 @@ def linear_mix_qat(qphi, comp, Hall, o_s, alpha, eps_l=1e-5, bq=E_TILE):
     return o, o_l, den
 
 
+SCORE_FORM_MAX_J = 4
+
+
+def linear_mix_score(qphi, k, v, st, lut, o_s, alpha, eps_l=1e-5, bq=E_TILE):
+    """Score form of linear_mix_qat (the reference's branch for LUTs of at most
+    SCORE_FORM_MAX_J columns): the routed tiles are subtracted as
+    round16(qphi kphi_j^T) v_j from qphi round16(Hall), not from the state.
+    st: linear_states_qat's dict (Hall, zall); lut (B,H,ceil(L/bq),J) int32,
+    ids in [0, ceil(L/64)).  Returns (o, o_l 16-bit, den fp32)."""
+    _need_gpu(qphi, k, v, lut, o_s, alpha)
+    B, H, L, D = qphi.shape
+    Mq = -(-L // bq)
+    lut = lut.to(torch.int32).contiguous()
+    if lut.dim() != 4 or tuple(lut.shape[:3]) != (B, H, Mq):
+        raise ValueError(f"linear_mix_score: lut must be (B, H, {Mq}, J), got {tuple(lut.shape)}")
+    for t in (k, v, o_s):
+        if tuple(t.shape) != (B, H, L, D) or t.dtype != qphi.dtype:
+            raise ValueError("linear_mix_score: k, v, o_s must match qphi")
+    alpha = _alpha_rows(alpha, H, Mq, qphi.device)
+    o = torch.empty_like(o_s)
+    o_l = torch.empty_like(o_s)
+    den = torch.empty(B, H, L, device=qphi.device, dtype=torch.float32)
+    _lib.check(_lib.load().sla2h_linear_mix_score(
+        qphi.data_ptr(), k.contiguous().data_ptr(), v.contiguous().data_ptr(),
+        st["Hall"].contiguous().data_ptr(), st["zall"].contiguous().data_ptr(), lut.data_ptr(),
+        lut.shape[-1], o_s.data_ptr(), alpha.data_ptr(), alpha.stride(0), _dtype_code(qphi),
+        B, H, L, D, bq, float(eps_l), o.data_ptr(), o_l.data_ptr(), den.data_ptr(),
+        _stream(qphi.device)), "sla2h_linear_mix_score")
+    return o, o_l, den
+
+
 def augment_lut(lut, Np, n_tail):
     """lut (B,H,Mb,T) -> lut_aug (B,H,Mb,T+n_tail) int32 with the prefix tail blocks appended."""
     B, H, Mb, _ = lut.shape
@@ -381,7 +412,9 @@ def train_fwd(q, k, v, alpha, lut, Np, eps_l=1e-5, int8=True):
     lut: (B,H,Mb,T) routed video tiles.  int8: the INT8 sparse branch of
     _attn_fwd_qat (truncating Q/K/V quantisation, INT8 P.V), else its 16-bit
     branch (S = q.k^T on 16-bit MFMA, O += round16(P).V), as the reference
-    module's use_int8 flag selects (models/sla2_cube_qat.py:395, 413).
+    module's use_int8 flag selects (models/sla2_cube_qat.py:395, 413).  The
+    linear branch runs in the score form while the augmented LUT has at most
+    SCORE_FORM_MAX_J columns, else in the state form (models/sla2_cube_qat.py:739).
     Returns a dict with the module output o and the tensors the reference
     saves for its backward: o_s, o_l, lse, den, qphi, htot (rounded to 16
     bits, held in fp32), ztot, lut_aug, and (int8) the quantised operands.
@@ -400,8 +433,12 @@ def train_fwd(q, k, v, alpha, lut, Np, eps_l=1e-5, int8=True):
     else:
         st = linear_states_qat(k, v, with_vt=True)
         o_s, lse, qphi = sparse_fwd_16(q, k, st["vt"], lut_aug, E_TILE)
+    # the complement records also feed the backward's dqphi
     comp = complement(st, lut_aug, nb, check_ids=False)
-    o, o_l, den = linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha, eps_l)
+    if lut_aug.shape[-1] <= SCORE_FORM_MAX_J:
+        o, o_l, den = linear_mix_score(qphi, k, v, st, lut_aug, o_s, alpha, eps_l)
+    else:
+        o, o_l, den = linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha, eps_l)
     htot = st["Hall"].to(q.dtype).float()
     return dict(o=o, o_s=o_s, o_l=o_l, lse=lse, den=den, qphi=qphi, htot=htot,
                 ztot=st["zall"], Hall=st["Hall"], comp=comp, lut_aug=lut_aug, **qz)
@@ -604,7 +641,10 @@ def train_fwd_1d(q, k, v, alpha, lut, bq, eps_l=1e-5, int8=False):
     else:
         o_s, lse, qphi = sparse_fwd_16(q, k, st["vt"], lut, bq)
     comp = complement(st, lut, nb, check_ids=False)
-    o, o_l, den = linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha, eps_l, bq=bq)
+    if lut.shape[-1] <= SCORE_FORM_MAX_J:
+        o, o_l, den = linear_mix_score(qphi, k, v, st, lut, o_s, alpha, eps_l, bq=bq)
+    else:
+        o, o_l, den = linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha, eps_l, bq=bq)
     return dict(o=o, o_s=o_s, o_l=o_l, lse=lse, den=den, qphi=qphi,
                 htot=st["Hall"].to(q.dtype).float(), ztot=st["zall"], Hall=st["Hall"], comp=comp,
                 lut_aug=lut)

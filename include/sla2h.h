@@ -407,6 +407,27 @@ int sla2h_linear_mix_qat(const void* qphi, const void* comp, const float* Hall,
                          void* o_l, float* den, void* stream);
 
 /*
+ * Score form of the same linear branch and mix, which the reference runs while
+ * the augmented LUT has at most 4 columns (T + n_tail <= 4):
+ *   W_j = qphi kphi_j^T (fp32), kphi_j = round16(softmax_D(k rows of tile j)),
+ *     rows past L zero;
+ *   num = qphi round16(Hall) - sum_j round16(W_j) v_j (fp32 accumulate);
+ *   den = qphi . zall - sum_j rowsum(W_j), then +-eps_l (signed);
+ *   o_l, o and den as sla2h_linear_mix_qat.
+ * k, v (B,H,L,D) 16-bit; Hall (B,H,D,D), zall (B,H,D) fp32 from
+ * sla2h_linear_states_qat; lut (B,H,ceil(L/E),J) int32, ids in [0, ceil(L/64))
+ * (ids outside are clamped; the Python layer rejects them), J <= 1024.
+ * Replaces _lin_fwd2 with SCORE_FORM (models/sla2_vendor/kernel_linear.py:
+ * 206-272) as selected at models/sla2_cube_qat.py:424, 739 and
+ * models/sla2_vendor/kernel_linear.py:357.
+ */
+int sla2h_linear_mix_score(const void* qphi, const void* k, const void* v, const float* Hall,
+                           const float* zall, const int32_t* lut, int J, const void* o_s,
+                           const float* alpha, int alpha_stride, int dtype, int B, int H,
+                           int64_t L, int D, int E, float eps_l, void* o, void* o_l, float* den,
+                           void* stream);
+
+/*
  * 16-bit sparse branch of the 1-D training forward (no INT8): S = q.k^T on
  * 16-bit MFMA (fp32 accumulate) * scale * log2(e) over the routed key blocks
  * of each query block of bq rows (lut (B,H,ceil(L/bq),T)), exact running

@@ -375,8 +375,8 @@ def dense_jvp(q, k, v, dq, dk, dv, alpha, lut, Np, prefix_len, quant=None):
 # ---------------------------------------------------------------------------
 # Training-forward semantics (b): _CubeQATFunction.forward
 # (models/sla2_cube_qat.py:696-751) = _attn_fwd_qat (kernel_sparse_qat.py:28-117)
-# + kphi / _precompute_global (kernel_linear.py:305-313) + _lin_fwd2 state
-# form (kernel_linear.py:205-302) + the alpha mix in 16-bit.
+# + kphi / _precompute_global (kernel_linear.py:305-313) + _lin_fwd2 in its
+# state or score form (kernel_linear.py:205-302) + the alpha mix in 16-bit.
 # ---------------------------------------------------------------------------
 def quantize_blocks_trunc(x, block=E):
     """In-kernel quantisation of _attn_fwd_qat (kernel_sparse_qat.py:56-58, 88-90,
@@ -407,7 +407,7 @@ def _expand_1d(lut, alpha, bq, nb):
 
 
 def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L, int8=True,
-              bq=E):
+              bq=E, score_form=None):
     """Training-forward semantics (b), blockwise, CPU.
 
     q, k, v: (B,H,L,D) float tensors holding 16-bit values.  alpha: (H, Mb)
@@ -421,6 +421,10 @@ def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L
     query blocks of bq rows (LUT rows, alpha and, with int8, the Q scale per
     block), Np = Nb key blocks and no prefix tail; int8=False: 16-bit scores
     and O += round16(P).V.
+    score_form: the linear branch's form; None selects it as the reference's
+    callers do (score form while the augmented LUT has at most 4 columns,
+    models/sla2_cube_qat.py:424, 739; models/sla2_vendor/kernel_linear.py:357),
+    True / False force the score / state form.
     """
     B, H, L, D = q.shape
     nb = -(-L // E)
@@ -488,15 +492,32 @@ def train_fwd(q, k, v, alpha, lut, Np, prefix_len, t16=torch.bfloat16, eps=EPS_L
     ztot = kphi.sum(-2)                                        # (B,H,D)
     kpt, vvt = _tiles(kphi, nb), _tiles(vf, nb)
     qpt = _tiles(qphi, nb)
-    hi = htot[:, :, None].expand(B, H, Mb, D, D).clone()
-    zi = ztot[:, :, None].expand(B, H, Mb, D).clone()
-    for j in range(J):
-        n = lut_aug[..., j]
-        kp, vv = _gather_tiles(kpt, n), _gather_tiles(vvt, n)
-        hi = hi - kp.transpose(-1, -2) @ vv
-        zi = zi - kp.sum(-2)
-    num = qpt[:, :, :Mb] @ _round16(hi, t16)                  # (B,H,Mb,E,D)
-    den = (qpt[:, :, :Mb] * zi[..., None, :]).sum(-1)
+    if score_form is None:
+        score_form = J <= 4
+    if score_form:
+        # _lin_fwd2 with SCORE_FORM (kernel_linear.py:260-272): the selected
+        # tiles are subtracted in the score domain, w = phi(Q) phi(K_j)^T in
+        # fp32, rounded to 16 bits for the product with V_j, unrounded in den
+        qp = qpt[:, :, :Mb]                                    # (B,H,Mb,E,D)
+        num = qp @ htot[:, :, None]
+        den = (qp * ztot[:, :, None, None, :]).sum(-1)
+        for j in range(J):
+            n = lut_aug[..., j]
+            kp, vv = _gather_tiles(kpt, n), _gather_tiles(vvt, n)
+            w = qp @ kp.transpose(-1, -2)                      # (B,H,Mb,E,E)
+            num = num - _round16(w, t16) @ vv
+            den = den - w.sum(-1)
+    else:
+        # state form (kernel_linear.py:274-285)
+        hi = htot[:, :, None].expand(B, H, Mb, D, D).clone()
+        zi = ztot[:, :, None].expand(B, H, Mb, D).clone()
+        for j in range(J):
+            n = lut_aug[..., j]
+            kp, vv = _gather_tiles(kpt, n), _gather_tiles(vvt, n)
+            hi = hi - kp.transpose(-1, -2) @ vv
+            zi = zi - kp.sum(-2)
+        num = qpt[:, :, :Mb] @ _round16(hi, t16)              # (B,H,Mb,E,D)
+        den = (qpt[:, :, :Mb] * zi[..., None, :]).sum(-1)
     den = torch.where(den >= 0, den + eps, den - eps)
     o_l = (num / den[..., None]).reshape(B, H, Mb * E, D)[:, :, :L]
     den = den.reshape(B, H, Mb * E)[:, :, :L]

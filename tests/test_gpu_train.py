@@ -104,6 +104,58 @@ def test_train_fwd_ragged_fp16_and_alpha_endpoints():
             assert torch.equal(out["o"], out["o_l"])
 
 
+@pytest.mark.parametrize("dt,T", [(torch.bfloat16, 3), (torch.float16, 2), (torch.bfloat16, 4)])
+def test_train_fwd_score_form(dt, T):
+    """Augmented LUTs of at most 4 columns run the score form of the linear branch
+    (kernel_linear.py:260-272), wider ones the state form, as the reference
+    selects (models/sla2_cube_qat.py:739).  Where the two forms round at
+    different points, the GPU result is the nearer to the form it claims."""
+    from imfvideo_amd import ops
+    say("train_fwd score form", dt, "T", T)
+    B, H, Np, P = 2, 2, 6, 29
+    L = Np * 64 + P
+    q, k, v = make_inputs(41 + T, B, H, L, dtype=dt, tangent=False)
+    ins = dict(q=q, k=k, v=v)
+    f = {n: t.float() for n, t in ins.items()}
+    g = torch.Generator().manual_seed(T)
+    lut = np.stack([np.stack([np.stack([torch.randperm(Np, generator=g)[:T].numpy()
+                                        for _ in range(Np + 1)]) for _ in range(H)])
+                    for _ in range(B)]).astype(np.int32)
+    alpha = torch.rand(H, Np + 1, generator=g) * 0.8 + 0.1
+    out = run_train(ins, alpha, lut, Np)
+    score = T + 1 <= ops.SCORE_FORM_MAX_J
+    ref = O.train_fwd(f["q"], f["k"], f["v"], alpha, lut, Np, P, t16=dt)
+    compare(out, ref)
+    other = O.train_fwd(f["q"], f["k"], f["v"], alpha, lut, Np, P, t16=dt, score_form=not score)
+    got = out["o_l"].cpu().float()
+    near, far = rel_l2(got, ref["o_l"]), rel_l2(got, other["o_l"])
+    print(f"  o_l rel to its form {near:.2e}, to the other form {far:.2e}", flush=True)
+    assert near < 0.5 * far
+
+
+def test_train_fwd_1d_score_form():
+    """1-D module forward (bq = 128, 16-bit scores) with a 2-column LUT: the score
+    form of _complement_linear_attention (kernel_linear.py:357)."""
+    from imfvideo_amd import ops
+    say("train_fwd_1d score form bq=128 T=2")
+    B, H, L, bq = 1, 2, 777, 128
+    q, k, v = make_inputs(47, B, H, L, dtype=torch.float16, tangent=False)
+    nb, mq = -(-L // 64), -(-L // bq)
+    g = torch.Generator().manual_seed(3)
+    lut = torch.stack([torch.randperm(nb, generator=g)[:2] for _ in range(B * H * mq)])
+    lut = lut.view(B, H, mq, 2).int()
+    alpha = torch.rand(H, mq, generator=g) * 0.8 + 0.1
+    out = ops.train_fwd_1d(cuda(q), cuda(k), cuda(v), cuda(alpha), cuda(lut), bq)
+    torch.cuda.synchronize()
+    ref = O.train_fwd(q.float(), k.float(), v.float(), alpha, lut.numpy(), nb, 0,
+                      t16=torch.float16, int8=False, bq=bq)
+    for n in ("o", "o_s", "o_l", "qphi"):
+        got = out[n].cpu().float()
+        print(f"  {n} max {max_abs(got, ref[n]):.2e} rel {rel_l2(got, ref[n]):.2e}", flush=True)
+        assert max_abs(got, ref[n]) < TOL_MAX and rel_l2(got, ref[n]) < TOL_REL, n
+    assert rel_l2(out["den"].cpu(), ref["den"]) < 1e-3
+
+
 def test_train_fwd_all_tiles_routed_and_zero_tiles():
     say("train_fwd T = Np, zero tiles")
     B, H, Np, P = 1, 2, 3, 10

@@ -370,6 +370,37 @@ def test_train_fwd_linear_branch_and_mix_endpoints():
     assert rel_l2(rb["o"], rf["o"]) < 1e-2
 
 
+def test_train_fwd_score_form_is_the_state_form_up_to_rounding():
+    """The two forms of the linear branch are one sum regrouped: without 16-bit
+    rounding they agree to fp32 precision (and with the dense complement of the
+    (a) path); the 16-bit rounding points differ, so with bf16 they differ at
+    bf16 level only.  The form follows the reference's switch, an augmented LUT
+    of at most 4 columns (here T = 2 plus one prefix tail)."""
+    q, k, v, alpha, lut, Np, P = _train_case(seed=8)
+    H, Mb = alpha.shape
+    zero = torch.zeros(H, Mb)
+    sf = O.train_fwd(q, k, v, zero, lut, Np, P, t16=torch.float32, score_form=True)
+    tf = O.train_fwd(q, k, v, zero, lut, Np, P, t16=torch.float32, score_form=False)
+    ol_a, _ = O.cube_jvp(q, k, v, None, None, None, zero, lut, Np, P, t16=torch.float32)
+    assert rel_l2(sf["o_l"], tf["o_l"]) < 1e-5 and rel_l2(sf["o_l"], ol_a) < 1e-5
+    assert (sf["den"] - tf["den"]).abs().max() < 1e-4 * tf["den"].abs().max()
+    sb = O.train_fwd(q, k, v, alpha, lut, Np, P, t16=torch.bfloat16, score_form=True)
+    tb = O.train_fwd(q, k, v, alpha, lut, Np, P, t16=torch.bfloat16, score_form=False)
+    assert not torch.equal(sb["o_l"], tb["o_l"])
+    assert rel_l2(sb["o_l"], tb["o_l"]) < 1e-2
+    # a dropped score term (one selected tile not subtracted) is an O(1) error
+    lut1 = torch.as_tensor(np.asarray(lut))[..., :1]
+    s1 = O.train_fwd(q, k, v, zero, lut1, Np, P, t16=torch.float32, score_form=True)
+    assert rel_l2(s1["o_l"], sf["o_l"]) > 1e-2
+    # the default follows the width of the augmented LUT
+    auto = O.train_fwd(q, k, v, alpha, lut, Np, P, t16=torch.bfloat16)
+    assert lut.shape[-1] + 1 <= 4 and torch.equal(auto["o"], sb["o"])
+    wide = O.route(q, k, 1.0, Np, P)[0]                       # T = 4, 5 columns with the tail
+    auto_w = O.train_fwd(q, k, v, alpha, wide, Np, P, t16=torch.bfloat16)
+    state_w = O.train_fwd(q, k, v, alpha, wide, Np, P, t16=torch.bfloat16, score_form=False)
+    assert torch.equal(auto_w["o"], state_w["o"])
+
+
 def _bwd_case(seed, B=1, H=2, Np=3, P=10, T=2, dtype=torch.float64):
     g = torch.Generator().manual_seed(seed)
     L = Np * 64 + P
