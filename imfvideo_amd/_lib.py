@@ -77,6 +77,10 @@ SIGNATURES = {
     "sla2h_linear_mix_score": (_c_int, [_p, _p, _p, _p, _p, _p, _c_int, _p, _p, _c_int, _c_int,
                                         _c_int, _c_int, _c_i64, _c_int, _c_int, _c_f, _p, _p, _p,
                                         _p]),
+    "sla2h_sla2_fused_workspace_bytes": (ctypes.c_size_t, [_c_int, _c_int, _c_i64, _c_int]),
+    "sla2h_sla2_forward_fused": (_c_int, [_p, _p, _p, _p, _p, _c_int, _p, _p, _p, _p, _p, _p, _p,
+                                          _p, _c_int, _p, _c_int, _c_int, _c_int, _c_int, _c_i64,
+                                          _c_int, _c_int, _c_f, _c_f, _p, _p, _p]),
     "sla2h_quantize_v8f": (_c_int, [_p, _c_int, _c_i64, _c_i64, _c_int, _c_int, _p, _p, _p]),
     "sla2h_quantize_trunc": (_c_int, [_p, _c_int, _c_i64, _c_i64, _c_int, _c_int, _p, _p, _p]),
     "sla2h_sparse_fwd_int8": (_c_int, [_p, _p, _p, _c_int, _p, _p, _p, _p, _p, _c_int, _c_int,

@@ -39,6 +39,7 @@ struct TrainArgs {
   uint16_t* os;
   float* lse;
   uint16_t* qphi;
+  float* os32 = nullptr;  // set: o_s is written here in fp32 instead of os
   int64_t L;
   int Nb, Np, Mb, T, n_tail, nwork, per_xcd;
   int Mq, qshift;  // LUT rows: query blocks of 64 << qshift rows
@@ -218,9 +219,15 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
   if (qok) {
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
-      const uint32_t lo = pack_pair<T16>(acc[ct][0] * rl, acc[ct][1] * rl);
-      const uint32_t hi = pack_pair<T16>(acc[ct][2] * rl, acc[ct][3] * rl);
-      *reinterpret_cast<uint2*>(a.os + (qkbase + qrow) * kT + 16 * ct + 4 * g) = make_uint2(lo, hi);
+      const int64_t oo = (qkbase + qrow) * kT + 16 * ct + 4 * g;
+      if (a.os32 != nullptr) {
+        *reinterpret_cast<f32x4*>(a.os32 + oo) =
+            f32x4{acc[ct][0] * rl, acc[ct][1] * rl, acc[ct][2] * rl, acc[ct][3] * rl};
+      } else {
+        const uint32_t lo = pack_pair<T16>(acc[ct][0] * rl, acc[ct][1] * rl);
+        const uint32_t hi = pack_pair<T16>(acc[ct][2] * rl, acc[ct][3] * rl);
+        *reinterpret_cast<uint2*>(a.os + oo) = make_uint2(lo, hi);
+      }
     }
     if (g == 0) a.lse[qkbase + qrow] = m_i + __log2f(lt);
   }
@@ -242,6 +249,7 @@ struct Fwd16Args {
   uint16_t* os;
   float* lse;
   uint16_t* qphi;
+  float* os32 = nullptr;  // set: o_s is written here in fp32 instead of os
   int64_t L;
   int Nb, Mq, qshift, T, nwork, per_xcd;
   float c;  // fl32(scale * log2(e))
@@ -410,9 +418,15 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd16_kernel(Fwd16Args a) {
   if (qok) {
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
-      const uint32_t lo = pack_pair<T16>(acc[ct][0] * rl, acc[ct][1] * rl);
-      const uint32_t hi = pack_pair<T16>(acc[ct][2] * rl, acc[ct][3] * rl);
-      *reinterpret_cast<uint2*>(a.os + (qkbase + qrow) * kT + 16 * ct + 4 * g) = make_uint2(lo, hi);
+      const int64_t oo = (qkbase + qrow) * kT + 16 * ct + 4 * g;
+      if (a.os32 != nullptr) {
+        *reinterpret_cast<f32x4*>(a.os32 + oo) =
+            f32x4{acc[ct][0] * rl, acc[ct][1] * rl, acc[ct][2] * rl, acc[ct][3] * rl};
+      } else {
+        const uint32_t lo = pack_pair<T16>(acc[ct][0] * rl, acc[ct][1] * rl);
+        const uint32_t hi = pack_pair<T16>(acc[ct][2] * rl, acc[ct][3] * rl);
+        *reinterpret_cast<uint2*>(a.os + oo) = make_uint2(lo, hi);
+      }
     }
     if (g == 0) a.lse[qkbase + qrow] = m_i + __log2f(lt);
   }
@@ -543,12 +557,16 @@ __global__ __launch_bounds__(256) void linear_mix_qat_kernel(
 // num^T -= V_j^T round16(W^T) for contraction chunk ks, with the K slot
 // 8g + e standing for key 16 (2ks + e/4) + 4g + e%4; the A operand V_j^T is
 // read from LDS in that key order.  Tile ids outside [0, Nb) are clamped.
-template <typename T16>
+// FUSED: the mix of the fused Algorithm-2 kernel (models/sla2_vendor/
+// kernel_fused.py:116-124): o_s is fp32, o = a o_s + (1 - a) num / den in
+// fp32 with alpha unrounded, one rounding at the store; o_l and den are not
+// written.
+template <typename T16, bool FUSED = false>
 __global__ __launch_bounds__(256) void linear_mix_score_kernel(
     const uint16_t* __restrict__ qphi, const uint16_t* __restrict__ K,
     const uint16_t* __restrict__ V, const float* __restrict__ Hall,
     const float* __restrict__ zall, const int32_t* __restrict__ lut, int J, int Nb,
-    const uint16_t* __restrict__ o_s, const float* __restrict__ alpha, int alpha_stride,
+    const void* __restrict__ o_s, const float* __restrict__ alpha, int alpha_stride,
     int64_t L, int Mq, int qshift, int H, float eps_l, uint16_t* __restrict__ o,
     uint16_t* __restrict__ o_l, float* __restrict__ den_out) {
   __shared__ __align__(16) uint16_t hT[kT][kT + 8];  // round16(Hall)^T [value ch][key ch]
@@ -672,13 +690,30 @@ __global__ __launch_bounds__(256) void linear_mix_score_kernel(
   dn -= sum_over_groups(wsum);
   dn = dn >= 0.f ? dn + eps_l : dn - eps_l;
   const float rdn = 1.f / dn;
-  const float a16 = T16::to_f32(T16::from_f32(alpha[(int64_t)h * alpha_stride + mq]));
+  const float af = alpha[(int64_t)h * alpha_stride + mq];
+  if (FUSED) {
+    if (qok) {
+      const float* os32 = static_cast<const float*>(o_s);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const int64_t oo = rowoff + 16 * ct + 4 * g;
+        const f32x4 sv = *reinterpret_cast<const f32x4*>(os32 + oo);
+        float ov[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) ov[i] = af * sv[i] + (1.f - af) * (num[ct][i] / dn);
+        *reinterpret_cast<uint2*>(o + oo) =
+            make_uint2(pack_pair<T16>(ov[0], ov[1]), pack_pair<T16>(ov[2], ov[3]));
+      }
+    }
+    return;
+  }
+  const float a16 = T16::to_f32(T16::from_f32(af));
   const float b16 = T16::to_f32(T16::from_f32(1.f - a16));
   if (qok) {
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       const int64_t oo = rowoff + 16 * ct + 4 * g;
-      const uint2 sv = *reinterpret_cast<const uint2*>(o_s + oo);
+      const uint2 sv = *reinterpret_cast<const uint2*>(static_cast<const uint16_t*>(o_s) + oo);
       const uint32_t sw[2] = {sv.x, sv.y};
       float ol[4], ov[4];
 #pragma unroll
@@ -864,6 +899,116 @@ extern "C" int sla2h_linear_mix_score(const void* qphi, const void* k, const voi
     linear_mix_score_kernel<BF16><<<grid, 256, 0, st>>>(QP, Kp, Vp, Hall, zall, lut, J, Nb, OS, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, OL, den);
   else
     linear_mix_score_kernel<F16><<<grid, 256, 0, st>>>(QP, Kp, Vp, Hall, zall, lut, J, Nb, OS, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, OL, den);
+  return (int)hipGetLastError();
+}
+
+extern "C" size_t sla2h_sla2_fused_workspace_bytes(int B, int H, int64_t L, int D) {
+  if (B <= 0 || H <= 0 || L <= 0 || D != kT) return 0;
+  const size_t rows = (size_t)B * H * L;
+  const size_t os32 = (rows * kT * 4 + 255) / 256 * 256, qphi = (rows * kT * 2 + 255) / 256 * 256;
+  return os32 + qphi + rows * 4;
+}
+
+// Fused SLA2 inference forward with the arithmetic of the fused Algorithm-2
+// kernel (_sla2_fwd_fused, models/sla2_vendor/kernel_fused.py:29-124): the
+// sparse branch (INT8 with Q scales per block_m rows, or 16-bit) writes o_s
+// in fp32 to the workspace, then the score-form linear branch against the
+// whole-sequence state and the fp32 mix produce o.  Two launches on one
+// stream; the workspace holds o_s, phi(Q) and the row statistics.
+extern "C" int sla2h_sla2_forward_fused(
+    const void* q, const void* k, const void* v, const int8_t* q8, const float* qs, int block_m,
+    const int8_t* k8, const float* ks, const int8_t* v8f, const float* vs, const void* vt,
+    const float* Hall, const float* zall, const int32_t* lut, int T, const float* alpha,
+    int alpha_stride, int dtype, int B, int H, int64_t L, int D, int bq, float scale,
+    float eps_l, void* workspace, void* o, void* stream) {
+  const bool int8 = q8 != nullptr;
+  SLA2H_CHECK_ARG(q && k && v && Hall && zall && lut && alpha && workspace && o);
+  SLA2H_CHECK_ARG(int8 ? (qs && k8 && ks && v8f && vs) : (vt != nullptr));
+  SLA2H_CHECK_ARG(D == kT && (bq == 64 || bq == 128 || bq == 256) && alpha_stride >= 0);
+  SLA2H_CHECK_ARG(!int8 || ((block_m == 32 || block_m == 64 || block_m == 128 || block_m == 256) &&
+                            bq % block_m == 0));
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(B > 0 && H > 0 && B * H <= 65535 && L > 0 && L * kT * 2 < (1ll << 31));
+  const int Nb = (int)((L + kT - 1) / kT);
+  SLA2H_CHECK_ARG(T >= 1 && T <= Nb && T <= kMaxJ);
+  const int64_t nwork = (int64_t)Nb * B * H;
+  const int64_t per_xcd = (nwork + 7) / 8;
+  SLA2H_CHECK_ARG(8 * per_xcd < (1ll << 31));
+  const size_t rows = (size_t)B * H * L;
+  unsigned char* ws = static_cast<unsigned char*>(workspace);
+  float* os32 = reinterpret_cast<float*>(ws);
+  uint16_t* qphi = reinterpret_cast<uint16_t*>(ws + (rows * kT * 4 + 255) / 256 * 256);
+  float* lse = reinterpret_cast<float*>(ws + (rows * kT * 4 + 255) / 256 * 256 +
+                                        (rows * kT * 2 + 255) / 256 * 256);
+  const int Mq = (int)((L + bq - 1) / bq);
+  const int qshift = bq == 64 ? 0 : (bq == 128 ? 1 : 2);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  const int nblocks = (int)(8 * per_xcd);
+  const bool bf = dtype == SLA2H_DTYPE_BF16;
+  if (int8) {
+    TrainArgs a;
+    a.q = static_cast<const uint16_t*>(q);
+    a.q8 = q8;
+    a.k8 = k8;
+    a.v8f = v8f;
+    a.qs = qs;
+    a.ks = ks;
+    a.vs = vs;
+    a.lut = lut;
+    a.os = nullptr;
+    a.os32 = os32;
+    a.lse = lse;
+    a.qphi = qphi;
+    a.L = L;
+    a.Nb = Nb;
+    a.Np = Nb;
+    a.Mb = Nb;
+    a.T = T;
+    a.n_tail = 0;
+    a.Mq = Mq;
+    a.qshift = qshift;
+    a.Mqs = (int)((L + block_m - 1) / block_m);
+    a.qsb = log2_exact(block_m);
+    a.nwork = (int)nwork;
+    a.per_xcd = (int)per_xcd;
+    a.c2 = scale * 1.4426950408889634f;
+    if (bf)
+      sparse_fwd_qat_kernel<BF16><<<nblocks, 256, 0, st>>>(a);
+    else
+      sparse_fwd_qat_kernel<F16><<<nblocks, 256, 0, st>>>(a);
+  } else {
+    Fwd16Args a;
+    a.q = static_cast<const uint16_t*>(q);
+    a.k = static_cast<const uint16_t*>(k);
+    a.vt = static_cast<const uint16_t*>(vt);
+    a.lut = lut;
+    a.os = nullptr;
+    a.os32 = os32;
+    a.lse = lse;
+    a.qphi = qphi;
+    a.L = L;
+    a.Nb = Nb;
+    a.Mq = Mq;
+    a.qshift = qshift;
+    a.T = T;
+    a.nwork = (int)nwork;
+    a.per_xcd = (int)per_xcd;
+    a.c = scale * 1.4426950408889634f;
+    if (bf)
+      sparse_fwd16_kernel<BF16><<<nblocks, 256, 0, st>>>(a);
+    else
+      sparse_fwd16_kernel<F16><<<nblocks, 256, 0, st>>>(a);
+  }
+  const int err = (int)hipGetLastError();
+  if (err != 0) return err;
+  dim3 grid(Nb, B * H);
+  auto Kp = static_cast<const uint16_t*>(k);
+  auto Vp = static_cast<const uint16_t*>(v);
+  auto O = static_cast<uint16_t*>(o);
+  if (bf)
+    linear_mix_score_kernel<BF16, true><<<grid, 256, 0, st>>>(qphi, Kp, Vp, Hall, zall, lut, T, Nb, os32, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, nullptr, nullptr);
+  else
+    linear_mix_score_kernel<F16, true><<<grid, 256, 0, st>>>(qphi, Kp, Vp, Hall, zall, lut, T, Nb, os32, alpha, alpha_stride, L, Mq, qshift, H, eps_l, O, nullptr, nullptr);
   return (int)hipGetLastError();
 }
 

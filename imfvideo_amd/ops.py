@@ -768,6 +768,50 @@ def sla2_infer(q, k, v, alpha, lut, bq, use_int8=True, qblock=None, eps_l=1e-5,
     return o
 
 
+def sla2_infer_fused(q, k, v, alpha, lut, bq, use_int8=True, block_m=None, eps_l=1e-5,
+                     scale=None):
+    """SLA2 inference forward with the fused Algorithm-2 kernel's arithmetic
+    (sla2_forward_fused, models/sla2_vendor/kernel_fused.py:127-160): Q scales
+    per block_m rows (default max(32, bq // 2), as SLA2.forward picks), o_s in
+    fp32 into the mix, the score-form linear branch against the whole-sequence
+    state.  alpha (H, ceil(L/bq)) or a head-shared (ceil(L/bq),) row.
+    Returns o (16-bit)."""
+    _need_gpu(q, k, v, lut)
+    q, k, v = (_bhld(t, "qkv") for t in (q, k, v))
+    B, H, L, D = q.shape
+    mq = -(-L // bq)
+    lut = lut.to(torch.int32).contiguous()
+    if lut.dim() != 4 or tuple(lut.shape[:3]) != (B, H, mq):
+        raise ValueError(f"lut: expected (B, H, {mq}, T), got {tuple(lut.shape)}")
+    block_m = block_m or max(32, bq // 2)
+    alpha = torch.as_tensor(alpha).detach().to(q.device, torch.float32)
+    if alpha.dim() == 1:
+        alpha, stride = alpha.contiguous(), 0
+    else:
+        alpha = _alpha_rows(alpha, H, mq, q.device)
+        stride = alpha.stride(0)
+    if alpha.shape[-1] != mq:
+        raise ValueError(f"alpha: expected {mq} query blocks, got {alpha.shape[-1]}")
+    st = linear_states_qat(k, v, with_vt=not use_int8)
+    q8 = qs = k8 = ks = v8f = vs = None
+    if use_int8:
+        q8, qs = quantize(q, block_m)
+        k8, ks = quantize(k)
+        v8f, vs = quantize_v8f(v)
+    lib = _lib.load()
+    ws = torch.empty(lib.sla2h_sla2_fused_workspace_bytes(B, H, L, D), device=q.device,
+                     dtype=torch.uint8)
+    o = torch.empty_like(q)
+    scale = D ** -0.5 if scale is None else scale
+    _lib.check(lib.sla2h_sla2_forward_fused(
+        q.data_ptr(), k.data_ptr(), v.data_ptr(), _ptr(q8), _ptr(qs), block_m, _ptr(k8),
+        _ptr(ks), _ptr(v8f), _ptr(vs), _ptr(st.get("vt")), st["Hall"].data_ptr(),
+        st["zall"].data_ptr(), lut.data_ptr(), lut.shape[-1], alpha.data_ptr(), stride,
+        _dtype_code(q), B, H, L, D, bq, float(scale), float(eps_l), ws.data_ptr(),
+        o.data_ptr(), _stream(q.device)), "sla2h_sla2_forward_fused")
+    return o
+
+
 # ---------------------------------------------------------------------------
 # DiT block, training forward / backward: fused SituAndMul
 # (models/imf_dit_video.py:136-171)

@@ -66,10 +66,11 @@ class SLA2(nn.Module):
         use_bf16 picks bf16 over fp16 as the 16-bit type; use_int8 quantises
         the exact branch; learnable_router gives the router trainable
         projections; alpha_init is the mixing weight every (head, query block)
-        starts from.  fused selects the fused inference kernel's conventions
+        starts from.  fused selects the fused Algorithm-2 inference kernel
         (alpha averaged over heads, Q scales per block_m rows, by default
-        max(32, bq // 2)).  backend is accepted and ignored: one set of HIP
-        kernels serves every backend name."""
+        max(32, bq // 2), o_s kept in fp32, the score-form linear branch).
+        backend is accepted and ignored: one set of HIP kernels serves every
+        backend name."""
         super().__init__()
         if bk != ops.E_TILE:
             raise ValueError(f"bk must be {ops.E_TILE}, got {bk}")
@@ -108,12 +109,11 @@ class SLA2(nn.Module):
             # inference (core.py:98-128): INT8 or 16-bit sparse branch, the
             # state-subtraction linear branch and the mix
             a = torch.sigmoid(alpha_logit.detach().float())
-            qblock = self.bq
             if self.fused:  # sla2_forward_fused: head-shared alpha, Q tiles of block_m
-                a = a.mean(0, keepdim=True).expand(H, -1)
-                qblock = self.block_m or max(32, self.bq // 2)
-            o = ops.sla2_infer(qh, kh, vh, a, lut, self.bq, use_int8=self.use_int8,
-                               qblock=qblock)
+                o = ops.sla2_infer_fused(qh, kh, vh, a.mean(0), lut, self.bq,
+                                         use_int8=self.use_int8, block_m=self.block_m)
+            else:
+                o = ops.sla2_infer(qh, kh, vh, a, lut, self.bq, use_int8=self.use_int8)
         if return_sparsity:
             return o.to(out_dtype), 1.0 - topk / -(-L // self.bk)
         return o.to(out_dtype)

@@ -428,6 +428,37 @@ int sla2h_linear_mix_score(const void* qphi, const void* k, const void* v, const
                            void* stream);
 
 /*
+ * Workspace of sla2h_sla2_forward_fused in bytes (0 for invalid sizes).
+ */
+size_t sla2h_sla2_fused_workspace_bytes(int B, int H, int64_t L, int D);
+
+/*
+ * Fused SLA2 inference forward with the arithmetic of the fused Algorithm-2
+ * kernel, for the 1-D module with fused=True:
+ *   sparse branch: INT8 (q8 != NULL; Q scales qs per block_m rows from
+ *     sla2h_quantize, K8, V8 as for sla2h_sparse_fwd_int8) or 16-bit (q8 ==
+ *     NULL; vt the value operand tiles of sla2h_linear_states_qat), o_s = O / l
+ *     kept in fp32;
+ *   linear branch: the score form of sla2h_linear_mix_score against
+ *     round16(Hall), zall (sla2h_linear_states_qat over the whole sequence);
+ *   o = round16(a o_s + (1 - a) num / den) in fp32, a = alpha[h*alpha_stride + m]
+ *     unrounded (the reference averages alpha over heads for this kernel: pass
+ *     alpha_stride 0 with the averaged row).
+ * lut (B,H,ceil(L/bq),T) int32 key blocks of 64 rows; workspace of
+ * sla2h_sla2_fused_workspace_bytes(B,H,L,D) bytes.  Two launches on stream.
+ * Replaces sla2_forward_fused / _sla2_fwd_fused
+ * (models/sla2_vendor/kernel_fused.py:29-160) as called at
+ * models/sla2_vendor/core.py:93-106.
+ */
+int sla2h_sla2_forward_fused(const void* q, const void* k, const void* v, const int8_t* q8,
+                             const float* qs, int block_m, const int8_t* k8, const float* ks,
+                             const int8_t* v8f, const float* vs, const void* vt,
+                             const float* Hall, const float* zall, const int32_t* lut, int T,
+                             const float* alpha, int alpha_stride, int dtype, int B, int H,
+                             int64_t L, int D, int bq, float scale, float eps_l, void* workspace,
+                             void* o, void* stream);
+
+/*
  * 16-bit sparse branch of the 1-D training forward (no INT8): S = q.k^T on
  * 16-bit MFMA (fp32 accumulate) * scale * log2(e) over the routed key blocks
  * of each query block of bq rows (lut (B,H,ceil(L/bq),T)), exact running

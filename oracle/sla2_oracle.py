@@ -713,7 +713,8 @@ def train_dense_f64(q, k, v, alpha_logit, lut, Np, prefix_len, eps=EPS_L, bq=E):
 # 1-D SLA2 blocks (query blocks of bq rows, key blocks of bk = 64 rows):
 # route_blocks and sla2_mla_jvp (models/sla2_mla_jvp.py:51-99, 108-385).
 # ---------------------------------------------------------------------------
-def infer_1d(q, k, v, alpha, lut, bq, int8=True, qblock=None, t16=torch.float16, eps=EPS_L):
+def infer_1d(q, k, v, alpha, lut, bq, int8=True, qblock=None, t16=torch.float16, eps=EPS_L,
+             fused=False):
     """Inference forward of the 1-D SLA2 module (SLA2.forward without gradients,
     models/sla2_vendor/core.py:93-128), blockwise, CPU.
 
@@ -728,6 +729,16 @@ def infer_1d(q, k, v, alpha, lut, bq, int8=True, qblock=None, t16=torch.float16,
     ZALL_j = colsum kphi_j (fp32); H_i = sum_j HALL_j - sum_{j in lut_i} HALL_j,
     z_i likewise (fp32); num = qphi round16(H_i), den = qphi . z_i +- eps,
     o = round16(a o_s + (1 - a) o_l) with o_l = num / den, a fp32.
+
+    fused: the arithmetic of the fused Algorithm-2 kernel instead
+    (_sla2_fwd_fused, models/sla2_vendor/kernel_fused.py:29-124, Q scales per
+    qblock = block_m rows): o_s stays fp32 (O / l, unrounded) into the mix,
+    and the linear branch is the score form against the whole-sequence state,
+    htot = round16(kphi^T V) over all L rows, ztot = colsum kphi (fp32),
+    num = qphi htot - sum_{j in lut_i} round16(W_j) V_j,
+    den = qphi . ztot - sum_j rowsum(W_j) +- eps, W_j = qphi kphi_j^T (fp32);
+    o = round16(a o_s + (1 - a) num / den).  The caller averages alpha over
+    heads, as the reference's SLA2.forward does for this kernel.
 
     q, k, v: (B,H,L,D) float tensors holding 16-bit values; alpha (H, ceil(L/bq))
     after the sigmoid; lut (B,H,ceil(L/bq),T).  Returns dict(o, o_s, lse, qphi,
@@ -800,12 +811,29 @@ def infer_1d(q, k, v, alpha, lut, bq, int8=True, qblock=None, t16=torch.float16,
     hi = htot[:, :, None] - hsel
     zi = ztot[:, :, None] - zsel
     qrow = torch.arange(L) // bq                               # query block of each row
-    num = torch.einsum("bhld,bhlde->bhle", qphi, _round16(hi[:, :, qrow], t16))
-    den = (qphi * zi[:, :, qrow]).sum(-1)
+    if fused:
+        # kernel_fused.py:64-67, 108-114: per selected tile, in the score domain
+        htot16 = _round16(kpt.reshape(B, H, nb * E, D).transpose(-1, -2)
+                          @ vvt.reshape(B, H, nb * E, D), t16)           # (B,H,D,D)
+        ztot = kpt.sum((2, 3))                                           # (B,H,D)
+        num = qphi @ htot16
+        den = (qphi * ztot[:, :, None, :]).sum(-1)
+        lutr = lutq[:, :, qrow]                                          # (B,H,L,T)
+        for j in range(lutq.shape[-1]):
+            kp = torch.gather(kpt, 2, lutr[..., j].view(B, H, L, 1, 1).expand(B, H, L, E, D))
+            vv = torch.gather(vvt, 2, lutr[..., j].view(B, H, L, 1, 1).expand(B, H, L, E, D))
+            w = (qphi[..., None, :] * kp).sum(-1)                        # (B,H,L,E)
+            num = num - (_round16(w, t16)[..., None] * vv).sum(-2)
+            den = den - w.sum(-1)
+        o_sm = o_s
+    else:
+        num = torch.einsum("bhld,bhlde->bhle", qphi, _round16(hi[:, :, qrow], t16))
+        den = (qphi * zi[:, :, qrow]).sum(-1)
+        o_sm = o_s16
     den = torch.where(den >= 0, den + eps, den - eps)
     o_l = num / den[..., None]
     a = torch.as_tensor(alpha).float()[:, qrow][None, :, :, None]
-    o = _round16(a * o_s16 + (1.0 - a) * o_l, t16)
+    o = _round16(a * o_sm + (1.0 - a) * o_l, t16)
     return {"o": o, "o_s": o_s16, "lse": lse, "qphi": qphi, "hall": hall, "zall": zall,
             "o_l": o_l}
 

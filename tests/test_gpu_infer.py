@@ -151,9 +151,65 @@ def test_sla2_module_no_grad_is_the_inference_path(fused):
         a = a.mean(0, keepdim=True).expand(H, -1)
     lut, _ = O.route_1d(q.float(), k.float(), 0.25, 128)
     ref = O.infer_1d(q.float(), k.float(), v.float(), a, lut, 128, int8=True,
-                     qblock=64 if fused else 128, t16=torch.float16)
+                     qblock=64 if fused else 128, t16=torch.float16, fused=fused)
     print(f"  o max {max_abs(o, ref['o']):.2e} rel {rel_l2(o, ref['o']):.2e}", flush=True)
     assert max_abs(o, ref["o"]) < TOL_MAX and rel_l2(o, ref["o"]) < TOL_REL
+
+
+@pytest.mark.parametrize("int8", [True, False])
+@pytest.mark.parametrize("bq", [64, 128, 256])
+@pytest.mark.parametrize("dt", [torch.float16, torch.bfloat16])
+def test_sla2_infer_fused_matches_oracle(int8, bq, dt):
+    """The fused Algorithm-2 arithmetic (kernel_fused.py:29-124): Q scales per
+    block_m = max(32, bq / 2) rows, o_s in fp32 into the mix, the score-form
+    complement against the whole-sequence state, head-shared alpha.  The result
+    is nearer to the oracle's fused form than to its unfused one."""
+    from imfvideo_amd import ops
+    say("sla2_infer_fused int8", int8, "bq", bq, dt)
+    L, H = 1000, 2
+    q, k, v = _inputs(150 + bq, 2, H, L, dt)
+    mq = -(-L // bq)
+    lut, _ = O.route_1d(q.float(), k.float(), 0.25, bq)
+    g = torch.Generator().manual_seed(11)
+    a = (0.1 + 0.8 * torch.rand(mq, generator=g))
+    o = ops.sla2_infer_fused(cuda(q), cuda(k), cuda(v), cuda(a), cuda(torch.as_tensor(lut)), bq,
+                             use_int8=int8)
+    torch.cuda.synchronize()
+    qb = max(32, bq // 2) if int8 else None
+    kw = dict(int8=int8, qblock=qb, t16=dt)
+    ah = a.view(1, -1).expand(H, -1)
+    ref = O.infer_1d(q.float(), k.float(), v.float(), ah, lut, bq, fused=True, **kw)
+    other = O.infer_1d(q.float(), k.float(), v.float(), ah, lut, bq, **kw)
+    got = o.cpu().float()
+    near, far = rel_l2(got, ref["o"]), rel_l2(got, other["o"])
+    print(f"  o max {max_abs(got, ref['o']):.2e} rel {near:.2e} (unfused form {far:.2e})",
+          flush=True)
+    assert max_abs(got, ref["o"]) < TOL_MAX and near < TOL_REL
+    assert near < far
+
+
+@pytest.mark.parametrize("L,topk,bq", [(256, 0.01, 128), (640, 0.5, 256), (700, 0.1, 64)])
+def test_sla2_infer_fused_edge_shapes(L, topk, bq):
+    """T = 1, one ragged block, three batch rows (an empty complement is left
+    out: the score form then returns a rounding residual over eps, in the
+    reference as here)."""
+    from imfvideo_amd import ops
+    say("sla2_infer_fused edge L", L, "topk", topk, "bq", bq)
+    H = 2
+    q, k, v = _inputs(160 + L, 3, H, L, torch.bfloat16)
+    mq = -(-L // bq)
+    lut, T = O.route_1d(q.float(), k.float(), topk, bq)
+    g = torch.Generator().manual_seed(12)
+    a = 0.1 + 0.8 * torch.rand(mq, generator=g)
+    o = ops.sla2_infer_fused(cuda(q), cuda(k), cuda(v), cuda(a), cuda(torch.as_tensor(lut)), bq)
+    torch.cuda.synchronize()
+    ref = O.infer_1d(q.float(), k.float(), v.float(), a.view(1, -1).expand(H, -1), lut, bq,
+                     int8=True, qblock=max(32, bq // 2), t16=torch.bfloat16, fused=True)
+    got = o.cpu().float()
+    print(f"  T {T} o max {max_abs(got, ref['o']):.2e} rel {rel_l2(got, ref['o']):.2e}",
+          flush=True)
+    assert torch.isfinite(got).all()
+    assert max_abs(got, ref["o"]) < TOL_MAX and rel_l2(got, ref["o"]) < TOL_REL
 
 
 # ---------------------------------------------------------------------------

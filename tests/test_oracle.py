@@ -675,6 +675,37 @@ def test_infer_1d_int8_matches_dense_of_the_dequantised_operands(bq, qblock):
     assert torch.equal(got1["o"], got1["o_s"])
 
 
+@pytest.mark.parametrize("int8", [False, True])
+def test_infer_1d_fused_is_the_unfused_op_up_to_rounding(int8):
+    """The fused Algorithm-2 arithmetic regroups the same sums (the complement as
+    whole-sequence state minus the selected tiles' scores) and keeps o_s in
+    fp32: without 16-bit rounding it equals the unfused inference path to fp32
+    precision, with fp16 it differs at fp16 level, and it matches the dense
+    fp64 form as well as the unfused path does."""
+    L, bq = 583, 128
+    q, k, v, lut, alpha = _infer_case(53, L, bq)
+    kw = dict(int8=int8, qblock=64 if int8 else None)
+    f32 = O.infer_1d(q, k, v, alpha, lut, bq, t16=torch.float32, fused=True, **kw)
+    u32 = O.infer_1d(q, k, v, alpha, lut, bq, t16=torch.float32, **kw)
+    assert rel_l2(f32["o"], u32["o"]) < 1e-5
+    f16 = O.infer_1d(q, k, v, alpha, lut, bq, fused=True, **kw)
+    u16 = O.infer_1d(q, k, v, alpha, lut, bq, **kw)
+    assert not torch.equal(f16["o"], u16["o"])
+    assert rel_l2(f16["o"], u16["o"]) < 5e-3
+    # o_s enters the mix unrounded: with alpha = 1 the output is round16(o_s fp32)
+    one = O.infer_1d(q, k, v, torch.ones_like(alpha), lut, bq, fused=True, **kw)
+    assert torch.equal(one["o"], one["o_s"])
+    if not int8:
+        want = O.dense_1d_f64(q.double(), k.double(), v.double(), lut, alpha.double(), bq)
+        assert rel_l2(f16["o"], want) < 1e-3 and max_abs(f16["o"], want) < 2e-3
+    # a dropped correction (one selected tile left in the complement) is an O(1) error
+    lut1 = torch.as_tensor(np.asarray(lut))[..., :1]
+    zero = torch.zeros_like(alpha)
+    d1 = O.infer_1d(q, k, v, zero, lut1, bq, t16=torch.float32, fused=True, **kw)
+    u1 = O.infer_1d(q, k, v, zero, lut, bq, t16=torch.float32, fused=True, **kw)
+    assert rel_l2(d1["o"], u1["o"]) > 1e-2
+
+
 @pytest.mark.parametrize("bq", [128, 256])
 def test_train_fwd_1d_int8_matches_dense_of_the_dequantised_operands(bq):
     # INT8 1-D training forward: sparse branch on the truncation-law Q8 (scales
