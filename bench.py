@@ -91,6 +91,20 @@ def hbm_bytes(B, H, N, Np, tangent):
     return quant, states, layout
 
 
+def complement_work(B, H, Mb, Np, T, tangent):
+    """Algorithmic work of the complement stage: (read bytes, written bytes,
+    MFMA flops).  Reads the tile states (Hb, zb; with the tangent dHb, dzb) and
+    the LUT, writes the per-query-block records (Hc, zc; dHc, dzc); the 0/1-mask
+    GEMM runs on bf16 MFMA with the states split hi + lo (two products) over
+    the padded extents (query blocks to 16, tiles to 32)."""
+    parts = 2 if tangent else 1
+    read = parts * B * H * Np * (64 * 64 + 64) * 4 + B * H * Mb * T * 4
+    write = parts * B * H * Mb * (64 * 64 + 64) * 4
+    mp, npad = -(-Mb // 16) * 16, -(-Np // 32) * 32
+    flops = 2 * 2 * B * H * mp * npad * parts * (64 * 64 + 64)
+    return read, write, flops
+
+
 PROBE_SRC = os.path.join(ROOT, "bench_stream_probe.hip")
 PROBE_LIB = os.path.join(ROOT, "bench_stream_probe.so")
 
@@ -517,6 +531,8 @@ def main():
     s_read = (4 if tangent else 2) * t_in
     ceil_q = stream_ceiling(q_read, qb - q_read)
     ceil_s = stream_ceiling(s_read, sb + sl - s_read)
+    c_read, c_write, c_flops = complement_work(B, H, Mb, Np, T, tangent)
+    ceil_c = stream_ceiling(c_read, c_write)
 
     def hbm_entry(name, alg, moved, ceil):
         us = stage_us[name]
@@ -556,9 +572,17 @@ def main():
         "hbm_kernels": {
             "quant_pool": hbm_entry("quant_pool", qb, qb, ceil_q),
             "linear_states": hbm_entry("linear_states", sb, sb + sl, ceil_s),
+            "complement": dict(hbm_entry("complement", c_read + c_write, c_read + c_write,
+                                         ceil_c),
+                               mfma={"bf16_flops": c_flops,
+                                     "TFLOP/s": round(c_flops / stage_us["complement"] / 1e6, 2),
+                                     "frac": round(c_flops / stage_us["complement"] / 1e6
+                                                   / PEAK_BF16_TFLOPS, 4)}),
             "note": "bytes: algorithmic (each tensor once); frac: of 8 TB/s; ceiling: a "
                     "streaming kernel moving the same bytes at the same read:write mix; "
-                    "frac_of_ceiling = flushed ceiling time / kernel time",
+                    "frac_of_ceiling = flushed ceiling time / kernel time; complement: mask "
+                    "and GEMM kernels together, mfma = the 0/1-mask GEMM's bf16 work (states "
+                    "split hi + lo) against the dense bf16 peak",
         },
     }
     if args.cpu_baseline:
