@@ -393,10 +393,11 @@ __device__ inline float group_sum(float v) {  // over the LPR lanes of a row (al
   return v;
 }
 
-template <int DT, int LPR>
+// OT: the output's type (fp32, or a 16-bit type: the fp32 result rounded once)
+template <int DT, int LPR, int OT = kF32>
 __global__ __launch_bounds__(256) void rms_fwd_vec_kernel(const void* __restrict__ X, int64_t rows,
                                                           int64_t sx, const float* __restrict__ W,
-                                                          float eps, float* __restrict__ Y) {
+                                                          float eps, void* __restrict__ Y) {
   constexpr int D = 8 * LPR, RPW = 64 / LPR;
   const int l = threadIdx.x & 63;
   const int64_t row = ((int64_t)blockIdx.x * 4 + (threadIdx.x >> 6)) * RPW + l / LPR;
@@ -415,15 +416,22 @@ __global__ __launch_bounds__(256) void rms_fwd_vec_kernel(const void* __restrict
   ld8f(W, c0, w);
 #pragma unroll
   for (int e = 0; e < 8; ++e) y[e] = round_to<DT>(x[e] * r) * w[e];
-  if (ok) st8<kF32>(Y, row * D + c0, y);
+  if (ok) st8<OT>(Y, row * D + c0, y);
 }
 
 // backward: 4 passes of 64 / LPR rows per wave, loads first; dw partials of the
 // workgroup's 16 * 64 / LPR rows
-template <int DT, int LPR>
+// DYT = kF32: one fp32 output gradient DY0.  DYT 16-bit: the output gradient
+// is DY0 + DY1 + DY2 summed in fp32 in that order (DY1, DY2 may be null: the
+// gradients of the consumers of a shared 16-bit output), and DADD (fp32, may
+// be null) is added to dx (the gradient the input also receives elsewhere).
+template <int DT, int LPR, int DYT = kF32>
 __global__ __launch_bounds__(256) void rms_bwd_vec_kernel(const void* __restrict__ X, int64_t rows,
                                                           int64_t sx, const float* __restrict__ W,
-                                                          const float* __restrict__ DY, float eps,
+                                                          const void* __restrict__ DY0,
+                                                          const void* __restrict__ DY1,
+                                                          const void* __restrict__ DY2,
+                                                          const float* __restrict__ DADD, float eps,
                                                           void* __restrict__ DX,
                                                           float* __restrict__ DWP) {
   constexpr int D = 8 * LPR, RPW = 64 / LPR, P = 4;
@@ -440,7 +448,22 @@ __global__ __launch_bounds__(256) void rms_bwd_vec_kernel(const void* __restrict
     const int64_t row = row0 + ((int64_t)(k * 4 + w)) * RPW + l / LPR;
     if (row < rows) {
       ld8<DT>(X, row * sx + c0, x[k]);
-      ld8f(DY, row * D + c0, dy[k]);
+      if (DYT == kF32) {
+        ld8f(static_cast<const float*>(DY0), row * D + c0, dy[k]);
+      } else {
+        ld8<DYT>(DY0, row * D + c0, dy[k]);
+        float t[8];
+        if (DY1 != nullptr) {
+          ld8<DYT>(DY1, row * D + c0, t);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dy[k][e] += t[e];
+        }
+        if (DY2 != nullptr) {
+          ld8<DYT>(DY2, row * D + c0, t);
+#pragma unroll
+          for (int e = 0; e < 8; ++e) dy[k][e] += t[e];
+        }
+      }
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) x[k][e] = dy[k][e] = 0.f;
@@ -465,7 +488,15 @@ __global__ __launch_bounds__(256) void rms_bwd_vec_kernel(const void* __restrict
     float dx[8];
 #pragma unroll
     for (int e = 0; e < 8; ++e) dx[e] = r * g[e] - x[k][e] * r3 * mgx;
-    if (row < rows) st8<DT>(DX, row * D + c0, dx);
+    if (row < rows) {
+      if (DYT != kF32 && DADD != nullptr) {
+        float t[8];
+        ld8f(DADD, row * D + c0, t);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) dx[e] = dx[e] + t[e];
+      }
+      st8<DT>(DX, row * D + c0, dx);
+    }
   }
   // combine the wave's row slots (lanes l, l ^ LPR, ...), fixed order
 #pragma unroll
@@ -531,7 +562,7 @@ void launch_rms_bwd(const void* x, int64_t rows, int D, int64_t sx, const float*
   if (lpr) {
     const int64_t rpb = 16 * (64 / lpr);
     const unsigned g = (unsigned)((rows + rpb - 1) / rpb);
-#define SLA2H_RMSB(LPR) rms_bwd_vec_kernel<DT, LPR><<<g, 256, 0, st>>>(x, rows, sx, w, dy, eps, dx, dwp)
+#define SLA2H_RMSB(LPR) rms_bwd_vec_kernel<DT, LPR><<<g, 256, 0, st>>>(x, rows, sx, w, dy, nullptr, nullptr, nullptr, eps, dx, dwp)
     switch (lpr) {
       case 1: SLA2H_RMSB(1); return;
       case 2: SLA2H_RMSB(2); return;
@@ -552,6 +583,42 @@ void launch_rms_bwd(const void* x, int64_t rows, int D, int64_t sx, const float*
     rms_bwd_kernel<DT, 8><<<grid, 256, 0, st>>>(x, rows, D, sx, w, dy, eps, dx, dwp);
   else
     rms_bwd_kernel<DT, 16><<<grid, 256, 0, st>>>(x, rows, D, sx, w, dy, eps, dx, dwp);
+}
+
+// fp32 x, D = 8 LPR: the 16-bit-output forward and the multi-gradient backward
+template <int OT>
+void launch_rms_fwd16(const float* x, int64_t rows, int lpr, int64_t sx, const float* w, float eps,
+                      void* y, hipStream_t st) {
+  const unsigned g = (unsigned)((rows + 4 * (64 / lpr) - 1) / (4 * (64 / lpr)));
+#define SLA2H_RMSF16(LPR) rms_fwd_vec_kernel<kF32, LPR, OT><<<g, 256, 0, st>>>(x, rows, sx, w, eps, y)
+  switch (lpr) {
+    case 1: SLA2H_RMSF16(1); return;
+    case 2: SLA2H_RMSF16(2); return;
+    case 4: SLA2H_RMSF16(4); return;
+    case 8: SLA2H_RMSF16(8); return;
+    case 16: SLA2H_RMSF16(16); return;
+    case 32: SLA2H_RMSF16(32); return;
+    default: SLA2H_RMSF16(64); return;
+  }
+#undef SLA2H_RMSF16
+}
+template <int DYT>
+void launch_rms_bwd_sum(const float* x, int64_t rows, int lpr, int64_t sx, const float* w,
+                        const void* dy0, const void* dy1, const void* dy2, const float* dadd,
+                        float eps, float* dx, float* dwp, hipStream_t st) {
+  const int64_t rpb = 16 * (64 / lpr);
+  const unsigned g = (unsigned)((rows + rpb - 1) / rpb);
+#define SLA2H_RMSBS(LPR) rms_bwd_vec_kernel<kF32, LPR, DYT><<<g, 256, 0, st>>>(x, rows, sx, w, dy0, dy1, dy2, dadd, eps, dx, dwp)
+  switch (lpr) {
+    case 1: SLA2H_RMSBS(1); return;
+    case 2: SLA2H_RMSBS(2); return;
+    case 4: SLA2H_RMSBS(4); return;
+    case 8: SLA2H_RMSBS(8); return;
+    case 16: SLA2H_RMSBS(16); return;
+    case 32: SLA2H_RMSBS(32); return;
+    default: SLA2H_RMSBS(64); return;
+  }
+#undef SLA2H_RMSBS
 }
 
 }  // namespace
@@ -597,6 +664,49 @@ extern "C" int sla2h_rmsnorm_bwd(const void* x, int dtype, int64_t rows, int D, 
     launch_rms_bwd<SLA2H_DTYPE_F16>(x, rows, D, sx, w, dy, eps, dx, dwp, st);
   else
     launch_rms_bwd<kF32>(x, rows, D, sx, w, dy, eps, dx, dwp, st);
+  int err = (int)hipGetLastError();
+  if (err) return err;
+  col_sum_kernel<<<D, 256, 0, st>>>(dwp, nb, D, dw);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_rmsnorm_fwd16(const float* x, int64_t rows, int D, int64_t sx,
+                                   const float* w, float eps, int out_dtype, void* y,
+                                   void* stream) {
+  SLA2H_CHECK_ARG(x && w && y);
+  SLA2H_CHECK_ARG(out_dtype == SLA2H_DTYPE_F16 || out_dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(rows > 0 && D > 0 && sx >= D);
+  const int lpr = rms_vec_lpr<kF32>(x, D, sx);
+  SLA2H_CHECK_ARG(lpr > 0 && reinterpret_cast<uintptr_t>(y) % 16 == 0);
+  SLA2H_CHECK_ARG((rows + 4 * (64 / lpr) - 1) / (4 * (64 / lpr)) < (1ll << 31));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (out_dtype == SLA2H_DTYPE_BF16)
+    launch_rms_fwd16<SLA2H_DTYPE_BF16>(x, rows, lpr, sx, w, eps, y, st);
+  else
+    launch_rms_fwd16<SLA2H_DTYPE_F16>(x, rows, lpr, sx, w, eps, y, st);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_rmsnorm_bwd_sum(const float* x, int64_t rows, int D, int64_t sx,
+                                     const float* w, const void* dy0, const void* dy1,
+                                     const void* dy2, int dy_dtype, const float* dadd, float eps,
+                                     float* dx, float* dw, void* workspace, void* stream) {
+  SLA2H_CHECK_ARG(x && w && dy0 && dx && dw && workspace);
+  SLA2H_CHECK_ARG(dy_dtype == SLA2H_DTYPE_F16 || dy_dtype == SLA2H_DTYPE_BF16);
+  SLA2H_CHECK_ARG(rows > 0 && D > 0 && sx >= D);
+  const int lpr = rms_vec_lpr<kF32>(x, D, sx);
+  SLA2H_CHECK_ARG(lpr > 0);
+  for (const void* p : {dy0, dy1, dy2, static_cast<const void*>(dadd), static_cast<const void*>(dx)})
+    SLA2H_CHECK_ARG(reinterpret_cast<uintptr_t>(p) % 16 == 0);
+  const int64_t rpb = 16 * (64 / lpr);
+  const int64_t nb = (rows + rpb - 1) / rpb;
+  SLA2H_CHECK_ARG(nb < (1ll << 31));
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  float* dwp = static_cast<float*>(workspace);
+  if (dy_dtype == SLA2H_DTYPE_BF16)
+    launch_rms_bwd_sum<SLA2H_DTYPE_BF16>(x, rows, lpr, sx, w, dy0, dy1, dy2, dadd, eps, dx, dwp, st);
+  else
+    launch_rms_bwd_sum<SLA2H_DTYPE_F16>(x, rows, lpr, sx, w, dy0, dy1, dy2, dadd, eps, dx, dwp, st);
   int err = (int)hipGetLastError();
   if (err) return err;
   col_sum_kernel<<<D, 256, 0, st>>>(dwp, nb, D, dw);

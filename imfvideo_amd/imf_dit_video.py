@@ -74,6 +74,49 @@ class RMSNorm(nn.Module):
         return normed.to(x.dtype) * self.weight
 
 
+class _NormFanoutFunction(torch.autograd.Function):
+    """RMSNorm of the fp32 residual stream for n linear consumers under
+    autocast: one HIP kernel writes the normalised rows already rounded to the
+    autocast dtype (what each consumer's cast would produce) and the function
+    returns them as n outputs, one per consumer, plus x itself for its other
+    use (the residual add).  The backward sums the consumers' 16-bit gradients
+    in fp32 and adds the residual's gradient to dx in the same kernel."""
+
+    @staticmethod
+    def forward(ctx, x, weight, eps, n, dtype):
+        from . import ops
+        y = ops.rmsnorm_fwd16(x, weight, eps, dtype)
+        ctx.eps = eps
+        ctx.save_for_backward(x, weight)
+        return (x.view_as(x), y) + tuple(y.view_as(y) for _ in range(n - 1))
+
+    @staticmethod
+    def backward(ctx, dpass, *dys):
+        from . import ops
+        x, weight = ctx.saved_tensors
+        dys = [d for d in dys if d is not None]
+        if not dys:
+            return dpass, None, None, None, None
+        dx, dw = ops.rmsnorm_bwd_sum(dys, x, weight, ctx.eps, dadd=dpass)
+        return dx, dw.to(weight.dtype), None, None, None
+
+
+def _norm_fanout(x, norm, n):
+    """(x, n consumer inputs) of norm(x): the fused kernels when x is the fp32
+    residual stream on the GPU under a 16-bit autocast, else (x, norm(x) n
+    times)."""
+    D = x.shape[-1]
+    if (x.is_cuda and x.dtype == torch.float32 and torch.is_autocast_enabled("cuda")
+            and norm.weight.dtype == torch.float32 and norm.weight.is_cuda
+            and 8 <= D <= 512 and D & (D - 1) == 0 and x.is_contiguous()
+            and x.data_ptr() % 16 == 0
+            and torch.get_autocast_dtype("cuda") in (torch.bfloat16, torch.float16)):
+        return _NormFanoutFunction.apply(x, norm.weight, float(norm.eps), n,
+                                         torch.get_autocast_dtype("cuda"))
+    y = norm(x)
+    return (x,) + (y,) * n
+
+
 class _SituMulFunction(torch.autograd.Function):
     """SituAndMul on the GPU: one fused HIP kernel forward, one backward; saves
     only the inputs (the eager form keeps several fp32 intermediates)."""
@@ -137,7 +180,11 @@ class SwiGLUMlp(nn.Module):
         self.act = SituAndMul(beta=situ_beta, linear_beta=situ_linear_beta)
 
     def forward(self, x):
-        return self.w2(self.act(self.w1(x), self.w3(x)))
+        return self._forward(x, x)
+
+    def _forward(self, x1, x3):
+        """The MLP with w1 reading x1 and w3 reading x3 (the same values)."""
+        return self.w2(self.act(self.w1(x1), self.w3(x3)))
 
 
 class _RopeFunction(torch.autograd.Function):
@@ -231,12 +278,17 @@ class MLAAttention(nn.Module):
         self.k_norm = RMSNorm(qk_nope_head_dim, eps=norm_eps)
 
     def forward(self, x, rope_cos, rope_sin):
-        b, l, _ = x.shape
+        return self._forward(x, x, x, rope_cos, rope_sin)
+
+    def _forward(self, xq, xkv, xg, rope_cos, rope_sin):
+        """The sublayer with q_a_proj, kv_a_proj and g_proj reading xq, xkv and
+        xg (the same values)."""
+        b, l, _ = xq.shape
         H = self.num_heads
         dn, dr, dv = self.qk_nope_head_dim, self.qk_rope_head_dim, self.v_head_dim
-        q = self.q_b_proj(self.q_a_layernorm(self.q_a_proj(x))).reshape(b, l, H, dn + dr)
+        q = self.q_b_proj(self.q_a_layernorm(self.q_a_proj(xq))).reshape(b, l, H, dn + dr)
         q_nope, q_rope = q.split([dn, dr], dim=-1)
-        kv_latent, k_rope = self.kv_a_proj(x).split([self.kv_lora_rank, dr], dim=-1)
+        kv_latent, k_rope = self.kv_a_proj(xkv).split([self.kv_lora_rank, dr], dim=-1)
         kv = self.kv_b_proj(self.kv_a_layernorm(kv_latent)).reshape(b, l, H, dn + dv)
         k_nope, v = kv.split([dn, dv], dim=-1)
         q_nope, k_nope = self.q_norm(q_nope), self.k_norm(k_nope)
@@ -246,7 +298,7 @@ class MLAAttention(nn.Module):
         k = torch.cat([k_nope, k_rope], dim=-1)
         attn = self.attn_impl(q, k, v).reshape(b, l, H * dv)
         if self.use_output_gate:
-            attn = attn * torch.sigmoid(self.g_proj(x))
+            attn = attn * torch.sigmoid(self.g_proj(xg))
         return self.out_proj(attn)
 
 
@@ -310,5 +362,12 @@ class TransformerBlock(nn.Module):
                                                        init_constant=weight_init_constant)
 
     def forward(self, x, rope_cos, rope_sin):
-        x = _residual(x, self.attn(self.norm1(x), rope_cos, rope_sin), self.attn_scale)
-        return _residual(x, self.mlp(self.norm2(x)), self.mlp_scale)
+        # each norm's output feeds several linears (three in the attention with
+        # its output gate, two in the MLP); _norm_fanout hands each its own copy
+        na = 3 if self.attn.use_output_gate else 2
+        x, *n1 = _norm_fanout(x, self.norm1, na)
+        if na == 2:
+            n1.append(n1[0])
+        x = _residual(x, self.attn._forward(*n1, rope_cos, rope_sin), self.attn_scale)
+        x, n2a, n2b = _norm_fanout(x, self.norm2, 2)
+        return _residual(x, self.mlp._forward(n2a, n2b), self.mlp_scale)

@@ -896,6 +896,49 @@ def rmsnorm_bwd(dy, x, w, eps):
     return dx, dw
 
 
+_F16_CODES = {torch.float16: 0, torch.bfloat16: 1}
+
+
+def rmsnorm_fwd16(x, w, eps, dtype):
+    """round16(rmsnorm_fwd(x, w, eps)) in `dtype` (bf16 / fp16) for an fp32 x of
+    a power-of-two width <= 512: the norm and the autocast cast of its output
+    in one pass."""
+    _need_gpu(x, w)
+    if x.dtype != torch.float32 or dtype not in _F16_CODES:
+        raise ValueError("rmsnorm_fwd16: fp32 x and a 16-bit output dtype")
+    x2, D, sx = _rows_view(x)
+    w = w.detach().to(torch.float32).contiguous()
+    y = torch.empty(x.shape, device=x.device, dtype=dtype)
+    _lib.check(_lib.load().sla2h_rmsnorm_fwd16(
+        x2.data_ptr(), x2.shape[0], D, sx, w.data_ptr(), float(eps), _F16_CODES[dtype],
+        y.data_ptr(), _stream(x.device)), "sla2h_rmsnorm_fwd16")
+    return y
+
+
+def rmsnorm_bwd_sum(dys, x, w, eps, dadd=None):
+    """(dx fp32, dw fp32) of rmsnorm_fwd16 for output gradients `dys` (1 to 3
+    tensors of one 16-bit dtype, summed in fp32 in list order); dadd (fp32 or
+    None) is added to dx."""
+    _need_gpu(x, w, *dys)
+    if not 1 <= len(dys) <= 3 or len({d.dtype for d in dys}) != 1 or dys[0].dtype not in _F16_CODES:
+        raise ValueError("rmsnorm_bwd_sum: 1 to 3 output gradients of one 16-bit dtype")
+    x2, D, sx = _rows_view(x)
+    w = w.detach().to(torch.float32).contiguous()
+    dys = [d.contiguous() for d in dys]
+    dadd = None if dadd is None else dadd.to(torch.float32).contiguous()
+    dx = torch.empty(x.shape, device=x.device, dtype=torch.float32)
+    dw = torch.empty(D, device=x.device, dtype=torch.float32)
+    lib = _lib.load()
+    ws = torch.empty(lib.sla2h_rmsnorm_bwd_workspace_bytes(x2.shape[0], D) // 4,
+                     device=x.device, dtype=torch.float32)
+    ptr = lambda i: dys[i].data_ptr() if i < len(dys) else None
+    _lib.check(lib.sla2h_rmsnorm_bwd_sum(
+        x2.data_ptr(), x2.shape[0], D, sx, w.data_ptr(), ptr(0), ptr(1), ptr(2),
+        _F16_CODES[dys[0].dtype], _ptr(dadd), float(eps), dx.data_ptr(), dw.data_ptr(),
+        ws.data_ptr(), _stream(x.device)), "sla2h_rmsnorm_bwd_sum")
+    return dx, dw
+
+
 # ---------------------------------------------------------------------------
 # DiT block, training forward / backward: RoPE (models/imf_dit_video.py:266-284)
 # ---------------------------------------------------------------------------

@@ -309,6 +309,29 @@ int sla2h_rmsnorm_bwd(const void* x, int dtype, int64_t rows, int D, int64_t sx,
                       void* stream);
 
 /*
+ * The same RMSNorm for an fp32 residual stream feeding 16-bit consumers (the
+ * block's linears under autocast): y16 = round16(x r w) in out_dtype, the
+ * fp32 output of sla2h_rmsnorm_fwd rounded once (what the consumers' casts
+ * would produce), contiguous (rows, D).  Backward: the output gradient is
+ * dy0 + dy1 + dy2 (16-bit, dy1 / dy2 may be NULL), summed in fp32 in that
+ * order (the consumers' gradients, each cast to fp32 as autocast's cast
+ * backward does), then sla2h_rmsnorm_bwd's math, plus dadd (fp32 or NULL:
+ * the gradient x receives from its other use, the residual add) added to dx
+ * (fp32).  D a power of two <= 512; every pointer 16-byte aligned; workspace
+ * of sla2h_rmsnorm_bwd_workspace_bytes.  Replaces RMSNorm.forward
+ * (models/imf_dit_video.py:129-133) at norm1 / norm2 of TransformerBlock.forward
+ * (:529-532) under torch.autocast, the casts of its output at the linears that
+ * read it (:436, :440, :466; :187) and the fp32 gradient accumulations of the
+ * backward.
+ */
+int sla2h_rmsnorm_fwd16(const float* x, int64_t rows, int D, int64_t sx, const float* w,
+                        float eps, int out_dtype, void* y, void* stream);
+int sla2h_rmsnorm_bwd_sum(const float* x, int64_t rows, int D, int64_t sx, const float* w,
+                          const void* dy0, const void* dy1, const void* dy2, int dy_dtype,
+                          const float* dadd, float eps, float* dx, float* dw, void* workspace,
+                          void* stream);
+
+/*
  * RoPE of the DiT block's training forward and its backward: channel pairs
  * (2i, 2i+1) of x (B, L, H, hd), strides sb / sl / sh elements and unit
  * channel stride, rotated by the angles of token l (cos_t / sin_t (L, hd/2)

@@ -151,6 +151,97 @@ def test_rmsnorm_forward_backward(case):
     assert ((dwg - dwc).abs().max() / dwc.abs().max()).item() < tol
 
 
+@pytest.mark.parametrize("dt,n", [(torch.bfloat16, 3), (torch.bfloat16, 2), (torch.float16, 3)])
+def test_norm_fanout_under_autocast(dt, n):
+    """The block's residual-stream RMSNorm with n linear consumers under
+    autocast: the fused forward equals the cast of the module's fp32 output bit
+    for bit, and the backward (the consumers' 16-bit gradients summed in fp32,
+    plus the residual's gradient of x) matches eager autograd of
+    x + norm(x).to(dt) used n times, on the CPU in fp32."""
+    from imfvideo_amd.imf_dit_video import RMSNorm, _norm_fanout
+    say("norm fan-out", dt, n)
+    g = torch.Generator().manual_seed(n + (1 if dt == torch.float16 else 0))
+    D = 512
+    x = torch.randn(2, 777, D, generator=g) * 2
+    w = 1 + 0.5 * torch.randn(D, generator=g)
+    dys = [torch.randn(2, 777, D, generator=g).to(dt) for _ in range(n)]
+    dpass = torch.randn(2, 777, D, generator=g)
+    m = RMSNorm(D, eps=1e-6).cuda()
+    with torch.no_grad():
+        m.weight.copy_(w)
+    xg = x.cuda().requires_grad_(True)
+    with torch.autocast("cuda", dtype=dt):
+        outs = _norm_fanout(xg, m, n)
+    xp, ys = outs[0], outs[1:]
+    assert len(ys) == n and all(y.dtype == dt for y in ys)
+    want = _rms_eager(x, w, 1e-6).to(dt)
+    assert torch.equal(ys[0].cpu(), want) or (ys[0].cpu().float() - want.float()).abs().max() <= \
+        ULP[dt] * want.float().abs().max()
+    torch.autograd.backward([xp] + list(ys), [dpass.cuda()] + [d.cuda() for d in dys])
+    torch.cuda.synchronize()
+    xc = x.clone().requires_grad_(True)
+    wc = w.clone().requires_grad_(True)
+    yc = _rms_eager(xc, wc, 1e-6)
+    (xc * 1.0).backward(dpass, retain_graph=True)
+    yc.backward(sum(d.float() for d in dys))
+    ok = ((xg.grad.cpu() - xc.grad).abs() <= 1e-5 * xc.grad.abs() + 1e-5 * xc.grad.abs().max()).all()
+    print(f"  dx max rel {((xg.grad.cpu() - xc.grad).abs().max() / xc.grad.abs().max()).item():.2e}",
+          flush=True)
+    assert ok
+    dwg = m.weight.grad.cpu()
+    assert ((dwg - wc.grad).abs().max() / wc.grad.abs().max()).item() < 1e-5
+
+
+def test_block_forward_backward_fanout_matches_plain_norms():
+    """A TransformerBlock under bf16 autocast with the fused norm fan-out and
+    the same block with the fan-out switched off (norm(x) then the consumers'
+    own casts) agree: outputs bit for bit, gradients to fp32 summation order."""
+    from functools import partial
+    import imfvideo_amd.imf_dit_video as M
+    from imfvideo_amd.sla2_cube_qat import SLA2CubeQATAttentionImpl
+    say("block with / without the norm fan-out")
+    torch.manual_seed(0)
+    impl = partial(SLA2CubeQATAttentionImpl, seq_len=640, num_heads=8, grid=(4, 8, 20),
+                   tile=(4, 4, 4), topk=0.5, pre_permuted=True)
+    blk = M.TransformerBlock(512, 8, 256, 128, 32, 32, 64, mlp_ratio=4,
+                             weight_init_constant=0.5, attn_impl=impl).cuda()
+    with torch.no_grad():
+        blk.attn_scale.fill_(0.1)
+        blk.mlp_scale.fill_(0.1)
+    g = torch.Generator().manual_seed(1)
+    L = 640
+    x = torch.randn(2, L, 512, generator=g).cuda()
+    cos, sin = (t.cuda() for t in M.precompute_axial_rope_3d(32, (4, 8, 20), 0,
+                                                             axis_dims=(8, 12, 12)))
+    dy = torch.randn(2, L, 512, generator=g).cuda()
+
+    def run(fanout):
+        saved = M._norm_fanout
+        if not fanout:
+            M._norm_fanout = lambda x, norm, n: (x,) + (norm(x),) * n
+        try:
+            blk.zero_grad(set_to_none=True)
+            xg = x.clone().requires_grad_(True)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                out = blk(xg, cos, sin)
+            out.backward(dy)
+            torch.cuda.synchronize()
+            return out.detach(), xg.grad, {k: p.grad.clone() for k, p in blk.named_parameters()
+                                           if p.grad is not None}
+        finally:
+            M._norm_fanout = saved
+
+    o1, dx1, g1 = run(True)
+    o0, dx0, g0 = run(False)
+    assert torch.equal(o1, o0)
+    rel = lambda a, b: ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+    print(f"  dx rel {rel(dx1, dx0):.2e}", flush=True)
+    assert rel(dx1, dx0) < 1e-5
+    assert g1.keys() == g0.keys() and len(g0) > 10
+    for k in g0:
+        assert rel(g1[k], g0[k]) < 1e-4, k
+
+
 def _rope_eager(x, c, s):
     """apply_rotary_pos_emb's eager expression (models/imf_dit_video.py:266-284)."""
     xf = x.float()
