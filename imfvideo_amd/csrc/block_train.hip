@@ -837,6 +837,97 @@ extern "C" int sla2h_residual_scale_fwd(const float* x, const void* a, int dtype
   return (int)hipGetLastError();
 }
 
+// ---------------------------------------------------------------------------
+// Output gate of the MLA sublayer (models/imf_dit_video.py:466, attn *
+// sigmoid(g) on 16-bit tensors under autocast), eight elements per thread:
+//   s = round16(1 / (1 + exp(-g))), out = round16(a s);
+//   backward: da = round16(dout s), ds = round16(dout a),
+//   dg = round16(round16(ds round16(1 - s)) s)  (s recomputed from g,
+//   bit-identical; torch's GPU sigmoid backward computes a (1 - b) b in the
+//   16-bit type itself, one rounding per operation).
+// ---------------------------------------------------------------------------
+namespace sla2h {
+namespace {
+
+template <int DT>
+__device__ inline float gate_sig(float g) {
+  return round_to<DT>(1.f / (1.f + expf(-g)));
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void gate_fwd_kernel(const void* __restrict__ A,
+                                                       const void* __restrict__ G, int64_t n8,
+                                                       void* __restrict__ O) {
+#pragma clang fp contract(off)
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  float a[8], g[8], o[8];
+  Vec<DT>::ld(A, 8 * i, a);
+  Vec<DT>::ld(G, 8 * i, g);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = a[e] * gate_sig<DT>(g[e]);
+  Vec<DT>::st(O, 8 * i, o);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void gate_bwd_kernel(const void* __restrict__ DO,
+                                                       const void* __restrict__ A,
+                                                       const void* __restrict__ G, int64_t n8,
+                                                       void* __restrict__ DA,
+                                                       void* __restrict__ DG) {
+#pragma clang fp contract(off)
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  float d[8], a[8], g[8], da[8], dg[8];
+  Vec<DT>::ld(DO, 8 * i, d);
+  Vec<DT>::ld(A, 8 * i, a);
+  Vec<DT>::ld(G, 8 * i, g);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float sg = gate_sig<DT>(g[e]);
+    da[e] = d[e] * sg;
+    const float ds = round_to<DT>(d[e] * a[e]);
+    dg[e] = round_to<DT>(ds * round_to<DT>(1.f - sg)) * sg;
+  }
+  Vec<DT>::st(DA, 8 * i, da);
+  Vec<DT>::st(DG, 8 * i, dg);
+}
+
+}  // namespace
+}  // namespace sla2h
+
+extern "C" int sla2h_gate_mul_fwd(const void* a, const void* g, int dtype, int64_t n, void* out,
+                                  void* stream) {
+  SLA2H_CHECK_ARG(a && g && out && n > 0 && n % 8 == 0);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  for (const void* p : {a, g, static_cast<const void*>(out)})
+    SLA2H_CHECK_ARG(reinterpret_cast<uintptr_t>(p) % 16 == 0);
+  const unsigned grid = grid_of(n / 8);
+  SLA2H_CHECK_ARG(grid > 0);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SLA2H_DTYPE_BF16)
+    gate_fwd_kernel<SLA2H_DTYPE_BF16><<<grid, 256, 0, st>>>(a, g, n / 8, out);
+  else
+    gate_fwd_kernel<SLA2H_DTYPE_F16><<<grid, 256, 0, st>>>(a, g, n / 8, out);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_gate_mul_bwd(const void* dout, const void* a, const void* g, int dtype,
+                                  int64_t n, void* da, void* dg, void* stream) {
+  SLA2H_CHECK_ARG(dout && a && g && da && dg && n > 0 && n % 8 == 0);
+  SLA2H_CHECK_ARG(dtype == SLA2H_DTYPE_F16 || dtype == SLA2H_DTYPE_BF16);
+  for (const void* p : {dout, a, g, static_cast<const void*>(da), static_cast<const void*>(dg)})
+    SLA2H_CHECK_ARG(reinterpret_cast<uintptr_t>(p) % 16 == 0);
+  const unsigned grid = grid_of(n / 8);
+  SLA2H_CHECK_ARG(grid > 0);
+  hipStream_t st = static_cast<hipStream_t>(stream);
+  if (dtype == SLA2H_DTYPE_BF16)
+    gate_bwd_kernel<SLA2H_DTYPE_BF16><<<grid, 256, 0, st>>>(dout, a, g, n / 8, da, dg);
+  else
+    gate_bwd_kernel<SLA2H_DTYPE_F16><<<grid, 256, 0, st>>>(dout, a, g, n / 8, da, dg);
+  return (int)hipGetLastError();
+}
+
 extern "C" size_t sla2h_residual_scale_bwd_workspace_bytes(int64_t rows, int D) {
   return sla2h_rmsnorm_bwd_workspace_bytes(rows, D);
 }

@@ -117,6 +117,34 @@ def _norm_fanout(x, norm, n):
     return (x,) + (y,) * n
 
 
+class _GateMulFunction(torch.autograd.Function):
+    """a * sigmoid(g) on 16-bit GPU tensors: one HIP kernel forward, one
+    backward (sigmoid recomputed from g); saves a and g only."""
+
+    @staticmethod
+    def forward(ctx, a, g):
+        from . import ops
+        ctx.save_for_backward(a, g)
+        return ops.gate_mul_fwd(a, g)
+
+    @staticmethod
+    def backward(ctx, dout):
+        from . import ops
+        a, g = ctx.saved_tensors
+        return ops.gate_mul_bwd(dout, a, g)
+
+
+def _gate_mul(a, g):
+    """a * sigmoid(g): the fused kernels for 16-bit GPU tensors of one shape and
+    dtype (16-byte aligned, a multiple of 8 elements), else the eager form."""
+    if (a.is_cuda and g.is_cuda and a.dtype == g.dtype and a.shape == g.shape
+            and a.dtype in (torch.bfloat16, torch.float16) and a.numel() % 8 == 0
+            and a.is_contiguous() and g.is_contiguous()
+            and a.data_ptr() % 16 == 0 and g.data_ptr() % 16 == 0):
+        return _GateMulFunction.apply(a, g)
+    return a * torch.sigmoid(g)
+
+
 class _SituMulFunction(torch.autograd.Function):
     """SituAndMul on the GPU: one fused HIP kernel forward, one backward; saves
     only the inputs (the eager form keeps several fp32 intermediates)."""
@@ -298,7 +326,7 @@ class MLAAttention(nn.Module):
         k = torch.cat([k_nope, k_rope], dim=-1)
         attn = self.attn_impl(q, k, v).reshape(b, l, H * dv)
         if self.use_output_gate:
-            attn = attn * torch.sigmoid(self.g_proj(xg))
+            attn = _gate_mul(attn, self.g_proj(xg))
         return self.out_proj(attn)
 
 

@@ -899,6 +899,29 @@ def rmsnorm_bwd(dy, x, w, eps):
 _F16_CODES = {torch.float16: 0, torch.bfloat16: 1}
 
 
+def gate_mul_fwd(a, g):
+    """a * sigmoid(g) for 16-bit a, g of one shape and dtype (torch's rounding)."""
+    _need_gpu(a, g)
+    a, g = a.contiguous(), g.contiguous()
+    out = torch.empty_like(a)
+    _lib.check(_lib.load().sla2h_gate_mul_fwd(a.data_ptr(), g.data_ptr(), _F16_CODES[a.dtype],
+                                              a.numel(), out.data_ptr(), _stream(a.device)),
+               "sla2h_gate_mul_fwd")
+    return out
+
+
+def gate_mul_bwd(dout, a, g):
+    """(da, dg) of gate_mul_fwd for the output gradient dout."""
+    _need_gpu(dout, a, g)
+    dout, a, g = dout.to(a.dtype).contiguous(), a.contiguous(), g.contiguous()
+    da, dg = torch.empty_like(a), torch.empty_like(g)
+    _lib.check(_lib.load().sla2h_gate_mul_bwd(dout.data_ptr(), a.data_ptr(), g.data_ptr(),
+                                              _F16_CODES[a.dtype], a.numel(), da.data_ptr(),
+                                              dg.data_ptr(), _stream(a.device)),
+               "sla2h_gate_mul_bwd")
+    return da, dg
+
+
 def rmsnorm_fwd16(x, w, eps, dtype):
     """round16(rmsnorm_fwd(x, w, eps)) in `dtype` (bf16 / fp16) for an fp32 x of
     a power-of-two width <= 512: the norm and the autocast cast of its output

@@ -324,6 +324,21 @@ int sla2h_rmsnorm_bwd(const void* x, int dtype, int64_t rows, int D, int64_t sx,
  * read it (:436, :440, :466; :187) and the fp32 gradient accumulations of the
  * backward.
  */
+/*
+ * The MLA sublayer's output gate on 16-bit tensors (autocast), n elements
+ * (n % 8 == 0, 16-byte aligned, same dtype):
+ *   s = round16(1 / (1 + exp(-g))), out = round16(a s);
+ *   backward: da = round16(dout s),
+ *   dg = round16(round16(round16(dout a) round16(1 - s)) s),
+ * the rounding points of torch's GPU sigmoid, mul and their backward (the
+ * sigmoid backward works in the 16-bit type, one rounding per operation).  Replaces
+ * attn * torch.sigmoid(self.g_proj(x)) (models/imf_dit_video.py:466).
+ */
+int sla2h_gate_mul_fwd(const void* a, const void* g, int dtype, int64_t n, void* out,
+                       void* stream);
+int sla2h_gate_mul_bwd(const void* dout, const void* a, const void* g, int dtype, int64_t n,
+                       void* da, void* dg, void* stream);
+
 int sla2h_rmsnorm_fwd16(const float* x, int64_t rows, int D, int64_t sx, const float* w,
                         float eps, int out_dtype, void* y, void* stream);
 int sla2h_rmsnorm_bwd_sum(const float* x, int64_t rows, int D, int64_t sx, const float* w,

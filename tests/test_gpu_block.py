@@ -192,6 +192,32 @@ def test_norm_fanout_under_autocast(dt, n):
     assert ((dwg - wc.grad).abs().max() / wc.grad.abs().max()).item() < 1e-5
 
 
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_gate_mul_matches_torch(dt):
+    """The fused output gate a * sigmoid(g) against torch's own elementwise
+    kernels on the same 16-bit GPU tensors (sigmoid, mul and their backward):
+    forward and both gradients within one unit in the last place (the
+    exponential's implementation may differ by an fp32 ulp)."""
+    from imfvideo_amd.imf_dit_video import _GateMulFunction
+    say("gate mul", dt)
+    g = torch.Generator().manual_seed(4)
+    a = (torch.randn(2, 999, 512, generator=g) * 3).to(dt).cuda()
+    gt = (torch.randn(2, 999, 512, generator=g) * 4).to(dt).cuda()
+    dout = torch.randn(2, 999, 512, generator=g).to(dt).cuda()
+    a1, g1 = a.clone().requires_grad_(True), gt.clone().requires_grad_(True)
+    o1 = _GateMulFunction.apply(a1, g1)
+    o1.backward(dout)
+    a2, g2 = a.clone().requires_grad_(True), gt.clone().requires_grad_(True)
+    o2 = a2 * torch.sigmoid(g2)
+    o2.backward(dout)
+    torch.cuda.synchronize()
+    for got, want in ((o1, o2), (a1.grad, a2.grad), (g1.grad, g2.grad)):
+        got, want = got.detach().float().cpu(), want.detach().float().cpu()
+        bad = (got - want).abs() > ULP[dt] * want.abs() + 1e-30
+        print(f"  differ {bad.float().mean().item():.2e}", flush=True)
+        assert not bad.any()
+
+
 def test_block_forward_backward_fanout_matches_plain_norms():
     """A TransformerBlock under bf16 autocast with the fused norm fan-out and
     the same block with the fan-out switched off (norm(x) then the consumers'
