@@ -313,18 +313,20 @@ def test_rope_forward_backward(case):
     assert within(xg.grad, xc.grad)
 
 
+@pytest.mark.parametrize("dim", [512, 100])
 @pytest.mark.parametrize("dt", [torch.bfloat16, torch.float32])
-def test_residual_scale_forward_backward(dt):
+def test_residual_scale_forward_backward(dt, dim):
     """x + a * scale (the block's ReZero residual): forward and da bit-identical
     to the eager expression on the CPU (product and sum rounded separately);
-    the scale gradient, a sum over rows in another order, within 1e-6."""
+    the scale gradient, a sum over rows in another order, within 1e-6.  A
+    width of 512 takes the 16-byte-access forward, 100 the per-element one."""
     from imfvideo_amd.imf_dit_video import _residual
-    say("residual scale", dt)
+    say("residual scale", dt, dim)
     g = torch.Generator().manual_seed(11)
-    x = torch.randn(2, 333, 512, generator=g)
-    a = torch.randn(2, 333, 512, generator=g).to(dt)
-    s = (0.1 * torch.randn(512, generator=g))
-    dy = torch.randn(2, 333, 512, generator=g)
+    x = torch.randn(2, 333, dim, generator=g)
+    a = torch.randn(2, 333, dim, generator=g).to(dt)
+    s = (0.1 * torch.randn(dim, generator=g))
+    dy = torch.randn(2, 333, dim, generator=g)
     xc, ac, sc = (t.clone().requires_grad_(True) for t in (x, a, s))
     yc = xc + ac * sc
     yc.backward(dy)
