@@ -142,6 +142,21 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
 
   // MASK: the tile reaches past L (its keys there are masked); other tiles
   // skip the per-key test
+  // Unmasked tiles (all but a ragged last one) spend about half the VALU work
+  // per score of the reference's written steps:
+  //  * the tile's row maximum comes from the integer scores: with c > 0 and
+  //    monotonic rounding, max_j fl(s_j c) = fl(max_j s_j c), one v_max3 per
+  //    two scores instead of a conversion, two products and a maximum each;
+  //  * the exponent is one fma(s, c, -m) with c = fl(sq sk scale log2 e)
+  //    (the reference rounds s sq sk, then the product by scale log2 e, then
+  //    the difference: the results differ by an ulp or two of the exponent);
+  //  * P8 = rne(127 p) is read from the low byte of fl(127 p + 2^23) (0..127
+  //    for p <= 1 + 2^-20) and four of them are packed by byte permutes.
+  //    rne(127 p) equals trunc(127 p + 0.5) exactly: 127 p lies on a
+  //    half-integer only for p = 1/2 (127 is odd and prime), where both give
+  //    64; the reference's trunc(fl(127 p + 0.5)) differs where that sum
+  //    rounds up onto an integer (one entry in about 10^5).
+  // The masked tail tile keeps the reference's rounding steps.
   auto tile = [&](const Frags& f, int j, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
@@ -149,16 +164,28 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
     const int64_t key0 = (int64_t)n * kT + 4 * g;
     float s[16];
     float lm = -INFINITY;
+    const float c = sqk * a.c2;
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
       const i32x4 si = mfma_i8_16x16x64(f.k[kb], q8f, i32x4{0, 0, 0, 0});
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        float x = ((float)si[i] * sqk) * a.c2;
-        if (MASK && key0 + 16 * kb + i >= L) x = -INFINITY;
-        s[4 * kb + i] = x;
-        lm = fmaxf(lm, x);
+        if (MASK) {
+          float x = ((float)si[i] * sqk) * a.c2;
+          if (key0 + 16 * kb + i >= L) x = -INFINITY;
+          s[4 * kb + i] = x;
+          lm = fmaxf(lm, x);
+        } else {
+          const int v = si[i];
+          s[4 * kb + i] = (float)v;
+        }
       }
+    }
+    if (!MASK) {
+      float smx = s[0];
+#pragma unroll
+      for (int i = 1; i < 16; ++i) smx = fmaxf(smx, s[i]);
+      lm = smx * c;
     }
     lm = max_over_groups(lm);
     const float mn = fmaxf(m_i, lm);
@@ -167,14 +194,28 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
     uint32_t pk[4];
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb) {
-      uint32_t wd = 0;
+      if (MASK) {
+        uint32_t wd = 0;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float p = fast_exp2(s[4 * kb + i] - mn);
-        ls += p;
-        wd |= ((uint32_t)(int)fmaf(p, 127.f, 0.5f)) << (8 * i);  // p in [0, 1]: 0..127
+        for (int i = 0; i < 4; ++i) {
+          const float p = fast_exp2(s[4 * kb + i] - mn);
+          ls += p;
+          wd |= ((uint32_t)(int)fmaf(p, 127.f, 0.5f)) << (8 * i);  // p in [0, 1]: 0..127
+        }
+        pk[kb] = wd;
+      } else {
+        uint32_t y[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const float p = fast_exp2(fmaf(s[4 * kb + i], c, -mn));
+          ls += p;
+          y[i] = __builtin_bit_cast(uint32_t, fmaf(p, 127.f, 8388608.f));
+        }
+        // bytes 0 of y0, y1, y2, y3
+        const uint32_t lo = __builtin_amdgcn_perm(y[1], y[0], 0x0c0c0400u);
+        const uint32_t hi = __builtin_amdgcn_perm(y[3], y[2], 0x0c0c0400u);
+        pk[kb] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
       }
-      pk[kb] = wd;
     }
     l_i = l_i * alpha + ls;
     // the exact maximum moves on few tiles: where no lane's does (alpha == 1
