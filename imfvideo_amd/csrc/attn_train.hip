@@ -51,6 +51,11 @@ template <typename T16>
 __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
   __shared__ int2 tiles[kMaxJ];  // (tile id, bits of sk)
   __shared__ float vsc[kMaxJ];   // sv / 127 of each visited tile
+  // the visited key tile's K8 and V8 MFMA fragments, double-buffered: each
+  // tile is fetched once per workgroup (wave w fetching fragment w of each)
+  // and read by all four waves
+  __shared__ __align__(16) i32x4 kfr[2][4][64];
+  __shared__ __align__(16) i32x4 vfr[2][4][64];
 
   const int logical = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
   if (logical >= a.nwork) return;
@@ -125,14 +130,23 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
     i32x4 k[4];  // K8[16kb + r][16g ..]
     i32x4 v[4];  // V8 fragments of column tile ct
   };
-  auto load = [&](int j, Frags& f) {
+  // wave w fetches K8 fragment w (keys 16w + r, channels 16g..16g+15) and V8
+  // fragment w (column tile w) of tile j into registers ...
+  auto gload = [&](int j, i32x4& kr, i32x4& vr) {
     const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
+    kr = __builtin_bit_cast(i32x4, buf_load16(rk8, k8off + (n * kT + 16 * w) * kT, 0));
+    vr = __builtin_bit_cast(i32x4, buf_load16(rv8, w * 1024 + l * 16, n * 4096));
+  };
+  // ... stores them in LDS slot s, and every wave reads all eight
+  auto lstore = [&](int s, const i32x4& kr, const i32x4& vr) {
+    kfr[s][w][l] = kr;
+    vfr[s][w][l] = vr;
+  };
+  auto lread = [&](int s, Frags& f) {
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb)
-      f.k[kb] = __builtin_bit_cast(i32x4, buf_load16(rk8, k8off + (n * kT + 16 * kb) * kT, 0));
+    for (int kb = 0; kb < 4; ++kb) f.k[kb] = kfr[s][kb][l];
 #pragma unroll
-    for (int ct = 0; ct < 4; ++ct)
-      f.v[ct] = __builtin_bit_cast(i32x4, buf_load16(rv8, ct * 1024 + l * 16, n * 4096));
+    for (int ct = 0; ct < 4; ++ct) f.v[ct] = vfr[s][ct][l];
   };
 
   f32x4 acc[4];
@@ -243,16 +257,24 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
       tile(f, j, std::false_type{});
   };
 
-  Frags fa, fb;
-  load(0, fa);
-  int j = 0;
-  for (; j + 1 < J; j += 2) {
-    load(j + 1, fb);
-    tile_any(fa, j);
-    load(j + 2 < J ? j + 2 : J - 1, fa);
-    tile_any(fb, j + 1);
+  // tile j in slot j & 1; tile j + 1 is fetched while tile j is computed and
+  // stored after it (the slot was last read before the previous barrier)
+  {
+    i32x4 kr, vr;
+    gload(0, kr, vr);
+    lstore(0, kr, vr);
   }
-  if (j < J) tile_any(fa, j);
+  __syncthreads();
+  for (int j = 0; j < J; ++j) {
+    Frags f;
+    lread(j & 1, f);
+    i32x4 kr, vr;
+    const bool more = j + 1 < J;
+    if (more) gload(j + 1, kr, vr);
+    tile_any(f, j);
+    if (more) lstore((j + 1) & 1, kr, vr);
+    __syncthreads();
+  }
 
   const float lt = sum_over_groups(l_i);
   const float rl = 1.f / lt;
