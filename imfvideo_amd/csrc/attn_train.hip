@@ -321,6 +321,11 @@ struct Fwd16Args {
 template <typename T16>
 __global__ __launch_bounds__(256, 2) void sparse_fwd16_kernel(Fwd16Args a) {
   __shared__ int tiles[kMaxJ];
+  // the visited key tile's K and V^T MFMA fragments, double-buffered: each
+  // tile is fetched once per workgroup (wave w fetching K rows 16w..16w+15 and
+  // V^T column tile w) and read by all four waves
+  __shared__ __align__(16) u32x4 ksh[2][4][2][64];  // [slot][kb][ks][lane]
+  __shared__ __align__(16) u32x2 vsh[2][4][4][64];  // [slot][ct][w'][lane]
 
   const int logical = (blockIdx.x & 7) * a.per_xcd + (blockIdx.x >> 3);
   if (logical >= a.nwork) return;
@@ -390,17 +395,38 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd16_kernel(Fwd16Args a) {
     u32x4 k[4][2];  // K[16kb + r][32ks + 8g ..]
     u32x2 v[4][4];  // [ct][w'] = V[16w' + 4g + 0..3][16ct + r]
   };
-  auto load = [&](int j, Frags& f) {
+  // wave w fetches K fragment kb = w (both ks) and the 2 KB of V^T column tile
+  // ct = w (32 contiguous bytes per lane) into registers ...
+  struct Stage {
+    u32x4 k[2];
+    u32x4 v[2];
+  };
+  auto gload = [&](int j, Stage& st) {
     const int n = __builtin_amdgcn_readfirstlane(tiles[j]);
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+      st.k[ks] = buf_load16(rk, n * 8192 + ((16 * w + r) * kT + 32 * ks + 8 * g) * 2, 0);
+#pragma unroll
+    for (int h = 0; h < 2; ++h) st.v[h] = buf_load16(rv, w * 2048 + l * 32 + 16 * h, n * 8192);
+  };
+  // ... stores them in LDS slot sl (the same layout as in global memory for
+  // V^T), and every wave reads the whole tile's fragments
+  auto lstore = [&](int sl, const Stage& st) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) ksh[sl][w][ks][l] = st.k[ks];
+    u32x4* vd = reinterpret_cast<u32x4*>(&vsh[sl][w][0][0]);
+    vd[2 * l] = st.v[0];
+    vd[2 * l + 1] = st.v[1];
+  };
+  auto lread = [&](int sl, Frags& f) {
 #pragma unroll
     for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
-        f.k[kb][ks] = buf_load16(rk, n * 8192 + ((16 * kb + r) * kT + 32 * ks + 8 * g) * 2, 0);
+      for (int ks = 0; ks < 2; ++ks) f.k[kb][ks] = ksh[sl][kb][ks][l];
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-      for (int ww = 0; ww < 4; ++ww) f.v[ct][ww] = buf_load8(rv, ((ct * 4 + ww) * 64 + l) * 8, n * 8192);
+      for (int ww = 0; ww < 4; ++ww) f.v[ct][ww] = vsh[sl][ct][ww][l];
   };
 
   f32x4 acc[4];
@@ -464,17 +490,25 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd16_kernel(Fwd16Args a) {
       tile(f, j, std::false_type{});
   };
 
+  // tile j in slot j & 1; tile j + 1 is fetched while tile j is computed and
+  // stored after it (the slot was last read before the previous barrier)
   const int J = a.T;
-  Frags fa, fb;
-  load(0, fa);
-  int j = 0;
-  for (; j + 1 < J; j += 2) {
-    load(j + 1, fb);
-    tile_any(fa, j);
-    load(j + 2 < J ? j + 2 : J - 1, fa);
-    tile_any(fb, j + 1);
+  {
+    Stage st;
+    gload(0, st);
+    lstore(0, st);
   }
-  if (j < J) tile_any(fa, j);
+  __syncthreads();
+  for (int j = 0; j < J; ++j) {
+    Frags f;
+    lread(j & 1, f);
+    Stage st;
+    const bool more = j + 1 < J;
+    if (more) gload(j + 1, st);
+    tile_any(f, j);
+    if (more) lstore((j + 1) & 1, st);
+    __syncthreads();
+  }
 
   const float lt = sum_over_groups(l_i);
   const float rl = 1.f / lt;
