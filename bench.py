@@ -242,7 +242,7 @@ def train_bench(args):
         st = ops.linear_states_qat(k, v)
         rec(4)
         lut_aug = ops.augment_lut(lut, Np, nb - Np)
-        comp = ops.complement(st, lut_aug, nb)
+        comp = ops.complement(st, lut_aug, nb, check_ids=False)  # LUT from route_topk
         rec(5)
         o, o_l, den = ops.linear_mix_qat(qphi, comp, st["Hall"], o_s, alpha)
         rec(6)

@@ -54,6 +54,12 @@ SIGNATURES = {
     "sla2h_rmsnorm_bwd_workspace_bytes": (ctypes.c_size_t, [_c_i64, _c_int]),
     "sla2h_gate_mul_fwd": (_c_int, [_p, _p, _c_int, _c_i64, _p, _p]),
     "sla2h_gate_mul_bwd": (_c_int, [_p, _p, _p, _c_int, _c_i64, _p, _p, _p]),
+    "sla2h_attn_in_fwd": (_c_int, [_p, _c_int, _c_i64, _c_i64, _c_i64, _p, _c_int, _c_i64,
+                                   _c_i64, _c_i64, _c_int, _c_int, _c_i64, _p, _p]),
+    "sla2h_attn_in_bwd": (_c_int, [_p, _p, _c_int, _c_i64, _c_i64, _c_i64, _p, _c_int, _c_i64,
+                                   _c_i64, _c_i64, _c_int, _c_int, _c_i64, _p]),
+    "sla2h_attn_gate_fwd": (_c_int, [_p, _p, _c_int, _c_int, _c_int, _c_i64, _p, _p]),
+    "sla2h_attn_gate_bwd": (_c_int, [_p, _p, _p, _c_int, _c_int, _c_int, _c_i64, _p, _p, _p]),
     "sla2h_rmsnorm_fwd16": (_c_int, [_p, _c_i64, _c_int, _c_i64, _p, _c_f, _c_int, _p, _p]),
     "sla2h_rmsnorm_bwd_sum": (_c_int, [_p, _c_i64, _c_int, _c_i64, _p, _p, _p, _p, _c_int, _p,
                                        _c_f, _p, _p, _p, _p]),

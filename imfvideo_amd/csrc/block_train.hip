@@ -990,3 +990,252 @@ extern "C" int sla2h_residual_scale_bwd(const float* dy, const void* a, int dtyp
   col_sum_kernel<<<D, 256, 0, st>>>(dsp, nb, D, ds);
   return (int)hipGetLastError();
 }
+
+// ---------------------------------------------------------------------------
+// Attention operands and output gate of the MLA sublayer around a tile-major
+// SLA2 op (models/imf_dit_video.py:458-466 with models/sla2_cube_qat.py:
+// 340-350, 397-400).  The sublayer builds q = cat([q_nope, q_rope]) and
+// k = cat([k_nope, k_rope shared by the heads]), each (B, L, H, 64), where the
+// nope halves are the per-head RMSNorm outputs (fp32: the norm's 16-bit
+// result times its fp32 weight) and the rope halves and v are 16-bit; the op
+// takes permute(0, 2, 1, 3).half() of q, k, v and returns (B, H, L, 64) fp16
+// rows, which go back through permute(...).to(fp32) and the gate
+// attn * sigmoid(g) into the output projection's autocast cast.
+//
+// attn_in: the three operand tensors straight from their halves into the
+// op's fp16 rows, eight channels per thread (channels 0..31 from the "lo"
+// half, 32..63 from the "hi" half; a half is addressed by (b, t, h) strides
+// in elements, h stride 0 for the band the heads share).  Every value is
+// converted once to fp16, as .half() of the exact concatenation does.  The
+// backward writes each half's gradient in the half's own dtype: fp32 exactly,
+// a 16-bit half rounded once from fp16 (the concatenation's fp32 gradient cast
+// back to the half's dtype); the shared band's gradient is the fp32 sum over
+// the heads, in head order, of the per-head 16-bit gradients, rounded once
+// (the expand's backward sum).
+//
+// attn_gate: out = round16(fp32(o) s), s = round16(sigmoid(g)) (the gate's
+// fp32 product, then the output projection's cast to the autocast dtype);
+// backward from the projection's 16-bit input gradient d:
+//   do = fp16(d s)  (the gate's fp32 da, cast back to the op's fp16 output),
+//   dg = round16(round16(ds round16(1 - s)) s),  ds = round16(d fp32(o))
+// (the sigmoid output is 16-bit, so its gradient is rounded to 16 bits and
+// torch's sigmoid backward runs in the 16-bit type).
+// ---------------------------------------------------------------------------
+namespace sla2h {
+namespace {
+
+struct HalfRef {  // one 32-channel half of an operand, (b, t, h) strides in elements
+  const void* p;
+  int64_t sb, st, sh;
+};
+struct HalfOut {
+  void* p;
+  int64_t sb, st, sh;
+};
+
+// thread i: output row (b, h, t) = i >> 3 of the (B, H, L, 64) fp16 operand,
+// channels 8 (i & 7) ..
+template <int LO, int HI>
+__global__ __launch_bounds__(256) void attn_in_fwd_kernel(HalfRef lo, HalfRef hi, int H, int L,
+                                                          int n8, uint16_t* __restrict__ out) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const int c8 = i & 7, row = i >> 3;
+  const int t = row % L, bh = row / L;
+  const int h = bh % H, b = bh / H;
+  float x[8];
+  if (c8 < 4)
+    ld8<LO>(lo.p, b * lo.sb + t * lo.st + h * lo.sh + 8 * c8, x);
+  else
+    ld8<HI>(hi.p, b * hi.sb + t * hi.st + h * hi.sh + 8 * (c8 - 4), x);
+  st8<SLA2H_DTYPE_F16>(out, 8 * (int64_t)i, x);
+}
+
+// thread i: token (b, t), head h, channels 8 c8 .. in (c8, h, t, b) order, so
+// the halves' (B, L, H, 32) gradients are written contiguously.  SUMHI: the
+// hi half is shared by the heads; the h = 0 thread of each (b, t, c8) sums it.
+template <int LO, int HI, bool SUMHI>
+__global__ __launch_bounds__(256) void attn_in_bwd_kernel(const uint16_t* __restrict__ dout,
+                                                          HalfOut lo, HalfOut hi, int H, int L,
+                                                          int n8) {
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const int c8 = i & 7, rest = i >> 3;
+  const int h = rest % H, tok = rest / H;
+  const int t = tok % L, b = tok / L;
+  float x[8];
+  if (c8 < 4) {
+    ld8<SLA2H_DTYPE_F16>(dout, ((int64_t)(b * H + h) * L + t) * 64 + 8 * c8, x);
+    st8<LO>(lo.p, b * lo.sb + t * lo.st + h * lo.sh + 8 * c8, x);
+  } else if (!SUMHI) {
+    ld8<SLA2H_DTYPE_F16>(dout, ((int64_t)(b * H + h) * L + t) * 64 + 8 * c8, x);
+    st8<HI>(hi.p, b * hi.sb + t * hi.st + h * hi.sh + 8 * (c8 - 4), x);
+  } else if (h == 0) {
+    float acc[8] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    for (int hh = 0; hh < H; ++hh) {
+      ld8<SLA2H_DTYPE_F16>(dout, ((int64_t)(b * H + hh) * L + t) * 64 + 8 * c8, x);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) acc[e] += round_to<HI>(x[e]);
+    }
+    st8<HI>(hi.p, b * hi.sb + t * hi.st + 8 * (c8 - 4), acc);
+  }
+}
+
+// thread i: token (b, t), head h, channels 8 c8 .. (c8, h, t, b) order, i.e.
+// element 8 i of the (B, L, H * 64) gate and output
+template <int DT>
+__global__ __launch_bounds__(256) void attn_gate_fwd_kernel(const uint16_t* __restrict__ o,
+                                                            const void* __restrict__ g, int H,
+                                                            int L, int n8, void* __restrict__ out) {
+#pragma clang fp contract(off)
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const int c8 = i & 7, rest = i >> 3;
+  const int h = rest % H, tok = rest / H;
+  const int t = tok % L, b = tok / L;
+  float a[8], gv[8], y[8];
+  ld8<SLA2H_DTYPE_F16>(o, ((int64_t)(b * H + h) * L + t) * 64 + 8 * c8, a);
+  ld8<DT>(g, 8 * (int64_t)i, gv);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) y[e] = a[e] * gate_sig<DT>(gv[e]);
+  st8<DT>(out, 8 * (int64_t)i, y);
+}
+
+template <int DT>
+__global__ __launch_bounds__(256) void attn_gate_bwd_kernel(const void* __restrict__ dy,
+                                                            const uint16_t* __restrict__ o,
+                                                            const void* __restrict__ g, int H,
+                                                            int L, int n8,
+                                                            uint16_t* __restrict__ dout,
+                                                            void* __restrict__ dg) {
+#pragma clang fp contract(off)
+  const int i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n8) return;
+  const int c8 = i & 7, rest = i >> 3;
+  const int h = rest % H, tok = rest / H;
+  const int t = tok % L, b = tok / L;
+  const int64_t oi = ((int64_t)(b * H + h) * L + t) * 64 + 8 * c8;
+  float d[8], a[8], gv[8], da[8], dgv[8];
+  ld8<DT>(dy, 8 * (int64_t)i, d);
+  ld8<SLA2H_DTYPE_F16>(o, oi, a);
+  ld8<DT>(g, 8 * (int64_t)i, gv);
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float sg = gate_sig<DT>(gv[e]);
+    da[e] = d[e] * sg;
+    const float ds = round_to<DT>(d[e] * a[e]);
+    dgv[e] = round_to<DT>(ds * round_to<DT>(1.f - sg)) * sg;
+  }
+  st8<SLA2H_DTYPE_F16>(dout, oi, da);
+  st8<DT>(dg, 8 * (int64_t)i, dgv);
+}
+
+bool aligned16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+bool half_ok(const void* p, int dt, int64_t sb, int64_t st, int64_t sh) {
+  // 16-byte accesses: the base and every stride a multiple of 16 bytes
+  const int64_t es = dt == kF32 ? 4 : 2;
+  return p != nullptr && aligned16(p) && (sb * es) % 16 == 0 && (st * es) % 16 == 0 &&
+         (sh * es) % 16 == 0 && sb >= 0 && st >= 0 && sh >= 0;
+}
+bool dt_ok(int dt, bool allow_f32) {
+  return dt == SLA2H_DTYPE_F16 || dt == SLA2H_DTYPE_BF16 || (allow_f32 && dt == kF32);
+}
+
+// dispatch over (lo dtype in {f16, bf16, f32}) x (hi dtype in {f16, bf16})
+template <typename F>
+void attn_in_dispatch(int lo_dt, int hi_dt, F&& f) {
+  auto hi = [&](auto lo_c) {
+    if (hi_dt == SLA2H_DTYPE_BF16)
+      f(lo_c, std::integral_constant<int, SLA2H_DTYPE_BF16>{});
+    else
+      f(lo_c, std::integral_constant<int, SLA2H_DTYPE_F16>{});
+  };
+  if (lo_dt == kF32)
+    hi(std::integral_constant<int, kF32>{});
+  else if (lo_dt == SLA2H_DTYPE_BF16)
+    hi(std::integral_constant<int, SLA2H_DTYPE_BF16>{});
+  else
+    hi(std::integral_constant<int, SLA2H_DTYPE_F16>{});
+}
+
+}  // namespace
+}  // namespace sla2h
+
+extern "C" int sla2h_attn_in_fwd(const void* lo, int lo_dtype, int64_t lo_sb, int64_t lo_st,
+                                 int64_t lo_sh, const void* hi, int hi_dtype, int64_t hi_sb,
+                                 int64_t hi_st, int64_t hi_sh, int B, int H, int64_t L, void* out,
+                                 void* stream) {
+  SLA2H_CHECK_ARG(dt_ok(lo_dtype, true) && dt_ok(hi_dtype, false));
+  SLA2H_CHECK_ARG(half_ok(lo, lo_dtype, lo_sb, lo_st, lo_sh));
+  SLA2H_CHECK_ARG(half_ok(hi, hi_dtype, hi_sb, hi_st, hi_sh));
+  SLA2H_CHECK_ARG(out && aligned16(out) && B > 0 && H > 0 && L > 0);
+  const int64_t n8 = (int64_t)B * H * L * 8;
+  SLA2H_CHECK_ARG(n8 < (1ll << 31));
+  const unsigned grid = grid_of(n8);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const HalfRef rl{lo, lo_sb, lo_st, lo_sh}, rh{hi, hi_sb, hi_st, hi_sh};
+  attn_in_dispatch(lo_dtype, hi_dtype, [&](auto lc, auto hc) {
+    attn_in_fwd_kernel<decltype(lc)::value, decltype(hc)::value><<<grid, 256, 0, s>>>(
+        rl, rh, H, (int)L, (int)n8, static_cast<uint16_t*>(out));
+  });
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_attn_in_bwd(const void* dout, void* dlo, int lo_dtype, int64_t lo_sb,
+                                 int64_t lo_st, int64_t lo_sh, void* dhi, int hi_dtype,
+                                 int64_t hi_sb, int64_t hi_st, int64_t hi_sh, int B, int H,
+                                 int64_t L, void* stream) {
+  SLA2H_CHECK_ARG(dt_ok(lo_dtype, true) && dt_ok(hi_dtype, false));
+  SLA2H_CHECK_ARG(dout && aligned16(dout) && B > 0 && H > 0 && L > 0);
+  SLA2H_CHECK_ARG(half_ok(dlo, lo_dtype, lo_sb, lo_st, lo_sh));
+  SLA2H_CHECK_ARG(half_ok(dhi, hi_dtype, hi_sb, hi_st, hi_sh));
+  const int64_t n8 = (int64_t)B * H * L * 8;
+  SLA2H_CHECK_ARG(n8 < (1ll << 31));
+  const unsigned grid = grid_of(n8);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  const HalfOut rl{dlo, lo_sb, lo_st, lo_sh}, rh{dhi, hi_sb, hi_st, hi_sh};
+  auto d = static_cast<const uint16_t*>(dout);
+  attn_in_dispatch(lo_dtype, hi_dtype, [&](auto lc, auto hc) {
+    constexpr int LO = decltype(lc)::value, HI = decltype(hc)::value;
+    if (hi_sh == 0)
+      attn_in_bwd_kernel<LO, HI, true><<<grid, 256, 0, s>>>(d, rl, rh, H, (int)L, (int)n8);
+    else
+      attn_in_bwd_kernel<LO, HI, false><<<grid, 256, 0, s>>>(d, rl, rh, H, (int)L, (int)n8);
+  });
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_attn_gate_fwd(const void* o, const void* g, int dtype, int B, int H,
+                                   int64_t L, void* out, void* stream) {
+  SLA2H_CHECK_ARG(o && g && out && aligned16(o) && aligned16(g) && aligned16(out));
+  SLA2H_CHECK_ARG(dt_ok(dtype, false) && B > 0 && H > 0 && L > 0);
+  const int64_t n8 = (int64_t)B * H * L * 8;
+  SLA2H_CHECK_ARG(n8 < (1ll << 31));
+  const unsigned grid = grid_of(n8);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto op = static_cast<const uint16_t*>(o);
+  if (dtype == SLA2H_DTYPE_BF16)
+    attn_gate_fwd_kernel<SLA2H_DTYPE_BF16><<<grid, 256, 0, s>>>(op, g, H, (int)L, (int)n8, out);
+  else
+    attn_gate_fwd_kernel<SLA2H_DTYPE_F16><<<grid, 256, 0, s>>>(op, g, H, (int)L, (int)n8, out);
+  return (int)hipGetLastError();
+}
+
+extern "C" int sla2h_attn_gate_bwd(const void* dy, const void* o, const void* g, int dtype, int B,
+                                   int H, int64_t L, void* dout, void* dg, void* stream) {
+  SLA2H_CHECK_ARG(dy && o && g && dout && dg);
+  for (const void* p : {dy, o, g, static_cast<const void*>(dout), static_cast<const void*>(dg)})
+    SLA2H_CHECK_ARG(aligned16(p));
+  SLA2H_CHECK_ARG(dt_ok(dtype, false) && B > 0 && H > 0 && L > 0);
+  const int64_t n8 = (int64_t)B * H * L * 8;
+  SLA2H_CHECK_ARG(n8 < (1ll << 31));
+  const unsigned grid = grid_of(n8);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  auto op = static_cast<const uint16_t*>(o);
+  auto dp = static_cast<uint16_t*>(dout);
+  if (dtype == SLA2H_DTYPE_BF16)
+    attn_gate_bwd_kernel<SLA2H_DTYPE_BF16><<<grid, 256, 0, s>>>(dy, op, g, H, (int)L, (int)n8, dp, dg);
+  else
+    attn_gate_bwd_kernel<SLA2H_DTYPE_F16><<<grid, 256, 0, s>>>(dy, op, g, H, (int)L, (int)n8, dp, dg);
+  return (int)hipGetLastError();
+}

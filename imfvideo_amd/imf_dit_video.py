@@ -269,6 +269,82 @@ def precompute_axial_rope_3d(head_dim, grid_size, num_prefix_tokens, axis_dims=N
     return torch.cos(angles), torch.sin(angles)
 
 
+class _AttnInFunction(torch.autograd.Function):
+    """The (B, H, L, 64) fp16 operands of a tile-major SLA2 op straight from the
+    sublayer's halves: q = [q_nope | q_rope], k = [k_nope | k_rope shared by
+    the heads], v -- the reference's torch.cat and the op's permute + .half()
+    in one HIP kernel per operand each way (sla2h_attn_in_fwd / _bwd)."""
+
+    @staticmethod
+    def forward(ctx, q_nope, q_rope, k_nope, k_rope, v):
+        from . import ops
+        H = q_nope.shape[2]
+        ctx.meta = [(t.shape, t.dtype) for t in (q_nope, q_rope, k_nope, k_rope, v)]
+        return (ops.attn_in_fwd((q_nope, q_rope), H), ops.attn_in_fwd((k_nope, k_rope), H),
+                ops.attn_in_fwd((v[..., :32], v[..., 32:]), H))
+
+    @staticmethod
+    def backward(ctx, dqh, dkh, dvh):
+        from . import ops
+        grads = []
+        for d, (lo, hi) in ((dqh, ctx.meta[0:2]), (dkh, ctx.meta[2:4])):
+            if d is None:
+                grads += [None, None]
+                continue
+            dlo = torch.empty(lo[0], device=d.device, dtype=lo[1])
+            dhi = torch.empty(hi[0], device=d.device, dtype=hi[1])
+            ops.attn_in_bwd(d, dlo, dhi)
+            grads += [dlo, dhi]
+        if dvh is None:
+            grads.append(None)
+        else:
+            dv = torch.empty(ctx.meta[4][0], device=dvh.device, dtype=ctx.meta[4][1])
+            ops.attn_in_bwd(dvh, dv[..., :32], dv[..., 32:])
+            grads.append(dv)
+        return tuple(grads)
+
+
+class _AttnGateFunction(torch.autograd.Function):
+    """round16(fp32(o) * sigmoid(g)) from a tile-major SLA2 op's fp16 output o
+    (B, H, L, 64): the reference's permute / .to(float32) of o, its fp32 gate
+    and the output projection's autocast cast in one HIP kernel each way
+    (sla2h_attn_gate_fwd / _bwd); saves o and g only."""
+
+    @staticmethod
+    def forward(ctx, o, g):
+        from . import ops
+        ctx.save_for_backward(o, g)
+        return ops.attn_gate_fwd(o, g)
+
+    @staticmethod
+    def backward(ctx, dy):
+        from . import ops
+        o, g = ctx.saved_tensors
+        return ops.attn_gate_bwd(dy, o, g)
+
+
+def _aligned16(*ts):
+    return all(t.data_ptr() % 16 == 0 and all((st * t.element_size()) % 16 == 0
+                                               for st in t.stride()[:-1]) and t.stride()[-1] == 1
+               for t in ts)
+
+
+def _tile_major_operands_ok(impl, q_nope, q_rope, k_nope, k_rope, v):
+    """The fused operand path applies: the impl keeps the sequence tile-major
+    and takes its operands directly (forward_tile_major), on GPU tensors with
+    32-channel halves, 64-channel v, 16-bit rope / v and 16-byte accesses."""
+    if not (getattr(impl, "pre_permuted", False) and hasattr(impl, "forward_tile_major")):
+        return False
+    ts = (q_nope, q_rope, k_nope, k_rope, v)
+    half16 = (torch.float16, torch.bfloat16)
+    return (all(t.is_cuda for t in ts) and q_nope.shape[-1] == 32 and q_rope.shape[-1] == 32
+            and k_nope.shape[-1] == 32 and k_rope.shape[-1] == 32 and v.shape[-1] == 64
+            and k_rope.shape[2] == 1 and q_nope.shape == q_rope.shape == k_nope.shape
+            and q_nope.dtype in half16 + (torch.float32,) and k_nope.dtype in half16 + (torch.float32,)
+            and q_rope.dtype in half16 and k_rope.dtype in half16 and v.dtype in half16
+            and _aligned16(*ts))
+
+
 class MLAAttention(nn.Module):
     """Multi-head latent attention with decoupled partial RoPE and the output
     gate.  q: d -> dq (RMSNorm) -> H (dn + dr); k/v: d -> [dc latent (RMSNorm) |
@@ -321,7 +397,23 @@ class MLAAttention(nn.Module):
         k_nope, v = kv.split([dn, dv], dim=-1)
         q_nope, k_nope = self.q_norm(q_nope), self.k_norm(k_nope)
         q_rope = apply_rotary_pos_emb(q_rope, rope_cos, rope_sin)
-        k_rope = apply_rotary_pos_emb(k_rope.unsqueeze(2), rope_cos, rope_sin).expand(b, l, H, dr)
+        k_rope = apply_rotary_pos_emb(k_rope.unsqueeze(2), rope_cos, rope_sin)
+        if _tile_major_operands_ok(self.attn_impl, q_nope, q_rope, k_nope, k_rope, v):
+            # the op's fp16 tile-major operands straight from the halves, and
+            # (under autocast) its output through the gate into the projection
+            qh, kh, vh = _AttnInFunction.apply(q_nope, q_rope, k_nope, k_rope, v)
+            o = self.attn_impl.forward_tile_major(qh, kh, vh)
+            if self.use_output_gate:
+                g = self.g_proj(xg)
+                if (torch.is_autocast_enabled("cuda") and g.dtype == torch.get_autocast_dtype("cuda")
+                        and g.dtype in (torch.float16, torch.bfloat16) and g.is_contiguous()
+                        and g.data_ptr() % 16 == 0):
+                    return self.out_proj(_AttnGateFunction.apply(o, g))
+                attn = o.permute(0, 2, 1, 3).to(torch.promote_types(q_nope.dtype, q_rope.dtype))
+                return self.out_proj(attn.reshape(b, l, H * dv) * torch.sigmoid(g))
+            attn = o.permute(0, 2, 1, 3).to(torch.promote_types(q_nope.dtype, q_rope.dtype))
+            return self.out_proj(attn.reshape(b, l, H * dv))
+        k_rope = k_rope.expand(b, l, H, dr)
         q = torch.cat([q_nope, q_rope], dim=-1)
         k = torch.cat([k_nope, k_rope], dim=-1)
         attn = self.attn_impl(q, k, v).reshape(b, l, H * dv)

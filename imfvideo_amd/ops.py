@@ -922,6 +922,70 @@ def gate_mul_bwd(dout, a, g):
     return da, dg
 
 
+def _half_args(t):
+    """(tensor, dtype code, sb, st, sh) of a (B, L, H, 32) half (H may be 1 and
+    broadcast: head stride 0)."""
+    sb, st, sh, sc = t.stride()
+    if sc != 1:
+        raise ValueError("attention operand halves need unit channel stride")
+    return t, _SITU_DTYPES[t.dtype], sb, st, (0 if t.shape[2] == 1 else sh)
+
+
+def attn_in_fwd(halves, H):
+    """(B, H, L, 64) fp16 operand from two (B, L, H|1, 32) halves (lo: channels
+    0..31, hi: 32..63; fp32 or 16-bit lo, 16-bit hi) -- the sublayer's
+    torch.cat(...).permute(0, 2, 1, 3).half() in one pass."""
+    lo, hi = halves
+    _need_gpu(lo, hi)
+    B, L = lo.shape[:2]
+    out = torch.empty(B, H, L, 64, device=lo.device, dtype=torch.float16)
+    a, b = _half_args(lo), _half_args(hi)
+    _lib.check(_lib.load().sla2h_attn_in_fwd(
+        a[0].data_ptr(), *a[1:], b[0].data_ptr(), *b[1:], B, H, L, out.data_ptr(),
+        _stream(lo.device)), "sla2h_attn_in_fwd")
+    return out
+
+
+def attn_in_bwd(dout, dlo, dhi):
+    """Gradients of the two halves of attn_in_fwd from the (B, H, L, 64) fp16
+    gradient, written into dlo and dhi (preallocated (B, L, H|1, 32) tensors
+    or views in the halves' dtypes; a head-shared dhi gets the sum over the
+    heads)."""
+    _need_gpu(dout, dlo, dhi)
+    B, H, L, _ = dout.shape
+    dout = dout.to(torch.float16).contiguous()
+    a, b = _half_args(dlo), _half_args(dhi)
+    _lib.check(_lib.load().sla2h_attn_in_bwd(
+        dout.data_ptr(), a[0].data_ptr(), *a[1:], b[0].data_ptr(), *b[1:], B, H, L,
+        _stream(dout.device)), "sla2h_attn_in_bwd")
+
+
+def attn_gate_fwd(o, g):
+    """round16(fp32(o) sigmoid16(g)) as (B, L, H * 64) in g's dtype, from the
+    op's (B, H, L, 64) fp16 output o and the gate logits g (B, L, H * 64)."""
+    _need_gpu(o, g)
+    B, H, L, D = o.shape
+    o, g = o.contiguous(), g.contiguous()
+    out = torch.empty(B, L, H * D, device=o.device, dtype=g.dtype)
+    _lib.check(_lib.load().sla2h_attn_gate_fwd(o.data_ptr(), g.data_ptr(), _F16_CODES[g.dtype],
+                                               B, H, L, out.data_ptr(), _stream(o.device)),
+               "sla2h_attn_gate_fwd")
+    return out
+
+
+def attn_gate_bwd(dy, o, g):
+    """(do (B, H, L, 64) fp16, dg) of attn_gate_fwd for the output gradient dy."""
+    _need_gpu(dy, o, g)
+    B, H, L, D = o.shape
+    dy, o, g = dy.to(g.dtype).contiguous(), o.contiguous(), g.contiguous()
+    do, dg = torch.empty_like(o), torch.empty_like(g)
+    _lib.check(_lib.load().sla2h_attn_gate_bwd(dy.data_ptr(), o.data_ptr(), g.data_ptr(),
+                                               _F16_CODES[g.dtype], B, H, L, do.data_ptr(),
+                                               dg.data_ptr(), _stream(o.device)),
+               "sla2h_attn_gate_bwd")
+    return do, dg
+
+
 def rmsnorm_fwd16(x, w, eps, dtype):
     """round16(rmsnorm_fwd(x, w, eps)) in `dtype` (bf16 / fp16) for an fp32 x of
     a power-of-two width <= 512: the norm and the autocast cast of its output

@@ -185,7 +185,6 @@ class SLA2CubeQATAttentionImpl(nn.Module):
 
     def forward(self, q, k, v):
         """q, k, v: (b, l, H, hd) -> (b, l, H, hd) attention output in q.dtype."""
-        B, L, H, D = q.shape
 
         def tm(x):
             x = x.permute(0, 2, 1, 3)
@@ -193,23 +192,30 @@ class SLA2CubeQATAttentionImpl(nn.Module):
                 x = x[:, :, self.perm]
             return x.half().contiguous()
 
-        qh, kh, vh = tm(q), tm(k), tm(v)
+        o = self.forward_tile_major(tm(q), tm(k), tm(v))
+        if self.pre_permuted:
+            return o.permute(0, 2, 1, 3).to(q.dtype)
+        return o[:, :, self.inv].permute(0, 2, 1, 3).to(q.dtype)
+
+    def forward_tile_major(self, qh, kh, vh):
+        """The op on operands already in its layout: qh, kh, vh (b, H, l, hd)
+        fp16, tile-major rows, contiguous -> o (b, H, l, hd) fp16 in the same
+        rows.  forward() is this between the reference's permute / .half() of
+        q, k, v and the permute / cast back of o; a caller that keeps the
+        sequence tile-major can build the operands and consume o directly."""
+        B, H, L, D = qh.shape
         with torch.no_grad():
             lut, T = route_tiles_fast(qh, kh, self.topk_frac, self.Np, self.E, self.prefix_len,
                                       proj_q=self.proj_q, proj_k=self.proj_k)
         needs_grad = torch.is_grad_enabled() and (
-            q.requires_grad or k.requires_grad or v.requires_grad
+            qh.requires_grad or kh.requires_grad or vh.requires_grad
             or self.alpha_logit.requires_grad)
         if needs_grad:
             if not hasattr(self, "logit_max_log2"):
-                self.logit_max_log2 = torch.zeros(H, device=q.device, dtype=torch.float32)
+                self.logit_max_log2 = torch.zeros(H, device=qh.device, dtype=torch.float32)
             lut_aug = ops.augment_lut(lut, self.Np, self.n_tail)
-            o = _CubeQATFunction.apply(qh, kh, vh, self.alpha_logit, lut, lut_aug, None, T,
-                                       self.E, self.use_int8, self.a_index, self.n_tail,
-                                       self.logit_max_log2)
-        else:
-            a = torch.sigmoid(self.alpha_logit.detach().float())
-            o = ops.train_fwd(qh, kh, vh, a, lut, self.Np, int8=self.use_int8)["o"]
-        if self.pre_permuted:
-            return o.permute(0, 2, 1, 3).to(q.dtype)
-        return o[:, :, self.inv].permute(0, 2, 1, 3).to(q.dtype)
+            return _CubeQATFunction.apply(qh, kh, vh, self.alpha_logit, lut, lut_aug, None, T,
+                                          self.E, self.use_int8, self.a_index, self.n_tail,
+                                          self.logit_max_log2)
+        a = torch.sigmoid(self.alpha_logit.detach().float())
+        return ops.train_fwd(qh, kh, vh, a, lut, self.Np, int8=self.use_int8)["o"]

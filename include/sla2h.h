@@ -339,6 +339,43 @@ int sla2h_gate_mul_fwd(const void* a, const void* g, int dtype, int64_t n, void*
 int sla2h_gate_mul_bwd(const void* dout, const void* a, const void* g, int dtype, int64_t n,
                        void* da, void* dg, void* stream);
 
+/*
+ * The MLA sublayer's attention operands for a tile-major SLA2 op: replaces
+ * q = torch.cat([q_nope, q_rope], -1), k = torch.cat([k_nope, k_rope], -1)
+ * and the op's permute(0, 2, 1, 3).half() of q, k, v
+ * (models/imf_dit_video.py:458-463, models/sla2_cube_qat.py:340-350).
+ * An operand is two 32-channel halves, each addressed by element strides
+ * (sb, st, sh) over (batch, token, head); sh = 0 for a half the heads share
+ * (the key's rope band).  lo_dtype: SLA2H_DTYPE_F16, SLA2H_DTYPE_BF16 or 2
+ * (fp32, the per-head RMSNorm output); hi_dtype 16-bit.  Bases and strides
+ * 16-byte multiples.  out: (B, H, L, 64) fp16, every value converted once.
+ * Backward: dout (B, H, L, 64) fp16 -> each half's gradient in the half's
+ * dtype at its strides (exact for fp32, one rounding for 16-bit); with
+ * hi_sh = 0 the shared half gets the fp32 sum over the heads, in head order,
+ * of the per-head 16-bit gradients, rounded once.
+ */
+int sla2h_attn_in_fwd(const void* lo, int lo_dtype, int64_t lo_sb, int64_t lo_st, int64_t lo_sh,
+                      const void* hi, int hi_dtype, int64_t hi_sb, int64_t hi_st, int64_t hi_sh,
+                      int B, int H, int64_t L, void* out, void* stream);
+int sla2h_attn_in_bwd(const void* dout, void* dlo, int lo_dtype, int64_t lo_sb, int64_t lo_st,
+                      int64_t lo_sh, void* dhi, int hi_dtype, int64_t hi_sb, int64_t hi_st,
+                      int64_t hi_sh, int B, int H, int64_t L, void* stream);
+
+/*
+ * The output gate after a tile-major SLA2 op under autocast: replaces
+ * o.permute(0, 2, 1, 3).to(float32) (models/sla2_cube_qat.py:397-400), the
+ * gate attn * torch.sigmoid(g) in fp32 (models/imf_dit_video.py:466) and the
+ * output projection's autocast cast of its input.  o: (B, H, L, 64) fp16;
+ * g, out: (B, L, H * 64) in dtype (16-bit, the autocast dtype):
+ *   s = round16(sigmoid(g)), out = round16(fp32(o) s);
+ *   backward from dy (B, L, H * 64) in dtype: do = fp16(dy s) in o's layout,
+ *   dg = round16(round16(round16(dy fp32(o)) round16(1 - s)) s).
+ */
+int sla2h_attn_gate_fwd(const void* o, const void* g, int dtype, int B, int H, int64_t L,
+                        void* out, void* stream);
+int sla2h_attn_gate_bwd(const void* dy, const void* o, const void* g, int dtype, int B, int H,
+                        int64_t L, void* dout, void* dg, void* stream);
+
 int sla2h_rmsnorm_fwd16(const float* x, int64_t rows, int D, int64_t sx, const float* w,
                         float eps, int out_dtype, void* y, void* stream);
 int sla2h_rmsnorm_bwd_sum(const float* x, int64_t rows, int D, int64_t sx, const float* w,

@@ -338,3 +338,108 @@ def test_residual_scale_forward_backward(dt, dim):
     assert torch.equal(xg.grad.cpu(), xc.grad)
     assert torch.equal(ag.grad.cpu(), ac.grad)
     assert ((sg.grad.cpu() - sc.grad).abs().max() / sc.grad.abs().max()).item() < 1e-6
+
+
+@pytest.mark.parametrize("dt", [torch.bfloat16, torch.float16])
+def test_attn_operands_and_gate_match_torch(dt):
+    """The fused operand layout (cat of the halves, the shared key band expanded
+    over the heads, permute, .half()) and the fused output gate (permute,
+    .to(float32), fp32 gate, the projection's autocast cast) against torch's own
+    ops on the same GPU tensors: operands and their gradients bit for bit; the
+    gate's output and gradients within one unit in the last place (the
+    sigmoid's exponential may differ by an fp32 ulp)."""
+    from imfvideo_amd.imf_dit_video import _AttnGateFunction, _AttnInFunction
+    say("attention operands and gate", dt)
+    g = torch.Generator().manual_seed(7)
+    B, L, H = 2, 333, 8
+    qn = torch.randn(B, L, H, 32, generator=g).cuda()            # fp32 norm output
+    qr = torch.randn(B, L, H, 32, generator=g).to(dt).cuda()
+    kn = torch.randn(B, L, H, 32, generator=g).cuda()
+    kr = torch.randn(B, L, 1, 32, generator=g).to(dt).cuda()
+    kv = torch.randn(B, L, H, 96, generator=g).to(dt).cuda()
+    dq, dk, dv = (torch.randn(B, H, L, 64, generator=g).half().cuda() for _ in range(3))
+    leaves = lambda: [t.clone().requires_grad_(True) for t in (qn, qr, kn, kr, kv)]
+
+    a = leaves()
+    qh, kh, vh = _AttnInFunction.apply(a[0], a[1], a[2], a[3], a[4][..., 32:])
+    torch.autograd.backward((qh, kh, vh), (dq, dk, dv))
+    b = leaves()
+    q = torch.cat([b[0], b[1]], -1)
+    k = torch.cat([b[2], b[3].expand(B, L, H, 32)], -1)
+    tm = lambda x: x.permute(0, 2, 1, 3).half().contiguous()
+    qe, ke, ve = tm(q), tm(k), tm(b[4][..., 32:])
+    torch.autograd.backward((qe, ke, ve), (dq, dk, dv))
+    torch.cuda.synchronize()
+    for got, want in ((qh, qe), (kh, ke), (vh, ve)):
+        assert torch.equal(got, want)
+    for i, (x, y) in enumerate(zip(a, b)):
+        assert x.grad.dtype == y.grad.dtype and torch.equal(x.grad, y.grad), i
+
+    o = (torch.randn(B, H, L, 64, generator=g) * 2).half().cuda()
+    gl = (torch.randn(B, L, H * 64, generator=g) * 3).to(dt).cuda()
+    dy = torch.randn(B, L, H * 64, generator=g).to(dt).cuda()
+    o1, g1 = o.clone().requires_grad_(True), gl.clone().requires_grad_(True)
+    y1 = _AttnGateFunction.apply(o1, g1)
+    y1.backward(dy)
+    o2, g2 = o.clone().requires_grad_(True), gl.clone().requires_grad_(True)
+    y2 = (o2.permute(0, 2, 1, 3).to(torch.float32).reshape(B, L, H * 64)
+          * torch.sigmoid(g2)).to(dt)
+    y2.backward(dy)
+    torch.cuda.synchronize()
+    assert y1.dtype == dt and o1.grad.dtype == torch.float16 and g1.grad.dtype == dt
+    for got, want, u in ((y1, y2, ULP[dt]), (o1.grad, o2.grad, ULP[torch.float16]),
+                         (g1.grad, g2.grad, ULP[dt])):
+        got, want = got.detach().float().cpu(), want.detach().float().cpu()
+        bad = (got - want).abs() > u * want.abs() + 1e-30
+        print(f"  differ {bad.float().mean().item():.2e}", flush=True)
+        assert not bad.any()
+
+
+def test_block_fused_attention_path_matches_eager_layout():
+    """A TransformerBlock under bf16 autocast with the fused attention operand /
+    gate path and the same block on the eager cat / permute / gate path: outputs
+    within one bf16 ulp and gradients to fp32 summation order."""
+    from functools import partial
+    import imfvideo_amd.imf_dit_video as M
+    from imfvideo_amd.sla2_cube_qat import SLA2CubeQATAttentionImpl
+    say("block with / without the fused attention operands")
+    torch.manual_seed(0)
+    impl = partial(SLA2CubeQATAttentionImpl, seq_len=640, num_heads=8, grid=(4, 8, 20),
+                   tile=(4, 4, 4), topk=0.5, pre_permuted=True)
+    blk = M.TransformerBlock(512, 8, 256, 128, 32, 32, 64, mlp_ratio=4,
+                             weight_init_constant=0.5, attn_impl=impl).cuda()
+    with torch.no_grad():
+        blk.attn_scale.fill_(0.1)
+        blk.mlp_scale.fill_(0.1)
+    g = torch.Generator().manual_seed(2)
+    L = 640
+    x = torch.randn(2, L, 512, generator=g).cuda()
+    cos, sin = (t.cuda() for t in M.precompute_axial_rope_3d(32, (4, 8, 20), 0,
+                                                             axis_dims=(8, 12, 12)))
+    dy = torch.randn(2, L, 512, generator=g).cuda()
+
+    def run(fused):
+        saved = M._tile_major_operands_ok
+        if not fused:
+            M._tile_major_operands_ok = lambda *a: False
+        try:
+            blk.zero_grad(set_to_none=True)
+            xg = x.clone().requires_grad_(True)
+            with torch.autocast("cuda", dtype=torch.bfloat16):
+                out = blk(xg, cos, sin)
+            out.backward(dy)
+            torch.cuda.synchronize()
+            return out.detach(), xg.grad, {k: p.grad.clone() for k, p in blk.named_parameters()
+                                           if p.grad is not None}
+        finally:
+            M._tile_major_operands_ok = saved
+
+    o1, dx1, g1 = run(True)
+    o0, dx0, g0 = run(False)
+    rel = lambda a, b: ((a - b).norm() / b.norm().clamp_min(1e-30)).item()
+    print(f"  out max {(o1 - o0).abs().max().item():.2e} dx rel {rel(dx1, dx0):.2e}", flush=True)
+    assert ((o1 - o0).abs() <= 2.0 ** -7 * o0.abs() + 1e-6).all()
+    assert rel(dx1, dx0) < 1e-4
+    assert g1.keys() == g0.keys() and len(g0) > 10
+    for k in g0:
+        assert rel(g1[k], g0[k]) < 1e-3, k
