@@ -251,8 +251,11 @@ __global__ __launch_bounds__(256, TAN ? 2 : 3) void fwd_jvp_kernel(FwdArgs a) {
     // from the integer maximum.  With fp16 operands and the tangent, T is
     // clamped to +-60000 before its fp16 conversion as in the reference: a
     // tile whose T would reach the clamp under the lazy maximum is recomputed
-    // at the exact running maximum of the wave's keys (mref), so the clamp
-    // acts exactly as with an exact online maximum and T always fits fp16.
+    // at the exact running maximum of the wave's keys (mref), so T always
+    // fits fp16 and the clamp cuts T about where an online maximum over the
+    // wave's keys would (the maximum is per wave, over half the keys, and the
+    // tiles go in ascending id order, so near the clamp the result depends on
+    // that split and order).
     constexpr float kThr = 8.f;
     constexpr bool kClampT = TAN && T16::kDtype == SLA2H_DTYPE_F16;
     // Row sum l = sum_k p on the matrix core: acc_lm accumulates an all-ones A
