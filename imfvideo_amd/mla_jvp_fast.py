@@ -23,7 +23,7 @@ import torch.nn.functional as F
 
 from . import _lib, ops
 from .sla2_cube_qat import sla2_cube_qat_jvp_fused
-from .sla2_mla_jvp import route_blocks, sla2_mla_jvp
+from .sla2_mla_jvp import _sla2_mla_jvp, route_blocks, sla2_mla_jvp
 
 __all__ = ["mla_params_from_block", "mla_fp16_cache", "attn_sublayer_jvp", "mlp_sublayer_jvp",
            "block_jvp", "pack_block", "build_fast_jvp_state"]
@@ -143,8 +143,9 @@ def _attn_sublayer_proj(h, dh, p, w16, cos, sin, eps, stage_events=None):
         sl = p["sla2"]
         lut, T = route_blocks(q, k, sl["topk"], sl["bq"], sl["bk"], proj_q=sl.get("proj_q"),
                               proj_k=sl.get("proj_k"))
-        o, do = sla2_mla_jvp(q, k, v, dq_, dk, dv_, sl["alpha"], sl["topk"], sl["bq"], sl["bk"],
-                             lut=lut, T=T)
+        # the LUT comes straight from route_blocks: no range check (a host sync)
+        o, do = _sla2_mla_jvp(q, k, v, dq_, dk, dv_, sl["alpha"], sl["topk"], sl["bq"], sl["bk"],
+                              lut, T, 64, False)
     else:  # dense softmax attention: every key block routed, alpha = 1
         nb = -(-S // 64)
         mq = -(-S // 64)

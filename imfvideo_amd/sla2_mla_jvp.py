@@ -62,6 +62,13 @@ def sla2_mla_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, bq, bk, lut=None, T=None
     divide bq; the kernel's work unit is fixed).  Returns (o, do), (B, H, L, 64)
     fp32.
     """
+    return _sla2_mla_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, bq, bk, lut, T, block_m, True)
+
+
+def _sla2_mla_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, bq, bk, lut, T, block_m, check_ids):
+    """sla2_mla_jvp; check_ids=False skips the range check of a LUT that comes
+    straight from route_blocks (the check reduces the LUT and reads the result
+    back to the host, a synchronisation per call)."""
     B, H, L, D = q.shape
     if bq % block_m != 0:
         raise ValueError(f"block_m must divide bq: {block_m}, {bq}")
@@ -71,7 +78,8 @@ def sla2_mla_jvp(q, k, v, dq, dk, dv, alpha, topk_frac, bq, bk, lut=None, T=None
         lut, T = ops.route_1d(qc, kc, topk_frac, bq, bk)
     else:
         lut = lut.to(device=q.device, dtype=torch.int32).contiguous()
-        ops.check_lut_ids(lut, -(-L // bk))
+        if check_ids:
+            ops.check_lut_ids(lut, -(-L // bk))
     mq = -(-L // bq)
     if torch.is_tensor(alpha) and alpha.dim() == 2:
         a = alpha.detach().to(q.device, torch.float32)
