@@ -270,6 +270,9 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
     lse_r[qb] = ok ? a.lse[base + row] : INFINITY;
     del_r[qb] = ok ? a.delta[base + row] : 0.f;
   }
+  f32x4 ndel[4];  // -delta of each query group, the dP accumulators' start
+#pragma unroll
+  for (int qb = 0; qb < 4; ++qb) ndel[qb] = f32x4{-del_r[qb], -del_r[qb], -del_r[qb], -del_r[qb]};
   const unsigned char* rec = a.comp + ((int64_t)bh * a.Mq + mq) * kRecBytes;
   {  // H16 = round16(Hc + (round16(Hall) - Hall)); thread: row tid / 4, 16 columns
     const int d = tid >> 2, c0 = (tid & 3) * 16;
@@ -347,13 +350,17 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
     for (int qb = 0; qb < 4; ++qb) {
       f32x4 sc = mfma_16x16x32<T16>(f.k[0], qf[qb][0], f32x4{0.f, 0.f, 0.f, 0.f});
       sc = mfma_16x16x32<T16>(f.k[1], qf[qb][1], sc);
-      f32x4 dp = mfma_16x16x32<T16>(f.v[0], df[qb][0], f32x4{0.f, 0.f, 0.f, 0.f});
+      // dP - delta straight from the matrix core: the accumulator starts at
+      // -delta of the query (this lane's column), one VALU subtraction less
+      // per score (the difference rounds once, as fl(dP - delta) does, but
+      // the products are summed onto -delta)
+      f32x4 dp = mfma_16x16x32<T16>(f.v[0], df[qb][0], ndel[qb]);
       dp = mfma_16x16x32<T16>(f.v[1], df[qb][1], dp);
       float ds[4];
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float p = fast_exp2(fminf(sc[i] * a.c - lse_r[qb], 4.f));
-        ds[i] = sat(p * (dp[i] - del_r[qb]));
+        ds[i] = sat(p * dp[i]);
       }
       dsp[qb] = pack4<T16>(ds[0], ds[1], ds[2], ds[3]);
     }
@@ -654,7 +661,10 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
     if (mn >= 0) prefetch(mn);
 #pragma unroll
       for (int kb = 0; kb < 4; ++kb) {
-        f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f}, dp = sc;
+        // dP - delta from the matrix core (accumulator started at -delta of
+        // the query rows 4g + i this lane holds)
+        f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 dp = f32x4{-del4[0], -del4[1], -del4[2], -del4[3]};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
           const u32x4 kbv = *reinterpret_cast<const u32x4*>(&kv[0][16 * kb + r][32 * ks + 8 * g]);
@@ -668,7 +678,7 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           p[i] = fast_exp2(fminf(sc[i] * a.c - lse4[i], 4.f));
-          ds[i] = sat(p[i] * (dp[i] - del4[i]));
+          ds[i] = sat(p[i] * dp[i]);
         }
         const u32x2 pp = pack4<T16>(p[0], p[1], p[2], p[3]);
         const u32x2 dsp = pack4<T16>(ds[0], ds[1], ds[2], ds[3]);
