@@ -233,6 +233,34 @@ def cpu_baseline(cfg_d, tangent):
                       f"after 1 warm-up"}
 
 
+def timed_steps(step, steps, n_events, after=None):
+    """The timed region: `steps` back-to-back calls of step(None) between two
+    events, with synchronisation on both sides (the reported ms per step).
+    Then, untimed, `steps` more calls of step(ev) that record the n_events
+    events of ev inside the step for the stage breakdown: an event between two
+    kernels costs a few microseconds and keeps them from overlapping, so it
+    stays out of the reported figure.  after() runs after every step.
+    Returns (ms per step, per-step event lists)."""
+    ev_new = lambda: torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    start, end = ev_new(), ev_new()
+    start.record()
+    for _ in range(steps):
+        step(None)
+        if after is not None:
+            after()
+    end.record()
+    torch.cuda.synchronize()
+    ms = start.elapsed_time(end) / steps
+    evs = [[ev_new() for _ in range(n_events)] for _ in range(steps)]
+    for i in range(steps):
+        step(evs[i])
+        if after is not None:
+            after()
+    torch.cuda.synchronize()
+    return ms, evs
+
+
 TRAIN_STAGES = ["route", "quant_train", "sparse_fwd_qat", "linear_states_qat", "complement",
                 "linear_mix_qat", "bwd_prep", "complement_bwd", "bwd_dq", "bwd_dkdv"]
 
@@ -283,14 +311,7 @@ def train_bench(args):
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(11)] for _ in range(args.steps)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(args.steps):
-        step(evs[i])
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    ms, evs = timed_steps(step, args.steps, 11)
     stage_us = {name: statistics.mean(e[si].elapsed_time(e[si + 1]) for e in evs) * 1e3
                 for si, name in enumerate(TRAIN_STAGES)}
     pairs = B * H * nb * T  # n_tail = 0 at this shape
@@ -382,15 +403,13 @@ def block_step_bench(args):
     for _ in range(args.warmup):
         step_zero()
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(args.steps):
-        loss = step(evs[i])
-        blocks.zero_grad(set_to_none=True)
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    losses = []
+
+    def step_keep(ev):
+        losses.append(step(ev))
+
+    ms, evs = timed_steps(step_keep, args.steps, 4, after=lambda: blocks.zero_grad(set_to_none=True))
+    loss = losses[-1]
     st = {name: statistics.mean(e[k].elapsed_time(e[k + 1]) for e in evs) / depth
           for k, name in enumerate(["forward", "fast_jvp", "backward"])}
     print(json.dumps({
@@ -441,15 +460,13 @@ def mla_bench(args):
     for _ in range(args.warmup):
         attn_sublayer_jvp(x, dx, p, w16, cos, sin, 1e-6)
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(4)] for _ in range(args.steps)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    start.record()
-    for i in range(args.steps):
-        evs[i][0].record()
-        attn_sublayer_jvp(x, dx, p, w16, cos, sin, 1e-6, stage_events=evs[i][1:])
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    def step(ev):
+        if ev is None:
+            return attn_sublayer_jvp(x, dx, p, w16, cos, sin, 1e-6)
+        ev[0].record()
+        return attn_sublayer_jvp(x, dx, p, w16, cos, sin, 1e-6, stage_events=ev[1:])
+
+    ms, evs = timed_steps(step, args.steps, 4)
     st = {name: statistics.mean(e[k].elapsed_time(e[k + 1]) for e in evs) * 1e3
           for k, name in enumerate(["norm_gemms_head_prep", "sla2_mla_jvp", "gate_out_proj"])}
     print(json.dumps({
@@ -543,15 +560,7 @@ def main():
     for _ in range(args.warmup):
         step()
     torch.cuda.synchronize()
-    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(6)] for _ in range(args.steps)]
-    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-    torch.cuda.synchronize()
-    start.record()
-    for i in range(args.steps):
-        step(evs[i])
-    end.record()
-    torch.cuda.synchronize()
-    ms = start.elapsed_time(end) / args.steps
+    ms, evs = timed_steps(step, args.steps, 6)
     stage_us = {}
     for si, name in enumerate(STAGES):
         stage_us[name] = statistics.mean(e[si].elapsed_time(e[si + 1]) for e in evs) * 1e3
