@@ -324,10 +324,11 @@ __device__ __forceinline__ u32x4 expand_mask8(uint32_t b) {
 // 1 where tile n = 32 kc + j < Np is not routed for query block m < Mb.
 // With zb given, the workgroup also writes the zc (and, with dzb, dzc) parts
 // of its 16 query blocks' records: the same 0/1-mask product as the GEMM
-// below (bf16 hi + lo halves of zb, chunks of 32 tiles in the same order),
-// wave w owning columns 16w..16w+15.  This keeps the 64- and 128-column z
-// parts out of the GEMM's grid.
-__global__ __launch_bounds__(256) void comp_mask_kernel(const int32_t* __restrict__ lut, int Mb,
+// below (bf16 hi + lo halves of zb, chunks of 32 tiles in the same order).
+// Wave w owns columns 16 (w % 4) .. + 15 of zc (w < 4) or of dzc (w >= 4,
+// eight waves with the tangent).  This keeps the 64- and 128-column z parts
+// out of the GEMM's grid.
+__global__ __launch_bounds__(512) void comp_mask_kernel(const int32_t* __restrict__ lut, int Mb,
                                                       int Np, int T, int MT, int NC,
                                                       uint32_t* __restrict__ cbits,
                                                       const float* __restrict__ zb,
@@ -335,9 +336,10 @@ __global__ __launch_bounds__(256) void comp_mask_kernel(const int32_t* __restric
                                                       unsigned char* __restrict__ comp) {
   extern __shared__ uint32_t selbits[];  // [16][NC]
   const int mt = blockIdx.x, bh = blockIdx.y, tid = threadIdx.x;
-  for (int i = tid; i < 16 * NC; i += 256) selbits[i] = 0u;
+  const int nthr = blockDim.x;
+  for (int i = tid; i < 16 * NC; i += nthr) selbits[i] = 0u;
   __syncthreads();
-  for (int i = tid; i < 16 * T; i += 256) {
+  for (int i = tid; i < 16 * T; i += nthr) {
     const int row = i / T, jj = i % T;
     const int m = mt * 16 + row;
     if (m >= Mb) continue;
@@ -345,7 +347,7 @@ __global__ __launch_bounds__(256) void comp_mask_kernel(const int32_t* __restric
     if ((unsigned)n < (unsigned)Np) atomicOr(&selbits[row * NC + (n >> 5)], 1u << (n & 31));
   }
   __syncthreads();
-  for (int i = tid; i < NC * 16; i += 256) {
+  for (int i = tid; i < NC * 16; i += nthr) {
     const int kc = i >> 4, row = i & 15;
     const int m = mt * 16 + row;
     const int nv = Np - 32 * kc;  // real tiles in this word
@@ -355,12 +357,11 @@ __global__ __launch_bounds__(256) void comp_mask_kernel(const int32_t* __restric
   if (zb == nullptr) return;
 
   const int w = tid >> 6, l = tid & 63, r = l & 15, g = l >> 4;
-  const bool tan = dzb != nullptr;
+  const int part = w >> 2, cw = w & 3;  // part 0: zc from zb, 1: dzc from dzb
   const bool rowok = mt * 16 + r < Mb;
   // tiles n >= Np read as 0 (buffer range check); four chunks of loads in flight
-  const auto rz = make_rsrc(zb + (int64_t)bh * Np * kT, (int64_t)Np * kT * 4);
-  const auto rdz = make_rsrc(tan ? dzb + (int64_t)bh * Np * kT : zb, (int64_t)Np * kT * 4);
-  const int coff = (16 * w + r) * 4;
+  const auto rz = make_rsrc((part ? dzb : zb) + (int64_t)bh * Np * kT, (int64_t)Np * kT * 4);
+  const int coff = (16 * cw + r) * 4;
   auto split = [](const float* x, u32x4& hi, u32x4& lo) {
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
@@ -370,18 +371,16 @@ __global__ __launch_bounds__(256) void comp_mask_kernel(const int32_t* __restric
                               x[2 * e + 1] - __builtin_bit_cast(float, h & 0xffff0000u));
     }
   };
-  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f}, dacc = acc;
+  f32x4 acc = f32x4{0.f, 0.f, 0.f, 0.f};
   constexpr int kU = 4;
   for (int kc0 = 0; kc0 < NC; kc0 += kU) {
-    float x[kU][8], dx[kU][8];
+    float x[kU][8];
 #pragma unroll
     for (int u = 0; u < kU; ++u)
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         const int off = (32 * (kc0 + u) + 8 * g + j) * (kT * 4) + coff;
         x[u][j] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rz, off, 0, 0));
-        dx[u][j] = tan ? __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(rdz, off, 0, 0))
-                       : 0.f;
       }
 #pragma unroll
     for (int u = 0; u < kU; ++u) {
@@ -395,21 +394,15 @@ __global__ __launch_bounds__(256) void comp_mask_kernel(const int32_t* __restric
       split(x[u], hi, lo);
       acc = mfma_bf16_16x16x32(am, hi, acc);
       acc = mfma_bf16_16x16x32(am, lo, acc);
-      if (tan) {
-        split(dx[u], hi, lo);
-        dacc = mfma_bf16_16x16x32(am, hi, dacc);
-        dacc = mfma_bf16_16x16x32(am, lo, dacc);
-      }
     }
   }
-  // lane (g, r) element i = C[query block 16 mt + 4g + i][column 16w + r]
+  // lane (g, r) element i = C[query block 16 mt + 4g + i][column 16 cw + r]
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
     const int m = mt * 16 + 4 * g + i;
     if (m >= Mb) continue;
     unsigned char* rec = comp + ((int64_t)bh * Mb + m) * kRecBytes;
-    reinterpret_cast<float*>(rec + 32768)[16 * w + r] = acc[i];
-    if (tan) reinterpret_cast<float*>(rec + 33024)[16 * w + r] = dacc[i];
+    reinterpret_cast<float*>(rec + 32768 + 256 * part)[16 * cw + r] = acc[i];
   }
 }
 
@@ -776,8 +769,8 @@ extern "C" int sla2h_complement(const float* Hb, const float* dHb, const float* 
   auto out = static_cast<unsigned char*>(comp);
   // mask bits plus the z parts of the records; the GEMM takes the H parts only
   // (128 or 64 column tiles per head: whole rounds of workgroups)
-  comp_mask_kernel<<<dim3(MT, B * H), 256, (size_t)16 * NC * 4, st>>>(lut, Mb, Np, T, MT, NC,
-                                                                      cbits, zb, dzb, out);
+  comp_mask_kernel<<<dim3(MT, B * H), tan ? 512 : 256, (size_t)16 * NC * 4, st>>>(
+      lut, Mb, Np, T, MT, NC, cbits, zb, dzb, out);
   int err = (int)hipGetLastError();
   if (err) return err;
   const int ncols = tan ? 8192 : 4096;
