@@ -301,31 +301,49 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
 
   const auto rk = make_rsrc(a.k + base * kT, L * kT * 2);  // key rows past L read as 0
   const auto rv = make_rsrc(a.v + base * kT, L * kT * 2);
-  const int rowoff = ((16 * w + r) * kT + 8 * g) * 2;
-  // The wave's K rows of two tiles, staged in its own 8 KB of the merge
-  // buffer (free during the key loop: the sort is done, the partial sums come
-  // after it) for the transposed reads of the K^T operands; rows padded to
-  // 144 bytes against bank conflicts.
+  // The wave's K and V rows of a tile (its 16 keys, 2 KB each) load as two
+  // contiguous 1 KB halves (lane l: row 8 h + l / 8 of the 16, bytes
+  // 16 (l % 8) ..): whole cache lines per load, where loading the MFMA
+  // fragments directly (lane: one row, 16 bytes of each half-row) touches
+  // twice the lines per instruction.  The rows go to the wave's own staging
+  // slots in the merge buffer (free during the key loop: the sort is done,
+  // the partial sums come after it), K in its first 8 KB and V in its second,
+  // rows padded to 144 bytes against bank conflicts; the K and V fragments
+  // and the transposed K^T operands are read back from there.
   constexpr int kKs = 144;
+  const int rowoff = ((16 * w + (l >> 3)) * kT) * 2 + 16 * (l & 7);
   unsigned char* kst = reinterpret_cast<unsigned char*>(&mb[0][w][0][0][0]);
+  unsigned char* vst = reinterpret_cast<unsigned char*>(&mb[1][w][0][0][0]);
 
-  // score-side operands: the K and V rows of the wave's 16 keys (the K rows
-  // also give the K^T operands of the dq product through the staging slots)
+  // score-side operands: the K and V rows of the wave's 16 keys as loaded
+  // (the K rows also give the K^T operands of the dq product)
   struct Frags {
     u32x4 k[2], v[2];
   };
   auto load = [&](int j, Frags& f) {
     const int n = __builtin_amdgcn_readfirstlane(tiles[j]);
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {  // tile offset in voffset: range-checked, rows past L read 0
-      f.k[ks] = buf_load16(rk, n * kT * kT * 2 + rowoff + 64 * ks, 0);
-      f.v[ks] = buf_load16(rv, n * kT * kT * 2 + rowoff + 64 * ks, 0);
+    for (int h = 0; h < 2; ++h) {  // tile offset in voffset: range-checked, rows past L read 0
+      f.k[h] = buf_load16(rk, n * kT * kT * 2 + rowoff + h * 8 * kT * 2, 0);
+      f.v[h] = buf_load16(rv, n * kT * kT * 2 + rowoff + h * 8 * kT * 2, 0);
     }
   };
-  auto stage_k = [&](const Frags& f, int slot) {
+  auto stage = [&](const Frags& f, int slot) {
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks)
-      *reinterpret_cast<u32x4*>(kst + slot * 16 * kKs + r * kKs + 64 * ks + 16 * g) = f.k[ks];
+    for (int h = 0; h < 2; ++h) {
+      const int o = slot * 16 * kKs + (8 * h + (l >> 3)) * kKs + 16 * (l & 7);
+      *reinterpret_cast<u32x4*>(kst + o) = f.k[h];
+      *reinterpret_cast<u32x4*>(vst + o) = f.v[h];
+    }
+  };
+  // MFMA fragments: lane (g, r) row r of the 16, channels 32 ks + 8 g .. + 7
+  auto read_kv = [&](int slot, Frags& f) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      const int o = slot * 16 * kKs + r * kKs + 64 * ks + 16 * g;
+      f.k[ks] = *reinterpret_cast<const u32x4*>(kst + o);
+      f.v[ks] = *reinterpret_cast<const u32x4*>(vst + o);
+    }
   };
   // K^T operand [channel 16 ct + r][key 16 w + 4 g + e]: this lane addresses
   // key row 4 g + r / 4, channels 16 ct + 4 (r % 4) .. + 3
@@ -384,31 +402,34 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
                                          acc[qb][ct]);
   };
 
-  // Tiles in pairs: the second tile's operands are requested before the
-  // first tile's scores, the next pair's first tile right after them.  Each
-  // tile's K rows go to the wave's staging slot once they arrive; the K^T
-  // operands of the pair product are read back transposed.
+  // Tiles in pairs: the second tile's rows are requested before the first
+  // tile's scores, the next pair's first tile right after them.  Each tile's
+  // rows go to the wave's staging slot once they arrive; its fragments, and
+  // the K^T operands of the pair product, are read back from there.
   const int J = a.J;
-  Frags fa, fb;
+  Frags fa, fb, op;
   u32x2 kta[4], ktb[4];
   load(0, fa);
   int j = 0;
   for (; j + 1 < J; j += 2) {
     u32x2 dsa[4], dsb[4];
     load(j + 1, fb);
-    stage_k(fa, 0);
-    tile_ds(fa, dsa);
+    stage(fa, 0);
+    read_kv(0, op);
+    tile_ds(op, dsa);
     load(j + 2 < J ? j + 2 : J - 1, fa);
-    stage_k(fb, 1);
-    tile_ds(fb, dsb);
+    stage(fb, 1);
+    read_kv(1, op);
+    tile_ds(op, dsb);
     read_kt(0, kta);
     read_kt(1, ktb);
     dq_pair(kta, dsa, ktb, dsb);
   }
   if (j < J) {
     u32x2 dsa[4];
-    stage_k(fa, 0);
-    tile_ds(fa, dsa);
+    stage(fa, 0);
+    read_kv(0, op);
+    tile_ds(op, dsa);
     read_kt(0, kta);
     dq_single(kta, dsa);
   }
