@@ -609,9 +609,11 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
   // Query blocks m routed to this tile, ascending.  The operands of block m
   // (this wave's 16 query rows) are fetched one block ahead straight into the
   // wave's LDS region (buffer loads to LDS: no registers held in flight):
-  // slots of 64 lanes x 16 B -- Q rows (ks 0, 1), do_s rows (ks 0, 1), lane
-  // (g, r) holding row 16w + r, channels 32 ks + 8 g .. + 7 -- then 64 dwords
-  // of lse and 64 of delta (query 16w + (lane & 15)).  The Q^T and do_s^T
+  // slots of 64 lanes x 16 B -- Q rows 0-7, Q rows 8-15, do_s rows 0-7, do_s
+  // rows 8-15, each slot one contiguous 1 KB of the row-major tensor, lane l
+  // fetching row l / 8, 16-byte chunk (l % 8) ^ (l / 8) (the XOR spreads the
+  // 16 rows read by one fragment load over all banks) -- then 64 dwords of
+  // lse and 64 of delta (query 16w + (lane & 15)).  The Q^T and do_s^T
   // operands of dk and dv are read transposed from the same rows.  Rows past
   // L read as zero: such a query then has p = 1 but zero Q and do_s rows, so
   // it adds exactly zero to dk and dv (as with a masked p).
@@ -621,12 +623,12 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
   const auto rdl = make_rsrc(a.delta + base, L * 4);
   unsigned char* pf = pool + w * kPfWave;
   auto prefetch = [&](int m) {
-    const int rowb = (m * kT + 16 * w + r) * (kT * 2) + 16 * g;
+    const int rowb = (m * kT + 16 * w + (l >> 3)) * (kT * 2) + 16 * ((l & 7) ^ (l >> 3));
     const int qo = (m * kT + 16 * w + (l & 15)) * 4;
     lds_load16(rq, pf + 0 * kPfSlot, rowb);
-    lds_load16(rq, pf + 1 * kPfSlot, rowb + 64);
+    lds_load16(rq, pf + 1 * kPfSlot, rowb + 8 * kT * 2);
     lds_load16(rdo, pf + 2 * kPfSlot, rowb);
-    lds_load16(rdo, pf + 3 * kPfSlot, rowb + 64);
+    lds_load16(rdo, pf + 3 * kPfSlot, rowb + 8 * kT * 2);
     lds_load4(rls, pf + 4 * kPfSlot, qo);
     lds_load4(rdl, pf + 4 * kPfSlot + 256, qo);
   };
@@ -651,20 +653,22 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
     u32x2 qT[4], dT[4];
     float lse4[4], del4[4];
     {
-      const unsigned char* src = pf + l * 16;
+      // Q, do_s A operands: lane (g, r) takes row r, chunk 4 ks + g
 #pragma unroll
       for (int ks = 0; ks < 2; ++ks) {
-        qa[ks] = *reinterpret_cast<const u32x4*>(src + ks * kPfSlot);
-        da[ks] = *reinterpret_cast<const u32x4*>(src + (2 + ks) * kPfSlot);
+        const int off = (r >> 3) * kPfSlot + ((r & 7) * 8 + ((4 * ks + g) ^ (r & 7))) * 16;
+        qa[ks] = *reinterpret_cast<const u32x4*>(pf + off);
+        da[ks] = *reinterpret_cast<const u32x4*>(pf + 2 * kPfSlot + off);
       }
       // Q^T, do_s^T operands [channel 16 ct + r][query 16 w + 4 g + e], read
-      // transposed from the rows: this lane addresses row 4 g + r / 4,
-      // channels 16 ct + 4 (r % 4) .. + 3, held in slot ct / 2 by the prefetch
-      // lane 16 (2 (ct % 2) + (r % 4) / 2) + row, at byte 8 (r % 2) of its 16
+      // transposed from the rows: this lane addresses row rho = 4 g + r / 4,
+      // channels 16 ct + 4 (r % 4) .. + 3, i.e. chunk 2 ct + (r % 4) / 2 of
+      // that row at byte 8 (r % 2), placed by the prefetch as above
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
-        const int off = (ct >> 1) * kPfSlot +
-                        (16 * (2 * (ct & 1) + ((r & 3) >> 1)) + 4 * g + (r >> 2)) * 16 + 8 * (r & 1);
+        const int rho = 4 * g + (r >> 2);
+        const int off = (rho >> 3) * kPfSlot +
+                        ((rho & 7) * 8 + ((2 * ct + ((r & 3) >> 1)) ^ (rho & 7))) * 16 + 8 * (r & 1);
         qT[ct] = lds_read_tr16(pf + off);
         dT[ct] = lds_read_tr16(pf + 2 * kPfSlot + off);
       }
