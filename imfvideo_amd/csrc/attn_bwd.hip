@@ -645,6 +645,14 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
     return m;
   };
 
+  u32x4 kres[4][2], vres[4][2];  // K, V fragments of the tile, held for the whole loop
+#pragma unroll
+  for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      kres[kb][ks] = *reinterpret_cast<const u32x4*>(&kv[0][16 * kb + r][32 * ks + 8 * g]);
+      vres[kb][ks] = *reinterpret_cast<const u32x4*>(&kv[1][16 * kb + r][32 * ks + 8 * g]);
+    }
   int m = next_block();
   if (m >= 0) prefetch(m);
   while (m >= 0) {
@@ -692,8 +700,8 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
         f32x4 dp = f32x4{-del4[0], -del4[1], -del4[2], -del4[3]};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const u32x4 kbv = *reinterpret_cast<const u32x4*>(&kv[0][16 * kb + r][32 * ks + 8 * g]);
-          const u32x4 vbv = *reinterpret_cast<const u32x4*>(&kv[1][16 * kb + r][32 * ks + 8 * g]);
+          const u32x4 kbv = kres[kb][ks];
+          const u32x4 vbv = vres[kb][ks];
           sc = mfma_16x16x32<T16>(qa[ks], kbv, sc);
           dp = mfma_16x16x32<T16>(da[ks], vbv, dp);
         }
