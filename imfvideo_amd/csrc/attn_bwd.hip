@@ -81,74 +81,78 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
   __shared__ float qps[kT][kT + 1];  // qphi [row][d]
   __shared__ float gs[kT][kT + 1];   // saturated g [row][e]
   __shared__ float ss[kT];
+  __shared__ float zp[4][kT];        // partial z sums of the four row quarters
   __shared__ float red[4];
 
+  // thread: rows rb and rb + 32, channels c0 .. c0 + 7 (a wave's 16-byte
+  // loads of one tensor cover 8 whole rows, 1 KB contiguous)
   const int blk = blockIdx.x, bh = blockIdx.y, h = bh % a.H;
-  const int tid = threadIdx.x, r = tid >> 2, c0 = (tid & 3) * 16;
-  const int64_t row = (int64_t)blk * kT + r;
-  const bool valid = row < a.L;
-  const int64_t off = ((int64_t)bh * a.L + row) * kT + c0;
-
-  auto ld = [&](const uint16_t* src, uint16_t* x) {
-    if (valid) {
-      const uint4* p = reinterpret_cast<const uint4*>(src + off);
-      const uint4 u0 = p[0], u1 = p[1];
-      const uint32_t w[8] = {u0.x, u0.y, u0.z, u0.w, u1.x, u1.y, u1.z, u1.w};
-#pragma unroll
-      for (int i = 0; i < 8; ++i) {
-        x[2 * i] = (uint16_t)(w[i] & 0xffff);
-        x[2 * i + 1] = (uint16_t)(w[i] >> 16);
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 16; ++i) x[i] = 0;
-    }
-  };
-  auto st16 = [&](uint16_t* dst, const uint16_t* x) {
-    uint32_t w[8];
-#pragma unroll
-    for (int i = 0; i < 8; ++i) w[i] = pack2(x[2 * i], x[2 * i + 1]);
-    uint4* p = reinterpret_cast<uint4*>(dst + off);
-    p[0] = make_uint4(w[0], w[1], w[2], w[3]);
-    p[1] = make_uint4(w[4], w[5], w[6], w[7]);
-  };
-
-  uint16_t dob[16], osb[16], olb[16], qpb[16], g16b[16], dsb[16];
-  ld(a.dout, dob);
-  ld(a.o_s, osb);
-  ld(a.o_l, olb);
-  ld(a.qphi, qpb);
+  const int tid = threadIdx.x, rb = tid >> 3, c0 = (tid & 7) * 8;
   const float al = a.alpha[(int64_t)h * a.alpha_stride + (blk >> a.qshift)];
-  const float den = valid ? a.den[(int64_t)bh * a.L + row] : 1.f;
-  float dsum = 0.f, segp = 0.f, ssum = 0.f;
+
+  uint4 u[2][4];  // [row half][dout, o_s, o_l, qphi]
 #pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const float d = T16::to_f32(dob[i]);
-    const float os = T16::to_f32(osb[i]), ol = T16::to_f32(olb[i]);
-    // (do * a).to(16-bit), (do * (1 - a)).to(16-bit) of the reference's split
-    // kernel: the fp32 products round before the 16-bit conversion
-    dsb[i] = T16::from_f32(d * al);
-    const float dl = r16<T16>(d * (1.f - al));
-    dsum += os * T16::to_f32(dsb[i]);
-    segp += d * (os - ol);
-    ssum += dl * ol;
-    const float g = sat(dl / den);
-    gs[r][c0 + i] = g;
-    g16b[i] = T16::from_f32(g);
-    qps[r][c0 + i] = T16::to_f32(qpb[i]);
+  for (int hf = 0; hf < 2; ++hf) {
+    const int64_t row = (int64_t)blk * kT + rb + 32 * hf;
+    const int64_t off = ((int64_t)bh * a.L + row) * kT + c0;
+    const bool valid = row < a.L;
+    const uint16_t* src[4] = {a.dout, a.o_s, a.o_l, a.qphi};
+#pragma unroll
+    for (int t = 0; t < 4; ++t)
+      u[hf][t] = valid ? *reinterpret_cast<const uint4*>(src[t] + off) : make_uint4(0, 0, 0, 0);
   }
-  dsum += __shfl_xor(dsum, 1, 64);
-  dsum += __shfl_xor(dsum, 2, 64);
-  ssum += __shfl_xor(ssum, 1, 64);
-  ssum += __shfl_xor(ssum, 2, 64);
-  const float srow = valid ? ssum / den : 0.f;
-  if ((tid & 3) == 0) ss[r] = srow;
-  if (valid) {
-    st16(a.dos, dsb);
-    st16(a.g16, g16b);
-    if ((tid & 3) == 0) {
-      a.delta[(int64_t)bh * a.L + row] = dsum;
-      a.s[(int64_t)bh * a.L + row] = srow;
+  float segp = 0.f;
+#pragma unroll
+  for (int hf = 0; hf < 2; ++hf) {
+    const int r = rb + 32 * hf;
+    const int64_t row = (int64_t)blk * kT + r;
+    const bool valid = row < a.L;
+    const int64_t off = ((int64_t)bh * a.L + row) * kT + c0;
+    const float den = valid ? a.den[(int64_t)bh * a.L + row] : 1.f;
+    const uint32_t wd[4][4] = {{u[hf][0].x, u[hf][0].y, u[hf][0].z, u[hf][0].w},
+                               {u[hf][1].x, u[hf][1].y, u[hf][1].z, u[hf][1].w},
+                               {u[hf][2].x, u[hf][2].y, u[hf][2].z, u[hf][2].w},
+                               {u[hf][3].x, u[hf][3].y, u[hf][3].z, u[hf][3].w}};
+    float dsum = 0.f, ssum = 0.f;
+    uint32_t dso[4], g16o[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      uint16_t dsb[2], gb[2];
+#pragma unroll
+      for (int x = 0; x < 2; ++x) {
+        const int sh = 16 * x;
+        const float d = T16::to_f32((uint16_t)(wd[0][e] >> sh));
+        const float os = T16::to_f32((uint16_t)(wd[1][e] >> sh));
+        const float ol = T16::to_f32((uint16_t)(wd[2][e] >> sh));
+        // (do * a).to(16-bit), (do * (1 - a)).to(16-bit) of the reference's
+        // split kernel: the fp32 products round before the 16-bit conversion
+        dsb[x] = T16::from_f32(d * al);
+        const float dl = r16<T16>(d * (1.f - al));
+        dsum += os * T16::to_f32(dsb[x]);
+        segp += d * (os - ol);
+        ssum += dl * ol;
+        const float g = sat(dl / den);
+        gs[r][c0 + 2 * e + x] = g;
+        gb[x] = T16::from_f32(g);
+        qps[r][c0 + 2 * e + x] = T16::to_f32((uint16_t)(wd[3][e] >> sh));
+      }
+      dso[e] = pack2(dsb[0], dsb[1]);
+      g16o[e] = pack2(gb[0], gb[1]);
+    }
+#pragma unroll
+    for (int m = 1; m <= 4; m <<= 1) {
+      dsum += __shfl_xor(dsum, m, 64);
+      ssum += __shfl_xor(ssum, m, 64);
+    }
+    const float srow = valid ? ssum / den : 0.f;
+    if ((tid & 7) == 0) ss[r] = srow;
+    if (valid) {
+      *reinterpret_cast<uint4*>(a.dos + off) = make_uint4(dso[0], dso[1], dso[2], dso[3]);
+      *reinterpret_cast<uint4*>(a.g16 + off) = make_uint4(g16o[0], g16o[1], g16o[2], g16o[3]);
+      if ((tid & 7) == 0) {
+        a.delta[(int64_t)bh * a.L + row] = dsum;
+        a.s[(int64_t)bh * a.L + row] = srow;
+      }
     }
   }
 #pragma unroll
@@ -158,7 +162,9 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
   if (tid == 0)
     atomicAdd(a.seg + (int64_t)h * a.Mq + (blk >> a.qshift), (red[0] + red[1]) + (red[2] + red[3]));
 
-  // P[d][e] = sum_rows qphi[row][d] g[row][e] on fp32 MFMA: wave w owns d rows 16w..16w+15
+  // P[d][e] = sum_rows qphi[row][d] g[row][e] on fp32 MFMA, computed as P^T so
+  // that a lane holds four consecutive e of one d (16-byte stores): wave w owns
+  // d 16w .. 16w + 15, lane (lg, lr) d = 16w + lr, e = 16et + 4lg .. + 3
   {
     const int w = tid >> 6, l = tid & 63, lr = l & 15, lg = l >> 4;
     f32x4 acc[4];
@@ -167,21 +173,24 @@ __global__ __launch_bounds__(256) void bwd_prep_kernel(PrepArgs a) {
 #pragma unroll 4
     for (int kk = 0; kk < 16; ++kk) {
       const int rw = 4 * kk + lg;
-      const float av = qps[rw][16 * w + lr];
+      const float bv = qps[rw][16 * w + lr];
 #pragma unroll
-      for (int et = 0; et < 4; ++et) acc[et] = mfma_f32_16x16x4(av, gs[rw][16 * et + lr], acc[et]);
+      for (int et = 0; et < 4; ++et) acc[et] = mfma_f32_16x16x4(gs[rw][16 * et + lr], bv, acc[et]);
     }
-    float* P = a.P + ((int64_t)bh * a.Nb + blk) * (kT * kT);
+    float* P = a.P + ((int64_t)bh * a.Nb + blk) * (kT * kT) + (16 * w + lr) * kT + 4 * lg;
 #pragma unroll
-    for (int et = 0; et < 4; ++et)
-#pragma unroll
-      for (int i = 0; i < 4; ++i) P[(16 * w + 4 * lg + i) * kT + 16 * et + lr] = acc[et][i];
+    for (int et = 0; et < 4; ++et) *reinterpret_cast<f32x4*>(P + 16 * et) = acc[et];
   }
-  if (tid < kT) {
+  {  // z[d] = sum_rows qphi[row][d] s[row]: four row quarters, then their sum
+    const int d = tid & 63, qr = tid >> 6;
     float z = 0.f;
-    for (int rw = 0; rw < kT; ++rw) z += qps[rw][tid] * ss[rw];
-    a.Pz[((int64_t)bh * a.Nb + blk) * kT + tid] = z;
+#pragma unroll 4
+    for (int rw = 16 * qr; rw < 16 * qr + 16; ++rw) z += qps[rw][d] * ss[rw];
+    zp[qr][d] = z;
   }
+  __syncthreads();
+  if (tid < kT)
+    a.Pz[((int64_t)bh * a.Nb + blk) * kT + tid] = (zp[0][tid] + zp[1][tid]) + (zp[2][tid] + zp[3][tid]);
 }
 
 // gfx950 transposing LDS read (ds_read_b64_tr_b16): within each group of 16
