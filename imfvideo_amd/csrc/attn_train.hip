@@ -47,6 +47,8 @@ struct TrainArgs {
   float c2;        // fl32(scale * log2(e))
 };
 
+constexpr float kLog2_127 = 6.98868469f;  // log2(127)
+
 template <typename T16>
 __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
   __shared__ int2 tiles[kMaxJ];  // (tile id, bits of sk)
@@ -161,16 +163,19 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
   //  * the tile's row maximum comes from the integer scores: with c > 0 and
   //    monotonic rounding, max_j fl(s_j c) = fl(max_j s_j c), one v_max3 per
   //    two scores instead of a conversion, two products and a maximum each;
-  //  * the exponent is one fma(s, c, -m) with c = fl(sq sk scale log2 e)
-  //    (the reference rounds s sq sk, then the product by scale log2 e, then
-  //    the difference: the results differ by an ulp or two of the exponent);
-  //  * P8 = rne(127 p) is read from the low byte of fl(127 p + 2^23) (0..127
-  //    for p <= 1 + 2^-20) and four of them are packed by byte permutes.
-  //    rne(127 p) equals trunc(127 p + 0.5) exactly: 127 p lies on a
-  //    half-integer only for p = 1/2 (127 is odd and prime), where both give
-  //    64; the reference's trunc(fl(127 p + 0.5)) differs where that sum
-  //    rounds up onto an integer (one entry in about 10^5).
-  // The masked tail tile keeps the reference's rounding steps.
+  //  * the exponent is one fma(s, c, -(m - log2 127)) with c = fl(sq sk
+  //    scale log2 e), which gives 127 p directly (the reference rounds s sq
+  //    sk, then the product by scale log2 e, then the difference, then p,
+  //    then 127 p: the results differ by a few ulps of 127 p);
+  //  * P8 = rne(127 p) by v_cvt_pk_u8_f32, which converts with round to
+  //    nearest even and packs the byte in one instruction.  rne(127 p) equals
+  //    trunc(127 p + 0.5) exactly: 127 p lies on a half-integer only for
+  //    p = 1/2 (127 is odd and prime), where both give 64; the reference's
+  //    trunc(fl(127 p + 0.5)) differs where that sum rounds up onto an
+  //    integer (one entry in about 10^5);
+  //  * l sums 127 p (divided by 127 once at the end).
+  // The masked tail tile keeps the reference's rounding steps (its l term is
+  // scaled by 127 once per tile).
   auto tile = [&](const Frags& f, int j, auto mask_tag) {
     constexpr bool MASK = decltype(mask_tag)::value;
     const int n = __builtin_amdgcn_readfirstlane(tiles[j].x);
@@ -204,6 +209,7 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
     lm = max_over_groups(lm);
     const float mn = fmaxf(m_i, lm);
     const float alpha = fast_exp2(m_i - mn);  // 0 on the first tile (m_i = -inf)
+    const float mn127 = mn - kLog2_127;       // exponent shift of 127 p
     float ls = 0.f;
     uint32_t pk[4];
 #pragma unroll
@@ -217,18 +223,19 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
           wd |= ((uint32_t)(int)fmaf(p, 127.f, 0.5f)) << (8 * i);  // p in [0, 1]: 0..127
         }
         pk[kb] = wd;
+        if (kb == 3) ls *= 127.f;  // l in units of p / 127, as on unmasked tiles
       } else {
-        uint32_t y[4];
+        // p127 = 127 p from the exponent (one shift per tile), l summed in
+        // units of p / 127, P8 = rne(p127) converted and packed in one
+        // instruction per byte (v_cvt_pk_u8_f32 rounds to nearest even)
+        uint32_t wd = 0;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const float p = fast_exp2(fmaf(s[4 * kb + i], c, -mn));
-          ls += p;
-          y[i] = __builtin_bit_cast(uint32_t, fmaf(p, 127.f, 8388608.f));
+          const float p127 = fast_exp2(fmaf(s[4 * kb + i], c, -mn127));
+          ls += p127;
+          wd = __builtin_amdgcn_cvt_pk_u8_f32(p127, i, wd);
         }
-        // bytes 0 of y0, y1, y2, y3
-        const uint32_t lo = __builtin_amdgcn_perm(y[1], y[0], 0x0c0c0400u);
-        const uint32_t hi = __builtin_amdgcn_perm(y[3], y[2], 0x0c0c0400u);
-        pk[kb] = __builtin_amdgcn_perm(hi, lo, 0x05040100u);
+        pk[kb] = wd;
       }
     }
     l_i = l_i * alpha + ls;
@@ -276,7 +283,7 @@ __global__ __launch_bounds__(256, 2) void sparse_fwd_qat_kernel(TrainArgs a) {
     __syncthreads();
   }
 
-  const float lt = sum_over_groups(l_i);
+  const float lt = sum_over_groups(l_i) * (1.f / 127.f);  // l_i counts 127 p
   const float rl = 1.f / lt;
   // lane (g, r) holds O^T[16 ct + 4g + i][query r]
   if (qok) {
