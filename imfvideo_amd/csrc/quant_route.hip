@@ -466,7 +466,7 @@ __global__ __launch_bounds__(256) void route_topk_kernel(const float* __restrict
 //      indices among them fill up to T (a 12-bit binary search over n);
 //   3. the T winners are compacted through LDS and bitonic-sorted across
 //      the lanes by their 64-bit keys (score word, then lower index first).
-template <int NK, int R>
+template <int NK, int R, bool V4>
 __global__ __launch_bounds__(256) void route_select_kernel(const float* __restrict__ qpool,
                                                            const float* __restrict__ kpool_t,
                                                            int Mb, int Np, int T, float scale,
@@ -500,12 +500,23 @@ __global__ __launch_bounds__(256) void route_select_kernel(const float* __restri
   const auto rk = make_rsrc(kt, (int64_t)kTile * Np * 4);
   for (int d0 = 0; d0 < kTile; d0 += DC) {
     __syncthreads();  // the previous chunk is consumed
+    if constexpr (V4) {
+      // Np % 4 == 0: a channel's row of Np floats is 16-byte aligned, so one
+      // 16-byte load carries 4 keys (a load at n < Np lies inside the row)
 #pragma unroll
-    for (int k = 0; k < DC * 64 * NK / 256; ++k) {
-      const int e = tid + 256 * k;
-      const int dd = e / (64 * NK), n = e % (64 * NK);
-      ksh[dd][n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
-                                                 rk, ((d0 + dd) * Np + n) * 4, 0, 0));
+      for (int k = 0; k < DC * 16 * NK / 256; ++k) {
+        const int e = tid + 256 * k;
+        const int dd = e / (16 * NK), n = 4 * (e % (16 * NK));
+        *reinterpret_cast<u32x4*>(&ksh[dd][n]) = buf_load16(rk, ((d0 + dd) * Np + n) * 4, 0);
+      }
+    } else {
+#pragma unroll
+      for (int k = 0; k < DC * 64 * NK / 256; ++k) {
+        const int e = tid + 256 * k;
+        const int dd = e / (64 * NK), n = e % (64 * NK);
+        ksh[dd][n] = __builtin_bit_cast(float, __builtin_amdgcn_raw_buffer_load_b32(
+                                                   rk, ((d0 + dd) * Np + n) * 4, 0, 0));
+      }
     }
     __syncthreads();
     if (active) {
@@ -876,7 +887,10 @@ extern "C" int sla2h_route_topk(const float* qpool, const float* kpool_t, int B,
     auto go = [&](auto nk, auto rows) {
       constexpr int NK = decltype(nk)::value, R = decltype(rows)::value;
       dim3 grid((Mb + 4 * R - 1) / (4 * R), B * H);
-      route_select_kernel<NK, R><<<grid, 256, 0, st>>>(qpool, kpool_t, Mb, Np, T, scale, lut, mask);
+      if (Np % 4 == 0)
+        route_select_kernel<NK, R, true><<<grid, 256, 0, st>>>(qpool, kpool_t, Mb, Np, T, scale, lut, mask);
+      else
+        route_select_kernel<NK, R, false><<<grid, 256, 0, st>>>(qpool, kpool_t, Mb, Np, T, scale, lut, mask);
     };
     if (Np <= 512)
       go(std::integral_constant<int, 8>{}, std::integral_constant<int, 1>{});
