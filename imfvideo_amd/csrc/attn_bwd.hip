@@ -18,11 +18,11 @@
 // Kernels: bwd_prep (per 64-row block: gradient split, delta, g, s, the alpha
 // segment sums and the per-block partial states P = qphi^T g and Pz =
 // qphi^T s), then the dq kernel (per query block, key-split waves) and the
-// dk/dv kernel (per key tile, query-split waves).  The complement GEMM of the
+// dk/dv kernel (per key tile, waves split as query half x key half).  The complement GEMM of the
 // partial states lives with the forward's complement (states.hip).
 //
-// The products that contract over 16 rows of a wave (dq over keys, dk and dv
-// over queries) take those rows transposed as their A operand: the wave holds
+// The products that contract over a wave's rows (dq over 16 keys, dk and dv over 32
+// queries) take those rows transposed as their A operand: the wave holds
 // the rows row-major in LDS and reads the operand with the gfx950 transposing
 // LDS read, so no transposed copy of q, k or do_s goes through memory.
 #include "common.h"
@@ -508,14 +508,16 @@ __global__ __launch_bounds__(256, 2) void bwd_dq_kernel(DqArgs a) {
 }
 
 // ---------------------------------------------------------------------------
-// dk, dv: one key tile per workgroup; wave w owns queries 16w..16w+15 of each
-// query block that routes the tile (ascending block order), all 64 keys.  K
-// and V rows sit in LDS.  Per block and key group kb: S^T = Q K^T and
-// dP = do_s V^T (lane (g, r) holds queries 16w+4g+i of key 16kb+r), p and
-// ds, then dv^T += do_s^T p and dk^T += Q^T ds over the wave's 16 queries.
-// The query-split partials are summed through LDS; wave w finishes keys
-// 16w..16w+15: dk_s, dv_s, the linear dkphi / dv_l from the backward
-// complement record, and the phi chain of K.
+// dk, dv: one key tile per workgroup; wave w = 2 qh + kh owns queries
+// 32qh..32qh+31 of each query block that routes the tile (ascending block
+// order) and keys 32kh..32kh+31, whose K and V fragments it holds in
+// registers.  Per block, key group kb and query sub-tile qt: S^T = Q K^T and
+// dP = do_s V^T (lane (g, r) holds queries 32qh+16qt+4g+i of key
+// 32kh+16kb+r), p and ds; then dv^T += do_s^T p and dk^T += Q^T ds over the
+// wave's 32 queries on K = 32 products.  The two query-half partials are
+// summed through LDS; wave w finishes keys 16w..16w+15: dk_s, dv_s, the
+// linear dkphi / dv_l from the backward complement record, and the phi
+// chain of K.
 // ---------------------------------------------------------------------------
 struct DkdvArgs {
   const uint16_t* q;
@@ -537,7 +539,7 @@ struct DkdvArgs {
 // (64 dwords each).  The four regions also hold the partial-sum exchange
 // after the loop (32 KB).
 constexpr int kPfSlot = 1024;
-constexpr int kPfWave = 4 * kPfSlot + 2 * 256;
+constexpr int kPfWave = 8 * kPfSlot + 2 * 256;
 constexpr int kPoolBytes = 4 * kPfWave > 32768 ? 4 * kPfWave : 32768;
 constexpr int kSelLds = 128;  // mask words staged in LDS (query blocks 0 .. 4095)
 // s_waitcnt immediates (gfx9 encoding): vmcnt(0) alone, lgkmcnt(0) alone
@@ -609,37 +611,52 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
   for (int j = tid; j < a.NCq && j < kSelLds; j += 256) selsh[j] = selrow[j];
   __syncthreads();
 
-  f32x4 dkT[4][4], dvT[4][4];  // [ct][kb]
+  // Wave w = 2 qh + kh takes query half qh (rows 32 qh .. + 31 of each routed
+  // block, two 16-row sub-tiles qt) and key half kh (keys 32 kh .. + 31, two
+  // 16-key groups kb'): 16 scores per lane per block, and the dk / dv products
+  // contract over the wave's 32 queries on K = 32 MFMAs (32 MFMAs per wave and
+  // block).  The two partials of a key half are summed after the loop.
+  const int qh = w >> 1, kh = w & 1;
+  f32x4 dkT[4][2], dvT[4][2];  // [ct][kb'] for keys 32 kh + 16 kb' + r
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) dkT[ct][kb] = dvT[ct][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int kb = 0; kb < 2; ++kb) dkT[ct][kb] = dvT[ct][kb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  u32x4 kres[2][2], vres[2][2];  // K, V fragments of the wave's keys, held for the whole loop
+#pragma unroll
+  for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) {
+      kres[kb][ks] = *reinterpret_cast<const u32x4*>(&kv[0][32 * kh + 16 * kb + r][32 * ks + 8 * g]);
+      vres[kb][ks] = *reinterpret_cast<const u32x4*>(&kv[1][32 * kh + 16 * kb + r][32 * ks + 8 * g]);
+    }
 
   // Query blocks m routed to this tile, ascending.  The operands of block m
-  // (this wave's 16 query rows) are fetched one block ahead straight into the
+  // (this wave's 32 query rows) are fetched one block ahead straight into the
   // wave's LDS region (buffer loads to LDS: no registers held in flight):
-  // slots of 64 lanes x 16 B -- Q rows 0-7, Q rows 8-15, do_s rows 0-7, do_s
-  // rows 8-15, each slot one contiguous 1 KB of the row-major tensor, lane l
-  // fetching row l / 8, 16-byte chunk (l % 8) ^ (l / 8) (the XOR spreads the
-  // 16 rows read by one fragment load over all banks) -- then 64 dwords of
-  // lse and 64 of delta (query 16w + (lane & 15)).  The Q^T and do_s^T
-  // operands of dk and dv are read transposed from the same rows.  Rows past
-  // L read as zero: such a query then has p = 1 but zero Q and do_s rows, so
-  // it adds exactly zero to dk and dv (as with a masked p).
+  // eight slots of 64 lanes x 16 B -- Q rows 0-7, 8-15, 16-23, 24-31, then the
+  // do_s rows alike, each slot one contiguous 1 KB of the row-major tensor,
+  // lane l fetching row l / 8, 16-byte chunk (l % 8) ^ (l / 8) (the XOR
+  // spreads the 16 rows read by one fragment load over all banks) -- then 64
+  // dwords of lse and 64 of delta (query 32 qh + (lane & 31)).  The two waves
+  // of a query half fetch the same rows, each into its own region, so no wave
+  // waits on another inside the loop.  Rows past L read as zero: such a query
+  // then has p = 1 but zero Q and do_s rows, so it adds exactly zero to dk and
+  // dv (as with a masked p).
   const auto rq = make_rsrc(a.q + base * kT, L * kT * 2);
   const auto rdo = make_rsrc(a.dos + base * kT, L * kT * 2);
   const auto rls = make_rsrc(a.lse + base, L * 4);
   const auto rdl = make_rsrc(a.delta + base, L * 4);
   unsigned char* pf = pool + w * kPfWave;
   auto prefetch = [&](int m) {
-    const int rowb = (m * kT + 16 * w + (l >> 3)) * (kT * 2) + 16 * ((l & 7) ^ (l >> 3));
-    const int qo = (m * kT + 16 * w + (l & 15)) * 4;
-    lds_load16(rq, pf + 0 * kPfSlot, rowb);
-    lds_load16(rq, pf + 1 * kPfSlot, rowb + 8 * kT * 2);
-    lds_load16(rdo, pf + 2 * kPfSlot, rowb);
-    lds_load16(rdo, pf + 3 * kPfSlot, rowb + 8 * kT * 2);
-    lds_load4(rls, pf + 4 * kPfSlot, qo);
-    lds_load4(rdl, pf + 4 * kPfSlot + 256, qo);
+    const int rowb = (m * kT + 32 * qh + (l >> 3)) * (kT * 2) + 16 * ((l & 7) ^ (l >> 3));
+    const int qo = (m * kT + 32 * qh + (l & 31)) * 4;
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl) lds_load16(rq, pf + sl * kPfSlot, rowb + sl * 8 * kT * 2);
+#pragma unroll
+    for (int sl = 0; sl < 4; ++sl) lds_load16(rdo, pf + (4 + sl) * kPfSlot, rowb + sl * 8 * kT * 2);
+    lds_load4(rls, pf + 8 * kPfSlot, qo);
+    lds_load4(rdl, pf + 8 * kPfSlot + 256, qo);
   };
   int kc = 0;
   uint32_t bits = 0u;
@@ -654,108 +671,116 @@ __global__ __launch_bounds__(256, 2) void bwd_dkdv_kernel(DkdvArgs a) {
     return m;
   };
 
-  u32x4 kres[4][2], vres[4][2];  // K, V fragments of the tile, held for the whole loop
-#pragma unroll
-  for (int kb = 0; kb < 4; ++kb)
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      kres[kb][ks] = *reinterpret_cast<const u32x4*>(&kv[0][16 * kb + r][32 * ks + 8 * g]);
-      vres[kb][ks] = *reinterpret_cast<const u32x4*>(&kv[1][16 * kb + r][32 * ks + 8 * g]);
-    }
   int m = next_block();
   if (m >= 0) prefetch(m);
   while (m >= 0) {
     __builtin_amdgcn_s_waitcnt(kWaitVm0);  // this wave's prefetch of block m has landed
-    u32x4 qa[2], da[2];
-    u32x2 qT[4], dT[4];
-    float lse4[4], del4[4];
+    u32x4 qa[2][2], da[2][2];  // [qt][ks]
+    u32x4 qT[4], dT[4];        // [ct]: queries of sub-tile 0 in .xy, of sub-tile 1 in .zw
+    float lse4[2][4], del4[2][4];
     {
-      // Q, do_s A operands: lane (g, r) takes row r, chunk 4 ks + g
+      // Q, do_s A operands: lane (g, r) takes row 16 qt + r, chunk 4 ks + g
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        const int off = (r >> 3) * kPfSlot + ((r & 7) * 8 + ((4 * ks + g) ^ (r & 7))) * 16;
-        qa[ks] = *reinterpret_cast<const u32x4*>(pf + off);
-        da[ks] = *reinterpret_cast<const u32x4*>(pf + 2 * kPfSlot + off);
-      }
-      // Q^T, do_s^T operands [channel 16 ct + r][query 16 w + 4 g + e], read
-      // transposed from the rows: this lane addresses row rho = 4 g + r / 4,
-      // channels 16 ct + 4 (r % 4) .. + 3, i.e. chunk 2 ct + (r % 4) / 2 of
-      // that row at byte 8 (r % 2), placed by the prefetch as above
+      for (int qt = 0; qt < 2; ++qt)
+#pragma unroll
+        for (int ks = 0; ks < 2; ++ks) {
+          const int rho = 16 * qt + r;
+          const int off = (rho >> 3) * kPfSlot + ((rho & 7) * 8 + ((4 * ks + g) ^ (rho & 7))) * 16;
+          qa[qt][ks] = *reinterpret_cast<const u32x4*>(pf + off);
+          da[qt][ks] = *reinterpret_cast<const u32x4*>(pf + 4 * kPfSlot + off);
+        }
+      // Q^T, do_s^T operands [channel 16 ct + r][query 16 qt + 4 g + e], read
+      // transposed from the rows: this lane addresses row rho = 16 qt + 4 g +
+      // r / 4, channels 16 ct + 4 (r % 4) .. + 3, i.e. chunk 2 ct + (r % 4) / 2
+      // of that row at byte 8 (r % 2), placed by the prefetch as above
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
-        const int rho = 4 * g + (r >> 2);
-        const int off = (rho >> 3) * kPfSlot +
-                        ((rho & 7) * 8 + ((2 * ct + ((r & 3) >> 1)) ^ (rho & 7))) * 16 + 8 * (r & 1);
-        qT[ct] = lds_read_tr16(pf + off);
-        dT[ct] = lds_read_tr16(pf + 2 * kPfSlot + off);
-      }
-      // lse, delta of queries 16w + 4g + i
-      const f32x4 ls = *reinterpret_cast<const f32x4*>(pf + 4 * kPfSlot + 16 * g);
-      const f32x4 dl = *reinterpret_cast<const f32x4*>(pf + 4 * kPfSlot + 256 + 16 * g);
+        u32x2 t[2][2];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        lse4[i] = ls[i];
-        del4[i] = dl[i];
+        for (int qt = 0; qt < 2; ++qt) {
+          const int rho = 16 * qt + 4 * g + (r >> 2);
+          const int off = (rho >> 3) * kPfSlot +
+                          ((rho & 7) * 8 + ((2 * ct + ((r & 3) >> 1)) ^ (rho & 7))) * 16 + 8 * (r & 1);
+          t[0][qt] = lds_read_tr16(pf + off);
+          t[1][qt] = lds_read_tr16(pf + 4 * kPfSlot + off);
+        }
+        qT[ct] = u32x4{t[0][0].x, t[0][0].y, t[0][1].x, t[0][1].y};
+        dT[ct] = u32x4{t[1][0].x, t[1][0].y, t[1][1].x, t[1][1].y};
+      }
+      // lse, delta of queries 32 qh + 16 qt + 4 g + i
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
+        const f32x4 ls = *reinterpret_cast<const f32x4*>(pf + 8 * kPfSlot + 64 * qt + 16 * g);
+        const f32x4 dl = *reinterpret_cast<const f32x4*>(pf + 8 * kPfSlot + 256 + 64 * qt + 16 * g);
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          lse4[qt][i] = ls[i];
+          del4[qt][i] = dl[i];
+        }
       }
     }
     __builtin_amdgcn_s_waitcnt(kWaitLgkm0);  // the region is read: free for the next block
     const int mn = next_block();
     if (mn >= 0) prefetch(mn);
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
+    for (int kb = 0; kb < 2; ++kb) {
+      u32x2 pp[2], dsp[2];
+#pragma unroll
+      for (int qt = 0; qt < 2; ++qt) {
         // dP - delta from the matrix core (accumulator started at -delta of
-        // the query rows 4g + i this lane holds)
+        // the query rows 16 qt + 4g + i this lane holds)
         f32x4 sc = f32x4{0.f, 0.f, 0.f, 0.f};
-        f32x4 dp = f32x4{-del4[0], -del4[1], -del4[2], -del4[3]};
+        f32x4 dp = f32x4{-del4[qt][0], -del4[qt][1], -del4[qt][2], -del4[qt][3]};
 #pragma unroll
         for (int ks = 0; ks < 2; ++ks) {
-          const u32x4 kbv = kres[kb][ks];
-          const u32x4 vbv = vres[kb][ks];
-          sc = mfma_16x16x32<T16>(qa[ks], kbv, sc);
-          dp = mfma_16x16x32<T16>(da[ks], vbv, dp);
+          sc = mfma_16x16x32<T16>(qa[qt][ks], kres[kb][ks], sc);
+          dp = mfma_16x16x32<T16>(da[qt][ks], vres[kb][ks], dp);
         }
-        // a key past L (zero K row, finite p) only feeds its own dk / dv
-        // column, which is never stored: no mask
+        // p and ds of a (query, key) pair feed only that key's dk / dv column.
+        // A key past L (zero K row) needs no mask and its p no clamp: whatever
+        // its p, its column is never stored.  A query past L has zero Q and
+        // do_s rows and lse 0, so p = 1 and it adds exactly zero.
         float p[4], ds[4];
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          p[i] = fast_exp2(fminf(sc[i] * a.c - lse4[i], 4.f));
+          p[i] = fast_exp2(sc[i] * a.c - lse4[qt][i]);
           ds[i] = sat(p[i] * dp[i]);
         }
-        const u32x2 pp = pack4<T16>(p[0], p[1], p[2], p[3]);
-        const u32x2 dsp = pack4<T16>(ds[0], ds[1], ds[2], ds[3]);
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          dvT[ct][kb] = mfma_16x16x16<T16>(dT[ct], pp, dvT[ct][kb]);
-          dkT[ct][kb] = mfma_16x16x16<T16>(qT[ct], dsp, dkT[ct][kb]);
-        }
+        pp[qt] = pack4<T16>(p[0], p[1], p[2], p[3]);
+        dsp[qt] = pack4<T16>(ds[0], ds[1], ds[2], ds[3]);
       }
+      // K = 32 over the wave's queries: k index 8 g + j is query 16 (j / 4) +
+      // 4 g + j % 4 in both operands
+      const u32x4 pb = u32x4{pp[0].x, pp[0].y, pp[1].x, pp[1].y};
+      const u32x4 db = u32x4{dsp[0].x, dsp[0].y, dsp[1].x, dsp[1].y};
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        dvT[ct][kb] = mfma_16x16x32<T16>(dT[ct], pb, dvT[ct][kb]);
+        dkT[ct][kb] = mfma_16x16x32<T16>(qT[ct], db, dkT[ct][kb]);
+      }
+    }
     m = mn;
   }
 
-  // sum the query-split partials: wave w keeps key group kb = w
+  // sum the two query-half partials of each key half: wave w keeps key group
+  // 16 w .. 16 w + 15 = key half w / 2, group w % 2, from waves w / 2 and 2 + w / 2
   f32x4 dkt[4], dvt[4];
 #pragma unroll
   for (int x = 0; x < 2; ++x) {
+    __syncthreads();
 #pragma unroll
-    for (int t = 0; t < 2; ++t) {
-      __syncthreads();
+    for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks)
+      for (int ct = 0; ct < 4; ++ct) mb[w][kb][ct][l] = x == 0 ? dkT[ct][kb] : dvT[ct][kb];
+    __syncthreads();
+    const int sh = w >> 1, sk = w & 1;
 #pragma unroll
-        for (int ct = 0; ct < 4; ++ct) mb[w][ks][ct][l] = x == 0 ? dkT[ct][2 * t + ks] : dvT[ct][2 * t + ks];
-      __syncthreads();
-      if ((w >> 1) == t) {
-        const int ks = w & 1;
-#pragma unroll
-        for (int ct = 0; ct < 4; ++ct) {
-          const f32x4 sum = (mb[0][ks][ct][l] + mb[1][ks][ct][l]) + (mb[2][ks][ct][l] + mb[3][ks][ct][l]);
-          if (x == 0)
-            dkt[ct] = sum;
-          else
-            dvt[ct] = sum;
-        }
-      }
+    for (int ct = 0; ct < 4; ++ct) {
+      const f32x4 sum = mb[sh][sk][ct][l] + mb[2 + sh][sk][ct][l];
+      if (x == 0)
+        dkt[ct] = sum;
+      else
+        dvt[ct] = sum;
     }
   }
 
